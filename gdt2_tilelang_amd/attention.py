@@ -1,0 +1,303 @@
+"""The functional op and the ``GatedDeltaNet2`` token mixer on the hip backend.
+
+Mirrors the reference's ``gdn2/attention.py``: ``gdn2_attention`` (``:102-164``),
+``resolve_backend`` (``:44-61``), ``GDN2Cache`` (``:172-183``) and the
+``GatedDeltaNet2`` module (``:232-491``) with the same parameter names, so a
+reference ``state_dict`` loads unchanged.
+
+Backends: ``"auto"`` resolves to ``"hip"`` on a GPU and to ``"torch"``
+elsewhere, like the reference's ``"tilelang"`` policy. The ``"torch"`` backend
+is the reference package's own CPU path and is not part of this package, so it
+raises ``NotImplementedError`` here; so does the backward.
+
+Two layer details differ on purpose:
+
+* ``init_cache`` keeps the recurrent state in ``dtype`` (fp32 by default) but
+  allocates the short-conv tail in the conv weights' dtype, so a bf16 layer can
+  decode (the reference allocates both in ``dtype`` and a bf16 layer's
+  ``conv1d`` then fails on the mixed dtypes);
+* the short-conv decode casts a cached tail to the activation dtype.
+"""
+
+from __future__ import annotations
+
+from dataclasses import dataclass
+
+import torch
+import torch.nn.functional as F
+from torch import nn
+
+from .config import DEFAULT_KERNEL_CONFIG, GDN2Config, GatedDeltaNet2Config
+from .forward import chunk_gdn2_fwd
+from .inference import gdn2_decode, gdn2_prefill
+
+__all__ = ["gdn2_attention", "GatedDeltaNet2", "GDN2Cache", "resolve_backend"]
+
+_BACKENDS = ("auto", "hip", "torch")
+
+
+def resolve_backend(backend: str, on_cuda: bool, needs_grad: bool) -> str:
+    """Turn ``"auto"`` into a concrete backend, or validate an explicit one.
+
+    Returns ``"hip"`` or ``"torch"``; raises ``ValueError`` for an unknown name
+    or for ``"hip"`` without a GPU.
+    """
+    if backend not in _BACKENDS:
+        raise ValueError(f"unknown backend {backend!r}; expected one of {_BACKENDS}")
+    if backend == "auto":
+        return "hip" if on_cuda else "torch"
+    if backend != "torch" and not on_cuda:
+        raise ValueError(f"backend {backend!r} requires a CUDA device")
+    return backend
+
+
+class _GDN2Function(torch.autograd.Function):
+    """hip forward; the backward is not provided by this backend."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, b, w, scale, initial_state, output_final_state, config):
+        return chunk_gdn2_fwd(q, k, v, g, b, w, scale, initial_state, output_final_state, config)
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, do, dfinal_state):
+        raise NotImplementedError("the hip backend is forward-only; the GDN-2 backward is not implemented")
+
+
+def gdn2_attention(q, k, v, g, b, w, scale=None, initial_state=None, output_final_state=False,
+                   config: GDN2Config = DEFAULT_KERNEL_CONFIG, cu_seqlens=None):
+    """Gated DeltaNet-2 attention over a full sequence.
+
+    Args:
+        q, k: ``[B, S, H, DK]`` (the layer L2-normalises them); v: ``[B, S, H, DV]``.
+        g: ``[B, S, H, DK]`` log decay (<= 0); b: ``[B, S, H, DK]`` erase gate;
+        w: ``[B, S, H, DV]`` write gate.
+        scale: query scale; defaults to ``DK ** -0.5``.
+        initial_state: ``[B, H, DK, DV]`` or ``None``; never modified.
+        output_final_state: also return the state after the last token.
+        config: execution configuration.
+        cu_seqlens: packed-sequence offsets; not implemented, raises.
+
+    Returns:
+        ``(o [B, S, H, DV], final_state or None)``.
+    """
+    scale = q.shape[-1] ** -0.5 if scale is None else scale
+    needs_grad = torch.is_grad_enabled() and any(
+        t is not None and t.requires_grad for t in (q, k, v, g, b, w, initial_state))
+    backend = resolve_backend(config.backend, q.device.type == "cuda", needs_grad)
+    if cu_seqlens is not None:
+        raise NotImplementedError(
+            "packed variable-length batches are not implemented yet; pad the batch instead")
+    if backend == "torch":
+        raise NotImplementedError(
+            "the 'torch' backend is the reference package's CPU path (gdn2.reference); "
+            "this package provides the 'hip' backend only")
+    if needs_grad:
+        return _GDN2Function.apply(q, k, v, g, b, w, scale, initial_state, output_final_state, config)
+    return chunk_gdn2_fwd(q, k, v, g, b, w, scale, initial_state, output_final_state, config)
+
+
+# ---------------------------------------------------------------------------
+# Module
+# ---------------------------------------------------------------------------
+
+
+@dataclass
+class GDN2Cache:
+    """Per-layer decoding cache.
+
+    Attributes:
+        recurrent_state: ``[B, H_v, DK, DV]`` fp32 carried state.
+        conv_state: ``[B, C, conv_size - 1]`` tail of the short-conv input, or
+            ``None`` when the layer has no short convolution.
+    """
+
+    recurrent_state: torch.Tensor
+    conv_state: torch.Tensor | None = None
+
+
+class _ShortConv(nn.Module):
+    """Causal depthwise conv1d + SiLU over ``[B, S, C]``, with a decode tail."""
+
+    def __init__(self, channels: int, kernel_size: int = 4, activation: bool = True):
+        super().__init__()
+        self.channels = channels
+        self.kernel_size = kernel_size
+        self.activation = activation
+        self.conv = nn.Conv1d(channels, channels, kernel_size, groups=channels, padding=kernel_size - 1)
+
+    def _act(self, y):
+        return F.silu(y) if self.activation else y
+
+    def forward(self, x: torch.Tensor) -> torch.Tensor:
+        y = self.conv(x.transpose(1, 2))[..., : x.shape[1]]
+        return self._act(y.transpose(1, 2))
+
+    def step(self, x: torch.Tensor, state: torch.Tensor):
+        y, state = self.decode(x.unsqueeze(1), state)
+        return y[:, 0], state
+
+    def decode(self, x: torch.Tensor, state: torch.Tensor):
+        """``x [B, n, C]`` continuing from the cached ``kernel_size - 1`` inputs."""
+        buf = torch.cat([state.to(x.dtype), x.transpose(1, 2)], dim=-1)
+        y = F.conv1d(buf, self.conv.weight, self.conv.bias, groups=self.channels)
+        return self._act(y.transpose(1, 2)), buf[..., buf.shape[-1] - (self.kernel_size - 1):]
+
+
+class _GatedRMSNorm(nn.Module):
+    """Per-head RMSNorm followed by a SiLU output gate."""
+
+    def __init__(self, dim: int, eps: float = 1e-5):
+        super().__init__()
+        self.eps = eps
+        self.weight = nn.Parameter(torch.ones(dim))
+
+    def forward(self, x: torch.Tensor, gate: torch.Tensor) -> torch.Tensor:
+        xf = x.float()
+        xf = xf * torch.rsqrt(xf.pow(2).mean(-1, keepdim=True) + self.eps)
+        return (xf * self.weight * F.silu(gate.float())).to(gate.dtype)
+
+
+class GatedDeltaNet2(nn.Module):
+    """Gated DeltaNet-2 token mixer with a serving cache.
+
+    The erase gate ``b`` lives on the key axis, the write gate ``w`` on the
+    value axis; decay ``g = -exp(A_log) * softplus(f + dt_bias)`` is per key
+    channel. Key heads are repeated up to ``num_heads`` value heads.
+    """
+
+    def __init__(self, config: GatedDeltaNet2Config):
+        super().__init__()
+        self.cfg = config
+        H = config.num_heads
+        HK = config.num_kv_heads or H
+        if H % HK:
+            raise ValueError(f"num_heads {H} must be a multiple of num_kv_heads {HK}")
+        DK = config.head_dim_k
+        DV = config.head_dim_v or DK
+        self.num_heads, self.num_kv_heads = H, HK
+        self.head_dim_k, self.head_dim_v = DK, DV
+        self.head_repeat = H // HK
+        d_qk, d_v, hid = HK * DK, H * DV, config.hidden_size
+
+        self.q_proj = nn.Linear(hid, d_qk, bias=False)
+        self.k_proj = nn.Linear(hid, d_qk, bias=False)
+        self.v_proj = nn.Linear(hid, d_v, bias=False)
+        self.b_proj = nn.Linear(hid, d_qk, bias=False)
+        self.w_proj = nn.Linear(hid, d_v, bias=False)
+        self.f_proj = nn.Linear(hid, d_qk, bias=False)
+        self.o_gate_proj = nn.Linear(hid, d_v, bias=False)
+        self.o_proj = nn.Linear(d_v, hid, bias=False)
+        if config.conv_size > 0:
+            self.q_conv = _ShortConv(d_qk, config.conv_size)
+            self.k_conv = _ShortConv(d_qk, config.conv_size)
+            self.v_conv = _ShortConv(d_v, config.conv_size)
+        else:
+            self.q_conv = self.k_conv = self.v_conv = None
+
+        lo, hi = config.a_init_range
+        self.A_log = nn.Parameter(torch.empty(HK).uniform_(lo, hi).log_())
+        dt_lo, dt_hi = config.dt_init_range
+        dt = torch.empty(HK, DK).uniform_(dt_lo, dt_hi)
+        # softplus^-1(dt) so the initial step is exactly dt
+        self.dt_bias = nn.Parameter(dt + torch.log(-torch.expm1(-dt)))
+        self.o_norm = _GatedRMSNorm(DV, config.norm_eps)
+        self.scale = DK ** -0.5
+        self.erase_scale = config.erase_gate_scale
+
+    # -- pieces shared by forward / prefill / decode -----------------------
+    def _decay(self, x, lead):
+        f = self.f_proj(x).view(*lead, self.num_kv_heads, self.head_dim_k)
+        return -self.A_log.exp().unsqueeze(-1) * F.softplus(f.float() + self.dt_bias)
+
+    def _to_value_heads(self, t):
+        return t if self.head_repeat == 1 else t.repeat_interleave(self.head_repeat, dim=-2)
+
+    def _conv_with_cache(self, q, k, v, cache):
+        if self.q_conv is None:
+            return q, k, v
+        d = self.num_kv_heads * self.head_dim_k
+        cs = cache.conv_state
+        q, cq = self.q_conv.decode(q, cs[:, :d])
+        k, ck = self.k_conv.decode(k, cs[:, d:2 * d])
+        v, cv = self.v_conv.decode(v, cs[:, 2 * d:])
+        cache.conv_state = torch.cat([cq, ck, cv], dim=1)
+        return q, k, v
+
+    def _project(self, x, cache):
+        """Projections, short conv, L2 norm and gates -> value-head op inputs."""
+        B, S, _ = x.shape
+        HK, H, DK, DV = self.num_kv_heads, self.num_heads, self.head_dim_k, self.head_dim_v
+        q, k, v = self.q_proj(x), self.k_proj(x), self.v_proj(x)
+        if cache is not None:
+            q, k, v = self._conv_with_cache(q, k, v, cache)
+        elif self.q_conv is not None:
+            q, k, v = self.q_conv(q), self.k_conv(k), self.v_conv(v)
+        q = F.normalize(q.view(B, S, HK, DK), p=2, dim=-1)
+        k = F.normalize(k.view(B, S, HK, DK), p=2, dim=-1)
+        v = v.view(B, S, H, DV)
+        g = self._decay(x, (B, S))
+        b = torch.sigmoid(self.b_proj(x).view(B, S, HK, DK)) * self.erase_scale
+        w = torch.sigmoid(self.w_proj(x).view(B, S, H, DV))
+        q, k, b, g = (self._to_value_heads(t).contiguous() for t in (q, k, b, g))
+        return q, k, v.contiguous(), g, b, w.contiguous()
+
+    def _finish(self, x, o):
+        B, S, _ = x.shape
+        gate = self.o_gate_proj(x).view(B, S, self.num_heads, self.head_dim_v)
+        return self.o_proj(self.o_norm(o, gate).reshape(B, S, -1))
+
+    # -- public API ---------------------------------------------------------
+    def forward(self, hidden_states, cache=None, use_cache=False, cu_seqlens=None):
+        """Full-sequence mixer (training form). Returns ``(output, cache or None)``."""
+        B, S, _ = hidden_states.shape
+        conv_state = None
+        if self.q_conv is not None and use_cache:
+            width = self.cfg.conv_size - 1
+            raw = torch.cat([self.q_proj(hidden_states), self.k_proj(hidden_states),
+                             self.v_proj(hidden_states)], dim=-1).transpose(1, 2)
+            padded = F.pad(raw, (max(0, width - S), 0))
+            conv_state = padded[..., padded.shape[-1] - width:]
+        q, k, v, g, b, w = self._project(hidden_states, None)
+        o, final_state = gdn2_attention(
+            q, k, v, g, b, w, scale=self.scale,
+            initial_state=cache.recurrent_state if cache is not None else None,
+            output_final_state=use_cache, config=self.cfg.kernel, cu_seqlens=cu_seqlens)
+        out = self._finish(hidden_states, o)
+        return out, (GDN2Cache(final_state, conv_state) if use_cache else None)
+
+    @torch.no_grad()
+    def prefill(self, hidden_states, cache=None):
+        """Prefill a prompt (or one segment of it); returns ``(output, cache)``."""
+        if cache is None:
+            cache = self.init_cache(hidden_states.shape[0], device=hidden_states.device)
+        q, k, v, g, b, w = self._project(hidden_states, cache)
+        o, state = gdn2_prefill(q, k, v, g, b, w, cache.recurrent_state, scale=self.scale,
+                                config=self.cfg.kernel)
+        cache.recurrent_state = state
+        return self._finish(hidden_states, o), cache
+
+    @torch.no_grad()
+    def decode(self, hidden_states, cache):
+        """Decode ``n`` tokens ``[B, n, hidden]``, updating ``cache`` in place."""
+        q, k, v, g, b, w = self._project(hidden_states, cache)
+        o = gdn2_decode(q, k, v, g, b, w, cache.recurrent_state, scale=self.scale)
+        return self._finish(hidden_states, o), cache
+
+    @torch.no_grad()
+    def step(self, hidden_states, cache):
+        """Decode one token ``[B, hidden]``."""
+        out, cache = self.decode(hidden_states.unsqueeze(1), cache)
+        return out[:, 0], cache
+
+    def init_cache(self, batch_size, device=None, dtype=torch.float32):
+        """Empty cache: zero recurrent state in ``dtype``, zero conv tail in the
+        conv weights' dtype."""
+        state = torch.zeros(batch_size, self.num_heads, self.head_dim_k, self.head_dim_v,
+                            device=device, dtype=dtype)
+        conv_state = None
+        if self.q_conv is not None:
+            C = 2 * self.num_kv_heads * self.head_dim_k + self.num_heads * self.head_dim_v
+            conv_state = torch.zeros(batch_size, C, self.cfg.conv_size - 1, device=device,
+                                     dtype=self.q_conv.conv.weight.dtype)
+        return GDN2Cache(state, conv_state)

@@ -1,0 +1,121 @@
+// extern "C" entry points of libgdn2_hip.so (declared in include/gdn2_hip.h).
+// Arguments are validated here, before anything is launched.
+#include "../../include/gdn2_hip.h"
+#include "gdn2_common.h"
+#include "gdn2_prefill_layout.h"
+
+namespace gdn2 {
+hipError_t launch_decode(const void*, const void*, const void*, const float*, const void*,
+                         const void*, float*, void*, int, int, int, int, long, long, int, float,
+                         int, int, hipStream_t);
+int decode_dvt_for(int DV);
+hipError_t launch_chunk_local(const void*, const void*, const void*, const float*, int, int, int,
+                              int, long, long, int, float, unsigned short*, hipStream_t);
+hipError_t launch_scan(const void*, const void*, int, const unsigned short*, const float*, float*,
+                       void*, int, int, int, int, int, long, long, int, hipStream_t);
+}  // namespace gdn2
+
+namespace {
+
+constexpr int kAbiVersion = 1;
+
+bool dtype_ok(int dt) { return dt == GDN2_DTYPE_F32 || dt == GDN2_DTYPE_BF16 || dt == GDN2_DTYPE_F16; }
+
+long record_elems(int DK) {
+  if (DK == 64) return gdn2::ChunkLayout<64>::STRIDE;
+  if (DK == 128) return gdn2::ChunkLayout<128>::STRIDE;
+  return 0;
+}
+
+int status(hipError_t e) { return e == hipSuccess ? 0 : static_cast<int>(e); }
+
+// shared checks of the prefill stages
+int check_prefill(int B, int H, int DK, long s_alloc, long t0, long n_tokens) {
+  if (B < 1 || H < 1 || t0 < 0 || n_tokens < 0 || s_alloc < t0 + n_tokens) return GDN2_ERR_ARG;
+  if (DK != 64 && DK != 128) return GDN2_ERR_SHAPE;
+  if (n_tokens % gdn2::kBS) return GDN2_ERR_SHAPE;
+  if (static_cast<long>(B) * H * (n_tokens / gdn2::kBS) > 0x7fffffffL) return GDN2_ERR_SHAPE;
+  return 0;
+}
+
+}  // namespace
+
+extern "C" {
+
+int gdn2_hip_version(void) { return kAbiVersion; }
+
+const char* gdn2_hip_status_string(int s) {
+  if (s == 0) return "success";
+  if (s == GDN2_ERR_ARG) return "invalid argument (null pointer, negative size or bad dtype code)";
+  if (s == GDN2_ERR_SHAPE) return "unsupported shape for the gfx950 kernels";
+  if (s > 0) return hipGetErrorString(static_cast<hipError_t>(s));
+  return "unknown status";
+}
+
+int gdn2_hip_decode(const void* q, const void* k, const void* v, const float* g, const void* b,
+                    const void* w, int in_dtype, float* state, void* o, int out_dtype, int B,
+                    int H, int DK, int DV, long s_alloc, long t0, long n, float scale,
+                    void* stream) {
+  if (!q || !k || !v || !g || !b || !w || !state || !o) return GDN2_ERR_ARG;
+  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return GDN2_ERR_ARG;
+  if (B < 1 || H < 1 || n < 0 || t0 < 0 || s_alloc < t0 + n) return GDN2_ERR_ARG;
+  if (DK != 32 && DK != 64 && DK != 128 && DK != 256) return GDN2_ERR_SHAPE;
+  if (gdn2::decode_dvt_for(DV) == 0 || DV > 4096) return GDN2_ERR_SHAPE;
+  if (static_cast<long>(B) * H > 65535L || n > 0x7fffffffL) return GDN2_ERR_SHAPE;
+  return status(gdn2::launch_decode(q, k, v, g, b, w, state, o, B, H, DK, DV, s_alloc, t0,
+                                    static_cast<int>(n), scale, in_dtype, out_dtype,
+                                    static_cast<hipStream_t>(stream)));
+}
+
+size_t gdn2_hip_prefill_workspace_bytes(int B, int H, int DK, long n_tokens) {
+  const long rec = record_elems(DK);
+  if (rec == 0 || B < 1 || H < 1 || n_tokens < 0) return 0;
+  const long nc = (n_tokens + gdn2::kBS - 1) / gdn2::kBS;
+  return static_cast<size_t>(B) * H * nc * rec * 2;
+}
+
+int gdn2_hip_chunk_local(const void* q, const void* k, const void* b, const float* g,
+                         int in_dtype, void* workspace, int B, int H, int DK, long s_alloc,
+                         long t0, long n_tokens, float scale, void* stream) {
+  if (!q || !k || !b || !g || !workspace || !dtype_ok(in_dtype)) return GDN2_ERR_ARG;
+  if (int e = check_prefill(B, H, DK, s_alloc, t0, n_tokens)) return e;
+  if (n_tokens == 0) return 0;
+  return status(gdn2::launch_chunk_local(q, k, b, g, in_dtype, B, H, DK, s_alloc, t0,
+                                         static_cast<int>(n_tokens / gdn2::kBS), scale,
+                                         static_cast<unsigned short*>(workspace),
+                                         static_cast<hipStream_t>(stream)));
+}
+
+int gdn2_hip_prefill_scan(const void* v, const void* w, int in_dtype, const void* workspace,
+                          const float* state_in, float* state_out, void* o, int out_dtype, int B,
+                          int H, int DK, int DV, long s_alloc, long t0, long n_tokens,
+                          void* stream) {
+  if (!v || !w || !workspace || !state_out || !o) return GDN2_ERR_ARG;
+  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return GDN2_ERR_ARG;
+  if (int e = check_prefill(B, H, DK, s_alloc, t0, n_tokens)) return e;
+  if (DV < 16 || DV % 16 || DV > 4096) return GDN2_ERR_SHAPE;
+  if (n_tokens == 0) return GDN2_ERR_SHAPE;
+  return status(gdn2::launch_scan(v, w, in_dtype, static_cast<const unsigned short*>(workspace),
+                                  state_in, state_out, o, out_dtype, B, H, DK, DV, s_alloc, t0,
+                                  static_cast<int>(n_tokens / gdn2::kBS),
+                                  static_cast<hipStream_t>(stream)));
+}
+
+int gdn2_hip_prefill_chunks(const void* q, const void* k, const void* v, const float* g,
+                            const void* b, const void* w, int in_dtype, const float* state_in,
+                            float* state_out, void* o, int out_dtype, void* workspace, int B,
+                            int H, int DK, int DV, long s_alloc, long t0, long n_tokens,
+                            float scale, void* stream) {
+  if (!q || !k || !b || !g) return GDN2_ERR_ARG;
+  if (!v || !w || !workspace || !state_out || !o) return GDN2_ERR_ARG;
+  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return GDN2_ERR_ARG;
+  if (int e = check_prefill(B, H, DK, s_alloc, t0, n_tokens)) return e;
+  if (DV < 16 || DV % 16 || DV > 4096 || n_tokens == 0) return GDN2_ERR_SHAPE;
+  int s = gdn2_hip_chunk_local(q, k, b, g, in_dtype, workspace, B, H, DK, s_alloc, t0, n_tokens,
+                               scale, stream);
+  if (s) return s;
+  return gdn2_hip_prefill_scan(v, w, in_dtype, workspace, state_in, state_out, o, out_dtype, B, H,
+                               DK, DV, s_alloc, t0, n_tokens, stream);
+}
+
+}  // extern "C"

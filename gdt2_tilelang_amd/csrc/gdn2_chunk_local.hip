@@ -1,0 +1,422 @@
+// GDN-2 prefill, stage 1: everything that is local to one 64-token chunk.
+//
+// One 256-thread workgroup (4 waves) per (b, h, chunk). It fuses what the
+// reference runs as five kernels (gdn2/forward.py:65-535: cumsum, intra-diag,
+// inter-blocks, solve, wy) and writes the chunk's record (layout in
+// gdn2_prefill_layout.h) for the state scan. Notation, per chunk, G = log2(e)
+// * cumsum(g) (log2-space decay), gamma = 2^G:
+//
+//   Aqk[r,s] = scale * sum_c q_rc k_sc 2^(G_rc - G_sc)   s <= r
+//   Akk[r,s] =         sum_c b_rc k_rc k_sc 2^(G_rc - G_sc)   s < r
+//   Ai = (I + Akk)^-1,  W = Ai (b*k*gamma),  KG = k * 2^(G_last - G)
+//   Q' = scale*q*gamma - Aqk W      (so the scan's output is Q' S + Aqk U)
+//
+// Overflow safety (reference forward.py:21-32): every 16x16 block of Aqk/Akk
+// is an MFMA product of row factors 2^(G_r - ref) and column factors
+// 2^(ref - G_s), ref a per-channel reference for the row block.
+//  * fast path: ref = midpoint of the row block's G range. Within the block
+//    both factors are <= 2^(spread/2), so with every 16-row spread <= 120
+//    (log2 units) nothing overflows and the diagonal blocks go on MFMA too.
+//    Off-diagonal column factors are <= 1.
+//  * exact path, taken for the whole chunk when some spread exceeds 120 (a
+//    channel losing > 83 nats in 16 tokens): ref = the block's first row as in
+//    the reference, all factors <= 1, and the diagonal blocks are summed
+//    exactly with 2^(G_r - G_s) on the VALU.
+//
+// Precision (bf16 MFMA, fp32 accumulate): the Aqk product uses hi+lo split
+// operands (three MFMAs); Akk, W and Aqk*W use single bf16 operands; the solve
+// is fp32. Q', KG and Aqk are exported as hi/lo pairs, W and Ai as bf16.
+#include "gdn2_common.h"
+#include "gdn2_prefill_layout.h"
+
+namespace gdn2 {
+
+constexpr float kSpreadLimit = 120.0f;
+
+template <int IN_DT>
+__device__ __forceinline__ void load8(const void* base, size_t idx, float* out) {
+  if constexpr (IN_DT == DT_F32) {
+    const float4* p = reinterpret_cast<const float4*>(static_cast<const float*>(base) + idx);
+    const float4 a = p[0], b = p[1];
+    out[0] = a.x; out[1] = a.y; out[2] = a.z; out[3] = a.w;
+    out[4] = b.x; out[5] = b.y; out[6] = b.z; out[7] = b.w;
+  } else {
+    const u16x8 r = *reinterpret_cast<const u16x8*>(static_cast<const unsigned short*>(base) + idx);
+#pragma unroll
+    for (int j = 0; j < 8; ++j)
+      out[j] = (IN_DT == DT_BF16) ? bf16_bits_to_f32(r[j]) : f16_bits_to_f32(r[j]);
+  }
+}
+
+template <int DK>
+struct ChunkSmem {
+  static constexpr int GP = DK + 4;    // fp32 pitch of [64][DK] arrays
+  static constexpr int AP = 68;        // fp32 pitch of [64][64] arrays
+  static constexpr int AP2 = 72;       // fp32 pitch of the Akk region (reused for W^T)
+  static constexpr int TP = 72;        // bf16 pitch of [DK][64] arrays
+  static constexpr int WP = DK + 8;    // bf16 pitch of [64][DK] arrays
+  static constexpr size_t G_OFF = 0;                                 // G, later Aqk*W staging
+  static constexpr size_t K_OFF = G_OFF + 64 * GP * 4;               // k, later W [64][WP]
+  static constexpr size_t ET_OFF = K_OFF + 64 * GP * 4;              // E^T bf16 [DK][TP]
+  static constexpr size_t A1_OFF = ET_OFF + DK * TP * 2;             // Aqk
+  static constexpr size_t A2_OFF = A1_OFF + 64 * AP * 4;             // Akk, later W^T [DK][TP]
+  static constexpr size_t AI_OFF = A2_OFF + 64 * AP2 * 4;            // Ai
+  static constexpr size_t T_OFF = AI_OFF + 64 * AP * 4;              // solve scratch [3][16][17]
+  static constexpr size_t REF_OFF = T_OFF + 3 * 16 * 17 * 4;         // [4][DK] per-block reference
+  static constexpr size_t TOT_OFF = REF_OFF + 4 * DK * 4;            // cumsum partials [4][DK]
+  static constexpr size_t BYTES = TOT_OFF + 4 * DK * 4;
+  static_assert(DK * TP * 2 <= 64 * AP2 * 4, "W^T must fit in the Akk region");
+  static_assert(64 * WP * 2 <= 64 * GP * 4, "W must fit in the k region");
+};
+
+template <int DK, int IN_DT>
+__global__ __launch_bounds__(256) void chunk_local_kernel(
+    const void* __restrict__ qp, const void* __restrict__ kp, const void* __restrict__ bp,
+    const float* __restrict__ g, int H, long s_alloc, long t0, int NC, float scale,
+    unsigned short* __restrict__ ws) {
+  using L = ChunkLayout<DK>;
+  using M = ChunkSmem<DK>;
+  constexpr int KT = DK / 32;
+  constexpr int MT = DK / 16;
+  constexpr int GP = M::GP, AP = M::AP, AP2 = M::AP2, TP = M::TP, WP = M::WP;
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  float* sG = reinterpret_cast<float*>(smem + M::G_OFF);
+  float* sK = reinterpret_cast<float*>(smem + M::K_OFF);
+  unsigned short* sET = reinterpret_cast<unsigned short*>(smem + M::ET_OFF);
+  float* sA1 = reinterpret_cast<float*>(smem + M::A1_OFF);
+  float* sA2 = reinterpret_cast<float*>(smem + M::A2_OFF);
+  float* sAI = reinterpret_cast<float*>(smem + M::AI_OFF);
+  float* sT = reinterpret_cast<float*>(smem + M::T_OFF);
+  float* sRef = reinterpret_cast<float*>(smem + M::REF_OFF);
+  float* sTot = reinterpret_cast<float*>(smem + M::TOT_OFF);
+  float* sQS = sG;                                                   // phase E staging
+  unsigned short* sW = reinterpret_cast<unsigned short*>(sK);        // phase D
+  unsigned short* sWT = reinterpret_cast<unsigned short*>(sA2);      // phase D/E
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = tid >> 6;
+  const int lr = lane & 15;        // row (A) / column (B, D) inside a 16-tile
+  const int lq = lane >> 4;        // 8-wide k group (A, B) / 4-row group (D)
+  const int ch = blockIdx.x;
+  const int bh = ch / NC;
+  const int n = ch % NC;
+  const int bi = bh / H;
+  const int h = bh % H;
+  const long tok0 = t0 + static_cast<long>(n) * kBS;
+  unsigned short* rec = ws + static_cast<size_t>(ch) * L::STRIDE;
+  auto row_base = [&](int r) -> size_t {
+    return ((static_cast<size_t>(bi) * s_alloc + tok0 + r) * H + h) * DK;
+  };
+
+  // ---- phase A.1: chunk-local cumsum of g in log2 units -> sG ------------
+  {
+    constexpr int NP = 256 / DK;     // row partitions
+    constexpr int RPP = kBS / NP;    // rows per partition
+    const int c = tid % DK;
+    const int part = tid / DK;
+    float run[RPP];
+#pragma unroll
+    for (int r = 0; r < RPP; ++r) run[r] = g[row_base(part * RPP + r) + c];
+#pragma unroll
+    for (int r = 1; r < RPP; ++r) run[r] += run[r - 1];
+    sTot[part * DK + c] = run[RPP - 1];
+    __syncthreads();
+    float off = 0.f;
+    for (int p = 0; p < part; ++p) off += sTot[p * DK + c];
+#pragma unroll
+    for (int r = 0; r < RPP; ++r) sG[(part * RPP + r) * GP + c] = (run[r] + off) * kLog2e;
+  }
+
+  // ---- phase A.2: this wave's 16 rows of q, k, b into registers ----------
+  // Lane holds row r = 16*wave + lr, channels 32*kk + 8*lq + j (A-operand order).
+  const int my_r = 16 * wave + lr;
+  float qv[KT][8], kv[KT][8], bv[KT][8];
+#pragma unroll
+  for (int kk = 0; kk < KT; ++kk) {
+    const int c0 = 32 * kk + 8 * lq;
+    const size_t idx = row_base(my_r) + c0;
+    load8<IN_DT>(qp, idx, qv[kk]);
+    load8<IN_DT>(kp, idx, kv[kk]);
+    load8<IN_DT>(bp, idx, bv[kk]);
+    float4* dst = reinterpret_cast<float4*>(&sK[my_r * GP + c0]);
+    dst[0] = make_float4(kv[kk][0], kv[kk][1], kv[kk][2], kv[kk][3]);
+    dst[1] = make_float4(kv[kk][4], kv[kk][5], kv[kk][6], kv[kk][7]);
+  }
+  __syncthreads();
+
+  // ---- phase A.3: per-block references and the fast/exact decision -------
+  bool unsafe = false;
+  for (int e = tid; e < 4 * DK; e += 256) {
+    const int i = e / DK, c = e % DK;
+    const float first = sG[(16 * i) * GP + c];
+    const float last = sG[(16 * i + 15) * GP + c];
+    const float spread = first - last;
+    unsafe |= !(spread <= kSpreadLimit);   // also catches NaN
+    sTot[e] = 0.5f * (first + last);
+  }
+  const bool exact = __syncthreads_or(unsafe) != 0;
+  for (int e = tid; e < 4 * DK; e += 256) {
+    const int i = e / DK, c = e % DK;
+    sRef[e] = exact ? sG[(16 * i) * GP + c] : sTot[e];
+  }
+  __syncthreads();
+
+  // ---- phase A.4: own-row products (registers), E^T, KG^T, gamma_last -----
+  float qg[KT][8];          // scale * q * gamma, kept for phase E
+  bf16x8 aqh[KT], aql[KT], ae[KT];   // Aqk / Akk row operands
+#pragma unroll
+  for (int kk = 0; kk < KT; ++kk) {
+    const int c0 = 32 * kk + 8 * lq;
+    float xq[8], xe[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const float Gr = sG[my_r * GP + c0 + j];
+      const float gam = fast_exp2(Gr);
+      const float bk = bv[kk][j] * kv[kk][j];
+      qg[kk][j] = scale * qv[kk][j] * gam;
+      sET[(c0 + j) * TP + my_r] = f32_to_bf16_bits(bk * gam);
+      const float fr = fast_exp2(Gr - sRef[wave * DK + c0 + j]);
+      xq[j] = qv[kk][j] * fr;
+      xe[j] = bk * fr;
+    }
+    split_bf16x8(xq, aqh[kk], aql[kk]);
+    ae[kk] = pack_bf16x8(xe);
+  }
+  if (tid < DK) {
+    reinterpret_cast<float*>(rec + L::GL_OFF)[tid] = fast_exp2(sG[63 * GP + tid]);
+  }
+  // KG^T fragments: rows c = 16m + lr, k index t = 32kk + 8lq + j
+  for (int f = wave; f < MT * 2; f += 4) {
+    const int m = f >> 1, kk = f & 1;
+    const int c = 16 * m + lr;
+    const float Gl = sG[63 * GP + c];
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      const int t = 32 * kk + 8 * lq + j;
+      x[j] = sK[t * GP + c] * fast_exp2(Gl - sG[t * GP + c]);
+    }
+    bf16x8 hi, lo;
+    split_bf16x8(x, hi, lo);
+    *reinterpret_cast<bf16x8*>(rec + L::kt_frag(m, kk, 0) + lane * 8) = hi;
+    *reinterpret_cast<bf16x8*>(rec + L::kt_frag(m, kk, 1) + lane * 8) = lo;
+  }
+
+  // ---- phase B: Aqk / Akk 16x16 blocks, row block i = wave ----------------
+  {
+    const int i = wave;
+    const int jmax = exact ? i - 1 : i;
+    for (int j = 0; j <= jmax; ++j) {
+      f32x4 accq = zero4(), acck = zero4();
+      const int s = 16 * j + lr;
+#pragma unroll
+      for (int kk = 0; kk < KT; ++kk) {
+        const int c0 = 32 * kk + 8 * lq;
+        float y[8];
+#pragma unroll
+        for (int jj = 0; jj < 8; ++jj)
+          y[jj] = sK[s * GP + c0 + jj] * fast_exp2(sRef[i * DK + c0 + jj] - sG[s * GP + c0 + jj]);
+        bf16x8 bh, bl;
+        split_bf16x8(y, bh, bl);
+        accq = mfma3(aqh[kk], aql[kk], bh, bl, accq);
+        acck = mfma(ae[kk], bh, acck);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 16 * i + 4 * lq + e;
+        float aq = accq[e] * scale, ak = acck[e];
+        if (j == i) {
+          if (s > r) aq = 0.f;
+          if (s >= r) ak = 0.f;
+        }
+        sA1[r * AP + s] = aq;
+        sA2[r * AP2 + s] = ak;
+      }
+    }
+    for (int j = i + 1; j < 4; ++j) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int r = 16 * i + 4 * lq + e;
+        sA1[r * AP + 16 * j + lr] = 0.f;
+        sA2[r * AP2 + 16 * j + lr] = 0.f;
+      }
+    }
+    if (exact) {
+      // diagonal block by the exact pairwise decay (rows r, columns s..s+3)
+      const int r = 16 * i + (lane >> 2);
+      const int sb = 16 * i + 4 * (lane & 3);
+      float aq[4] = {0.f, 0.f, 0.f, 0.f}, ak[4] = {0.f, 0.f, 0.f, 0.f};
+      const size_t rb = row_base(r);
+      for (int c = 0; c < DK; ++c) {
+        const float Gr = sG[r * GP + c];
+        const float qr = load_elem(qp, rb + c, IN_DT);
+        const float kr = sK[r * GP + c];
+        const float bkr = load_elem(bp, rb + c, IN_DT) * kr;
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+          const int s = sb + u;
+          const float d = fast_exp2(fminf(Gr - sG[s * GP + c], 0.f));
+          const float ks = sK[s * GP + c] * d;
+          aq[u] += qr * ks;
+          ak[u] += bkr * ks;
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int s = sb + u;
+        sA1[r * AP + s] = (s <= r) ? aq[u] * scale : 0.f;
+        sA2[r * AP2 + s] = (s < r) ? ak[u] : 0.f;
+      }
+    }
+  }
+  __syncthreads();
+
+  // ---- phase C: Ai = (I + Akk)^-1, block forward substitution in fp32 -----
+  {
+    const int w = wave;
+    if (lane < 16) {
+      // diagonal 16x16 block w: column `lane` of its inverse
+      float x[16];
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) {
+        float val = (rr == lane) ? 1.f : 0.f;
+        const float* arow = &sA2[(16 * w + rr) * AP2 + 16 * w];
+#pragma unroll
+        for (int s = 0; s < rr; ++s) val -= arow[s] * x[s];
+        x[rr] = val;
+      }
+#pragma unroll
+      for (int rr = 0; rr < 16; ++rr) sAI[(16 * w + rr) * AP + 16 * w + lane] = x[rr];
+    }
+    for (int j = w + 1; j < 4; ++j) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sAI[(16 * w + 4 * lq + e) * AP + 16 * j + lr] = 0.f;
+    }
+  }
+  __syncthreads();
+  for (int d = 1; d < 4; ++d) {
+    // T = sum_{k=j}^{i-1} A_ik X_kj for blocks (i, j) = (d + p, p)
+    for (int e = tid; e < (4 - d) * 256; e += 256) {
+      const int p = e >> 8, r = (e >> 4) & 15, s = e & 15;
+      const int i = d + p, j = p;
+      const float* arow = &sA2[(16 * i + r) * AP2];
+      float acc = 0.f;
+      for (int u = 16 * j; u < 16 * i; ++u) acc += arow[u] * sAI[u * AP + 16 * j + s];
+      sT[(p * 16 + r) * 17 + s] = acc;
+    }
+    __syncthreads();
+    // X_ij = -X_ii T
+    for (int e = tid; e < (4 - d) * 256; e += 256) {
+      const int p = e >> 8, r = (e >> 4) & 15, s = e & 15;
+      const int i = d + p, j = p;
+      const float* xrow = &sAI[(16 * i + r) * AP + 16 * i];
+      float acc = 0.f;
+#pragma unroll
+      for (int u = 0; u < 16; ++u) acc += xrow[u] * sT[(p * 16 + u) * 17 + s];
+      sAI[(16 * i + r) * AP + 16 * j + s] = -acc;
+    }
+    __syncthreads();
+  }
+
+  // ---- phase D: W = Ai E (bf16 MFMA); Ai and Aqk fragments out ------------
+  bf16x8 ai[2], aqk_hi[2];
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    const int s0 = 32 * kk + 8 * lq;
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = sAI[my_r * AP + s0 + j];
+    ai[kk] = pack_bf16x8(x);
+    *reinterpret_cast<bf16x8*>(rec + L::ai_frag(wave, kk) + lane * 8) = ai[kk];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = sA1[my_r * AP + s0 + j];
+    bf16x8 lo;
+    split_bf16x8(x, aqk_hi[kk], lo);
+    *reinterpret_cast<bf16x8*>(rec + L::aqk_frag(wave, kk, 0) + lane * 8) = aqk_hi[kk];
+    *reinterpret_cast<bf16x8*>(rec + L::aqk_frag(wave, kk, 1) + lane * 8) = lo;
+  }
+#pragma unroll
+  for (int nn = 0; nn < MT; ++nn) {
+    f32x4 acc = zero4();
+    const int c = 16 * nn + lr;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const bf16x8 bfr = *reinterpret_cast<const bf16x8*>(&sET[c * TP + 32 * kk + 8 * lq]);
+      acc = mfma(ai[kk], bfr, acc);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = 16 * wave + 4 * lq + e;
+      const unsigned short wb = f32_to_bf16_bits(acc[e]);
+      sW[t * WP + c] = wb;
+      sWT[c * TP + t] = wb;
+    }
+  }
+  __syncthreads();
+#pragma unroll
+  for (int kk = 0; kk < KT; ++kk) {
+    const bf16x8 x = *reinterpret_cast<const bf16x8*>(&sW[my_r * WP + 32 * kk + 8 * lq]);
+    *reinterpret_cast<bf16x8*>(rec + L::w_frag(wave, kk) + lane * 8) = x;
+  }
+
+  // ---- phase E: Q' = scale*q*gamma - Aqk W ---------------------------------
+#pragma unroll
+  for (int nn = 0; nn < MT; ++nn) {
+    f32x4 acc = zero4();
+    const int c = 16 * nn + lr;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      const bf16x8 bfr = *reinterpret_cast<const bf16x8*>(&sWT[c * TP + 32 * kk + 8 * lq]);
+      acc = mfma(aqk_hi[kk], bfr, acc);
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) sQS[(16 * wave + 4 * lq + e) * GP + c] = acc[e];
+  }
+  __syncthreads();
+#pragma unroll
+  for (int kk = 0; kk < KT; ++kk) {
+    const int c0 = 32 * kk + 8 * lq;
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = qg[kk][j] - sQS[my_r * GP + c0 + j];
+    bf16x8 hi, lo;
+    split_bf16x8(x, hi, lo);
+    *reinterpret_cast<bf16x8*>(rec + L::qp_frag(wave, kk, 0) + lane * 8) = hi;
+    *reinterpret_cast<bf16x8*>(rec + L::qp_frag(wave, kk, 1) + lane * 8) = lo;
+  }
+}
+
+template <int DK, int IN_DT>
+static hipError_t launch_chunk_local_t(const void* q, const void* k, const void* b, const float* g,
+                                       int B, int H, long s_alloc, long t0, int NC, float scale,
+                                       unsigned short* ws, hipStream_t stream) {
+  constexpr size_t smem = ChunkSmem<DK>::BYTES;
+  static bool configured = false;   // attribute set once per process (same value always)
+  if (!configured) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_local_kernel<DK, IN_DT>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       static_cast<int>(smem));
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
+  const unsigned grid = static_cast<unsigned>(B) * H * NC;
+  hipLaunchKernelGGL((chunk_local_kernel<DK, IN_DT>), dim3(grid), dim3(256), smem, stream, q, k,
+                     b, g, H, s_alloc, t0, NC, scale, ws);
+  return hipGetLastError();
+}
+
+hipError_t launch_chunk_local(const void* q, const void* k, const void* b, const float* g,
+                              int in_dt, int B, int H, int DK, long s_alloc, long t0, int NC,
+                              float scale, unsigned short* ws, hipStream_t stream) {
+#define GDN2_CL_CASE(DKV, DTV)                                                             \
+  if (DK == DKV && in_dt == DTV)                                                           \
+    return launch_chunk_local_t<DKV, DTV>(q, k, b, g, B, H, s_alloc, t0, NC, scale, ws, stream);
+  GDN2_CL_CASE(64, DT_BF16) GDN2_CL_CASE(64, DT_F16) GDN2_CL_CASE(64, DT_F32)
+  GDN2_CL_CASE(128, DT_BF16) GDN2_CL_CASE(128, DT_F16) GDN2_CL_CASE(128, DT_F32)
+#undef GDN2_CL_CASE
+  return hipErrorInvalidValue;
+}
+
+}  // namespace gdn2

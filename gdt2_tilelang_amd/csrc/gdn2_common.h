@@ -1,0 +1,99 @@
+// Shared device helpers for the GDN-2 HIP kernels (gfx950 / CDNA4 only).
+//
+// Conventions used by every kernel in this library:
+//   * Sequence tensors are [B, S_alloc, H, D] with D fastest; a kernel works on
+//     tokens [t0, t0 + n) of that allocation.
+//   * g is always fp32 natural-log decay (<= 0); q,k,v,b,w are fp32, bf16 or
+//     fp16 (runtime dtype code); the recurrent state is fp32 [B, H, DK, DV].
+//   * MFMA tiles use v_mfma_f32_16x16x32_bf16. For that instruction lane l of a
+//     wave64 holds A[l%16][8*(l/16) .. +7], B[8*(l/16) .. +7][l%16] and
+//     D[4*(l/16) .. +3][l%16]. A "fragment" below is one such 64-lane operand,
+//     stored as 64 x 8 bf16 = 1 KiB contiguous so it loads with one coalesced
+//     16-byte access per lane.
+#pragma once
+
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace gdn2 {
+
+typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
+typedef float f32x4 __attribute__((ext_vector_type(4)));
+typedef unsigned short u16x8 __attribute__((ext_vector_type(8)));
+
+enum DType : int { DT_F32 = 0, DT_BF16 = 1, DT_F16 = 2 };
+
+constexpr float kLog2e = 1.4426950408889634f;
+
+__device__ __forceinline__ float bf16_bits_to_f32(unsigned short h) {
+  return __uint_as_float(static_cast<uint32_t>(h) << 16);
+}
+
+// Round-to-nearest-even float -> bf16 bit pattern (finite inputs; NaN kept NaN).
+__device__ __forceinline__ unsigned short f32_to_bf16_bits(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<unsigned short>((u >> 16) | 0x40);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return static_cast<unsigned short>(u >> 16);
+}
+
+__device__ __forceinline__ float f16_bits_to_f32(unsigned short h) {
+  return static_cast<float>(__builtin_bit_cast(_Float16, h));
+}
+
+__device__ __forceinline__ unsigned short f32_to_f16_bits(float f) {
+  return __builtin_bit_cast(unsigned short, static_cast<_Float16>(f));
+}
+
+// Element i of a tensor whose dtype is only known at run time.
+__device__ __forceinline__ float load_elem(const void* p, size_t i, int dt) {
+  if (dt == DT_BF16) return bf16_bits_to_f32(static_cast<const unsigned short*>(p)[i]);
+  if (dt == DT_F16) return f16_bits_to_f32(static_cast<const unsigned short*>(p)[i]);
+  return static_cast<const float*>(p)[i];
+}
+
+__device__ __forceinline__ void store_elem(void* p, size_t i, int dt, float x) {
+  if (dt == DT_BF16) static_cast<unsigned short*>(p)[i] = f32_to_bf16_bits(x);
+  else if (dt == DT_F16) static_cast<unsigned short*>(p)[i] = f32_to_f16_bits(x);
+  else static_cast<float*>(p)[i] = x;
+}
+
+// Eight bf16 values from eight floats (round to nearest even).
+__device__ __forceinline__ bf16x8 pack_bf16x8(const float* x) {
+  u16x8 r;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) r[j] = f32_to_bf16_bits(x[j]);
+  return __builtin_bit_cast(bf16x8, r);
+}
+
+// Split eight floats into bf16 hi + lo with x ~= hi + lo to ~16 mantissa bits.
+__device__ __forceinline__ void split_bf16x8(const float* x, bf16x8& hi, bf16x8& lo) {
+  u16x8 h, l;
+#pragma unroll
+  for (int j = 0; j < 8; ++j) {
+    h[j] = f32_to_bf16_bits(x[j]);
+    l[j] = f32_to_bf16_bits(x[j] - bf16_bits_to_f32(h[j]));
+  }
+  hi = __builtin_bit_cast(bf16x8, h);
+  lo = __builtin_bit_cast(bf16x8, l);
+}
+
+__device__ __forceinline__ f32x4 mfma(const bf16x8& a, const bf16x8& b, const f32x4& c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_bf16(a, b, c, 0, 0, 0);
+}
+
+// a*b with both operands split: ah*bh + ah*bl + al*bh (the al*bl term is below
+// fp32 round-off of the result and is dropped).
+__device__ __forceinline__ f32x4 mfma3(const bf16x8& ah, const bf16x8& al, const bf16x8& bh,
+                                       const bf16x8& bl, f32x4 c) {
+  c = mfma(ah, bh, c);
+  c = mfma(ah, bl, c);
+  c = mfma(al, bh, c);
+  return c;
+}
+
+__device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
+
+__device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+}  // namespace gdn2

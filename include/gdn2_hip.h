@@ -1,0 +1,99 @@
+/*
+ * gdn2_hip.h -- C ABI of the MI355X (gfx950) GDN-2 attention library
+ * (libgdn2_hip.so, built from gdt2_tilelang_amd/csrc).
+ *
+ * Plain pointers and sizes only. Every tensor is device memory owned by the
+ * caller; the library never allocates or frees. Sequence tensors are
+ * [B, s_alloc, H, D] contiguous with D fastest and a call works on tokens
+ * [t0, t0 + n) of that allocation; g is fp32 natural-log decay (<= 0); the
+ * state is fp32 [B, H, DK, DV] contiguous. Work is enqueued on `stream`
+ * (a hipStream_t; NULL = the default stream) with no host synchronisation.
+ *
+ * Return value: 0 on success, a negative GDN2_ERR_* for a rejected argument
+ * (nothing was launched), or a positive hipError_t from the launch.
+ *
+ * The reference (amaranthine09/GDT2_TileLang) has no C ABI: its kernels are
+ * TileLang JIT objects called from Python. Each entry point below names the
+ * reference call site it replaces.
+ */
+#ifndef GDN2_HIP_H
+#define GDN2_HIP_H
+
+#include <stddef.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+/* dtype codes for q, k, v, b, w and for the output o */
+#define GDN2_DTYPE_F32 0
+#define GDN2_DTYPE_BF16 1
+#define GDN2_DTYPE_F16 2
+
+#define GDN2_ERR_ARG (-1)    /* null pointer, negative size, bad dtype code */
+#define GDN2_ERR_SHAPE (-2)  /* head dim / token count the kernels do not support */
+
+/* Library ABI version (bumped on any signature or layout change). */
+int gdn2_hip_version(void);
+
+/* Static description of a status code. */
+const char* gdn2_hip_status_string(int status);
+
+/*
+ * Decode n tokens with the state resident on chip: per token
+ *   S <- diag(exp g) S ; u = w*v - S^T (b*k) ; S <- S + k u^T ; o = scale S^T q
+ * state is updated in place; o is [B, s_alloc, H, DV] in out_dtype.
+ * Supports DK in {32, 64, 128, 256}, DV a multiple of 32, any n >= 0.
+ * Replaces: decode_multi_kernel(...)(...) in gdn2/inference.py:347-353
+ * (gdn2_decode) and decode_step_kernel(...)(...) in gdn2/inference.py:190-196
+ * (gdn2_decode_step, which is n = 1 with s_alloc = 1).
+ */
+int gdn2_hip_decode(const void* q, const void* k, const void* v, const float* g, const void* b,
+                    const void* w, int in_dtype, float* state, void* o, int out_dtype, int B,
+                    int H, int DK, int DV, long s_alloc, long t0, long n, float scale,
+                    void* stream);
+
+/* Bytes of workspace gdn2_hip_chunk_local / gdn2_hip_prefill_chunks need for
+ * n_tokens (a multiple of 64) tokens; 0 for an unsupported DK. */
+size_t gdn2_hip_prefill_workspace_bytes(int B, int H, int DK, long n_tokens);
+
+/*
+ * Prefill stage 1 (chunk-local, fully parallel): for every 64-token chunk of
+ * tokens [t0, t0 + n_tokens) build the log2-space decay cumsum, the Aqk / Akk
+ * blocks, Ai = (I + Akk)^-1 and the WY factors, and write one record per chunk
+ * into `workspace`. DK in {64, 128}; n_tokens a multiple of 64.
+ * Replaces: wy_stages kernels 1-5 in gdn2/forward.py:801-826
+ * (cumsum, intra_diag, inter_blocks, solve, wy).
+ */
+int gdn2_hip_chunk_local(const void* q, const void* k, const void* b, const float* g,
+                         int in_dtype, void* workspace, int B, int H, int DK, long s_alloc,
+                         long t0, long n_tokens, float scale, void* stream);
+
+/*
+ * Prefill stage 2 (sequential over chunks, parallel over B*H*DV-tiles): the
+ * state scan fused with the output; reads the stage-1 records and v, w.
+ * state_in may be NULL (zero state) and may equal state_out. DV a multiple of 16.
+ * Replaces: prefill_scan_kernel(...)(...) in gdn2/inference.py:544-550 and the
+ * state_kernel + output_kernel pair in gdn2/forward.py:879-892.
+ */
+int gdn2_hip_prefill_scan(const void* v, const void* w, int in_dtype, const void* workspace,
+                          const float* state_in, float* state_out, void* o, int out_dtype, int B,
+                          int H, int DK, int DV, long s_alloc, long t0, long n_tokens,
+                          void* stream);
+
+/*
+ * Both prefill stages back to back on one stream: o[t0 : t0+n_tokens] and the
+ * state after the last token. Replaces the device branch of gdn2_prefill
+ * (gdn2/inference.py:542-550) and of chunk_gdn2_fwd (gdn2/forward.py:870-895).
+ */
+int gdn2_hip_prefill_chunks(const void* q, const void* k, const void* v, const float* g,
+                            const void* b, const void* w, int in_dtype, const float* state_in,
+                            float* state_out, void* o, int out_dtype, void* workspace, int B,
+                            int H, int DK, int DV, long s_alloc, long t0, long n_tokens,
+                            float scale, void* stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* GDN2_HIP_H */

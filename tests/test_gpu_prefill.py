@@ -1,0 +1,114 @@
+"""Prefill / chunkwise-forward parity (GPU) against the CPU oracle.
+
+The bar: o and the final state within 2e-3 max-abs
+error relative to the fp32 reference, `rel_err = max|a - ref| / max|ref|`
+(reference tests/test_gdn2.py:38-39). o is compared in fp32
+(`GDN2Config(output_dtype=torch.float32)`) because rounding o to bf16 alone
+can cost up to 2^-8 relative; the bf16-output path is checked to be the fp32
+result rounded. Inputs are rounded to the kernel dtype before the oracle sees
+them, so input quantisation is not counted as error.
+"""
+
+from __future__ import annotations
+
+import pytest
+import torch
+
+import oracle
+from gdt2_tilelang_amd import GDN2Config, chunk_gdn2_fwd, gdn2_attention, gdn2_prefill
+from tests.helpers import device_inputs, seeded_state
+
+pytestmark = pytest.mark.gpu
+rel_err = oracle.rel_err
+TOL = 2e-3
+F32 = GDN2Config(output_dtype=torch.float32)
+
+
+def _check(B, S, H, DK, DV, dtype=torch.bfloat16, decay_scale=4.0, dist="ref", with_state=True, seed=0):
+    print(f"prefill B={B} S={S} H={H} DK={DK} DV={DV} {dtype} decay={decay_scale} {dist}", flush=True)
+    cpu, dev = device_inputs(B, S, H, DK, DV, dtype, decay_scale=decay_scale, seed=seed, dist=dist)
+    s0 = seeded_state(B, H, DK, DV) if with_state else None
+    o_ref, s_ref = oracle.prefill(*cpu, None if s0 is None else s0.clone())
+    o, st = gdn2_prefill(*dev, None if s0 is None else s0.cuda(), config=F32)
+    torch.cuda.synchronize()
+    assert o.shape == (B, S, H, DV) and o.dtype == torch.float32
+    eo, es = rel_err(o.cpu(), o_ref), rel_err(st.cpu(), s_ref)
+    print(f"  rel_err o={eo:.2e} state={es:.2e}", flush=True)
+    assert eo < TOL and es < TOL
+    return dev, o, st
+
+
+@pytest.mark.parametrize("B,S,H,DK,DV", [
+    (2, 512, 4, 64, 64), (1, 1024, 8, 128, 128), (2, 320, 2, 64, 128),
+    (2, 1000, 4, 64, 64), (1, 100, 2, 128, 64), (1, 7, 2, 64, 64), (3, 192, 2, 128, 96),
+])
+def test_prefill_matches_oracle(B, S, H, DK, DV):
+    _check(B, S, H, DK, DV)
+
+
+@pytest.mark.parametrize("decay_scale", [0.0, 1.0, 8.0, 30.0])
+def test_prefill_decay_scales(decay_scale):
+    """Covers both block-rescaling paths: 8 and 30 force the exact path
+    (a channel losing > 83 nats in 16 tokens) and must not overflow."""
+    _, o, _ = _check(1, 256, 2, 128, 128, decay_scale=decay_scale)
+    assert torch.isfinite(o).all()
+
+
+@pytest.mark.parametrize("dtype", [torch.float16, torch.float32])
+@pytest.mark.parametrize("DK", [64, 128])
+def test_prefill_input_dtypes(dtype, DK):
+    _check(2, 256, 2, DK, 64, dtype=dtype)
+
+
+def test_prefill_no_initial_state():
+    _check(2, 384, 3, 128, 128, with_state=False)
+
+
+def test_prefill_bf16_output_is_rounded_fp32():
+    B, S, H, D = 2, 512, 4, 128
+    _, dev = device_inputs(B, S, H, D, D, torch.bfloat16)
+    o32, s32 = gdn2_prefill(*dev, config=F32)
+    o16, s16 = gdn2_prefill(*dev)
+    torch.cuda.synchronize()
+    assert o16.dtype == torch.bfloat16
+    assert torch.equal(s32, s16)
+    assert ((o16.float() - o32).abs() <= o32.abs() * 2 ** -8 + 1e-30).all()
+
+
+def test_segmented_prefill_equals_one_pass():
+    """reference tests/test_inference.py:135-150, on the GPU kernels."""
+    B, S, H, D = 2, 448, 3, 64
+    _, dev = device_inputs(B, S, H, D, D, torch.bfloat16)
+    o_all, s_all = gdn2_prefill(*dev, config=F32)
+    outs, st = [], None
+    for lo, hi in ((0, 64), (64, 160), (160, 197), (197, 448)):
+        o, st = gdn2_prefill(*(t[:, lo:hi] for t in dev), st, config=F32)
+        outs.append(o)
+    torch.cuda.synchronize()
+    assert rel_err(torch.cat(outs, 1), o_all) < TOL
+    assert rel_err(st, s_all) < TOL
+
+
+def test_prefill_baseline_config1():
+    """B=2 S=4096 H=16 DK=DV=128, bf16 inputs, fp32 g,
+    q,k L2-normalised, g = logsigmoid(N(0,1)), b,w = sigmoid(N(0,1))."""
+    _check(2, 4096, 16, 128, 128, dist="cfg", with_state=False)
+
+
+def test_gdn2_attention_and_chunk_fwd():
+    """Functional op: zero-padding of a ragged length is inert; initial_state
+    is read, not written; final state only on request."""
+    B, S, H, D = 2, 200, 2, 64
+    cpu, dev = device_inputs(B, S, H, D, D, torch.bfloat16)
+    s0 = seeded_state(B, H, D, D)
+    o_ref, s_ref = oracle.recurrent_gdn2(*cpu, None, s0, True)
+    s0d = s0.cuda()
+    o, st = gdn2_attention(*dev, initial_state=s0d, output_final_state=True, config=F32)
+    o2, none = chunk_gdn2_fwd(*dev, D ** -0.5, s0d, False, F32)
+    torch.cuda.synchronize()
+    assert none is None
+    assert torch.equal(s0d.cpu(), s0)
+    assert rel_err(o.cpu(), o_ref) < TOL and rel_err(st.cpu(), s_ref) < TOL
+    assert torch.equal(o, o2)
+    o16, _ = gdn2_attention(*dev)
+    assert o16.dtype == torch.bfloat16 and o16.shape == (B, S, H, D)
