@@ -1,0 +1,261 @@
+"""Benchmark of the GDN-2 hip backend on one MI355X; prints ONE JSON line.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
+
+Headline (BASELINE.json ``metric``): prefill tokens/s at BASELINE config 1
+(B=2 S=4096 H=16 DK=DV=128, bf16 q,k,v,b,w, fp32 g, synthetic data with the
+config's distributions). A step is one prefill of the batch through the C ABI:
+``gdn2_hip_chunk_local`` then ``gdn2_hip_prefill_scan`` with inputs already
+resident in HBM. Two input sets are alternated so the 256 MB Infinity Cache
+cannot hold a step's working set.
+
+Also reported: decode state GB/s for BASELINE configs 2 (decode_step, B=64,
+64 calls) and 3 (decode_multi n=8, B=32), rotating enough independent states
+(> 256 MB in total) that every call streams its state from HBM, and the CPU
+baseline: the oracle's chunkwise torch path on the host cores.
+"""
+
+from __future__ import annotations
+
+import argparse
+import json
+import os
+import platform
+import sys
+import time
+
+import torch
+import torch.nn.functional as F
+
+HBM_PEAK_GBS = 8000.0            # MI355X HBM3E, GB/s
+BF16_DENSE_TFLOPS = 2500.0       # MI355X dense bf16 MFMA
+
+# BASELINE config 1
+B1, S1, H1, D1 = 2, 4096, 16, 128
+# algorithmic bytes of one config-1 prefill: q,k,v,b,w bf16 + g fp32 in, o bf16 out,
+# final fp32 state out (no initial state)
+ALG_BYTES_PREFILL = (5 * B1 * S1 * H1 * D1 * 2) + (B1 * S1 * H1 * D1 * 4) \
+    + (B1 * S1 * H1 * D1 * 2) + (B1 * H1 * D1 * D1 * 4)
+# dense GEMM flops of the chunkwise form per 64-token chunk (QK^T, EK^T, Ai E,
+# Ai Z, W S, Qg S, Aqk Un, KG^T Un)
+BS = 64
+FLOPS_PER_CHUNK = 2 * BS * BS * (3 * D1 + 2 * D1) + 6 * BS * D1 * D1
+ALG_FLOPS_PREFILL = FLOPS_PER_CHUNK * B1 * H1 * (S1 // BS)
+
+
+def log(msg):
+    print(msg, file=sys.stderr, flush=True)
+
+
+def cfg_inputs(B, S, H, DK, DV, seed, device="cuda", dtype=torch.bfloat16):
+    """q,k ~ N(0,1) L2-normalised, v ~ N(0,1), g = logsigmoid(N(0,1)), b,w = sigmoid(N(0,1))."""
+    gen = torch.Generator(device=device).manual_seed(seed)
+    kw = dict(generator=gen, device=device, dtype=torch.float32)
+    q = F.normalize(torch.randn(B, S, H, DK, **kw), dim=-1).to(dtype)
+    k = F.normalize(torch.randn(B, S, H, DK, **kw), dim=-1).to(dtype)
+    v = torch.randn(B, S, H, DV, **kw).to(dtype)
+    g = F.logsigmoid(torch.randn(B, S, H, DK, **kw))
+    b = torch.sigmoid(torch.randn(B, S, H, DK, **kw)).to(dtype)
+    w = torch.sigmoid(torch.randn(B, S, H, DV, **kw)).to(dtype)
+    return q, k, v, g, b, w
+
+
+def bench_prefill(steps, warmup):
+    from gdt2_tilelang_amd import _hip
+
+    lib = _hip.lib()
+    dev = torch.device("cuda")
+    stream = torch.cuda.current_stream()
+    sp = _hip.stream_of(dev)
+    sets = [cfg_inputs(B1, S1, H1, D1, D1, seed=s) for s in (11, 12)]
+    n_tok = S1
+    ws_bytes = lib.gdn2_hip_prefill_workspace_bytes(B1, H1, D1, n_tok)
+    ws = torch.empty(ws_bytes, dtype=torch.uint8, device=dev)
+    o = torch.empty(B1, S1, H1, D1, dtype=torch.bfloat16, device=dev)
+    st = torch.empty(B1, H1, D1, D1, dtype=torch.float32, device=dev)
+    P = _hip.ptr
+    scale = D1 ** -0.5
+
+    def step(i, ev=None):
+        q, k, v, g, b, w = sets[i % 2]
+        if ev is not None:
+            ev[0].record(stream)
+        _hip.check(lib.gdn2_hip_chunk_local(P(q), P(k), P(b), P(g), 1, P(ws), B1, H1, D1, S1, 0, n_tok,
+                                            scale, sp), "chunk_local")
+        if ev is not None:
+            ev[1].record(stream)
+        _hip.check(lib.gdn2_hip_prefill_scan(P(v), P(w), 1, P(ws), None, P(st), P(o), 1, B1, H1, D1, D1,
+                                             S1, 0, n_tok, sp), "prefill_scan")
+        if ev is not None:
+            ev[2].record(stream)
+
+    for i in range(warmup):
+        step(i)
+    torch.cuda.synchronize()
+    # whole-step timing (no per-kernel events inside)
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for i in range(steps):
+        step(i)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms_step = t0.elapsed_time(t1) / steps
+    # per-kernel timing with events around each launch on the launch stream
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(3)] for _ in range(steps)]
+    for i in range(steps):
+        step(i, evs[i])
+    torch.cuda.synchronize()
+    cl = sum(e[0].elapsed_time(e[1]) for e in evs) / steps
+    sc = sum(e[1].elapsed_time(e[2]) for e in evs) / steps
+    return ms_step, cl, sc
+
+
+def bench_decode(B, n, calls, steps_per_buf_min, H=16, D=128):
+    """Average µs per decode call with rotating states (> MALL) for config 2/3."""
+    from gdt2_tilelang_amd import _hip
+
+    lib = _hip.lib()
+    dev = torch.device("cuda")
+    sp = _hip.stream_of(dev)
+    state_bytes = B * H * D * D * 4
+    nbuf = max(2, -(-320 * 2 ** 20 // state_bytes))      # > 256 MB Infinity Cache in total
+    states = [torch.randn(B, H, D, D, device=dev) * 0.1 for _ in range(nbuf)]
+    tok = [cfg_inputs(B, n, H, D, D, seed=100 + i) for i in range(4)]
+    o = torch.empty(B, n, H, D, dtype=torch.bfloat16, device=dev)
+    P = _hip.ptr
+    scale = D ** -0.5
+
+    def call(i):
+        q, k, v, g, b, w = tok[i % 4]
+        _hip.check(lib.gdn2_hip_decode(P(q), P(k), P(v), P(g), P(b), P(w), 1, P(states[i % nbuf]), P(o), 1,
+                                       B, H, D, D, n, 0, n, scale, sp), "decode")
+
+    for i in range(2 * nbuf):
+        call(i)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0 = torch.cuda.Event(enable_timing=True)
+    e1 = torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for i in range(calls):
+        call(i)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    us = e0.elapsed_time(e1) * 1e3 / calls
+    st_traffic = 2 * state_bytes
+    tok_bytes = B * n * H * D * (4 * 2 + 4 + 2 * 2) + B * n * H * D * 2   # q,k,b bf16 + g fp32 + v,w + o
+    gbs = st_traffic / (us * 1e-6) / 1e9
+    return dict(B=B, n=n, H=H, DK=D, DV=D, calls=calls, state_buffers=nbuf, us_per_call=round(us, 3),
+                state_GBps=round(gbs, 1), state_frac_of_peak=round(gbs / HBM_PEAK_GBS, 4),
+                total_GBps=round((st_traffic + tok_bytes) / (us * 1e-6) / 1e9, 1),
+                tokens_per_s=round(B * n / (us * 1e-6), 1))
+
+
+def cpu_baseline(budget_s=12.0):
+    """The oracle's chunkwise torch path (reference gdn2/reference.py:168-261)
+    on the host cores, over repeated full config-1 prefills."""
+    sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    from oracle import chunk_gdn2
+
+    threads = os.cpu_count() or 1
+    torch.set_num_threads(threads)
+    q, k, v, g, b, w = cfg_inputs(B1, S1, H1, D1, D1, seed=11, device="cpu")
+    ins = tuple(t.float() for t in (q, k, v)) + (g,) + tuple(t.float() for t in (b, w))
+    chunk_gdn2(*(t[:, :256] for t in ins))          # warm-up
+    reps, t_start = 0, time.perf_counter()
+    while True:
+        chunk_gdn2(*ins, output_final_state=True)
+        reps += 1
+        el = time.perf_counter() - t_start
+        if el > budget_s or reps >= 20:
+            break
+    tps = reps * B1 * S1 / el
+    return {"value": round(tps, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+            "sample": f"{reps} full config-1 prefills (B=2 S=4096 H=16 D=128, fp32 torch "
+                      f"chunkwise oracle) in {el:.1f} s on {platform.processor() or 'host CPU'}"}
+
+
+def read_traffic():
+    """HBM bytes per prefill step from the committed rocprofv3 --pmc summary, if any."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
+                        "prefill_config1_pmc.txt")
+    if not os.path.exists(path):
+        return None
+    with open(path) as f:
+        for line in f:
+            if line.startswith("traffic_bytes_per_step:"):
+                return float(line.split(":")[1])
+    return None
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=50)
+    ap.add_argument("--warmup", type=int, default=10)
+    ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
+    ap.add_argument("--no-decode", action="store_true", help="skip the decode configs")
+    ap.add_argument("--prefill-only", action="store_true", help="prefill steps only (for profilers)")
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(json.dumps({"error": "this build runs on one GPU only; the GDN-2 path shards by "
+                                   "batch/head with no exchange (see DESIGN.md), --gpus must be 1"}))
+        sys.exit(2)
+    if not torch.cuda.is_available():
+        print(json.dumps({"error": "no GPU visible"}))
+        sys.exit(2)
+
+    log(f"device: {torch.cuda.get_device_name()}")
+    ms_step, cl_ms, sc_ms = bench_prefill(args.steps, args.warmup)
+    if args.prefill_only:
+        log(f"prefill {ms_step * 1e3:.1f} us/step (chunk_local {cl_ms * 1e3:.1f}, scan {sc_ms * 1e3:.1f})")
+        return
+    tokens = B1 * S1
+    value = tokens / (ms_step * 1e-3)
+    kern_s = (cl_ms + sc_ms) * 1e-3
+    achieved = ALG_BYTES_PREFILL / kern_s / 1e9
+    traffic = read_traffic()
+    out = {
+        "metric": "prefill tokens/s (S=4096) + decode state GB/s vs HBM peak, 1 MI355X",
+        "value": round(value, 1),
+        "unit": "tokens/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms_step, 5),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "bf16",
+        "data": "synthetic",
+        "config": {"workload": "gdn2 prefill, BASELINE config 1: B=2 S=4096 H=16 DK=DV=128, "
+                               "bf16 q,k,v,b,w + fp32 g in, bf16 o + fp32 state out, chunk 64",
+                   "global_batch": B1, "seq_len": S1, "heads": H1, "head_dim": D1,
+                   "arithmetic": "bf16 MFMA (hi/lo split where precision needs it), fp32 accumulate"},
+        "roofline": {
+            "bound": "hbm",
+            "kernel": "prefill step = gdn2 chunk_local_kernel + scan_kernel",
+            "achieved": round(achieved, 1),
+            "peak": HBM_PEAK_GBS,
+            "unit": "GB/s",
+            "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "traffic": traffic,
+            "algorithmic_bytes": ALG_BYTES_PREFILL,
+            "kernel_us": {"chunk_local": round(cl_ms * 1e3, 2), "scan": round(sc_ms * 1e3, 2)},
+            "gemm_tflops": round(ALG_FLOPS_PREFILL / kern_s / 1e12, 1),
+            "gemm_frac_of_bf16_peak": round(ALG_FLOPS_PREFILL / kern_s / 1e12 / BF16_DENSE_TFLOPS, 4),
+        },
+    }
+    if not args.no_decode:
+        out["decode"] = {
+            "config2_decode_step": bench_decode(64, 1, calls=64, steps_per_buf_min=1),
+            "config3_decode_multi_n8": bench_decode(32, 8, calls=64, steps_per_buf_min=1),
+        }
+    if not args.no_cpu:
+        out["cpu_baseline"] = cpu_baseline()
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -10,6 +10,7 @@
 //   Akk[r,s] =         sum_c b_rc k_rc k_sc 2^(G_rc - G_sc)   s < r
 //   Ai = (I + Akk)^-1,  W = Ai (b*k*gamma),  KG = k * 2^(G_last - G)
 //   Q' = scale*q*gamma - Aqk W      (so the scan's output is Q' S + Aqk U)
+//   MOZ = Aqk bf16(Ai)               (so the scan forms Aqk U as MOZ (w*v))
 //
 // Overflow safety (reference forward.py:21-32): every 16x16 block of Aqk/Akk
 // is an MFMA product of row factors 2^(G_r - ref) and column factors
@@ -25,7 +26,7 @@
 //
 // Precision (bf16 MFMA, fp32 accumulate): the Aqk product uses hi+lo split
 // operands (three MFMAs); Akk, W and Aqk*W use single bf16 operands; the solve
-// is fp32. Q', KG and Aqk are exported as hi/lo pairs, W and Ai as bf16.
+// is fp32. Q', KG and MOZ are exported as hi/lo pairs, W and Ai as bf16.
 #include "gdn2_common.h"
 #include "gdn2_prefill_layout.h"
 
@@ -320,8 +321,8 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
     __syncthreads();
   }
 
-  // ---- phase D: W = Ai E (bf16 MFMA); Ai and Aqk fragments out ------------
-  bf16x8 ai[2], aqk_hi[2];
+  // ---- phase D: W = Ai E (bf16 MFMA); Ai fragments out -------------------
+  bf16x8 ai[2], aqk_hi[2], aqk_lo[2];
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk) {
     const int s0 = 32 * kk + 8 * lq;
@@ -332,10 +333,7 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
     *reinterpret_cast<bf16x8*>(rec + L::ai_frag(wave, kk) + lane * 8) = ai[kk];
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] = sA1[my_r * AP + s0 + j];
-    bf16x8 lo;
-    split_bf16x8(x, aqk_hi[kk], lo);
-    *reinterpret_cast<bf16x8*>(rec + L::aqk_frag(wave, kk, 0) + lane * 8) = aqk_hi[kk];
-    *reinterpret_cast<bf16x8*>(rec + L::aqk_frag(wave, kk, 1) + lane * 8) = lo;
+    split_bf16x8(x, aqk_hi[kk], aqk_lo[kk]);
   }
 #pragma unroll
   for (int nn = 0; nn < MT; ++nn) {
@@ -360,6 +358,26 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
     const bf16x8 x = *reinterpret_cast<const bf16x8*>(&sW[my_r * WP + 32 * kk + 8 * lq]);
     *reinterpret_cast<bf16x8*>(rec + L::w_frag(wave, kk) + lane * 8) = x;
   }
+  // MOZ = Aqk (hi/lo) x bf16(Ai), staged in the (now dead) E^T region
+  {
+    float* sMZ = reinterpret_cast<float*>(sET);
+#pragma unroll
+    for (int nn = 0; nn < 4; ++nn) {
+      f32x4 acc = zero4();
+      const int col = 16 * nn + lr;
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+        float x[8];
+#pragma unroll
+        for (int j = 0; j < 8; ++j) x[j] = sAI[(32 * kk + 8 * lq + j) * AP + col];
+        const bf16x8 bfr = pack_bf16x8(x);
+        acc = mfma(aqk_hi[kk], bfr, acc);
+        acc = mfma(aqk_lo[kk], bfr, acc);
+      }
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sMZ[(16 * wave + 4 * lq + e) * AP + col] = acc[e];
+    }
+  }
 
   // ---- phase E: Q' = scale*q*gamma - Aqk W ---------------------------------
 #pragma unroll
@@ -375,6 +393,19 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
     for (int e = 0; e < 4; ++e) sQS[(16 * wave + 4 * lq + e) * GP + c] = acc[e];
   }
   __syncthreads();
+  {
+    const float* sMZ = reinterpret_cast<const float*>(sET);
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      float x[8];
+#pragma unroll
+      for (int j = 0; j < 8; ++j) x[j] = sMZ[my_r * AP + 32 * kk + 8 * lq + j];
+      bf16x8 hi, lo;
+      split_bf16x8(x, hi, lo);
+      *reinterpret_cast<bf16x8*>(rec + L::moz_frag(wave, kk, 0) + lane * 8) = hi;
+      *reinterpret_cast<bf16x8*>(rec + L::moz_frag(wave, kk, 1) + lane * 8) = lo;
+    }
+  }
 #pragma unroll
   for (int kk = 0; kk < KT; ++kk) {
     const int c0 = 32 * kk + 8 * lq;

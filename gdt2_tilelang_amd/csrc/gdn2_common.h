@@ -29,12 +29,16 @@ __device__ __forceinline__ float bf16_bits_to_f32(unsigned short h) {
   return __uint_as_float(static_cast<uint32_t>(h) << 16);
 }
 
-// Round-to-nearest-even float -> bf16 bit pattern (finite inputs; NaN kept NaN).
+typedef __bf16 bf16x2 __attribute__((ext_vector_type(2)));
+typedef float f32x2 __attribute__((ext_vector_type(2)));
+
+// Round-to-nearest-even float pair -> packed bf16 pair (one v_cvt_pk_bf16_f32).
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2{a, b}), bf16x2));
+}
+
 __device__ __forceinline__ unsigned short f32_to_bf16_bits(float f) {
-  uint32_t u = __float_as_uint(f);
-  if ((u & 0x7fffffffu) > 0x7f800000u) return static_cast<unsigned short>((u >> 16) | 0x40);
-  u += 0x7fffu + ((u >> 16) & 1u);
-  return static_cast<unsigned short>(u >> 16);
+  return static_cast<unsigned short>(cvt_pk_bf16(f, 0.f) & 0xffffu);
 }
 
 __device__ __forceinline__ float f16_bits_to_f32(unsigned short h) {
@@ -58,21 +62,35 @@ __device__ __forceinline__ void store_elem(void* p, size_t i, int dt, float x) {
   else static_cast<float*>(p)[i] = x;
 }
 
+typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
+
 // Eight bf16 values from eight floats (round to nearest even).
 __device__ __forceinline__ bf16x8 pack_bf16x8(const float* x) {
-  u16x8 r;
+  u32x4 r;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) r[j] = f32_to_bf16_bits(x[j]);
+  for (int j = 0; j < 4; ++j) r[j] = cvt_pk_bf16(x[2 * j], x[2 * j + 1]);
   return __builtin_bit_cast(bf16x8, r);
 }
 
-// Split eight floats into bf16 hi + lo with x ~= hi + lo to ~16 mantissa bits.
+// bf16 pair (packed) back to two floats.
+__device__ __forceinline__ float bf16_lo_f32(uint32_t p) { return __uint_as_float(p << 16); }
+__device__ __forceinline__ float bf16_hi_f32(uint32_t p) { return __uint_as_float(p & 0xffff0000u); }
+
+// Split a float pair into packed bf16 hi and lo with x ~= hi + lo (~16 mantissa bits).
+__device__ __forceinline__ void split_pk(float a, float b, uint32_t& hi, uint32_t& lo) {
+  hi = cvt_pk_bf16(a, b);
+  lo = cvt_pk_bf16(a - bf16_lo_f32(hi), b - bf16_hi_f32(hi));
+}
+
+// Split eight floats into bf16 hi + lo.
 __device__ __forceinline__ void split_bf16x8(const float* x, bf16x8& hi, bf16x8& lo) {
-  u16x8 h, l;
+  u32x4 h, l;
 #pragma unroll
-  for (int j = 0; j < 8; ++j) {
-    h[j] = f32_to_bf16_bits(x[j]);
-    l[j] = f32_to_bf16_bits(x[j] - bf16_bits_to_f32(h[j]));
+  for (int j = 0; j < 4; ++j) {
+    uint32_t a, b;
+    split_pk(x[2 * j], x[2 * j + 1], a, b);
+    h[j] = a;
+    l[j] = b;
   }
   hi = __builtin_bit_cast(bf16x8, h);
   lo = __builtin_bit_cast(bf16x8, l);

@@ -8,11 +8,16 @@
 //   W   [4 m][DK/32 kk]          bf16      W   = Ai (b*k*gamma)            64 x DK
 //   QP  [4 m][DK/32 kk][hi,lo]   bf16 x2   Q'  = scale*q*gamma - Aqk W     64 x DK
 //   KT  [DK/16 m][2 kk][hi,lo]   bf16 x2   KG^T, KG = k*gamma_last/gamma   DK x 64
-//   AQK [4 m][2 kk][hi,lo]       bf16 x2   Aqk (scale, diagonal included)  64 x 64
+//   MOZ [4 m][2 kk][hi,lo]       bf16 x2   Aqk Ai (Aqk: scale, diagonal in) 64 x 64
 //   AI  [4 m][2 kk]              bf16      Ai  = (I + Akk)^-1               64 x 64
 //   GL  [DK]                     fp32      gamma_last = exp(G_last)
 //
 // Within a fragment the 64 lanes' 8-element groups are contiguous.
+//
+// With Z = w * v, the scan needs U = Ai Z and the intra-chunk output
+// Aqk U = (Aqk Ai) Z; storing MOZ = Aqk Ai lets it take both from Z without
+// exchanging U between waves. Ai is rounded to bf16 once and the same rounded
+// matrix is used for U and inside MOZ, so the two stay consistent.
 #pragma once
 
 namespace gdn2 {
@@ -28,15 +33,15 @@ struct ChunkLayout {
   static constexpr long W_OFF = 0;
   static constexpr long QP_OFF = W_OFF + 4L * KT * kFrag;
   static constexpr long KT_OFF = QP_OFF + 4L * KT * 2 * kFrag;
-  static constexpr long AQK_OFF = KT_OFF + static_cast<long>(MT) * 2 * 2 * kFrag;
-  static constexpr long AI_OFF = AQK_OFF + 4L * 2 * 2 * kFrag;
+  static constexpr long MOZ_OFF = KT_OFF + static_cast<long>(MT) * 2 * 2 * kFrag;
+  static constexpr long AI_OFF = MOZ_OFF + 4L * 2 * 2 * kFrag;
   static constexpr long GL_OFF = AI_OFF + 4L * 2 * kFrag;   // in bf16 slots
   static constexpr long STRIDE = GL_OFF + 2L * DK;          // bf16 elements per record
 
   __device__ static long w_frag(int m, int kk) { return W_OFF + (m * KT + kk) * kFrag; }
   __device__ static long qp_frag(int m, int kk, int hl) { return QP_OFF + ((m * KT + kk) * 2 + hl) * kFrag; }
   __device__ static long kt_frag(int m, int kk, int hl) { return KT_OFF + ((m * 2 + kk) * 2 + hl) * kFrag; }
-  __device__ static long aqk_frag(int m, int kk, int hl) { return AQK_OFF + ((m * 2 + kk) * 2 + hl) * kFrag; }
+  __device__ static long moz_frag(int m, int kk, int hl) { return MOZ_OFF + ((m * 2 + kk) * 2 + hl) * kFrag; }
   __device__ static long ai_frag(int m, int kk) { return AI_OFF + (m * 2 + kk) * kFrag; }
 };
 

@@ -7,43 +7,118 @@
 // S[DK, DVT] stays in MFMA accumulators for the whole sequence. Per chunk, from
 // the chunk record (gdn2_prefill_layout.h) and v, w:
 //
-//   Z  = w * v                   U   = Ai Z           O_loc = Aqk U
-//   Un = U - W S                 o   = Q' S + O_loc
+//   Z  = w * v          U = Ai Z          Un = U - W S
+//   o  = Q' S + MOZ Z                      (= scale*(q*gamma) S + Aqk Un)
 //   S  = diag(gamma_last) S + KG^T Un
 //
-// which equals o = scale*(q*gamma) S + Aqk Un of the reference because
-// Q' = scale*q*gamma - Aqk W. Operands that carry the result's precision are
-// split into bf16 hi + lo (Z, U, S, Un, and the Aqk, Q', KG records), so the
-// products Ai Z, Aqk U, Q' S and KG^T Un keep ~16 mantissa bits; W S uses the
+// Operands that carry the result's precision are split into bf16 hi + lo
+// (Z, S, Un and the Q', MOZ, KG records) so those products keep ~16 mantissa
+// bits; Ai Z uses bf16 Ai (the same rounding MOZ was built with) and W S the
 // bf16 state only (its error is damped by the erase term).
 //
 // Wave w owns output rows 16w..16w+15 of the chunk and state rows
-// 16*(w*MPW) .. 16*(w*MPW+MPW)-1. Four barriers per chunk hand Z, U, Un and S
-// between waves through LDS in B-operand order ([column][k], k contiguous).
+// 16*(w*MPW) .. 16*(w*MPW+MPW)-1. Per chunk two barriers hand Un and then the
+// new state between waves through LDS in B-operand order ([column][k], k
+// contiguous); S and Z are double-buffered so the next chunk's Z is staged
+// while the current one is in use, and the next chunk's record fragments are
+// fetched into registers one chunk ahead.
+//
 // Workgroup -> (head, tile) is XCD-aware: the tiles of one head land on the
-// same XCD so its chunk records are fetched from HBM once into that L2.
+// same XCD so its chunk records come from HBM once into that XCD's L2.
 #include "gdn2_common.h"
 #include "gdn2_prefill_layout.h"
 
+#include <type_traits>
+
 namespace gdn2 {
 
-template <int DK, int NT>
+template <int DK>
+struct ScanFrags {
+  static constexpr int KT = DK / 32;
+  static constexpr int MPW = DK / 64;
+  bf16x8 ai[2], mzh[2], mzl[2];
+  bf16x8 w[KT], qh[KT], ql[KT];
+  bf16x8 kh[MPW][2], kl[MPW][2];
+  float4 gam[MPW];
+};
+
+template <int DK>
+__device__ __forceinline__ void load_frags(const unsigned short* __restrict__ rec, int wave, int lane,
+                                           int lq, ScanFrags<DK>& f) {
+  using L = ChunkLayout<DK>;
+  constexpr int KT = DK / 32, MPW = DK / 64;
+  const int o8 = lane * 8;
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk) {
+    f.ai[kk] = *reinterpret_cast<const bf16x8*>(rec + L::ai_frag(wave, kk) + o8);
+    f.mzh[kk] = *reinterpret_cast<const bf16x8*>(rec + L::moz_frag(wave, kk, 0) + o8);
+    f.mzl[kk] = *reinterpret_cast<const bf16x8*>(rec + L::moz_frag(wave, kk, 1) + o8);
+  }
+#pragma unroll
+  for (int kk = 0; kk < KT; ++kk) {
+    f.w[kk] = *reinterpret_cast<const bf16x8*>(rec + L::w_frag(wave, kk) + o8);
+    f.qh[kk] = *reinterpret_cast<const bf16x8*>(rec + L::qp_frag(wave, kk, 0) + o8);
+    f.ql[kk] = *reinterpret_cast<const bf16x8*>(rec + L::qp_frag(wave, kk, 1) + o8);
+  }
+  const float* gl = reinterpret_cast<const float*>(rec + L::GL_OFF);
+#pragma unroll
+  for (int mi = 0; mi < MPW; ++mi) {
+    const int m = wave * MPW + mi;
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      f.kh[mi][kk] = *reinterpret_cast<const bf16x8*>(rec + L::kt_frag(m, kk, 0) + o8);
+      f.kl[mi][kk] = *reinterpret_cast<const bf16x8*>(rec + L::kt_frag(m, kk, 1) + o8);
+    }
+    f.gam[mi] = *reinterpret_cast<const float4*>(gl + 16 * m + 4 * lq);
+  }
+}
+
+// Four consecutive v (or w) elements as floats, raw register form per dtype.
+template <int IN_DT>
+struct Raw4 {
+  using T = typename std::conditional<IN_DT == DT_F32, float4, uint2>::type;
+  T v;
+  __device__ __forceinline__ void load(const void* base, size_t idx) {
+    if constexpr (IN_DT == DT_F32) v = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + idx);
+    else v = *reinterpret_cast<const uint2*>(static_cast<const unsigned short*>(base) + idx);
+  }
+  __device__ __forceinline__ void get(float* x) const {
+    if constexpr (IN_DT == DT_F32) {
+      x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
+    } else if constexpr (IN_DT == DT_BF16) {
+      x[0] = bf16_lo_f32(v.x); x[1] = bf16_hi_f32(v.x); x[2] = bf16_lo_f32(v.y); x[3] = bf16_hi_f32(v.y);
+    } else {
+      x[0] = f16_bits_to_f32(v.x & 0xffff); x[1] = f16_bits_to_f32(v.x >> 16);
+      x[2] = f16_bits_to_f32(v.y & 0xffff); x[3] = f16_bits_to_f32(v.y >> 16);
+    }
+  }
+};
+
+// packed pair store of a D-layout quad (4 consecutive k for one column) as hi/lo
+__device__ __forceinline__ void put_quad(unsigned short* hi, unsigned short* lo, const f32x4& x) {
+  uint32_t h0, l0, h1, l1;
+  split_pk(x[0], x[1], h0, l0);
+  split_pk(x[2], x[3], h1, l1);
+  *reinterpret_cast<uint2*>(hi) = make_uint2(h0, h1);
+  *reinterpret_cast<uint2*>(lo) = make_uint2(l0, l1);
+}
+
+template <int DK, int NT, int IN_DT, int OUT_DT>
 __global__ __launch_bounds__(256) void scan_kernel(
-    const void* __restrict__ v, const void* __restrict__ w, int in_dt,
-    const unsigned short* __restrict__ ws, const float* __restrict__ s_in,
-    float* __restrict__ s_out, void* __restrict__ o, int out_dt, int BH, int H, int DV,
-    long s_alloc, long t0, int NC) {
+    const void* __restrict__ v, const void* __restrict__ w, const unsigned short* __restrict__ ws,
+    const float* __restrict__ s_in, float* __restrict__ s_out, void* __restrict__ o,
+    int BH, int H, int DV, long s_alloc, long t0, int NC) {
   using L = ChunkLayout<DK>;
   constexpr int KT = DK / 32;
-  constexpr int MT = DK / 16;
-  constexpr int MPW = MT / 4;          // state row tiles per wave
+  constexpr int MPW = DK / 64;         // 16-row state tiles per wave
   constexpr int DVT = 16 * NT;
   constexpr int SP = DK + 8;           // bf16 pitch of S^T [DVT][DK]
   constexpr int TP = kBS + 8;          // bf16 pitch of [DVT][64] arrays
+  constexpr int ZIT = kBS * (DVT / 4) / 256;   // Z quads per thread
+  static_assert(ZIT >= 1, "tile too narrow");
 
-  __shared__ __align__(16) unsigned short sSh[DVT * SP], sSl[DVT * SP];
-  __shared__ __align__(16) unsigned short sZh[DVT * TP], sZl[DVT * TP];
-  __shared__ __align__(16) unsigned short sUh[DVT * TP], sUl[DVT * TP];
+  __shared__ __align__(16) unsigned short sSh[2][DVT * SP], sSl[2][DVT * SP];
+  __shared__ __align__(16) unsigned short sZh[2][DVT * TP], sZl[2][DVT * TP];
   __shared__ __align__(16) unsigned short sNh[DVT * TP], sNl[DVT * TP];
 
   const int tid = threadIdx.x;
@@ -67,174 +142,151 @@ __global__ __launch_bounds__(256) void scan_kernel(
   const int bi = bh / H;
   const int h = bh % H;
   const int d0 = tile * DVT;
+  const unsigned short* rec0 = ws + static_cast<size_t>(bh) * NC * L::STRIDE;
+
+  // Z staging: thread handles token t = e / (DVT/4), columns 4*cq .. 4*cq+3
+  Raw4<IN_DT> zv[2][ZIT], zw[2][ZIT];    // [chunk parity]
+  // parity P (= chunk index & 1) is a compile-time constant so the two register
+  // copies stay in registers
+  auto fetch_z = [&](auto parity, int nc) {
+    constexpr int p = decltype(parity)::value;
+#pragma unroll
+    for (int it = 0; it < ZIT; ++it) {
+      const int e = tid + 256 * it;
+      const int t = e / (DVT / 4), cq = e % (DVT / 4);
+      const size_t idx = ((static_cast<size_t>(bi) * s_alloc + t0 + static_cast<long>(nc) * kBS + t) * H + h) * DV + d0 + 4 * cq;
+      zv[p][it].load(v, idx);
+      zw[p][it].load(w, idx);
+    }
+  };
+  auto put_z = [&](auto parity) {     // stage Z of the chunk with this parity into LDS buffer P
+    constexpr int buf = decltype(parity)::value;
+#pragma unroll
+    for (int it = 0; it < ZIT; ++it) {
+      const int e = tid + 256 * it;
+      const int t = e / (DVT / 4), cq = e % (DVT / 4);
+      float a[4], b[4];
+      zv[buf][it].get(a);
+      zw[buf][it].get(b);
+#pragma unroll
+      for (int u = 0; u < 4; u += 2) {
+        uint32_t hi, lo;
+        split_pk(a[u] * b[u], a[u + 1] * b[u + 1], hi, lo);
+        sZh[buf][(4 * cq + u) * TP + t] = static_cast<unsigned short>(hi);
+        sZl[buf][(4 * cq + u) * TP + t] = static_cast<unsigned short>(lo);
+        sZh[buf][(4 * cq + u + 1) * TP + t] = static_cast<unsigned short>(hi >> 16);
+        sZl[buf][(4 * cq + u + 1) * TP + t] = static_cast<unsigned short>(lo >> 16);
+      }
+    }
+  };
 
   // ---- state in: rows c = 16*(wave*MPW+mi) + 4*lq + e, column d0 + 16*nn + lr
   f32x4 S[MPW][NT];
 #pragma unroll
   for (int mi = 0; mi < MPW; ++mi)
 #pragma unroll
-    for (int nn = 0; nn < NT; ++nn) {
+    for (int nn = 0; nn < NT; ++nn)
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int c = 16 * (wave * MPW + mi) + 4 * lq + e;
         S[mi][nn][e] = s_in ? s_in[(static_cast<size_t>(bh) * DK + c) * DV + d0 + 16 * nn + lr] : 0.f;
       }
-    }
-  auto put_state = [&]() {
+  auto put_state = [&](int buf) {
 #pragma unroll
     for (int mi = 0; mi < MPW; ++mi)
 #pragma unroll
       for (int nn = 0; nn < NT; ++nn) {
         const int col = 16 * nn + lr;
         const int c = 16 * (wave * MPW + mi) + 4 * lq;
-        unsigned short hb[4], lb[4];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          hb[e] = f32_to_bf16_bits(S[mi][nn][e]);
-          lb[e] = f32_to_bf16_bits(S[mi][nn][e] - bf16_bits_to_f32(hb[e]));
-        }
-        *reinterpret_cast<uint2*>(&sSh[col * SP + c]) =
-            make_uint2(hb[0] | (uint32_t(hb[1]) << 16), hb[2] | (uint32_t(hb[3]) << 16));
-        *reinterpret_cast<uint2*>(&sSl[col * SP + c]) =
-            make_uint2(lb[0] | (uint32_t(lb[1]) << 16), lb[2] | (uint32_t(lb[3]) << 16));
+        put_quad(&sSh[buf][col * SP + c], &sSl[buf][col * SP + c], S[mi][nn]);
       }
   };
-  put_state();
+
+  // Record fragments are double-buffered in registers by chunk parity: chunk
+  // nc + 2 is fetched into the buffer chunk nc has just finished with, so each
+  // fetch has a whole chunk of work to land.
+  using P0 = std::integral_constant<int, 0>;
+  using P1 = std::integral_constant<int, 1>;
+  ScanFrags<DK> fr[2];
+  // Every step issues the same loads (the chunk index is clamped at the end)
+  // so the compiler's wait counts are identical on every path through the loop.
+  const int last = NC - 1;
+  fetch_z(P0{}, 0);
+  load_frags<DK>(rec0, wave, lane, lq, fr[0]);
+  put_state(0);
+  put_z(P0{});
+  fetch_z(P1{}, min(1, last));
+  load_frags<DK>(rec0 + static_cast<size_t>(min(1, last)) * L::STRIDE, wave, lane, lq, fr[1]);
   __syncthreads();
 
-  for (int nc = 0; nc < NC; ++nc) {
-    const unsigned short* rec = ws + (static_cast<size_t>(bh) * NC + nc) * L::STRIDE;
+  auto step = [&](auto parity, ScanFrags<DK>& cur, int nc) {
+    constexpr int buf = decltype(parity)::value;   // == nc & 1
+    using Other = std::integral_constant<int, buf ^ 1>;
     const long tok0 = t0 + static_cast<long>(nc) * kBS;
 
-    // ---- Z = w * v (tile columns), split into LDS as [col][t] ---------------
-    for (int e = tid; e < kBS * (DVT / 4); e += 256) {
-      const int t = e / (DVT / 4), cg = e % (DVT / 4);
-      const size_t idx = ((static_cast<size_t>(bi) * s_alloc + tok0 + t) * H + h) * DV + d0 + 4 * cg;
-#pragma unroll
-      for (int u = 0; u < 4; ++u) {
-        const float z = load_elem(w, idx + u, in_dt) * load_elem(v, idx + u, in_dt);
-        const unsigned short zh = f32_to_bf16_bits(z);
-        sZh[(4 * cg + u) * TP + t] = zh;
-        sZl[(4 * cg + u) * TP + t] = f32_to_bf16_bits(z - bf16_bits_to_f32(zh));
-      }
-    }
-    // this chunk's A-operand fragments for the wave's rows
-    const int lo8 = lane * 8;
-    bf16x8 fai[2], faqh[2], faql[2];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      fai[kk] = *reinterpret_cast<const bf16x8*>(rec + L::ai_frag(wave, kk) + lo8);
-      faqh[kk] = *reinterpret_cast<const bf16x8*>(rec + L::aqk_frag(wave, kk, 0) + lo8);
-      faql[kk] = *reinterpret_cast<const bf16x8*>(rec + L::aqk_frag(wave, kk, 1) + lo8);
-    }
-    __syncthreads();
-
-    // ---- U = Ai Z (Z split) ---------------------------------------------------
-    f32x4 U[NT];
-#pragma unroll
-    for (int nn = 0; nn < NT; ++nn) {
-      U[nn] = zero4();
-      const int col = 16 * nn + lr;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const bf16x8 zh = *reinterpret_cast<const bf16x8*>(&sZh[col * TP + 32 * kk + 8 * lq]);
-        const bf16x8 zl = *reinterpret_cast<const bf16x8*>(&sZl[col * TP + 32 * kk + 8 * lq]);
-        U[nn] = mfma(fai[kk], zh, U[nn]);
-        U[nn] = mfma(fai[kk], zl, U[nn]);
-      }
-      unsigned short hb[4], lb[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        hb[e] = f32_to_bf16_bits(U[nn][e]);
-        lb[e] = f32_to_bf16_bits(U[nn][e] - bf16_bits_to_f32(hb[e]));
-      }
-      const int t = 16 * wave + 4 * lq;
-      *reinterpret_cast<uint2*>(&sUh[col * TP + t]) =
-          make_uint2(hb[0] | (uint32_t(hb[1]) << 16), hb[2] | (uint32_t(hb[3]) << 16));
-      *reinterpret_cast<uint2*>(&sUl[col * TP + t]) =
-          make_uint2(lb[0] | (uint32_t(lb[1]) << 16), lb[2] | (uint32_t(lb[3]) << 16));
-    }
-    bf16x8 fw[KT], fqh[KT], fql[KT];
-#pragma unroll
-    for (int kk = 0; kk < KT; ++kk) {
-      fw[kk] = *reinterpret_cast<const bf16x8*>(rec + L::w_frag(wave, kk) + lo8);
-      fqh[kk] = *reinterpret_cast<const bf16x8*>(rec + L::qp_frag(wave, kk, 0) + lo8);
-      fql[kk] = *reinterpret_cast<const bf16x8*>(rec + L::qp_frag(wave, kk, 1) + lo8);
-    }
-    __syncthreads();
-
-    // ---- O = Aqk U + Q' S ; Un = U - W S ---------------------------------------
+    // ---- U = Ai Z, O = MOZ Z + Q' S, P = W S ; Un = U - P ---------------------
 #pragma unroll
     for (int nn = 0; nn < NT; ++nn) {
       const int col = 16 * nn + lr;
-      f32x4 O = zero4(), P = zero4();
+      f32x4 U = zero4(), O = zero4(), P = zero4();
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
-        const bf16x8 uh = *reinterpret_cast<const bf16x8*>(&sUh[col * TP + 32 * kk + 8 * lq]);
-        const bf16x8 ul = *reinterpret_cast<const bf16x8*>(&sUl[col * TP + 32 * kk + 8 * lq]);
-        O = mfma3(faqh[kk], faql[kk], uh, ul, O);
+        const bf16x8 zh = *reinterpret_cast<const bf16x8*>(&sZh[buf][col * TP + 32 * kk + 8 * lq]);
+        const bf16x8 zl = *reinterpret_cast<const bf16x8*>(&sZl[buf][col * TP + 32 * kk + 8 * lq]);
+        U = mfma(cur.ai[kk], zh, U);
+        U = mfma(cur.ai[kk], zl, U);
+        O = mfma3(cur.mzh[kk], cur.mzl[kk], zh, zl, O);
       }
 #pragma unroll
       for (int kk = 0; kk < KT; ++kk) {
-        const bf16x8 sh = *reinterpret_cast<const bf16x8*>(&sSh[col * SP + 32 * kk + 8 * lq]);
-        const bf16x8 sl = *reinterpret_cast<const bf16x8*>(&sSl[col * SP + 32 * kk + 8 * lq]);
-        P = mfma(fw[kk], sh, P);
-        O = mfma3(fqh[kk], fql[kk], sh, sl, O);
+        const bf16x8 sh = *reinterpret_cast<const bf16x8*>(&sSh[buf][col * SP + 32 * kk + 8 * lq]);
+        const bf16x8 sl = *reinterpret_cast<const bf16x8*>(&sSl[buf][col * SP + 32 * kk + 8 * lq]);
+        P = mfma(cur.w[kk], sh, P);
+        O = mfma3(cur.qh[kk], cur.ql[kk], sh, sl, O);
       }
-      // output rows t = 16*wave + 4*lq + e
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int t = 16 * wave + 4 * lq + e;
         const size_t oi = ((static_cast<size_t>(bi) * s_alloc + tok0 + t) * H + h) * DV + d0 + col;
-        store_elem(o, oi, out_dt, O[e]);
+        store_elem(o, oi, OUT_DT, O[e]);
       }
-      unsigned short hb[4], lb[4];
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const float un = U[nn][e] - P[e];
-        hb[e] = f32_to_bf16_bits(un);
-        lb[e] = f32_to_bf16_bits(un - bf16_bits_to_f32(hb[e]));
-      }
+      const f32x4 un = U - P;
       const int t = 16 * wave + 4 * lq;
-      *reinterpret_cast<uint2*>(&sNh[col * TP + t]) =
-          make_uint2(hb[0] | (uint32_t(hb[1]) << 16), hb[2] | (uint32_t(hb[3]) << 16));
-      *reinterpret_cast<uint2*>(&sNl[col * TP + t]) =
-          make_uint2(lb[0] | (uint32_t(lb[1]) << 16), lb[2] | (uint32_t(lb[3]) << 16));
+      put_quad(&sNh[col * TP + t], &sNl[col * TP + t], un);
     }
-    bf16x8 fkh[MPW][2], fkl[MPW][2];
-    float4 gam[MPW];
-    const float* gl = reinterpret_cast<const float*>(rec + L::GL_OFF);
-#pragma unroll
-    for (int mi = 0; mi < MPW; ++mi) {
-      const int m = wave * MPW + mi;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        fkh[mi][kk] = *reinterpret_cast<const bf16x8*>(rec + L::kt_frag(m, kk, 0) + lo8);
-        fkl[mi][kk] = *reinterpret_cast<const bf16x8*>(rec + L::kt_frag(m, kk, 1) + lo8);
-      }
-      gam[mi] = *reinterpret_cast<const float4*>(gl + 16 * m + 4 * lq);
-    }
+    put_z(Other{});     // that LDS buffer was last read in chunk nc-1 (a clamped copy at the end)
     __syncthreads();
 
-    // ---- S = diag(gamma_last) S + KG^T Un ---------------------------------------
+    // ---- S = diag(gamma_last) S + KG^T Un --------------------------------------
 #pragma unroll
     for (int mi = 0; mi < MPW; ++mi)
 #pragma unroll
       for (int nn = 0; nn < NT; ++nn) {
         const int col = 16 * nn + lr;
         f32x4 acc = S[mi][nn];
-        acc[0] *= gam[mi].x; acc[1] *= gam[mi].y; acc[2] *= gam[mi].z; acc[3] *= gam[mi].w;
+        acc[0] *= cur.gam[mi].x; acc[1] *= cur.gam[mi].y;
+        acc[2] *= cur.gam[mi].z; acc[3] *= cur.gam[mi].w;
 #pragma unroll
         for (int kk = 0; kk < 2; ++kk) {
           const bf16x8 nh = *reinterpret_cast<const bf16x8*>(&sNh[col * TP + 32 * kk + 8 * lq]);
           const bf16x8 nl = *reinterpret_cast<const bf16x8*>(&sNl[col * TP + 32 * kk + 8 * lq]);
-          acc = mfma3(fkh[mi][kk], fkl[mi][kk], nh, nl, acc);
+          acc = mfma3(cur.kh[mi][kk], cur.kl[mi][kk], nh, nl, acc);
         }
         S[mi][nn] = acc;
       }
-    put_state();
+    put_state(buf ^ 1);
+    const int pre = min(nc + 2, last);
+    fetch_z(parity, pre);
+    load_frags<DK>(rec0 + static_cast<size_t>(pre) * L::STRIDE, wave, lane, lq, cur);
     __syncthreads();
+  };
+
+  int nc = 0;
+  for (; nc + 1 < NC; nc += 2) {
+    step(P0{}, fr[0], nc);
+    step(P1{}, fr[1], nc + 1);
   }
+  if (nc < NC) step(P0{}, fr[0], nc);
 
 #pragma unroll
   for (int mi = 0; mi < MPW; ++mi)
@@ -247,14 +299,14 @@ __global__ __launch_bounds__(256) void scan_kernel(
       }
 }
 
-template <int DK, int NT>
-static hipError_t launch_scan_t(const void* v, const void* w, int in_dt, const unsigned short* ws,
-                                const float* s_in, float* s_out, void* o, int out_dt, int B, int H,
+template <int DK, int NT, int IN_DT, int OUT_DT>
+static hipError_t launch_scan_t(const void* v, const void* w, const unsigned short* ws,
+                                const float* s_in, float* s_out, void* o, int B, int H,
                                 int DV, long s_alloc, long t0, int NC, hipStream_t stream) {
   const int BH = B * H;
   const unsigned grid = static_cast<unsigned>(BH) * (DV / (16 * NT));
-  hipLaunchKernelGGL((scan_kernel<DK, NT>), dim3(grid), dim3(256), 0, stream, v, w, in_dt, ws,
-                     s_in, s_out, o, out_dt, BH, H, DV, s_alloc, t0, NC);
+  hipLaunchKernelGGL((scan_kernel<DK, NT, IN_DT, OUT_DT>), dim3(grid), dim3(256), 0, stream, v, w,
+                     ws, s_in, s_out, o, BH, H, DV, s_alloc, t0, NC);
   return hipGetLastError();
 }
 
@@ -269,11 +321,17 @@ hipError_t launch_scan(const void* v, const void* w, int in_dt, const unsigned s
                        const float* s_in, float* s_out, void* o, int out_dt, int B, int H, int DK,
                        int DV, long s_alloc, long t0, int NC, hipStream_t stream) {
   const int nt = scan_nt_for(B, H, DV);
-#define GDN2_SCAN_CASE(DKV, NTV)                                                            \
-  if (DK == DKV && nt == NTV)                                                               \
-    return launch_scan_t<DKV, NTV>(v, w, in_dt, ws, s_in, s_out, o, out_dt, B, H, DV, s_alloc, \
-                                   t0, NC, stream);
-  GDN2_SCAN_CASE(64, 1) GDN2_SCAN_CASE(64, 2) GDN2_SCAN_CASE(128, 1) GDN2_SCAN_CASE(128, 2)
+#define GDN2_SCAN_CASE(DKV, NTV, DTV, ODV)                                                     \
+  if (DK == DKV && nt == NTV && in_dt == DTV && out_dt == ODV)                                 \
+    return launch_scan_t<DKV, NTV, DTV, ODV>(v, w, ws, s_in, s_out, o, B, H, DV, s_alloc, t0,  \
+                                             NC, stream);
+#define GDN2_SCAN_OUT(DKV, NTV, DTV) \
+  GDN2_SCAN_CASE(DKV, NTV, DTV, DT_BF16) GDN2_SCAN_CASE(DKV, NTV, DTV, DT_F16) GDN2_SCAN_CASE(DKV, NTV, DTV, DT_F32)
+#define GDN2_SCAN_DT(DKV, NTV) \
+  GDN2_SCAN_OUT(DKV, NTV, DT_BF16) GDN2_SCAN_OUT(DKV, NTV, DT_F16) GDN2_SCAN_OUT(DKV, NTV, DT_F32)
+  GDN2_SCAN_DT(64, 1) GDN2_SCAN_DT(64, 2) GDN2_SCAN_DT(128, 1) GDN2_SCAN_DT(128, 2)
+#undef GDN2_SCAN_DT
+#undef GDN2_SCAN_OUT
 #undef GDN2_SCAN_CASE
   return hipErrorInvalidValue;
 }
