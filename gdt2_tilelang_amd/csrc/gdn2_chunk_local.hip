@@ -24,9 +24,11 @@
 //    the reference, all factors <= 1, and the diagonal blocks are summed
 //    exactly with 2^(G_r - G_s) on the VALU.
 //
-// Precision (bf16 MFMA, fp32 accumulate): the Aqk product uses hi+lo split
-// operands (three MFMAs); Akk, W and Aqk*W use single bf16 operands; the solve
-// is fp32. Q', KG and MOZ are exported as hi/lo pairs, W and Ai as bf16.
+// Precision (bf16 MFMA, fp32 accumulate): Aqk, Akk, W and Aqk*W use hi+lo split
+// operands (three MFMAs each); the solve is fp32. W, Q', KG and MOZ are
+// exported as hi/lo pairs, Ai as bf16.
+//
+// This kernel serves DK = 64; DK = 128 runs gdn2_chunk_local2.hip.
 #include "gdn2_common.h"
 #include "gdn2_prefill_layout.h"
 
@@ -58,16 +60,17 @@ struct ChunkSmem {
   static constexpr int WP = DK + 8;    // bf16 pitch of [64][DK] arrays
   static constexpr size_t G_OFF = 0;                                 // G, later Aqk*W staging
   static constexpr size_t K_OFF = G_OFF + 64 * GP * 4;               // k, later W [64][WP]
-  static constexpr size_t ET_OFF = K_OFF + 64 * GP * 4;              // E^T bf16 [DK][TP]
-  static constexpr size_t A1_OFF = ET_OFF + DK * TP * 2;             // Aqk
+  static constexpr size_t ET_OFF = K_OFF + 64 * GP * 4;              // E^T hi bf16 [DK][TP]
+  static constexpr size_t ETL_OFF = ET_OFF + DK * TP * 2;            // E^T lo bf16 [DK][TP]
+  static constexpr size_t A1_OFF = ETL_OFF + DK * TP * 2;            // Aqk
   static constexpr size_t A2_OFF = A1_OFF + 64 * AP * 4;             // Akk, later W^T [DK][TP]
   static constexpr size_t AI_OFF = A2_OFF + 64 * AP2 * 4;            // Ai
   static constexpr size_t T_OFF = AI_OFF + 64 * AP * 4;              // solve scratch [3][16][17]
   static constexpr size_t REF_OFF = T_OFF + 3 * 16 * 17 * 4;         // [4][DK] per-block reference
   static constexpr size_t TOT_OFF = REF_OFF + 4 * DK * 4;            // cumsum partials [4][DK]
   static constexpr size_t BYTES = TOT_OFF + 4 * DK * 4;
-  static_assert(DK * TP * 2 <= 64 * AP2 * 4, "W^T must fit in the Akk region");
-  static_assert(64 * WP * 2 <= 64 * GP * 4, "W must fit in the k region");
+  static_assert(2 * DK * TP * 2 <= 64 * AP2 * 4, "W^T hi/lo must fit in the Akk region");
+  static_assert(64 * AP * 4 <= 2 * DK * TP * 2, "MOZ staging must fit in the E^T region");
 };
 
 template <int DK, int IN_DT>
@@ -85,6 +88,7 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
   float* sG = reinterpret_cast<float*>(smem + M::G_OFF);
   float* sK = reinterpret_cast<float*>(smem + M::K_OFF);
   unsigned short* sET = reinterpret_cast<unsigned short*>(smem + M::ET_OFF);
+  unsigned short* sETl = reinterpret_cast<unsigned short*>(smem + M::ETL_OFF);
   float* sA1 = reinterpret_cast<float*>(smem + M::A1_OFF);
   float* sA2 = reinterpret_cast<float*>(smem + M::A2_OFF);
   float* sAI = reinterpret_cast<float*>(smem + M::AI_OFF);
@@ -92,8 +96,9 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
   float* sRef = reinterpret_cast<float*>(smem + M::REF_OFF);
   float* sTot = reinterpret_cast<float*>(smem + M::TOT_OFF);
   float* sQS = sG;                                                   // phase E staging
-  unsigned short* sW = reinterpret_cast<unsigned short*>(sK);        // phase D
-  unsigned short* sWT = reinterpret_cast<unsigned short*>(sA2);      // phase D/E
+  float* sWf = sK;                                                   // phase D, [64][GP] fp32
+  unsigned short* sWT = reinterpret_cast<unsigned short*>(sA2);      // phase D/E, hi
+  unsigned short* sWTl = sWT + DK * TP;                              // phase D/E, lo
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -166,7 +171,7 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
 
   // ---- phase A.4: own-row products (registers), E^T, KG^T, gamma_last -----
   float qg[KT][8];          // scale * q * gamma, kept for phase E
-  bf16x8 aqh[KT], aql[KT], ae[KT];   // Aqk / Akk row operands
+  bf16x8 aqh[KT], aql[KT], aeh[KT], ael[KT];   // Aqk / Akk row operands
 #pragma unroll
   for (int kk = 0; kk < KT; ++kk) {
     const int c0 = 32 * kk + 8 * lq;
@@ -177,13 +182,16 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
       const float gam = fast_exp2(Gr);
       const float bk = bv[kk][j] * kv[kk][j];
       qg[kk][j] = scale * qv[kk][j] * gam;
-      sET[(c0 + j) * TP + my_r] = f32_to_bf16_bits(bk * gam);
+      uint32_t eh, el;
+      split_pk(bk * gam, 0.f, eh, el);
+      sET[(c0 + j) * TP + my_r] = static_cast<unsigned short>(eh);
+      sETl[(c0 + j) * TP + my_r] = static_cast<unsigned short>(el);
       const float fr = fast_exp2(Gr - sRef[wave * DK + c0 + j]);
       xq[j] = qv[kk][j] * fr;
       xe[j] = bk * fr;
     }
     split_bf16x8(xq, aqh[kk], aql[kk]);
-    ae[kk] = pack_bf16x8(xe);
+    split_bf16x8(xe, aeh[kk], ael[kk]);
   }
   if (tid < DK) {
     reinterpret_cast<float*>(rec + L::GL_OFF)[tid] = fast_exp2(sG[63 * GP + tid]);
@@ -222,7 +230,7 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
         bf16x8 bh, bl;
         split_bf16x8(y, bh, bl);
         accq = mfma3(aqh[kk], aql[kk], bh, bl, accq);
-        acck = mfma(ae[kk], bh, acck);
+        acck = mfma3(aeh[kk], ael[kk], bh, bl, acck);
       }
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
@@ -321,16 +329,16 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
     __syncthreads();
   }
 
-  // ---- phase D: W = Ai E (bf16 MFMA); Ai fragments out -------------------
-  bf16x8 ai[2], aqk_hi[2], aqk_lo[2];
+  // ---- phase D: W = Ai E (split operands); Ai fragments out --------------
+  bf16x8 aih[2], ail[2], aqk_hi[2], aqk_lo[2];
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk) {
     const int s0 = 32 * kk + 8 * lq;
     float x[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] = sAI[my_r * AP + s0 + j];
-    ai[kk] = pack_bf16x8(x);
-    *reinterpret_cast<bf16x8*>(rec + L::ai_frag(wave, kk) + lane * 8) = ai[kk];
+    split_bf16x8(x, aih[kk], ail[kk]);
+    *reinterpret_cast<bf16x8*>(rec + L::ai_frag(wave, kk) + lane * 8) = aih[kk];
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] = sA1[my_r * AP + s0 + j];
     split_bf16x8(x, aqk_hi[kk], aqk_lo[kk]);
@@ -341,22 +349,29 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
     const int c = 16 * nn + lr;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      const bf16x8 bfr = *reinterpret_cast<const bf16x8*>(&sET[c * TP + 32 * kk + 8 * lq]);
-      acc = mfma(ai[kk], bfr, acc);
+      const bf16x8 bh = *reinterpret_cast<const bf16x8*>(&sET[c * TP + 32 * kk + 8 * lq]);
+      const bf16x8 bl = *reinterpret_cast<const bf16x8*>(&sETl[c * TP + 32 * kk + 8 * lq]);
+      acc = mfma3(aih[kk], ail[kk], bh, bl, acc);
     }
 #pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int t = 16 * wave + 4 * lq + e;
-      const unsigned short wb = f32_to_bf16_bits(acc[e]);
-      sW[t * WP + c] = wb;
-      sWT[c * TP + t] = wb;
-    }
+    for (int e = 0; e < 4; ++e) sWf[(16 * wave + 4 * lq + e) * GP + c] = acc[e];
+    const int t = 16 * wave + 4 * lq;
+    uint32_t h01, l01, h23, l23;
+    split_pk(acc[0], acc[1], h01, l01);
+    split_pk(acc[2], acc[3], h23, l23);
+    *reinterpret_cast<uint2*>(&sWT[c * TP + t]) = make_uint2(h01, h23);
+    *reinterpret_cast<uint2*>(&sWTl[c * TP + t]) = make_uint2(l01, l23);
   }
   __syncthreads();
 #pragma unroll
   for (int kk = 0; kk < KT; ++kk) {
-    const bf16x8 x = *reinterpret_cast<const bf16x8*>(&sW[my_r * WP + 32 * kk + 8 * lq]);
-    *reinterpret_cast<bf16x8*>(rec + L::w_frag(wave, kk) + lane * 8) = x;
+    float x[8];
+#pragma unroll
+    for (int j = 0; j < 8; ++j) x[j] = sWf[my_r * GP + 32 * kk + 8 * lq + j];
+    bf16x8 hi, lo;
+    split_bf16x8(x, hi, lo);
+    *reinterpret_cast<bf16x8*>(rec + L::w_frag(wave, kk, 0) + lane * 8) = hi;
+    *reinterpret_cast<bf16x8*>(rec + L::w_frag(wave, kk, 1) + lane * 8) = lo;
   }
   // MOZ = Aqk (hi/lo) x bf16(Ai), staged in the (now dead) E^T region
   {
@@ -379,15 +394,16 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
     }
   }
 
-  // ---- phase E: Q' = scale*q*gamma - Aqk W ---------------------------------
+  // ---- phase E: Q' = scale*q*gamma - Aqk W (split operands) -----------------
 #pragma unroll
   for (int nn = 0; nn < MT; ++nn) {
     f32x4 acc = zero4();
     const int c = 16 * nn + lr;
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      const bf16x8 bfr = *reinterpret_cast<const bf16x8*>(&sWT[c * TP + 32 * kk + 8 * lq]);
-      acc = mfma(aqk_hi[kk], bfr, acc);
+      const bf16x8 bh = *reinterpret_cast<const bf16x8*>(&sWT[c * TP + 32 * kk + 8 * lq]);
+      const bf16x8 bl = *reinterpret_cast<const bf16x8*>(&sWTl[c * TP + 32 * kk + 8 * lq]);
+      acc = mfma3(aqk_hi[kk], aqk_lo[kk], bh, bl, acc);
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) sQS[(16 * wave + 4 * lq + e) * GP + c] = acc[e];
@@ -438,14 +454,19 @@ static hipError_t launch_chunk_local_t(const void* q, const void* k, const void*
   return hipGetLastError();
 }
 
+hipError_t launch_chunk_local2(const void* q, const void* k, const void* b, const float* g,
+                               int in_dt, int B, int H, long s_alloc, long t0, int NC,
+                               float scale, unsigned short* ws, hipStream_t stream);
+
 hipError_t launch_chunk_local(const void* q, const void* k, const void* b, const float* g,
                               int in_dt, int B, int H, int DK, long s_alloc, long t0, int NC,
                               float scale, unsigned short* ws, hipStream_t stream) {
+  // DK = 128 runs the channel-sliced kernel (gdn2_chunk_local2.hip); DK = 64 this one.
+  if (DK == 128) return launch_chunk_local2(q, k, b, g, in_dt, B, H, s_alloc, t0, NC, scale, ws, stream);
 #define GDN2_CL_CASE(DKV, DTV)                                                             \
   if (DK == DKV && in_dt == DTV)                                                           \
     return launch_chunk_local_t<DKV, DTV>(q, k, b, g, B, H, s_alloc, t0, NC, scale, ws, stream);
   GDN2_CL_CASE(64, DT_BF16) GDN2_CL_CASE(64, DT_F16) GDN2_CL_CASE(64, DT_F32)
-  GDN2_CL_CASE(128, DT_BF16) GDN2_CL_CASE(128, DT_F16) GDN2_CL_CASE(128, DT_F32)
 #undef GDN2_CL_CASE
   return hipErrorInvalidValue;
 }

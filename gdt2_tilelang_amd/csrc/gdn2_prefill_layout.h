@@ -5,7 +5,7 @@
 // Every matrix is stored as MFMA A-operand fragments (see gdn2_common.h) so the
 // scan loads each one with a single coalesced 16-byte access per lane:
 //
-//   W   [4 m][DK/32 kk]          bf16      W   = Ai (b*k*gamma)            64 x DK
+//   W   [4 m][DK/32 kk][hi,lo]   bf16 x2   W   = Ai (b*k*gamma)            64 x DK
 //   QP  [4 m][DK/32 kk][hi,lo]   bf16 x2   Q'  = scale*q*gamma - Aqk W     64 x DK
 //   KT  [DK/16 m][2 kk][hi,lo]   bf16 x2   KG^T, KG = k*gamma_last/gamma   DK x 64
 //   MOZ [4 m][2 kk][hi,lo]       bf16 x2   Aqk Ai (Aqk: scale, diagonal in) 64 x 64
@@ -31,14 +31,14 @@ struct ChunkLayout {
   static constexpr int KT = DK / 32;   // 32-wide k steps over the key dim
   static constexpr int MT = DK / 16;   // 16-row tiles over the key dim
   static constexpr long W_OFF = 0;
-  static constexpr long QP_OFF = W_OFF + 4L * KT * kFrag;
+  static constexpr long QP_OFF = W_OFF + 4L * KT * 2 * kFrag;
   static constexpr long KT_OFF = QP_OFF + 4L * KT * 2 * kFrag;
   static constexpr long MOZ_OFF = KT_OFF + static_cast<long>(MT) * 2 * 2 * kFrag;
   static constexpr long AI_OFF = MOZ_OFF + 4L * 2 * 2 * kFrag;
   static constexpr long GL_OFF = AI_OFF + 4L * 2 * kFrag;   // in bf16 slots
   static constexpr long STRIDE = GL_OFF + 2L * DK;          // bf16 elements per record
 
-  __device__ static long w_frag(int m, int kk) { return W_OFF + (m * KT + kk) * kFrag; }
+  __device__ static long w_frag(int m, int kk, int hl) { return W_OFF + ((m * KT + kk) * 2 + hl) * kFrag; }
   __device__ static long qp_frag(int m, int kk, int hl) { return QP_OFF + ((m * KT + kk) * 2 + hl) * kFrag; }
   __device__ static long kt_frag(int m, int kk, int hl) { return KT_OFF + ((m * 2 + kk) * 2 + hl) * kFrag; }
   __device__ static long moz_frag(int m, int kk, int hl) { return MOZ_OFF + ((m * 2 + kk) * 2 + hl) * kFrag; }

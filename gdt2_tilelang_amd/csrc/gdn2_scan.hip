@@ -12,9 +12,10 @@
 //   S  = diag(gamma_last) S + KG^T Un
 //
 // Operands that carry the result's precision are split into bf16 hi + lo
-// (Z, S, Un and the Q', MOZ, KG records) so those products keep ~16 mantissa
-// bits; Ai Z uses bf16 Ai (the same rounding MOZ was built with) and W S the
-// bf16 state only (its error is damped by the erase term).
+// (Z, S, Un and the W, Q', MOZ, KG records) so those products keep ~16
+// mantissa bits; Ai Z uses bf16 Ai (the same rounding MOZ was built with).
+// W S needs the split on both sides: with little decay the state is large and
+// Un = U - W S is a small difference of large terms.
 //
 // Wave w owns output rows 16w..16w+15 of the chunk and state rows
 // 16*(w*MPW) .. 16*(w*MPW+MPW)-1. Per chunk two barriers hand Un and then the
@@ -37,7 +38,7 @@ struct ScanFrags {
   static constexpr int KT = DK / 32;
   static constexpr int MPW = DK / 64;
   bf16x8 ai[2], mzh[2], mzl[2];
-  bf16x8 w[KT], qh[KT], ql[KT];
+  bf16x8 wh[KT], wl[KT], qh[KT], ql[KT];
   bf16x8 kh[MPW][2], kl[MPW][2];
   float4 gam[MPW];
 };
@@ -56,7 +57,8 @@ __device__ __forceinline__ void load_frags(const unsigned short* __restrict__ re
   }
 #pragma unroll
   for (int kk = 0; kk < KT; ++kk) {
-    f.w[kk] = *reinterpret_cast<const bf16x8*>(rec + L::w_frag(wave, kk) + o8);
+    f.wh[kk] = *reinterpret_cast<const bf16x8*>(rec + L::w_frag(wave, kk, 0) + o8);
+    f.wl[kk] = *reinterpret_cast<const bf16x8*>(rec + L::w_frag(wave, kk, 1) + o8);
     f.qh[kk] = *reinterpret_cast<const bf16x8*>(rec + L::qp_frag(wave, kk, 0) + o8);
     f.ql[kk] = *reinterpret_cast<const bf16x8*>(rec + L::qp_frag(wave, kk, 1) + o8);
   }
@@ -241,7 +243,7 @@ __global__ __launch_bounds__(256) void scan_kernel(
       for (int kk = 0; kk < KT; ++kk) {
         const bf16x8 sh = *reinterpret_cast<const bf16x8*>(&sSh[buf][col * SP + 32 * kk + 8 * lq]);
         const bf16x8 sl = *reinterpret_cast<const bf16x8*>(&sSl[buf][col * SP + 32 * kk + 8 * lq]);
-        P = mfma(cur.w[kk], sh, P);
+        P = mfma3(cur.wh[kk], cur.wl[kk], sh, sl, P);
         O = mfma3(cur.qh[kk], cur.ql[kk], sh, sl, O);
       }
 #pragma unroll
