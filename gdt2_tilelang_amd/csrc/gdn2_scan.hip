@@ -21,8 +21,9 @@
 // 16*(w*MPW) .. 16*(w*MPW+MPW)-1. Per chunk two barriers hand Un and then the
 // new state between waves through LDS in B-operand order ([column][k], k
 // contiguous); S and Z are double-buffered so the next chunk's Z is staged
-// while the current one is in use, and the next chunk's record fragments are
-// fetched into registers one chunk ahead.
+// while the current one is in use. Record fragments are double-buffered in
+// registers: each half of chunk n+2's fragments is fetched as soon as chunk
+// n's copy of that half has been consumed, spreading the loads over the step.
 //
 // Workgroup -> (head, tile) is XCD-aware: the tiles of one head land on the
 // same XCD so its chunk records come from HBM once into that XCD's L2.
@@ -43,11 +44,12 @@ struct ScanFrags {
   float4 gam[MPW];
 };
 
+// Fragments used by the output / Un phase of a chunk.
 template <int DK>
-__device__ __forceinline__ void load_frags(const unsigned short* __restrict__ rec, int wave, int lane,
-                                           int lq, ScanFrags<DK>& f) {
+__device__ __forceinline__ void load_frags_p1(const unsigned short* __restrict__ rec, int wave,
+                                              int lane, ScanFrags<DK>& f) {
   using L = ChunkLayout<DK>;
-  constexpr int KT = DK / 32, MPW = DK / 64;
+  constexpr int KT = DK / 32;
   const int o8 = lane * 8;
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk) {
@@ -62,6 +64,15 @@ __device__ __forceinline__ void load_frags(const unsigned short* __restrict__ re
     f.qh[kk] = *reinterpret_cast<const bf16x8*>(rec + L::qp_frag(wave, kk, 0) + o8);
     f.ql[kk] = *reinterpret_cast<const bf16x8*>(rec + L::qp_frag(wave, kk, 1) + o8);
   }
+}
+
+// Fragments used by the state-update phase of a chunk.
+template <int DK>
+__device__ __forceinline__ void load_frags_p2(const unsigned short* __restrict__ rec, int wave,
+                                              int lane, int lq, ScanFrags<DK>& f) {
+  using L = ChunkLayout<DK>;
+  constexpr int MPW = DK / 64;
+  const int o8 = lane * 8;
   const float* gl = reinterpret_cast<const float*>(rec + L::GL_OFF);
 #pragma unroll
   for (int mi = 0; mi < MPW; ++mi) {
@@ -73,6 +84,13 @@ __device__ __forceinline__ void load_frags(const unsigned short* __restrict__ re
     }
     f.gam[mi] = *reinterpret_cast<const float4*>(gl + 16 * m + 4 * lq);
   }
+}
+
+template <int DK>
+__device__ __forceinline__ void load_frags(const unsigned short* __restrict__ rec, int wave, int lane,
+                                           int lq, ScanFrags<DK>& f) {
+  load_frags_p1<DK>(rec, wave, lane, f);
+  load_frags_p2<DK>(rec, wave, lane, lq, f);
 }
 
 // Four consecutive v (or w) elements as floats, raw register form per dtype.
@@ -257,6 +275,10 @@ __global__ __launch_bounds__(256) void scan_kernel(
       put_quad(&sNh[col * TP + t], &sNl[col * TP + t], un);
     }
     put_z(Other{});     // that LDS buffer was last read in chunk nc-1 (a clamped copy at the end)
+    // phase-1 fragments of this buffer are dead: fetch chunk nc + 2's now
+    const int pre = min(nc + 2, last);
+    const unsigned short* rec_pre = rec0 + static_cast<size_t>(pre) * L::STRIDE;
+    load_frags_p1<DK>(rec_pre, wave, lane, cur);
     __syncthreads();
 
     // ---- S = diag(gamma_last) S + KG^T Un --------------------------------------
@@ -277,9 +299,8 @@ __global__ __launch_bounds__(256) void scan_kernel(
         S[mi][nn] = acc;
       }
     put_state(buf ^ 1);
-    const int pre = min(nc + 2, last);
     fetch_z(parity, pre);
-    load_frags<DK>(rec0 + static_cast<size_t>(pre) * L::STRIDE, wave, lane, lq, cur);
+    load_frags_p2<DK>(rec_pre, wave, lane, lq, cur);
     __syncthreads();
   };
 
