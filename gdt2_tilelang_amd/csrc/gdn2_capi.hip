@@ -8,7 +8,6 @@ namespace gdn2 {
 hipError_t launch_decode(const void*, const void*, const void*, const float*, const void*,
                          const void*, float*, void*, int, int, int, int, long, long, int, float,
                          int, int, hipStream_t);
-int decode_dvt_for(int DV);
 hipError_t launch_chunk_local(const void*, const void*, const void*, const float*, int, int, int,
                               int, long, long, int, float, unsigned short*, hipStream_t);
 hipError_t launch_scan(const void*, const void*, int, const unsigned short*, const float*, float*,
@@ -60,8 +59,8 @@ int gdn2_hip_decode(const void* q, const void* k, const void* v, const float* g,
   if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return GDN2_ERR_ARG;
   if (B < 1 || H < 1 || n < 0 || t0 < 0 || s_alloc < t0 + n) return GDN2_ERR_ARG;
   if (DK != 32 && DK != 64 && DK != 128 && DK != 256) return GDN2_ERR_SHAPE;
-  if (gdn2::decode_dvt_for(DV) == 0 || DV > 4096) return GDN2_ERR_SHAPE;
-  if (static_cast<long>(B) * H > 65535L || n > 0x7fffffffL) return GDN2_ERR_SHAPE;
+  if (DV % 32 != 0 || DV > 4096) return GDN2_ERR_SHAPE;
+  if (static_cast<long>(B) * H * (DV / 32) > 0x7fffffffL || n > 0x7fffffffL) return GDN2_ERR_SHAPE;
   return status(gdn2::launch_decode(q, k, v, g, b, w, state, o, B, H, DK, DV, s_alloc, t0,
                                     static_cast<int>(n), scale, in_dtype, out_dtype,
                                     static_cast<hipStream_t>(stream)));

@@ -7,10 +7,15 @@
 //
 //   W   [4 m][DK/32 kk][hi,lo]   bf16 x2   W   = Ai (b*k*gamma)            64 x DK
 //   QP  [4 m][DK/32 kk][hi,lo]   bf16 x2   Q'  = scale*q*gamma - Aqk W     64 x DK
+//   AI  [4 m][2 kk]              bf16      Ai  = (I + Akk)^-1               64 x 64
 //   KT  [DK/16 m][2 kk][hi,lo]   bf16 x2   KG^T, KG = k*gamma_last/gamma   DK x 64
 //   MOZ [4 m][2 kk][hi,lo]       bf16 x2   Aqk Ai (Aqk: scale, diagonal in) 64 x 64
-//   AI  [4 m][2 kk]              bf16      Ai  = (I + Akk)^-1               64 x 64
 //   GL  [DK]                     fp32      gamma_last = exp(G_last)
+//
+// The first three are what the scan's output / Un phase reads, the last three
+// what its state-update phase reads; each set is one contiguous byte range
+// (SET_A_BYTES from the record start, then SET_B_BYTES), so the scan streams
+// one set into LDS while it computes with the other.
 //
 // Within a fragment the 64 lanes' 8-element groups are contiguous.
 //
@@ -32,17 +37,19 @@ struct ChunkLayout {
   static constexpr int MT = DK / 16;   // 16-row tiles over the key dim
   static constexpr long W_OFF = 0;
   static constexpr long QP_OFF = W_OFF + 4L * KT * 2 * kFrag;
-  static constexpr long KT_OFF = QP_OFF + 4L * KT * 2 * kFrag;
+  static constexpr long AI_OFF = QP_OFF + 4L * KT * 2 * kFrag;
+  static constexpr long KT_OFF = AI_OFF + 4L * 2 * kFrag;
   static constexpr long MOZ_OFF = KT_OFF + static_cast<long>(MT) * 2 * 2 * kFrag;
-  static constexpr long AI_OFF = MOZ_OFF + 4L * 2 * 2 * kFrag;
-  static constexpr long GL_OFF = AI_OFF + 4L * 2 * kFrag;   // in bf16 slots
-  static constexpr long STRIDE = GL_OFF + 2L * DK;          // bf16 elements per record
+  static constexpr long GL_OFF = MOZ_OFF + 4L * 2 * 2 * kFrag;  // in bf16 slots
+  static constexpr long STRIDE = GL_OFF + 2L * DK;               // bf16 elements per record
+  static constexpr int SET_A_BYTES = static_cast<int>(KT_OFF * 2);
+  static constexpr int SET_B_BYTES = static_cast<int>((STRIDE - KT_OFF) * 2);
 
-  __device__ static long w_frag(int m, int kk, int hl) { return W_OFF + ((m * KT + kk) * 2 + hl) * kFrag; }
-  __device__ static long qp_frag(int m, int kk, int hl) { return QP_OFF + ((m * KT + kk) * 2 + hl) * kFrag; }
-  __device__ static long kt_frag(int m, int kk, int hl) { return KT_OFF + ((m * 2 + kk) * 2 + hl) * kFrag; }
-  __device__ static long moz_frag(int m, int kk, int hl) { return MOZ_OFF + ((m * 2 + kk) * 2 + hl) * kFrag; }
-  __device__ static long ai_frag(int m, int kk) { return AI_OFF + (m * 2 + kk) * kFrag; }
+  __host__ __device__ static constexpr long w_frag(int m, int kk, int hl) { return W_OFF + ((m * KT + kk) * 2 + hl) * kFrag; }
+  __host__ __device__ static constexpr long qp_frag(int m, int kk, int hl) { return QP_OFF + ((m * KT + kk) * 2 + hl) * kFrag; }
+  __host__ __device__ static constexpr long kt_frag(int m, int kk, int hl) { return KT_OFF + ((m * 2 + kk) * 2 + hl) * kFrag; }
+  __host__ __device__ static constexpr long moz_frag(int m, int kk, int hl) { return MOZ_OFF + ((m * 2 + kk) * 2 + hl) * kFrag; }
+  __host__ __device__ static constexpr long ai_frag(int m, int kk) { return AI_OFF + (m * 2 + kk) * kFrag; }
 };
 
 static_assert((ChunkLayout<128>::STRIDE * 2) % 256 == 0, "record must keep 256-byte alignment");

@@ -20,7 +20,7 @@ rel_err = oracle.rel_err
 
 
 @pytest.mark.parametrize("n", [1, 3, 8, 16, 19])
-@pytest.mark.parametrize("DK,DV", [(64, 64), (128, 128), (32, 96), (256, 64), (128, 32)])
+@pytest.mark.parametrize("DK,DV", [(64, 64), (128, 128), (32, 96), (256, 64), (128, 32), (64, 160), (128, 256)])
 def test_decode_matches_oracle(n, DK, DV):
     print(f"decode n={n} DK={DK} DV={DV}", flush=True)
     B, H = 2, 3
