@@ -84,13 +84,14 @@ __device__ __forceinline__ float4 wave_sum_rowgroups(float4 x) {
   return x;
 }
 
-template <int DK>
+template <int DK, int TB>
 struct DecLds {
   // per staged token: exp(g), b*k, k, scale*q over the key channels
-  float ea[kDecTokBlock][DK], bk[kDecTokBlock][DK], kk[kDecTokBlock][DK], qs[kDecTokBlock][DK];
+  float ea[TB][DK], bk[TB][DK], kk[TB][DK], qs[TB][DK];
 };
 
-template <int DK, int IN_DT, int OUT_DT>
+// TB: tokens staged per block (1 for single-token calls, else kDecTokBlock)
+template <int DK, int IN_DT, int OUT_DT, int TB>
 __global__ __launch_bounds__(kDecMaxThreads) void decode_kernel(
     const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ v,
     const float* __restrict__ g, const void* __restrict__ b, const void* __restrict__ w,
@@ -98,7 +99,7 @@ __global__ __launch_bounds__(kDecMaxThreads) void decode_kernel(
     int n, float scale) {
   constexpr int RPT = DK / kDecRowGroups;
   constexpr int GPT = DK / 8;             // 8-channel groups per token
-  __shared__ __align__(16) DecLds<DK> sm;
+  __shared__ __align__(16) DecLds<DK, TB> sm;
 
   const int tid = threadIdx.x;
   const int nthr = blockDim.x;
@@ -126,13 +127,13 @@ __global__ __launch_bounds__(kDecMaxThreads) void decode_kernel(
     }
   }
 
-  for (int tb = 0; tb < n; tb += kDecTokBlock) {
-    const int nt = min(kDecTokBlock, n - tb);
+  for (int tb = 0; tb < n; tb += TB) {
+    const int nt = min(TB, n - tb);
     // this lane's v and w columns for the whole block (token index clamped)
-    Quad<IN_DT> vq[kDecTokBlock], wq[kDecTokBlock];
+    Quad<IN_DT> vq[TB], wq[TB];
     const int vcol = active ? col : 0;
 #pragma unroll
-    for (int tt = 0; tt < kDecTokBlock; ++tt) {
+    for (int tt = 0; tt < TB; ++tt) {
       const size_t vi = ((static_cast<size_t>(bi) * s_alloc + t0 + tb + min(tt, nt - 1)) * H + h) * DV + vcol;
       vq[tt].load(v, vi);
       wq[tt].load(w, vi);
@@ -166,7 +167,7 @@ __global__ __launch_bounds__(kDecMaxThreads) void decode_kernel(
     __syncthreads();
 
 #pragma unroll
-    for (int tt = 0; tt < kDecTokBlock; ++tt) {
+    for (int tt = 0; tt < TB; ++tt) {
       if (tt >= nt || !active) break;
       // decay, then the erase read  r = S^T (b*k)
       float4 r = make_float4(0.f, 0.f, 0.f, 0.f);
@@ -234,8 +235,13 @@ static hipError_t launch_decode_t(const void* q, const void* k, const void* v, c
   // one workgroup per (b, h, up to kDecMaxCols columns); one wave per 32 columns
   const int tiles = (DV + kDecMaxCols - 1) / kDecMaxCols;
   const int threads = 64 * (DV < kDecMaxCols ? DV : kDecMaxCols) / kDecCols;
-  hipLaunchKernelGGL((decode_kernel<DK, IN_DT, OUT_DT>), dim3(tiles, B * H), dim3(threads), 0, stream,
-                     q, k, v, g, b, w, state, o, H, DV, s_alloc, t0, n, scale);
+  if (n == 1)
+    hipLaunchKernelGGL((decode_kernel<DK, IN_DT, OUT_DT, 1>), dim3(tiles, B * H), dim3(threads), 0,
+                       stream, q, k, v, g, b, w, state, o, H, DV, s_alloc, t0, n, scale);
+  else
+    hipLaunchKernelGGL((decode_kernel<DK, IN_DT, OUT_DT, kDecTokBlock>), dim3(tiles, B * H),
+                       dim3(threads), 0, stream, q, k, v, g, b, w, state, o, H, DV, s_alloc, t0, n,
+                       scale);
   return hipGetLastError();
 }
 
