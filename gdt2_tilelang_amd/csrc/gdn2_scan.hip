@@ -34,56 +34,64 @@
 
 namespace gdn2 {
 
+constexpr int kScanWaves = 8;
+constexpr int kScanThreads = 64 * kScanWaves;
+
+// Record fragments one wave holds for a chunk. Waves 0-3 ("Un" role) use
+// a1 = Ai and x = W; waves 4-7 ("output" role) use a1/a2 = MOZ hi/lo and
+// x = Q'. Every wave holds the KG^T fragments and gamma_last of its state tile.
 template <int DK>
 struct ScanFrags {
   static constexpr int KT = DK / 32;
-  static constexpr int MPW = DK / 64;
-  bf16x8 ai[2], mzh[2], mzl[2];
-  bf16x8 wh[KT], wl[KT], qh[KT], ql[KT];
-  bf16x8 kh[MPW][2], kl[MPW][2];
-  float4 gam[MPW];
+  bf16x8 a1[2], a2[2];
+  bf16x8 xh[KT], xl[KT];
+  bf16x8 kh[2], kl[2];
+  float4 gam;
 };
 
-// Fragments used by the output / Un phase of a chunk.
+// Fragments of the output / Un phase of a chunk (output row block m = wave & 3).
 template <int DK>
 __device__ __forceinline__ void load_frags_p1(const unsigned short* __restrict__ rec, int wave,
                                               int lane, ScanFrags<DK>& f) {
   using L = ChunkLayout<DK>;
   constexpr int KT = DK / 32;
   const int o8 = lane * 8;
+  const int m = wave & 3;
+  if (wave < 4) {
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
-    f.ai[kk] = *reinterpret_cast<const bf16x8*>(rec + L::ai_frag(wave, kk) + o8);
-    f.mzh[kk] = *reinterpret_cast<const bf16x8*>(rec + L::moz_frag(wave, kk, 0) + o8);
-    f.mzl[kk] = *reinterpret_cast<const bf16x8*>(rec + L::moz_frag(wave, kk, 1) + o8);
-  }
+    for (int kk = 0; kk < 2; ++kk) f.a1[kk] = *reinterpret_cast<const bf16x8*>(rec + L::ai_frag(m, kk) + o8);
 #pragma unroll
-  for (int kk = 0; kk < KT; ++kk) {
-    f.wh[kk] = *reinterpret_cast<const bf16x8*>(rec + L::w_frag(wave, kk, 0) + o8);
-    f.wl[kk] = *reinterpret_cast<const bf16x8*>(rec + L::w_frag(wave, kk, 1) + o8);
-    f.qh[kk] = *reinterpret_cast<const bf16x8*>(rec + L::qp_frag(wave, kk, 0) + o8);
-    f.ql[kk] = *reinterpret_cast<const bf16x8*>(rec + L::qp_frag(wave, kk, 1) + o8);
+    for (int kk = 0; kk < KT; ++kk) {
+      f.xh[kk] = *reinterpret_cast<const bf16x8*>(rec + L::w_frag(m, kk, 0) + o8);
+      f.xl[kk] = *reinterpret_cast<const bf16x8*>(rec + L::w_frag(m, kk, 1) + o8);
+    }
+  } else {
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+      f.a1[kk] = *reinterpret_cast<const bf16x8*>(rec + L::moz_frag(m, kk, 0) + o8);
+      f.a2[kk] = *reinterpret_cast<const bf16x8*>(rec + L::moz_frag(m, kk, 1) + o8);
+    }
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk) {
+      f.xh[kk] = *reinterpret_cast<const bf16x8*>(rec + L::qp_frag(m, kk, 0) + o8);
+      f.xl[kk] = *reinterpret_cast<const bf16x8*>(rec + L::qp_frag(m, kk, 1) + o8);
+    }
   }
 }
 
-// Fragments used by the state-update phase of a chunk.
+// Fragments of the state-update phase (state tile wave, when DK/16 > wave).
 template <int DK>
 __device__ __forceinline__ void load_frags_p2(const unsigned short* __restrict__ rec, int wave,
                                               int lane, int lq, ScanFrags<DK>& f) {
   using L = ChunkLayout<DK>;
-  constexpr int MPW = DK / 64;
+  if (wave >= DK / 16) return;
   const int o8 = lane * 8;
-  const float* gl = reinterpret_cast<const float*>(rec + L::GL_OFF);
 #pragma unroll
-  for (int mi = 0; mi < MPW; ++mi) {
-    const int m = wave * MPW + mi;
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      f.kh[mi][kk] = *reinterpret_cast<const bf16x8*>(rec + L::kt_frag(m, kk, 0) + o8);
-      f.kl[mi][kk] = *reinterpret_cast<const bf16x8*>(rec + L::kt_frag(m, kk, 1) + o8);
-    }
-    f.gam[mi] = *reinterpret_cast<const float4*>(gl + 16 * m + 4 * lq);
+  for (int kk = 0; kk < 2; ++kk) {
+    f.kh[kk] = *reinterpret_cast<const bf16x8*>(rec + L::kt_frag(wave, kk, 0) + o8);
+    f.kl[kk] = *reinterpret_cast<const bf16x8*>(rec + L::kt_frag(wave, kk, 1) + o8);
   }
+  f.gam = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(rec + L::GL_OFF) + 16 * wave + 4 * lq);
 }
 
 template <int DK>
@@ -124,18 +132,18 @@ __device__ __forceinline__ void put_quad(unsigned short* hi, unsigned short* lo,
 }
 
 template <int DK, int NT, int IN_DT, int OUT_DT>
-__global__ __launch_bounds__(256) void scan_kernel(
+__global__ __launch_bounds__(kScanThreads) void scan_kernel(
     const void* __restrict__ v, const void* __restrict__ w, const unsigned short* __restrict__ ws,
     const float* __restrict__ s_in, float* __restrict__ s_out, void* __restrict__ o,
     int BH, int H, int DV, long s_alloc, long t0, int NC) {
   using L = ChunkLayout<DK>;
   constexpr int KT = DK / 32;
-  constexpr int MPW = DK / 64;         // 16-row state tiles per wave
+  constexpr int MT = DK / 16;          // 16-row state tiles; wave w < MT owns tile w
   constexpr int DVT = 16 * NT;
   constexpr int SP = DK + 8;           // bf16 pitch of S^T [DVT][DK]
   constexpr int TP = kBS + 8;          // bf16 pitch of [DVT][64] arrays
-  constexpr int ZIT = kBS * (DVT / 4) / 256;   // Z quads per thread
-  static_assert(ZIT >= 1, "tile too narrow");
+  constexpr int ZQ = kBS * DVT / 4;    // Z quads per chunk tile
+  constexpr int ZIT = (ZQ + kScanThreads - 1) / kScanThreads;
 
   __shared__ __align__(16) unsigned short sSh[2][DVT * SP], sSl[2][DVT * SP];
   __shared__ __align__(16) unsigned short sZh[2][DVT * TP], sZl[2][DVT * TP];
@@ -143,7 +151,10 @@ __global__ __launch_bounds__(256) void scan_kernel(
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = tid >> 6;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar branches
+  const bool un_role = wave < 4;
+  const bool owns = wave < MT;
+  const int m = wave & 3;              // output row block of the chunk
   const int lr = lane & 15;
   const int lq = lane >> 4;
 
@@ -164,7 +175,7 @@ __global__ __launch_bounds__(256) void scan_kernel(
   const int d0 = tile * DVT;
   const unsigned short* rec0 = ws + static_cast<size_t>(bh) * NC * L::STRIDE;
 
-  // Z staging: thread handles token t = e / (DVT/4), columns 4*cq .. 4*cq+3
+  // Z staging: quad e -> token t = e / (DVT/4), columns 4*cq .. 4*cq+3
   Raw4<IN_DT> zv[2][ZIT], zw[2][ZIT];    // [chunk parity]
   // parity P (= chunk index & 1) is a compile-time constant so the two register
   // copies stay in registers
@@ -172,7 +183,8 @@ __global__ __launch_bounds__(256) void scan_kernel(
     constexpr int p = decltype(parity)::value;
 #pragma unroll
     for (int it = 0; it < ZIT; ++it) {
-      const int e = tid + 256 * it;
+      const int e = tid + kScanThreads * it;
+      if (e >= ZQ) break;
       const int t = e / (DVT / 4), cq = e % (DVT / 4);
       const size_t idx = ((static_cast<size_t>(bi) * s_alloc + t0 + static_cast<long>(nc) * kBS + t) * H + h) * DV + d0 + 4 * cq;
       zv[p][it].load(v, idx);
@@ -183,7 +195,8 @@ __global__ __launch_bounds__(256) void scan_kernel(
     constexpr int buf = decltype(parity)::value;
 #pragma unroll
     for (int it = 0; it < ZIT; ++it) {
-      const int e = tid + 256 * it;
+      const int e = tid + kScanThreads * it;
+      if (e >= ZQ) break;
       const int t = e / (DVT / 4), cq = e % (DVT / 4);
       float a[4], b[4];
       zv[buf][it].get(a);
@@ -200,31 +213,29 @@ __global__ __launch_bounds__(256) void scan_kernel(
     }
   };
 
-  // ---- state in: rows c = 16*(wave*MPW+mi) + 4*lq + e, column d0 + 16*nn + lr
-  f32x4 S[MPW][NT];
+  // ---- state in: rows c = 16*wave + 4*lq + e, column d0 + 16*nn + lr
+  f32x4 S[NT];
 #pragma unroll
-  for (int mi = 0; mi < MPW; ++mi)
+  for (int nn = 0; nn < NT; ++nn)
 #pragma unroll
-    for (int nn = 0; nn < NT; ++nn)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int c = 16 * (wave * MPW + mi) + 4 * lq + e;
-        S[mi][nn][e] = s_in ? s_in[(static_cast<size_t>(bh) * DK + c) * DV + d0 + 16 * nn + lr] : 0.f;
-      }
+    for (int e = 0; e < 4; ++e) {
+      const int c = 16 * wave + 4 * lq + e;
+      S[nn][e] = (s_in && owns) ? s_in[(static_cast<size_t>(bh) * DK + c) * DV + d0 + 16 * nn + lr] : 0.f;
+    }
   auto put_state = [&](int buf) {
+    if (!owns) return;
 #pragma unroll
-    for (int mi = 0; mi < MPW; ++mi)
-#pragma unroll
-      for (int nn = 0; nn < NT; ++nn) {
-        const int col = 16 * nn + lr;
-        const int c = 16 * (wave * MPW + mi) + 4 * lq;
-        put_quad(&sSh[buf][col * SP + c], &sSl[buf][col * SP + c], S[mi][nn]);
-      }
+    for (int nn = 0; nn < NT; ++nn) {
+      const int col = 16 * nn + lr;
+      const int c = 16 * wave + 4 * lq;
+      put_quad(&sSh[buf][col * SP + c], &sSl[buf][col * SP + c], S[nn]);
+    }
   };
 
   // Record fragments are double-buffered in registers by chunk parity: chunk
-  // nc + 2 is fetched into the buffer chunk nc has just finished with, so each
-  // fetch has a whole chunk of work to land.
+  // n's buffer is refilled with chunk n+2's fragments one fragment at a time,
+  // right after that fragment's last MFMA, so the loads are spread over both
+  // phases and the memory pipe stays busy while the matrix cores run.
   using P0 = std::integral_constant<int, 0>;
   using P1 = std::integral_constant<int, 1>;
   ScanFrags<DK> fr[2];
@@ -239,68 +250,99 @@ __global__ __launch_bounds__(256) void scan_kernel(
   load_frags<DK>(rec0 + static_cast<size_t>(min(1, last)) * L::STRIDE, wave, lane, lq, fr[1]);
   __syncthreads();
 
+  const int o8 = lane * 8;
+  auto frag = [&](const unsigned short* rec, long off) {
+    return *reinterpret_cast<const bf16x8*>(rec + off + o8);
+  };
+
   auto step = [&](auto parity, ScanFrags<DK>& cur, int nc) {
     constexpr int buf = decltype(parity)::value;   // == nc & 1
     using Other = std::integral_constant<int, buf ^ 1>;
     const long tok0 = t0 + static_cast<long>(nc) * kBS;
-
-    // ---- U = Ai Z, O = MOZ Z + Q' S, P = W S ; Un = U - P ---------------------
-#pragma unroll
-    for (int nn = 0; nn < NT; ++nn) {
-      const int col = 16 * nn + lr;
-      f32x4 U = zero4(), O = zero4(), P = zero4();
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const bf16x8 zh = *reinterpret_cast<const bf16x8*>(&sZh[buf][col * TP + 32 * kk + 8 * lq]);
-        const bf16x8 zl = *reinterpret_cast<const bf16x8*>(&sZl[buf][col * TP + 32 * kk + 8 * lq]);
-        U = mfma(cur.ai[kk], zh, U);
-        U = mfma(cur.ai[kk], zl, U);
-        O = mfma3(cur.mzh[kk], cur.mzl[kk], zh, zl, O);
-      }
-#pragma unroll
-      for (int kk = 0; kk < KT; ++kk) {
-        const bf16x8 sh = *reinterpret_cast<const bf16x8*>(&sSh[buf][col * SP + 32 * kk + 8 * lq]);
-        const bf16x8 sl = *reinterpret_cast<const bf16x8*>(&sSl[buf][col * SP + 32 * kk + 8 * lq]);
-        P = mfma3(cur.wh[kk], cur.wl[kk], sh, sl, P);
-        O = mfma3(cur.qh[kk], cur.ql[kk], sh, sl, O);
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int t = 16 * wave + 4 * lq + e;
-        const size_t oi = ((static_cast<size_t>(bi) * s_alloc + tok0 + t) * H + h) * DV + d0 + col;
-        store_elem(o, oi, OUT_DT, O[e]);
-      }
-      const f32x4 un = U - P;
-      const int t = 16 * wave + 4 * lq;
-      put_quad(&sNh[col * TP + t], &sNl[col * TP + t], un);
-    }
-    put_z(Other{});     // that LDS buffer was last read in chunk nc-1 (a clamped copy at the end)
-    // phase-1 fragments of this buffer are dead: fetch chunk nc + 2's now
     const int pre = min(nc + 2, last);
-    const unsigned short* rec_pre = rec0 + static_cast<size_t>(pre) * L::STRIDE;
-    load_frags_p1<DK>(rec_pre, wave, lane, cur);
-    __syncthreads();
+    const unsigned short* rp = rec0 + static_cast<size_t>(pre) * L::STRIDE;
 
-    // ---- S = diag(gamma_last) S + KG^T Un --------------------------------------
+    // ---- phase 1, row block m: Un = Ai Z - W S (waves 0-3) or
+    //      o = MOZ Z + Q' S (waves 4-7) -----------------------------------------
+    f32x4 A[NT], X[NT];
 #pragma unroll
-    for (int mi = 0; mi < MPW; ++mi)
+    for (int nn = 0; nn < NT; ++nn) { A[nn] = zero4(); X[nn] = zero4(); }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
       for (int nn = 0; nn < NT; ++nn) {
         const int col = 16 * nn + lr;
-        f32x4 acc = S[mi][nn];
-        acc[0] *= cur.gam[mi].x; acc[1] *= cur.gam[mi].y;
-        acc[2] *= cur.gam[mi].z; acc[3] *= cur.gam[mi].w;
+        const bf16x8 zh = *reinterpret_cast<const bf16x8*>(&sZh[buf][col * TP + 32 * kk + 8 * lq]);
+        const bf16x8 zl = *reinterpret_cast<const bf16x8*>(&sZl[buf][col * TP + 32 * kk + 8 * lq]);
+        if (un_role) {
+          A[nn] = mfma(cur.a1[kk], zh, A[nn]);
+          A[nn] = mfma(cur.a1[kk], zl, A[nn]);
+        } else {
+          A[nn] = mfma3(cur.a1[kk], cur.a2[kk], zh, zl, A[nn]);
+        }
+      }
+      if (un_role) {
+        cur.a1[kk] = frag(rp, L::ai_frag(m, kk));
+      } else {
+        cur.a1[kk] = frag(rp, L::moz_frag(m, kk, 0));
+        cur.a2[kk] = frag(rp, L::moz_frag(m, kk, 1));
+      }
+    }
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) {
+    for (int kk = 0; kk < KT; ++kk) {
+#pragma unroll
+      for (int nn = 0; nn < NT; ++nn) {
+        const int col = 16 * nn + lr;
+        const bf16x8 sh = *reinterpret_cast<const bf16x8*>(&sSh[buf][col * SP + 32 * kk + 8 * lq]);
+        const bf16x8 sl = *reinterpret_cast<const bf16x8*>(&sSl[buf][col * SP + 32 * kk + 8 * lq]);
+        X[nn] = mfma3(cur.xh[kk], cur.xl[kk], sh, sl, X[nn]);
+      }
+      cur.xh[kk] = frag(rp, un_role ? L::w_frag(m, kk, 0) : L::qp_frag(m, kk, 0));
+      cur.xl[kk] = frag(rp, un_role ? L::w_frag(m, kk, 1) : L::qp_frag(m, kk, 1));
+    }
+#pragma unroll
+    for (int nn = 0; nn < NT; ++nn) {
+      const int col = 16 * nn + lr;
+      if (un_role) {
+        const f32x4 un = A[nn] - X[nn];
+        const int t = 16 * m + 4 * lq;
+        put_quad(&sNh[col * TP + t], &sNl[col * TP + t], un);
+      } else {
+        const f32x4 O = A[nn] + X[nn];
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int t = 16 * m + 4 * lq + e;
+          const size_t oi = ((static_cast<size_t>(bi) * s_alloc + tok0 + t) * H + h) * DV + d0 + col;
+          store_elem(o, oi, OUT_DT, O[e]);
+        }
+      }
+    }
+    put_z(Other{});     // that LDS buffer was last read in chunk nc-1 (a clamped copy at the end)
+    __syncthreads();
+
+    // ---- phase 2: S = diag(gamma_last) S + KG^T Un (state tile = wave) -------
+    if (owns) {
+#pragma unroll
+      for (int nn = 0; nn < NT; ++nn) {
+        S[nn][0] *= cur.gam.x; S[nn][1] *= cur.gam.y;
+        S[nn][2] *= cur.gam.z; S[nn][3] *= cur.gam.w;
+      }
+      cur.gam = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(rp + L::GL_OFF) + 16 * wave + 4 * lq);
+#pragma unroll
+      for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+        for (int nn = 0; nn < NT; ++nn) {
+          const int col = 16 * nn + lr;
           const bf16x8 nh = *reinterpret_cast<const bf16x8*>(&sNh[col * TP + 32 * kk + 8 * lq]);
           const bf16x8 nl = *reinterpret_cast<const bf16x8*>(&sNl[col * TP + 32 * kk + 8 * lq]);
-          acc = mfma3(cur.kh[mi][kk], cur.kl[mi][kk], nh, nl, acc);
+          S[nn] = mfma3(cur.kh[kk], cur.kl[kk], nh, nl, S[nn]);
         }
-        S[mi][nn] = acc;
+        cur.kh[kk] = frag(rp, L::kt_frag(wave, kk, 0));
+        cur.kl[kk] = frag(rp, L::kt_frag(wave, kk, 1));
       }
+    }
     put_state(buf ^ 1);
     fetch_z(parity, pre);
-    load_frags_p2<DK>(rec_pre, wave, lane, lq, cur);
     __syncthreads();
   };
 
@@ -311,15 +353,14 @@ __global__ __launch_bounds__(256) void scan_kernel(
   }
   if (nc < NC) step(P0{}, fr[0], nc);
 
+  if (!owns) return;
 #pragma unroll
-  for (int mi = 0; mi < MPW; ++mi)
+  for (int nn = 0; nn < NT; ++nn)
 #pragma unroll
-    for (int nn = 0; nn < NT; ++nn)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int c = 16 * (wave * MPW + mi) + 4 * lq + e;
-        s_out[(static_cast<size_t>(bh) * DK + c) * DV + d0 + 16 * nn + lr] = S[mi][nn][e];
-      }
+    for (int e = 0; e < 4; ++e) {
+      const int c = 16 * wave + 4 * lq + e;
+      s_out[(static_cast<size_t>(bh) * DK + c) * DV + d0 + 16 * nn + lr] = S[nn][e];
+    }
 }
 
 template <int DK, int NT, int IN_DT, int OUT_DT>
@@ -328,7 +369,7 @@ static hipError_t launch_scan_t(const void* v, const void* w, const unsigned sho
                                 int DV, long s_alloc, long t0, int NC, hipStream_t stream) {
   const int BH = B * H;
   const unsigned grid = static_cast<unsigned>(BH) * (DV / (16 * NT));
-  hipLaunchKernelGGL((scan_kernel<DK, NT, IN_DT, OUT_DT>), dim3(grid), dim3(256), 0, stream, v, w,
+  hipLaunchKernelGGL((scan_kernel<DK, NT, IN_DT, OUT_DT>), dim3(grid), dim3(kScanThreads), 0, stream, v, w,
                      ws, s_in, s_out, o, BH, H, DV, s_alloc, t0, NC);
   return hipGetLastError();
 }
