@@ -197,6 +197,9 @@ def main():
     ap.add_argument("--no-cpu", action="store_true", help="skip the CPU baseline")
     ap.add_argument("--no-decode", action="store_true", help="skip the decode configs")
     ap.add_argument("--prefill-only", action="store_true", help="prefill steps only (for profilers)")
+    ap.add_argument("--decode-only", action="store_true", help="decode configs only (for profilers)")
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="three plain 1 GiB device copies (scales rocprofv3 byte counters)")
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the GDN-2 path shards by "
@@ -207,6 +210,18 @@ def main():
         sys.exit(2)
 
     log(f"device: {torch.cuda.get_device_name()}")
+    if args.copy_calibration:
+        src = torch.ones(2 ** 28, device="cuda")          # 1 GiB fp32
+        dst = torch.empty_like(src)
+        for _ in range(3):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        log("copy calibration: 3 x 1073741824 bytes read + written")
+        return
+    if args.decode_only:
+        log(json.dumps({"config2_decode_step": bench_decode(64, 1, calls=64, steps_per_buf_min=1),
+                        "config3_decode_multi_n8": bench_decode(32, 8, calls=64, steps_per_buf_min=1)}))
+        return
     ms_step, cl_ms, sc_ms = bench_prefill(args.steps, args.warmup)
     if args.prefill_only:
         log(f"prefill {ms_step * 1e3:.1f} us/step (chunk_local {cl_ms * 1e3:.1f}, scan {sc_ms * 1e3:.1f})")

@@ -9,8 +9,7 @@
 //   Aqk[r,s] = scale * sum_c q_rc k_sc 2^(G_rc - G_sc)   s <= r
 //   Akk[r,s] =         sum_c b_rc k_rc k_sc 2^(G_rc - G_sc)   s < r
 //   Ai = (I + Akk)^-1,  W = Ai (b*k*gamma),  KG = k * 2^(G_last - G)
-//   Q' = scale*q*gamma - Aqk W      (so the scan's output is Q' S + Aqk U)
-//   MOZ = Aqk bf16(Ai)               (so the scan forms Aqk U as MOZ (w*v))
+//   Qg = scale*q*gamma               (the scan's output is Qg S + Aqk Un)
 //
 // Overflow safety (reference forward.py:21-32): every 16x16 block of Aqk/Akk
 // is an MFMA product of row factors 2^(G_r - ref) and column factors
@@ -24,8 +23,8 @@
 //    the reference, all factors <= 1, and the diagonal blocks are summed
 //    exactly with 2^(G_r - G_s) on the VALU.
 //
-// Precision (bf16 MFMA, fp32 accumulate): Aqk, Akk, W and Aqk*W use hi+lo split
-// operands (three MFMAs each); the solve is fp32. W, Q', KG and MOZ are
+// Precision (bf16 MFMA, fp32 accumulate): Aqk, Akk and W use hi+lo split
+// operands (three MFMAs each); the solve is fp32. W, Qg, KG and Aqk are
 // exported as hi/lo pairs, Ai as bf16.
 //
 // This kernel serves DK = 64; DK = 128 runs gdn2_chunk_local2.hip.
@@ -55,22 +54,20 @@ template <int DK>
 struct ChunkSmem {
   static constexpr int GP = DK + 4;    // fp32 pitch of [64][DK] arrays
   static constexpr int AP = 68;        // fp32 pitch of [64][64] arrays
-  static constexpr int AP2 = 72;       // fp32 pitch of the Akk region (reused for W^T)
+  static constexpr int AP2 = 72;       // fp32 pitch of the Akk region
   static constexpr int TP = 72;        // bf16 pitch of [DK][64] arrays
   static constexpr int WP = DK + 8;    // bf16 pitch of [64][DK] arrays
-  static constexpr size_t G_OFF = 0;                                 // G, later Aqk*W staging
+  static constexpr size_t G_OFF = 0;                                 // G
   static constexpr size_t K_OFF = G_OFF + 64 * GP * 4;               // k, later W [64][WP]
   static constexpr size_t ET_OFF = K_OFF + 64 * GP * 4;              // E^T hi bf16 [DK][TP]
   static constexpr size_t ETL_OFF = ET_OFF + DK * TP * 2;            // E^T lo bf16 [DK][TP]
   static constexpr size_t A1_OFF = ETL_OFF + DK * TP * 2;            // Aqk
-  static constexpr size_t A2_OFF = A1_OFF + 64 * AP * 4;             // Akk, later W^T [DK][TP]
+  static constexpr size_t A2_OFF = A1_OFF + 64 * AP * 4;             // Akk
   static constexpr size_t AI_OFF = A2_OFF + 64 * AP2 * 4;            // Ai
   static constexpr size_t T_OFF = AI_OFF + 64 * AP * 4;              // solve scratch [3][16][17]
   static constexpr size_t REF_OFF = T_OFF + 3 * 16 * 17 * 4;         // [4][DK] per-block reference
   static constexpr size_t TOT_OFF = REF_OFF + 4 * DK * 4;            // cumsum partials [4][DK]
   static constexpr size_t BYTES = TOT_OFF + 4 * DK * 4;
-  static_assert(2 * DK * TP * 2 <= 64 * AP2 * 4, "W^T hi/lo must fit in the Akk region");
-  static_assert(64 * AP * 4 <= 2 * DK * TP * 2, "MOZ staging must fit in the E^T region");
 };
 
 template <int DK, int IN_DT>
@@ -95,10 +92,7 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
   float* sT = reinterpret_cast<float*>(smem + M::T_OFF);
   float* sRef = reinterpret_cast<float*>(smem + M::REF_OFF);
   float* sTot = reinterpret_cast<float*>(smem + M::TOT_OFF);
-  float* sQS = sG;                                                   // phase E staging
   float* sWf = sK;                                                   // phase D, [64][GP] fp32
-  unsigned short* sWT = reinterpret_cast<unsigned short*>(sA2);      // phase D/E, hi
-  unsigned short* sWTl = sWT + DK * TP;                              // phase D/E, lo
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -342,6 +336,8 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] = sA1[my_r * AP + s0 + j];
     split_bf16x8(x, aqk_hi[kk], aqk_lo[kk]);
+    *reinterpret_cast<bf16x8*>(rec + L::aqk_frag(wave, kk, 0) + lane * 8) = aqk_hi[kk];
+    *reinterpret_cast<bf16x8*>(rec + L::aqk_frag(wave, kk, 1) + lane * 8) = aqk_lo[kk];
   }
 #pragma unroll
   for (int nn = 0; nn < MT; ++nn) {
@@ -355,12 +351,6 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) sWf[(16 * wave + 4 * lq + e) * GP + c] = acc[e];
-    const int t = 16 * wave + 4 * lq;
-    uint32_t h01, l01, h23, l23;
-    split_pk(acc[0], acc[1], h01, l01);
-    split_pk(acc[2], acc[3], h23, l23);
-    *reinterpret_cast<uint2*>(&sWT[c * TP + t]) = make_uint2(h01, h23);
-    *reinterpret_cast<uint2*>(&sWTl[c * TP + t]) = make_uint2(l01, l23);
   }
   __syncthreads();
 #pragma unroll
@@ -373,65 +363,13 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
     *reinterpret_cast<bf16x8*>(rec + L::w_frag(wave, kk, 0) + lane * 8) = hi;
     *reinterpret_cast<bf16x8*>(rec + L::w_frag(wave, kk, 1) + lane * 8) = lo;
   }
-  // MOZ = Aqk (hi/lo) x bf16(Ai), staged in the (now dead) E^T region
-  {
-    float* sMZ = reinterpret_cast<float*>(sET);
-#pragma unroll
-    for (int nn = 0; nn < 4; ++nn) {
-      f32x4 acc = zero4();
-      const int col = 16 * nn + lr;
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        float x[8];
-#pragma unroll
-        for (int j = 0; j < 8; ++j) x[j] = sAI[(32 * kk + 8 * lq + j) * AP + col];
-        const bf16x8 bfr = pack_bf16x8(x);
-        acc = mfma(aqk_hi[kk], bfr, acc);
-        acc = mfma(aqk_lo[kk], bfr, acc);
-      }
-#pragma unroll
-      for (int e = 0; e < 4; ++e) sMZ[(16 * wave + 4 * lq + e) * AP + col] = acc[e];
-    }
-  }
-
-  // ---- phase E: Q' = scale*q*gamma - Aqk W (split operands) -----------------
-#pragma unroll
-  for (int nn = 0; nn < MT; ++nn) {
-    f32x4 acc = zero4();
-    const int c = 16 * nn + lr;
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      const bf16x8 bh = *reinterpret_cast<const bf16x8*>(&sWT[c * TP + 32 * kk + 8 * lq]);
-      const bf16x8 bl = *reinterpret_cast<const bf16x8*>(&sWTl[c * TP + 32 * kk + 8 * lq]);
-      acc = mfma3(aqk_hi[kk], aqk_lo[kk], bh, bl, acc);
-    }
-#pragma unroll
-    for (int e = 0; e < 4; ++e) sQS[(16 * wave + 4 * lq + e) * GP + c] = acc[e];
-  }
-  __syncthreads();
-  {
-    const float* sMZ = reinterpret_cast<const float*>(sET);
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      float x[8];
-#pragma unroll
-      for (int j = 0; j < 8; ++j) x[j] = sMZ[my_r * AP + 32 * kk + 8 * lq + j];
-      bf16x8 hi, lo;
-      split_bf16x8(x, hi, lo);
-      *reinterpret_cast<bf16x8*>(rec + L::moz_frag(wave, kk, 0) + lane * 8) = hi;
-      *reinterpret_cast<bf16x8*>(rec + L::moz_frag(wave, kk, 1) + lane * 8) = lo;
-    }
-  }
+  // Qg = scale * q * gamma, row block `wave`
 #pragma unroll
   for (int kk = 0; kk < KT; ++kk) {
-    const int c0 = 32 * kk + 8 * lq;
-    float x[8];
-#pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] = qg[kk][j] - sQS[my_r * GP + c0 + j];
     bf16x8 hi, lo;
-    split_bf16x8(x, hi, lo);
-    *reinterpret_cast<bf16x8*>(rec + L::qp_frag(wave, kk, 0) + lane * 8) = hi;
-    *reinterpret_cast<bf16x8*>(rec + L::qp_frag(wave, kk, 1) + lane * 8) = lo;
+    split_bf16x8(qg[kk], hi, lo);
+    *reinterpret_cast<bf16x8*>(rec + L::qg_frag(wave, kk, 0) + lane * 8) = hi;
+    *reinterpret_cast<bf16x8*>(rec + L::qg_frag(wave, kk, 1) + lane * 8) = lo;
   }
 }
 

@@ -26,10 +26,8 @@
 //     lane per column), then the off-diagonal blocks by sub-diagonal with
 //     split-bf16 MFMA: X_ij = -X_ii sum_k A_ik X_kj.
 //  D  W = Ai E for the wave's channels (split operands, exported hi + lo).
-//  E  MOZ = Aqk bf16(Ai) (row block w); Q' = Qg - Aqk W (wave's channels).
-//
-// Qg is parked, fp32, in the record's own Q' slots (each lane in exactly the
-// 32 bytes its hi/lo fragments will later occupy) between phases A and E.
+//  E  Aqk fragments of row block w (hi + lo). Qg = scale q 2^G is exported in
+//     phase A straight from the lanes that formed it.
 //
 // LDS: a 40 KiB shared region (partial-product slabs, then Aqk / Akk / X
 // tiles) and a 9.5 KiB private region per wave for its transposes: < 80 KiB,
@@ -71,8 +69,6 @@ constexpr int P_BYTES = 9728;
 constexpr int P_ETH = 0;          // E^T hi bf16 [32 c][72 t]         4608  (A..D)
 constexpr int P_ETL = 4608;       // E^T lo bf16 [32 c][72 t]         4608  (A..D)
 constexpr int P_WS = 0;           // W staging fp32 [64 t][36]        9216  (D, after E^T is read)
-constexpr int P_MZ = 0;           // MOZ staging fp32 [16][68]        4352  (E, after W is read)
-constexpr int P_QS = 0;           // Aqk W staging fp32 [64 t][36]    9216  (E)
 constexpr int LDS_BYTES = S_BYTES + 4 * P_BYTES;
 static_assert(LDS_BYTES <= 81920, "two workgroups per CU");
 
@@ -239,7 +235,7 @@ __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
         for (int j = 0; j < 8; ++j) sref[i * CPW + 8 * lq + j] = first[i][j];
     }
 
-    // ---- A.4 lane-local products; Qg parked in its Q' slots; KG^T staged -------
+    // ---- A.4 lane-local products; Qg exported; KG^T staged ----------------------
     float* kgt = reinterpret_cast<float*>(smem + SKGT_OFF) + wave * 2048;   // [32 c][64 t]
 #pragma unroll
     for (int i = 0; i < 4; ++i) {
@@ -267,10 +263,12 @@ __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
         etl[a0] = static_cast<unsigned short>(lo);
         etl[a1] = static_cast<unsigned short>(lo >> 16);
       }
-      float* hs = reinterpret_cast<float*>(rec + L::qp_frag(i, wave, 0) + lane * 8);
-      float* ls = reinterpret_cast<float*>(rec + L::qp_frag(i, wave, 1) + lane * 8);
-      *reinterpret_cast<float4*>(hs) = make_float4(qg[0], qg[1], qg[2], qg[3]);
-      *reinterpret_cast<float4*>(ls) = make_float4(qg[4], qg[5], qg[6], qg[7]);
+      {   // Qg fragment (row block i, k step = this wave's channels)
+        bf16x8 hi, lo;
+        split_bf16x8(qg, hi, lo);
+        st_frag(rec + L::qg_frag(i, wave, 0) + lane * 8, hi);
+        st_frag(rec + L::qg_frag(i, wave, 1) + lane * 8, lo);
+      }
       split_bf16x8(xq, aqh[i], aql[i]);
     }
     // KG^T fragments m = 2w, 2w+1 (rows = channels), k = t
@@ -482,7 +480,6 @@ __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
   }
 
   // ---- D: W = Ai E over this wave's channels (split operands); Ai fragments out --
-  bf16x8 wbh[2][2], wbl[2][2];     // W as B operand of Aqk W: [kk][n], hi / lo
   {
     const int half = lq & 1;
     bf16x8 aifh[4][2], aifl[4][2];
@@ -532,24 +529,11 @@ __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
       st_frag(rec + L::w_frag(m, wave, 0) + lane * 8, hi);
       st_frag(rec + L::w_frag(m, wave, 1) + lane * 8, lo);
     }
-    // W as the B operand of Aqk W: element (t = 32kk + 8lq + jj, c = 16n + lr)
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk)
-#pragma unroll
-      for (int nn = 0; nn < 2; ++nn) {
-        float x[8];
-#pragma unroll
-        for (int jj = 0; jj < 8; ++jj) x[jj] = wsg[(32 * kk + 8 * lq + jj) * 36 + 16 * nn + lr];
-        split_bf16x8(x, wbh[kk][nn], wbl[kk][nn]);
-      }
   }
 
-  // ---- E: MOZ = Aqk bf16(Ai) for row block `wave`; Q' = Qg - Aqk W ---------------
+  // ---- E: Aqk fragments of row block `wave` (hi / lo) -------------------------
   {
     const int half = lq & 1;
-    f32x4 Mz[4];
-#pragma unroll
-    for (int nn = 0; nn < 4; ++nn) Mz[nn] = zero4();
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
       const int kt = 2 * kk + (lq >> 1);
@@ -559,77 +543,10 @@ __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) a[jj] = 0.f;
       }
-      bf16x8 ah, al;
-      split_bf16x8(a, ah, al);
-#pragma unroll
-      for (int nn = 0; nn < 4; ++nn) {
-        float x[8];
-        if (kt >= nn) ld8(&sXT[pair_idx(kt, nn) * TF + lr * TP + 8 * half], x);
-        else {
-#pragma unroll
-          for (int jj = 0; jj < 8; ++jj) x[jj] = 0.f;
-        }
-        const bf16x8 bx = pack_bf16x8(x);
-        Mz[nn] = mfma(ah, bx, Mz[nn]);
-        Mz[nn] = mfma(al, bx, Mz[nn]);
-      }
-    }
-    float* mz = reinterpret_cast<float*>(priv + P_MZ);       // [16][68]
-#pragma unroll
-    for (int nn = 0; nn < 4; ++nn)
-#pragma unroll
-      for (int e = 0; e < 4; ++e) mz[(4 * lq + e) * 68 + 16 * nn + lr] = Mz[nn][e];
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      float x[8];
-      ld8(&mz[lr * 68 + 32 * kk + 8 * lq], x);
       bf16x8 hi, lo;
-      split_bf16x8(x, hi, lo);
-      st_frag(rec + L::moz_frag(wave, kk, 0) + lane * 8, hi);
-      st_frag(rec + L::moz_frag(wave, kk, 1) + lane * 8, lo);
-    }
-
-    f32x4 Qd[4][2];
-#pragma unroll
-    for (int m = 0; m < 4; ++m) {
-      Qd[m][0] = zero4();
-      Qd[m][1] = zero4();
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        const int kt = 2 * kk + (lq >> 1);
-        float a[8];
-        if (kt <= m) ld8(&sAqk[pair_idx(m, kt) * TF + lr * TP + 8 * half], a);
-        else {
-#pragma unroll
-          for (int jj = 0; jj < 8; ++jj) a[jj] = 0.f;
-        }
-        bf16x8 ah, al;
-        split_bf16x8(a, ah, al);
-        Qd[m][0] = mfma3(ah, al, wbh[kk][0], wbl[kk][0], Qd[m][0]);
-        Qd[m][1] = mfma3(ah, al, wbh[kk][1], wbl[kk][1], Qd[m][1]);
-      }
-    }
-    float* qs = reinterpret_cast<float*>(priv + P_QS);       // [64 t][36]
-#pragma unroll
-    for (int m = 0; m < 4; ++m)
-#pragma unroll
-      for (int nn = 0; nn < 2; ++nn)
-#pragma unroll
-        for (int e = 0; e < 4; ++e) qs[(16 * m + 4 * lq + e) * 36 + 16 * nn + lr] = Qd[m][nn][e];
-#pragma unroll
-    for (int i = 0; i < 4; ++i) {
-      float aw[8];
-      ld8(&qs[(16 * i + lr) * 36 + 8 * lq], aw);
-      unsigned short* hs = rec + L::qp_frag(i, wave, 0) + lane * 8;
-      unsigned short* ls = rec + L::qp_frag(i, wave, 1) + lane * 8;
-      const float4 q0 = *reinterpret_cast<const float4*>(hs);
-      const float4 q1 = *reinterpret_cast<const float4*>(ls);
-      const float x[8] = {q0.x - aw[0], q0.y - aw[1], q0.z - aw[2], q0.w - aw[3],
-                          q1.x - aw[4], q1.y - aw[5], q1.z - aw[6], q1.w - aw[7]};
-      bf16x8 hi, lo;
-      split_bf16x8(x, hi, lo);
-      st_frag(hs, hi);
-      st_frag(ls, lo);
+      split_bf16x8(a, hi, lo);
+      st_frag(rec + L::aqk_frag(wave, kk, 0) + lane * 8, hi);
+      st_frag(rec + L::aqk_frag(wave, kk, 1) + lane * 8, lo);
     }
   }
 }

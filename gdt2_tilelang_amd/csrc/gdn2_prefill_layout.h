@@ -6,23 +6,16 @@
 // scan loads each one with a single coalesced 16-byte access per lane:
 //
 //   W   [4 m][DK/32 kk][hi,lo]   bf16 x2   W   = Ai (b*k*gamma)            64 x DK
-//   QP  [4 m][DK/32 kk][hi,lo]   bf16 x2   Q'  = scale*q*gamma - Aqk W     64 x DK
+//   QG  [4 m][DK/32 kk][hi,lo]   bf16 x2   Qg  = scale*q*gamma             64 x DK
 //   AI  [4 m][2 kk]              bf16      Ai  = (I + Akk)^-1               64 x 64
 //   KT  [DK/16 m][2 kk][hi,lo]   bf16 x2   KG^T, KG = k*gamma_last/gamma   DK x 64
-//   MOZ [4 m][2 kk][hi,lo]       bf16 x2   Aqk Ai (Aqk: scale, diagonal in) 64 x 64
+//   AQK [4 m][2 kk][hi,lo]       bf16 x2   Aqk (scale and diagonal in)     64 x 64
 //   GL  [DK]                     fp32      gamma_last = exp(G_last)
 //
-// The first three are what the scan's output / Un phase reads, the last three
-// what its state-update phase reads; each set is one contiguous byte range
-// (SET_A_BYTES from the record start, then SET_B_BYTES), so the scan streams
-// one set into LDS while it computes with the other.
+// W, QG and AI are what the scan's first phase reads (U = Ai Z, W S, Qg S),
+// KT, AQK and GL what its second phase reads (KG^T Un, Aqk Un).
 //
 // Within a fragment the 64 lanes' 8-element groups are contiguous.
-//
-// With Z = w * v, the scan needs U = Ai Z and the intra-chunk output
-// Aqk U = (Aqk Ai) Z; storing MOZ = Aqk Ai lets it take both from Z without
-// exchanging U between waves. Ai is rounded to bf16 once and the same rounded
-// matrix is used for U and inside MOZ, so the two stay consistent.
 #pragma once
 
 namespace gdn2 {
@@ -36,19 +29,17 @@ struct ChunkLayout {
   static constexpr int KT = DK / 32;   // 32-wide k steps over the key dim
   static constexpr int MT = DK / 16;   // 16-row tiles over the key dim
   static constexpr long W_OFF = 0;
-  static constexpr long QP_OFF = W_OFF + 4L * KT * 2 * kFrag;
-  static constexpr long AI_OFF = QP_OFF + 4L * KT * 2 * kFrag;
+  static constexpr long QG_OFF = W_OFF + 4L * KT * 2 * kFrag;
+  static constexpr long AI_OFF = QG_OFF + 4L * KT * 2 * kFrag;
   static constexpr long KT_OFF = AI_OFF + 4L * 2 * kFrag;
-  static constexpr long MOZ_OFF = KT_OFF + static_cast<long>(MT) * 2 * 2 * kFrag;
-  static constexpr long GL_OFF = MOZ_OFF + 4L * 2 * 2 * kFrag;  // in bf16 slots
+  static constexpr long AQK_OFF = KT_OFF + static_cast<long>(MT) * 2 * 2 * kFrag;
+  static constexpr long GL_OFF = AQK_OFF + 4L * 2 * 2 * kFrag;  // in bf16 slots
   static constexpr long STRIDE = GL_OFF + 2L * DK;               // bf16 elements per record
-  static constexpr int SET_A_BYTES = static_cast<int>(KT_OFF * 2);
-  static constexpr int SET_B_BYTES = static_cast<int>((STRIDE - KT_OFF) * 2);
 
   __host__ __device__ static constexpr long w_frag(int m, int kk, int hl) { return W_OFF + ((m * KT + kk) * 2 + hl) * kFrag; }
-  __host__ __device__ static constexpr long qp_frag(int m, int kk, int hl) { return QP_OFF + ((m * KT + kk) * 2 + hl) * kFrag; }
+  __host__ __device__ static constexpr long qg_frag(int m, int kk, int hl) { return QG_OFF + ((m * KT + kk) * 2 + hl) * kFrag; }
   __host__ __device__ static constexpr long kt_frag(int m, int kk, int hl) { return KT_OFF + ((m * 2 + kk) * 2 + hl) * kFrag; }
-  __host__ __device__ static constexpr long moz_frag(int m, int kk, int hl) { return MOZ_OFF + ((m * 2 + kk) * 2 + hl) * kFrag; }
+  __host__ __device__ static constexpr long aqk_frag(int m, int kk, int hl) { return AQK_OFF + ((m * 2 + kk) * 2 + hl) * kFrag; }
   __host__ __device__ static constexpr long ai_frag(int m, int kk) { return AI_OFF + (m * 2 + kk) * kFrag; }
 };
 

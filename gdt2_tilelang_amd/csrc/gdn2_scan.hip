@@ -3,27 +3,28 @@
 // gdn2/inference.py:356-479 prefill_scan_kernel; maths gdn2/reference.py:
 // 252-258).
 //
-// One 256-thread workgroup per (b, h, DVT-wide value tile); the fp32 state tile
-// S[DK, DVT] stays in MFMA accumulators for the whole sequence. Per chunk, from
-// the chunk record (gdn2_prefill_layout.h) and v, w:
+// One 512-thread workgroup per (b, h, DVT-wide value tile); the fp32 state
+// tile S[DK, DVT] stays in MFMA accumulators for the whole sequence. Per chunk,
+// from the chunk record (gdn2_prefill_layout.h) and v, w:
 //
 //   Z  = w * v          U = Ai Z          Un = U - W S
-//   o  = Q' S + MOZ Z                      (= scale*(q*gamma) S + Aqk Un)
+//   o  = Qg S + Aqk Un                     (Qg = scale * q * gamma)
 //   S  = diag(gamma_last) S + KG^T Un
 //
 // Operands that carry the result's precision are split into bf16 hi + lo
-// (Z, S, Un and the W, Q', MOZ, KG records) so those products keep ~16
-// mantissa bits; Ai Z uses bf16 Ai (the same rounding MOZ was built with).
-// W S needs the split on both sides: with little decay the state is large and
-// Un = U - W S is a small difference of large terms.
+// (Z, S, Un and the W, Qg, Aqk, KG records) so those products keep ~16
+// mantissa bits; Ai Z uses bf16 Ai. W S needs the split on both sides: with
+// little decay the state is large and Un = U - W S is a small difference of
+// large terms.
 //
-// Wave w owns output rows 16w..16w+15 of the chunk and state rows
-// 16*(w*MPW) .. 16*(w*MPW+MPW)-1. Per chunk two barriers hand Un and then the
-// new state between waves through LDS in B-operand order ([column][k], k
-// contiguous); S and Z are double-buffered so the next chunk's Z is staged
-// while the current one is in use. Record fragments are double-buffered in
-// registers: each half of chunk n+2's fragments is fetched as soon as chunk
-// n's copy of that half has been consumed, spreading the loads over the step.
+// Eight waves. Phase 1: waves 0-3 form Un for output row block m = w (U and
+// W S), waves 4-7 form Qg S for the same blocks. A barrier hands Un over
+// through LDS. Phase 2: wave w updates state rows 16w..16w+15 with KG^T Un and
+// waves 4-7 finish o with Aqk Un. A second barrier hands the new state over.
+// LDS holds S^T, Z and Un in B-operand order ([column][k], k contiguous); Z is
+// double-buffered so the next chunk's Z is staged while the current one is in
+// use. Record fragments are double-buffered in registers by chunk parity and
+// each one is refilled with chunk n+2's copy right after its last MFMA.
 //
 // Workgroup -> (head, tile) is XCD-aware: the tiles of one head land on the
 // same XCD so its chunk records come from HBM once into that XCD's L2.
@@ -38,8 +39,8 @@ constexpr int kScanWaves = 8;
 constexpr int kScanThreads = 64 * kScanWaves;
 
 // Record fragments one wave holds for a chunk. Waves 0-3 ("Un" role) use
-// a1 = Ai and x = W; waves 4-7 ("output" role) use a1/a2 = MOZ hi/lo and
-// x = Q'. Every wave holds the KG^T fragments and gamma_last of its state tile.
+// a1 = Ai and x = W; waves 4-7 ("output" role) use x = Qg and a1/a2 = Aqk
+// hi/lo. Every wave holds the KG^T fragments and gamma_last of its state tile.
 template <int DK>
 struct ScanFrags {
   static constexpr int KT = DK / 32;
@@ -68,13 +69,13 @@ __device__ __forceinline__ void load_frags_p1(const unsigned short* __restrict__
   } else {
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
-      f.a1[kk] = *reinterpret_cast<const bf16x8*>(rec + L::moz_frag(m, kk, 0) + o8);
-      f.a2[kk] = *reinterpret_cast<const bf16x8*>(rec + L::moz_frag(m, kk, 1) + o8);
+      f.a1[kk] = *reinterpret_cast<const bf16x8*>(rec + L::aqk_frag(m, kk, 0) + o8);
+      f.a2[kk] = *reinterpret_cast<const bf16x8*>(rec + L::aqk_frag(m, kk, 1) + o8);
     }
 #pragma unroll
     for (int kk = 0; kk < KT; ++kk) {
-      f.xh[kk] = *reinterpret_cast<const bf16x8*>(rec + L::qp_frag(m, kk, 0) + o8);
-      f.xl[kk] = *reinterpret_cast<const bf16x8*>(rec + L::qp_frag(m, kk, 1) + o8);
+      f.xh[kk] = *reinterpret_cast<const bf16x8*>(rec + L::qg_frag(m, kk, 0) + o8);
+      f.xl[kk] = *reinterpret_cast<const bf16x8*>(rec + L::qg_frag(m, kk, 1) + o8);
     }
   }
 }
@@ -262,30 +263,22 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
     const int pre = min(nc + 2, last);
     const unsigned short* rp = rec0 + static_cast<size_t>(pre) * L::STRIDE;
 
-    // ---- phase 1, row block m: Un = Ai Z - W S (waves 0-3) or
-    //      o = MOZ Z + Q' S (waves 4-7) -----------------------------------------
+    // ---- phase 1, row block m: Un = Ai Z - W S (waves 0-3), Qg S (waves 4-7)
     f32x4 A[NT], X[NT];
 #pragma unroll
     for (int nn = 0; nn < NT; ++nn) { A[nn] = zero4(); X[nn] = zero4(); }
+    if (un_role) {
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
+      for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
-      for (int nn = 0; nn < NT; ++nn) {
-        const int col = 16 * nn + lr;
-        const bf16x8 zh = *reinterpret_cast<const bf16x8*>(&sZh[buf][col * TP + 32 * kk + 8 * lq]);
-        const bf16x8 zl = *reinterpret_cast<const bf16x8*>(&sZl[buf][col * TP + 32 * kk + 8 * lq]);
-        if (un_role) {
+        for (int nn = 0; nn < NT; ++nn) {
+          const int col = 16 * nn + lr;
+          const bf16x8 zh = *reinterpret_cast<const bf16x8*>(&sZh[buf][col * TP + 32 * kk + 8 * lq]);
+          const bf16x8 zl = *reinterpret_cast<const bf16x8*>(&sZl[buf][col * TP + 32 * kk + 8 * lq]);
           A[nn] = mfma(cur.a1[kk], zh, A[nn]);
           A[nn] = mfma(cur.a1[kk], zl, A[nn]);
-        } else {
-          A[nn] = mfma3(cur.a1[kk], cur.a2[kk], zh, zl, A[nn]);
         }
-      }
-      if (un_role) {
         cur.a1[kk] = frag(rp, L::ai_frag(m, kk));
-      } else {
-        cur.a1[kk] = frag(rp, L::moz_frag(m, kk, 0));
-        cur.a2[kk] = frag(rp, L::moz_frag(m, kk, 1));
       }
     }
 #pragma unroll
@@ -297,30 +290,23 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
         const bf16x8 sl = *reinterpret_cast<const bf16x8*>(&sSl[buf][col * SP + 32 * kk + 8 * lq]);
         X[nn] = mfma3(cur.xh[kk], cur.xl[kk], sh, sl, X[nn]);
       }
-      cur.xh[kk] = frag(rp, un_role ? L::w_frag(m, kk, 0) : L::qp_frag(m, kk, 0));
-      cur.xl[kk] = frag(rp, un_role ? L::w_frag(m, kk, 1) : L::qp_frag(m, kk, 1));
+      cur.xh[kk] = frag(rp, un_role ? L::w_frag(m, kk, 0) : L::qg_frag(m, kk, 0));
+      cur.xl[kk] = frag(rp, un_role ? L::w_frag(m, kk, 1) : L::qg_frag(m, kk, 1));
     }
+    if (un_role) {
 #pragma unroll
-    for (int nn = 0; nn < NT; ++nn) {
-      const int col = 16 * nn + lr;
-      if (un_role) {
+      for (int nn = 0; nn < NT; ++nn) {
+        const int col = 16 * nn + lr;
         const f32x4 un = A[nn] - X[nn];
         const int t = 16 * m + 4 * lq;
         put_quad(&sNh[col * TP + t], &sNl[col * TP + t], un);
-      } else {
-        const f32x4 O = A[nn] + X[nn];
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int t = 16 * m + 4 * lq + e;
-          const size_t oi = ((static_cast<size_t>(bi) * s_alloc + tok0 + t) * H + h) * DV + d0 + col;
-          store_elem(o, oi, OUT_DT, O[e]);
-        }
       }
     }
     put_z(Other{});     // that LDS buffer was last read in chunk nc-1 (a clamped copy at the end)
     __syncthreads();
 
-    // ---- phase 2: S = diag(gamma_last) S + KG^T Un (state tile = wave) -------
+    // ---- phase 2: S = diag(gamma_last) S + KG^T Un (state tile = wave);
+    //      waves 4-7 finish o = Qg S + Aqk Un for row block m -------------------
     if (owns) {
 #pragma unroll
       for (int nn = 0; nn < NT; ++nn) {
@@ -328,17 +314,36 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
         S[nn][2] *= cur.gam.z; S[nn][3] *= cur.gam.w;
       }
       cur.gam = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(rp + L::GL_OFF) + 16 * wave + 4 * lq);
+    }
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
+    for (int kk = 0; kk < 2; ++kk) {
 #pragma unroll
-        for (int nn = 0; nn < NT; ++nn) {
-          const int col = 16 * nn + lr;
-          const bf16x8 nh = *reinterpret_cast<const bf16x8*>(&sNh[col * TP + 32 * kk + 8 * lq]);
-          const bf16x8 nl = *reinterpret_cast<const bf16x8*>(&sNl[col * TP + 32 * kk + 8 * lq]);
-          S[nn] = mfma3(cur.kh[kk], cur.kl[kk], nh, nl, S[nn]);
-        }
+      for (int nn = 0; nn < NT; ++nn) {
+        const int col = 16 * nn + lr;
+        const bf16x8 nh = *reinterpret_cast<const bf16x8*>(&sNh[col * TP + 32 * kk + 8 * lq]);
+        const bf16x8 nl = *reinterpret_cast<const bf16x8*>(&sNl[col * TP + 32 * kk + 8 * lq]);
+        if (owns) S[nn] = mfma3(cur.kh[kk], cur.kl[kk], nh, nl, S[nn]);
+        if (!un_role) X[nn] = mfma3(cur.a1[kk], cur.a2[kk], nh, nl, X[nn]);
+      }
+      if (owns) {
         cur.kh[kk] = frag(rp, L::kt_frag(wave, kk, 0));
         cur.kl[kk] = frag(rp, L::kt_frag(wave, kk, 1));
+      }
+      if (!un_role) {
+        cur.a1[kk] = frag(rp, L::aqk_frag(m, kk, 0));
+        cur.a2[kk] = frag(rp, L::aqk_frag(m, kk, 1));
+      }
+    }
+    if (!un_role) {
+#pragma unroll
+      for (int nn = 0; nn < NT; ++nn) {
+        const int col = 16 * nn + lr;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int t = 16 * m + 4 * lq + e;
+          const size_t oi = ((static_cast<size_t>(bi) * s_alloc + tok0 + t) * H + h) * DV + d0 + col;
+          store_elem(o, oi, OUT_DT, X[nn][e]);
+        }
       }
     }
     put_state(buf ^ 1);
