@@ -179,7 +179,7 @@ def cpu_baseline(budget_s=12.0):
 def read_traffic():
     """HBM bytes per prefill step from the committed rocprofv3 --pmc summary, if any."""
     path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles",
-                        "prefill_config1_pmc.txt")
+                        "hbm_traffic_pmc.txt")
     if not os.path.exists(path):
         return None
     with open(path) as f:
