@@ -84,7 +84,7 @@ def bench_prefill(steps, warmup):
                                             scale, sp), "chunk_local")
         if ev is not None:
             ev[1].record(stream)
-        _hip.check(lib.gdn2_hip_prefill_scan(P(v), P(w), 1, P(ws), None, P(st), P(o), 1, B1, H1, D1, D1,
+        _hip.check(lib.gdn2_hip_prefill_scan(P(v), P(w), 1, P(ws), None, P(st), P(o), 1, B1, H1, H1, D1, D1,
                                              S1, 0, n_tok, sp), "prefill_scan")
         if ev is not None:
             ev[2].record(stream)
@@ -129,7 +129,7 @@ def bench_decode(B, n, calls, steps_per_buf_min, H=16, D=128):
     def call(i):
         q, k, v, g, b, w = tok[i % 4]
         _hip.check(lib.gdn2_hip_decode(P(q), P(k), P(v), P(g), P(b), P(w), 1, P(states[i % nbuf]), P(o), 1,
-                                       B, H, D, D, n, 0, n, scale, sp), "decode")
+                                       B, H, H, D, D, n, 0, n, scale, sp), "decode")
 
     for i in range(2 * nbuf):
         call(i)

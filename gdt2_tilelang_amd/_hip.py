@@ -23,11 +23,11 @@ _P, _I, _L, _F, _S = ctypes.c_void_p, ctypes.c_int, ctypes.c_long, ctypes.c_floa
 SIGNATURES = {
     "gdn2_hip_version": (_I, []),
     "gdn2_hip_status_string": (ctypes.c_char_p, [_I]),
-    "gdn2_hip_decode": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _L, _L, _L, _F, _P]),
+    "gdn2_hip_decode": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _P, _I, _I, _I, _I, _I, _I, _L, _L, _L, _F, _P]),
     "gdn2_hip_prefill_workspace_bytes": (_S, [_I, _I, _I, _L]),
     "gdn2_hip_chunk_local": (_I, [_P, _P, _P, _P, _I, _P, _I, _I, _I, _L, _L, _L, _F, _P]),
-    "gdn2_hip_prefill_scan": (_I, [_P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _L, _L, _L, _P]),
-    "gdn2_hip_prefill_chunks": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I,
+    "gdn2_hip_prefill_scan": (_I, [_P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _L, _L, _L, _P]),
+    "gdn2_hip_prefill_chunks": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I,
                                      _L, _L, _L, _F, _P]),
 }
 

@@ -210,9 +210,6 @@ class GatedDeltaNet2(nn.Module):
         f = self.f_proj(x).view(*lead, self.num_kv_heads, self.head_dim_k)
         return -self.A_log.exp().unsqueeze(-1) * F.softplus(f.float() + self.dt_bias)
 
-    def _to_value_heads(self, t):
-        return t if self.head_repeat == 1 else t.repeat_interleave(self.head_repeat, dim=-2)
-
     def _conv_with_cache(self, q, k, v, cache):
         if self.q_conv is None:
             return q, k, v
@@ -225,7 +222,13 @@ class GatedDeltaNet2(nn.Module):
         return q, k, v
 
     def _project(self, x, cache):
-        """Projections, short conv, L2 norm and gates -> value-head op inputs."""
+        """Projections, short conv, L2 norm and gates -> op inputs.
+
+        q, k, b, g stay on the HK key heads: the hip op reads key head
+        h // (H // HK) for value head h, which is what the reference's
+        ``repeat_interleave`` (``attention.py:295-297``) computes, without
+        materialising the repeated tensors.
+        """
         B, S, _ = x.shape
         HK, H, DK, DV = self.num_kv_heads, self.num_heads, self.head_dim_k, self.head_dim_v
         q, k, v = self.q_proj(x), self.k_proj(x), self.v_proj(x)
@@ -239,8 +242,7 @@ class GatedDeltaNet2(nn.Module):
         g = self._decay(x, (B, S))
         b = torch.sigmoid(self.b_proj(x).view(B, S, HK, DK)) * self.erase_scale
         w = torch.sigmoid(self.w_proj(x).view(B, S, H, DV))
-        q, k, b, g = (self._to_value_heads(t).contiguous() for t in (q, k, b, g))
-        return q, k, v.contiguous(), g, b, w.contiguous()
+        return q.contiguous(), k.contiguous(), v.contiguous(), g.contiguous(), b.contiguous(), w.contiguous()
 
     def _finish(self, x, o):
         B, S, _ = x.shape

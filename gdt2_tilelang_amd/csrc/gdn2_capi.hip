@@ -6,17 +6,17 @@
 
 namespace gdn2 {
 hipError_t launch_decode(const void*, const void*, const void*, const float*, const void*,
-                         const void*, float*, void*, int, int, int, int, long, long, int, float,
-                         int, int, hipStream_t);
+                         const void*, float*, void*, int, int, int, int, int, long, long, int,
+                         float, int, int, hipStream_t);
 hipError_t launch_chunk_local(const void*, const void*, const void*, const float*, int, int, int,
                               int, long, long, int, float, unsigned short*, hipStream_t);
 hipError_t launch_scan(const void*, const void*, int, const unsigned short*, const float*, float*,
-                       void*, int, int, int, int, int, long, long, int, hipStream_t);
+                       void*, int, int, int, int, int, int, long, long, int, hipStream_t);
 }  // namespace gdn2
 
 namespace {
 
-constexpr int kAbiVersion = 1;
+constexpr int kAbiVersion = 2;   // 2: grouped key heads (HK)
 
 bool dtype_ok(int dt) { return dt == GDN2_DTYPE_F32 || dt == GDN2_DTYPE_BF16 || dt == GDN2_DTYPE_F16; }
 
@@ -53,33 +53,33 @@ const char* gdn2_hip_status_string(int s) {
 
 int gdn2_hip_decode(const void* q, const void* k, const void* v, const float* g, const void* b,
                     const void* w, int in_dtype, float* state, void* o, int out_dtype, int B,
-                    int H, int DK, int DV, long s_alloc, long t0, long n, float scale,
+                    int H, int HK, int DK, int DV, long s_alloc, long t0, long n, float scale,
                     void* stream) {
   if (!q || !k || !v || !g || !b || !w || !state || !o) return GDN2_ERR_ARG;
   if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return GDN2_ERR_ARG;
-  if (B < 1 || H < 1 || n < 0 || t0 < 0 || s_alloc < t0 + n) return GDN2_ERR_ARG;
+  if (B < 1 || H < 1 || HK < 1 || H % HK || n < 0 || t0 < 0 || s_alloc < t0 + n) return GDN2_ERR_ARG;
   if (DK != 32 && DK != 64 && DK != 128 && DK != 256) return GDN2_ERR_SHAPE;
   if (DV % 32 != 0 || DV > 4096) return GDN2_ERR_SHAPE;
   if (static_cast<long>(B) * H * (DV / 32) > 0x7fffffffL || n > 0x7fffffffL) return GDN2_ERR_SHAPE;
-  return status(gdn2::launch_decode(q, k, v, g, b, w, state, o, B, H, DK, DV, s_alloc, t0,
+  return status(gdn2::launch_decode(q, k, v, g, b, w, state, o, B, H, HK, DK, DV, s_alloc, t0,
                                     static_cast<int>(n), scale, in_dtype, out_dtype,
                                     static_cast<hipStream_t>(stream)));
 }
 
-size_t gdn2_hip_prefill_workspace_bytes(int B, int H, int DK, long n_tokens) {
+size_t gdn2_hip_prefill_workspace_bytes(int B, int HK, int DK, long n_tokens) {
   const long rec = record_elems(DK);
-  if (rec == 0 || B < 1 || H < 1 || n_tokens < 0) return 0;
+  if (rec == 0 || B < 1 || HK < 1 || n_tokens < 0) return 0;
   const long nc = (n_tokens + gdn2::kBS - 1) / gdn2::kBS;
-  return static_cast<size_t>(B) * H * nc * rec * 2;
+  return static_cast<size_t>(B) * HK * nc * rec * 2;
 }
 
 int gdn2_hip_chunk_local(const void* q, const void* k, const void* b, const float* g,
-                         int in_dtype, void* workspace, int B, int H, int DK, long s_alloc,
+                         int in_dtype, void* workspace, int B, int HK, int DK, long s_alloc,
                          long t0, long n_tokens, float scale, void* stream) {
   if (!q || !k || !b || !g || !workspace || !dtype_ok(in_dtype)) return GDN2_ERR_ARG;
-  if (int e = check_prefill(B, H, DK, s_alloc, t0, n_tokens)) return e;
+  if (int e = check_prefill(B, HK, DK, s_alloc, t0, n_tokens)) return e;
   if (n_tokens == 0) return 0;
-  return status(gdn2::launch_chunk_local(q, k, b, g, in_dtype, B, H, DK, s_alloc, t0,
+  return status(gdn2::launch_chunk_local(q, k, b, g, in_dtype, B, HK, DK, s_alloc, t0,
                                          static_cast<int>(n_tokens / gdn2::kBS), scale,
                                          static_cast<unsigned short*>(workspace),
                                          static_cast<hipStream_t>(stream)));
@@ -87,15 +87,16 @@ int gdn2_hip_chunk_local(const void* q, const void* k, const void* b, const floa
 
 int gdn2_hip_prefill_scan(const void* v, const void* w, int in_dtype, const void* workspace,
                           const float* state_in, float* state_out, void* o, int out_dtype, int B,
-                          int H, int DK, int DV, long s_alloc, long t0, long n_tokens,
+                          int H, int HK, int DK, int DV, long s_alloc, long t0, long n_tokens,
                           void* stream) {
   if (!v || !w || !workspace || !state_out || !o) return GDN2_ERR_ARG;
   if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return GDN2_ERR_ARG;
+  if (HK < 1 || H % HK) return GDN2_ERR_ARG;
   if (int e = check_prefill(B, H, DK, s_alloc, t0, n_tokens)) return e;
   if (DV < 16 || DV % 16 || DV > 4096) return GDN2_ERR_SHAPE;
   if (n_tokens == 0) return GDN2_ERR_SHAPE;
   return status(gdn2::launch_scan(v, w, in_dtype, static_cast<const unsigned short*>(workspace),
-                                  state_in, state_out, o, out_dtype, B, H, DK, DV, s_alloc, t0,
+                                  state_in, state_out, o, out_dtype, B, H, HK, DK, DV, s_alloc, t0,
                                   static_cast<int>(n_tokens / gdn2::kBS),
                                   static_cast<hipStream_t>(stream)));
 }
@@ -103,18 +104,19 @@ int gdn2_hip_prefill_scan(const void* v, const void* w, int in_dtype, const void
 int gdn2_hip_prefill_chunks(const void* q, const void* k, const void* v, const float* g,
                             const void* b, const void* w, int in_dtype, const float* state_in,
                             float* state_out, void* o, int out_dtype, void* workspace, int B,
-                            int H, int DK, int DV, long s_alloc, long t0, long n_tokens,
+                            int H, int HK, int DK, int DV, long s_alloc, long t0, long n_tokens,
                             float scale, void* stream) {
   if (!q || !k || !b || !g) return GDN2_ERR_ARG;
   if (!v || !w || !workspace || !state_out || !o) return GDN2_ERR_ARG;
   if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return GDN2_ERR_ARG;
   if (int e = check_prefill(B, H, DK, s_alloc, t0, n_tokens)) return e;
   if (DV < 16 || DV % 16 || DV > 4096 || n_tokens == 0) return GDN2_ERR_SHAPE;
-  int s = gdn2_hip_chunk_local(q, k, b, g, in_dtype, workspace, B, H, DK, s_alloc, t0, n_tokens,
+  if (HK < 1 || H % HK) return GDN2_ERR_ARG;
+  int s = gdn2_hip_chunk_local(q, k, b, g, in_dtype, workspace, B, HK, DK, s_alloc, t0, n_tokens,
                                scale, stream);
   if (s) return s;
   return gdn2_hip_prefill_scan(v, w, in_dtype, workspace, state_in, state_out, o, out_dtype, B, H,
-                               DK, DV, s_alloc, t0, n_tokens, stream);
+                               HK, DK, DV, s_alloc, t0, n_tokens, stream);
 }
 
 }  // extern "C"

@@ -1,7 +1,8 @@
 // GDN-2 decode: n recurrent steps per launch with the fp32 state resident in
 // registers (one HBM read and one HBM write of the state per launch).
 //
-// Per token t and head:
+// Per token t and (value) head h, with key-side tensors q, k, b, g read from key
+// head h / (H/HK) (grouped heads; HK = H is the ungrouped case):
 //   S <- diag(exp g_t) S ;  u = w_t*v_t - S^T (b_t*k_t) ;  S <- S + k_t u^T ;
 //   o_t = scale * S^T q_t
 // (reference: gdn2/inference.py:61-153 decode_step_kernel and :199-303
@@ -95,7 +96,7 @@ template <int DK, int IN_DT, int OUT_DT, int TB>
 __global__ __launch_bounds__(kDecMaxThreads) void decode_kernel(
     const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ v,
     const float* __restrict__ g, const void* __restrict__ b, const void* __restrict__ w,
-    float* __restrict__ state, void* __restrict__ o, int H, int DV, long s_alloc, long t0,
+    float* __restrict__ state, void* __restrict__ o, int H, int HK, int DV, long s_alloc, long t0,
     int n, float scale) {
   constexpr int RPT = DK / kDecRowGroups;
   constexpr int GPT = DK / 8;             // 8-channel groups per token
@@ -107,6 +108,7 @@ __global__ __launch_bounds__(kDecMaxThreads) void decode_kernel(
   const int bh = blockIdx.y;
   const int bi = bh / H;
   const int h = bh % H;
+  const int hk = h / (H / HK);   // key head of value head h (grouped heads: HK divides H)
   const int rg = lane >> 3;
   const int cg = lane & 7;
   const int c0 = rg * RPT;                                                     // first key row
@@ -141,7 +143,7 @@ __global__ __launch_bounds__(kDecMaxThreads) void decode_kernel(
     // stage the key-side vectors of the block, 8 channels per item
     for (int e = tid; e < nt * GPT; e += nthr) {
       const int tt = e / GPT, c = (e % GPT) * 8;
-      const size_t ki = ((static_cast<size_t>(bi) * s_alloc + t0 + tb + tt) * H + h) * DK + c;
+      const size_t ki = ((static_cast<size_t>(bi) * s_alloc + t0 + tb + tt) * HK + hk) * DK + c;
       RowSlice<IN_DT, 8> kr, br, qr;
       RowSlice<DT_F32, 8> gr;
       kr.load(k, ki);
@@ -230,29 +232,29 @@ __global__ __launch_bounds__(kDecMaxThreads) void decode_kernel(
 template <int DK, int IN_DT, int OUT_DT>
 static hipError_t launch_decode_t(const void* q, const void* k, const void* v, const float* g,
                                   const void* b, const void* w, float* state, void* o, int B,
-                                  int H, int DV, long s_alloc, long t0, int n, float scale,
+                                  int H, int HK, int DV, long s_alloc, long t0, int n, float scale,
                                   hipStream_t stream) {
   // one workgroup per (b, h, up to kDecMaxCols columns); one wave per 32 columns
   const int tiles = (DV + kDecMaxCols - 1) / kDecMaxCols;
   const int threads = 64 * (DV < kDecMaxCols ? DV : kDecMaxCols) / kDecCols;
   if (n == 1)
     hipLaunchKernelGGL((decode_kernel<DK, IN_DT, OUT_DT, 1>), dim3(tiles, B * H), dim3(threads), 0,
-                       stream, q, k, v, g, b, w, state, o, H, DV, s_alloc, t0, n, scale);
+                       stream, q, k, v, g, b, w, state, o, H, HK, DV, s_alloc, t0, n, scale);
   else
     hipLaunchKernelGGL((decode_kernel<DK, IN_DT, OUT_DT, kDecTokBlock>), dim3(tiles, B * H),
-                       dim3(threads), 0, stream, q, k, v, g, b, w, state, o, H, DV, s_alloc, t0, n,
+                       dim3(threads), 0, stream, q, k, v, g, b, w, state, o, H, HK, DV, s_alloc, t0, n,
                        scale);
   return hipGetLastError();
 }
 
 hipError_t launch_decode(const void* q, const void* k, const void* v, const float* g,
-                         const void* b, const void* w, float* state, void* o, int B, int H,
+                         const void* b, const void* w, float* state, void* o, int B, int H, int HK,
                          int DK, int DV, long s_alloc, long t0, int n, float scale, int in_dt,
                          int out_dt, hipStream_t stream) {
   if (DV % kDecCols != 0) return hipErrorInvalidValue;
 #define GDN2_DEC_CASE(DKV, IDT, ODT)                                                          \
   if (DK == DKV && in_dt == IDT && out_dt == ODT)                                             \
-    return launch_decode_t<DKV, IDT, ODT>(q, k, v, g, b, w, state, o, B, H, DV, s_alloc, t0, \
+    return launch_decode_t<DKV, IDT, ODT>(q, k, v, g, b, w, state, o, B, H, HK, DV, s_alloc, t0, \
                                           n, scale, stream);
 #define GDN2_DEC_OUT(DKV, IDT) GDN2_DEC_CASE(DKV, IDT, DT_BF16) GDN2_DEC_CASE(DKV, IDT, DT_F16) GDN2_DEC_CASE(DKV, IDT, DT_F32)
 #define GDN2_DEC_IN(DKV) GDN2_DEC_OUT(DKV, DT_BF16) GDN2_DEC_OUT(DKV, DT_F16) GDN2_DEC_OUT(DKV, DT_F32)

@@ -136,7 +136,7 @@ template <int DK, int NT, int IN_DT, int OUT_DT>
 __global__ __launch_bounds__(kScanThreads) void scan_kernel(
     const void* __restrict__ v, const void* __restrict__ w, const unsigned short* __restrict__ ws,
     const float* __restrict__ s_in, float* __restrict__ s_out, void* __restrict__ o,
-    int BH, int H, int DV, long s_alloc, long t0, int NC) {
+    int BH, int H, int HK, int DV, long s_alloc, long t0, int NC) {
   using L = ChunkLayout<DK>;
   constexpr int KT = DK / 32;
   constexpr int MT = DK / 16;          // 16-row state tiles; wave w < MT owns tile w
@@ -159,22 +159,29 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
   const int lr = lane & 15;
   const int lq = lane >> 4;
 
-  // XCD-aware block -> (head, tile) map (workgroups are dealt round-robin to 8 XCDs)
+  // XCD-aware block -> (head, tile) map (workgroups are dealt round-robin to 8
+  // XCDs): all tiles of the value heads that share a key head, hence a record
+  // stream, land on one XCD and share its L2.
   const int ntile = DV / DVT;
-  int bh, tile;
+  const int rep = H / HK;
+  const int per = ntile * rep;           // workgroups per key head
+  const int BHK = BH / rep;
+  int bhk, r;
   const int Lb = blockIdx.x;
-  if (BH % 8 == 0) {
+  if (BHK % 8 == 0) {
     const int xcd = Lb & 7, jj = Lb >> 3;
-    bh = (jj / ntile) * 8 + xcd;
-    tile = jj % ntile;
+    bhk = (jj / per) * 8 + xcd;
+    r = jj % per;
   } else {
-    bh = Lb / ntile;
-    tile = Lb % ntile;
+    bhk = Lb / per;
+    r = Lb % per;
   }
-  const int bi = bh / H;
-  const int h = bh % H;
+  const int bi = bhk / HK;
+  const int h = (bhk % HK) * rep + r / ntile;
+  const int tile = r % ntile;
+  const int bh = bi * H + h;
   const int d0 = tile * DVT;
-  const unsigned short* rec0 = ws + static_cast<size_t>(bh) * NC * L::STRIDE;
+  const unsigned short* rec0 = ws + static_cast<size_t>(bhk) * NC * L::STRIDE;   // key head's records
 
   // Z staging: quad e -> token t = e / (DVT/4), columns 4*cq .. 4*cq+3
   Raw4<IN_DT> zv[2][ZIT], zw[2][ZIT];    // [chunk parity]
@@ -370,12 +377,12 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
 
 template <int DK, int NT, int IN_DT, int OUT_DT>
 static hipError_t launch_scan_t(const void* v, const void* w, const unsigned short* ws,
-                                const float* s_in, float* s_out, void* o, int B, int H,
+                                const float* s_in, float* s_out, void* o, int B, int H, int HK,
                                 int DV, long s_alloc, long t0, int NC, hipStream_t stream) {
   const int BH = B * H;
   const unsigned grid = static_cast<unsigned>(BH) * (DV / (16 * NT));
   hipLaunchKernelGGL((scan_kernel<DK, NT, IN_DT, OUT_DT>), dim3(grid), dim3(kScanThreads), 0, stream, v, w,
-                     ws, s_in, s_out, o, BH, H, DV, s_alloc, t0, NC);
+                     ws, s_in, s_out, o, BH, H, HK, DV, s_alloc, t0, NC);
   return hipGetLastError();
 }
 
@@ -387,12 +394,12 @@ int scan_nt_for(int B, int H, int DV) {
 }
 
 hipError_t launch_scan(const void* v, const void* w, int in_dt, const unsigned short* ws,
-                       const float* s_in, float* s_out, void* o, int out_dt, int B, int H, int DK,
+                       const float* s_in, float* s_out, void* o, int out_dt, int B, int H, int HK, int DK,
                        int DV, long s_alloc, long t0, int NC, hipStream_t stream) {
   const int nt = scan_nt_for(B, H, DV);
 #define GDN2_SCAN_CASE(DKV, NTV, DTV, ODV)                                                     \
   if (DK == DKV && nt == NTV && in_dt == DTV && out_dt == ODV)                                 \
-    return launch_scan_t<DKV, NTV, DTV, ODV>(v, w, ws, s_in, s_out, o, B, H, DV, s_alloc, t0,  \
+    return launch_scan_t<DKV, NTV, DTV, ODV>(v, w, ws, s_in, s_out, o, B, H, HK, DV, s_alloc, t0, \
                                              NC, stream);
 #define GDN2_SCAN_OUT(DKV, NTV, DTV) \
   GDN2_SCAN_CASE(DKV, NTV, DTV, DT_BF16) GDN2_SCAN_CASE(DKV, NTV, DTV, DT_F16) GDN2_SCAN_CASE(DKV, NTV, DTV, DT_F32)

@@ -40,8 +40,8 @@ def chunk_gdn2_fwd(q, k, v, g, b, w, scale, initial_state=None, output_final_sta
     dev = _require_device(q, k, v, g, b, w)
     _check_shapes(q, k, v, g, b, w)
     check_prefill_config(config)
-    B, S, H, DK = q.shape
-    DV = v.shape[-1]
+    B, S, _, DK = q.shape
+    H, DV = v.shape[2], v.shape[3]
     if DK not in (64, 128) or DV % 32:
         raise ValueError(f"hip prefill supports DK in (64, 128) and DV % 32 == 0; got DK={DK}, DV={DV}")
     BS = config.chunk_size

@@ -12,6 +12,12 @@ per-chunk states) and a ragged tail through the decode kernel, exactly as the
 reference routes it (``gdn2/inference.py:517-555``). Decode keeps the state
 resident across the ``n`` tokens of a call.
 
+Grouped heads: q, k, b, g may carry HK key heads where v, w (and the state)
+carry H value heads, HK dividing H; value head h then reads key head
+h // (H // HK), which equals the reference's ``repeat_interleave`` expansion
+(``gdn2/attention.py:295-297``) without materialising it. With HK == H the
+calls are exactly the reference's.
+
 Every call enqueues on the current HIP stream and returns without syncing.
 There is no CPU path: CPU tensors raise ``ValueError``.
 """
@@ -45,8 +51,9 @@ def _check_shapes(q, k, v, g, b, w):
     for name, t in (("k", k), ("g", g), ("b", b)):
         if t.shape != q.shape:
             raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(q.shape)}")
-    if v.dim() != 4 or v.shape[:3] != q.shape[:3]:
-        raise ValueError(f"v has shape {tuple(v.shape)}, incompatible with q {tuple(q.shape)}")
+    if v.dim() != 4 or v.shape[:2] != q.shape[:2] or v.shape[2] % q.shape[2]:
+        raise ValueError(f"v has shape {tuple(v.shape)}, incompatible with q {tuple(q.shape)} "
+                         "(value heads must be a multiple of the key heads)")
     if w.shape != v.shape:
         raise ValueError(f"w has shape {tuple(w.shape)}, expected {tuple(v.shape)}")
     dts = {t.dtype for t in (q, k, v, b, w)}
@@ -74,22 +81,23 @@ def _check_state(state, B, H, DK, DV, dev):
 
 
 def _decode_into(q, k, v, g, b, w, state, o, s_alloc, t0, n, scale):
-    B, _, H, DK = q.shape
-    DV = v.shape[-1]
+    B, _, HK, DK = q.shape
+    H, DV = v.shape[2], v.shape[3]
     if DK not in _DECODE_DK or DV % 32:
         raise ValueError(f"hip decode supports DK in {_DECODE_DK} and DV % 32 == 0; got DK={DK}, DV={DV}")
     _hip.check(_hip.lib().gdn2_hip_decode(
         _hip.ptr(q), _hip.ptr(k), _hip.ptr(v), _hip.ptr(g), _hip.ptr(b), _hip.ptr(w),
         _hip.dtype_code(q.dtype), _hip.ptr(state), _hip.ptr(o), _hip.dtype_code(o.dtype),
-        B, H, DK, DV, s_alloc, t0, n, float(scale), _hip.stream_of(q.device)), "gdn2_hip_decode")
+        B, H, HK, DK, DV, s_alloc, t0, n, float(scale), _hip.stream_of(q.device)), "gdn2_hip_decode")
 
 
 def gdn2_decode(q, k, v, g, b, w, state, scale=None):
     """Decode ``n`` tokens, updating ``state`` in place.
 
     Args:
-        q, k, b: ``[B, n, H, DK]``; v, w: ``[B, n, H, DV]`` (fp32, bf16 or fp16).
-        g: ``[B, n, H, DK]`` log decay (<= 0), used as fp32.
+        q, k, b: ``[B, n, HK, DK]``; v, w: ``[B, n, H, DV]`` (fp32, bf16 or fp16);
+            HK == H as in the reference, or HK dividing H (grouped heads).
+        g: ``[B, n, HK, DK]`` log decay (<= 0), used as fp32.
         state: fp32 contiguous ``[B, H, DK, DV]``, mutated.
         scale: query scale; defaults to ``DK ** -0.5``.
 
@@ -98,8 +106,8 @@ def gdn2_decode(q, k, v, g, b, w, state, scale=None):
     """
     dev = _require_device(q, k, v, g, b, w, state)
     _check_shapes(q, k, v, g, b, w)
-    B, n, H, DK = q.shape
-    DV = v.shape[-1]
+    B, n, _, DK = q.shape
+    H, DV = v.shape[2], v.shape[3]
     _check_state(state, B, H, DK, DV, dev)
     if not state.is_contiguous():
         raise ValueError("state must be contiguous (it is updated in place)")
@@ -124,14 +132,14 @@ def gdn2_decode_step(q, k, v, g, b, w, state, scale=None):
 
 
 def _prefill_chunks(q, k, v, g, b, w, state_in, state_out, o, s_alloc, t0, n_tokens, scale):
-    B, _, H, DK = q.shape
-    DV = v.shape[-1]
-    nbytes = _hip.lib().gdn2_hip_prefill_workspace_bytes(B, H, DK, n_tokens)
+    B, _, HK, DK = q.shape
+    H, DV = v.shape[2], v.shape[3]
+    nbytes = _hip.lib().gdn2_hip_prefill_workspace_bytes(B, HK, DK, n_tokens)
     ws = torch.empty(nbytes, dtype=torch.uint8, device=q.device)
     _hip.check(_hip.lib().gdn2_hip_prefill_chunks(
         _hip.ptr(q), _hip.ptr(k), _hip.ptr(v), _hip.ptr(g), _hip.ptr(b), _hip.ptr(w),
         _hip.dtype_code(q.dtype), _hip.ptr(state_in), _hip.ptr(state_out), _hip.ptr(o),
-        _hip.dtype_code(o.dtype), _hip.ptr(ws), B, H, DK, DV, s_alloc, t0, n_tokens,
+        _hip.dtype_code(o.dtype), _hip.ptr(ws), B, H, HK, DK, DV, s_alloc, t0, n_tokens,
         float(scale), _hip.stream_of(q.device)), "gdn2_hip_prefill_chunks")
 
 
@@ -159,7 +167,8 @@ def gdn2_prefill(q, k, v, g, b, w, state=None, scale=None, config: GDN2Config = 
     Call repeatedly, passing the state back, to prefill in segments.
 
     Args:
-        q, k, b: ``[B, S, H, DK]``; v, w: ``[B, S, H, DV]``; g: ``[B, S, H, DK]``.
+        q, k, b: ``[B, S, HK, DK]``; v, w: ``[B, S, H, DV]``; g: ``[B, S, HK, DK]``
+            (HK == H as in the reference, or HK dividing H: grouped heads).
         state: ``[B, H, DK, DV]`` to continue from, or ``None`` for zeros. As in
             the reference, a prompt shorter than one chunk updates an fp32
             contiguous ``state`` in place.
@@ -172,8 +181,8 @@ def gdn2_prefill(q, k, v, g, b, w, state=None, scale=None, config: GDN2Config = 
     dev = _require_device(q, k, v, g, b, w)
     _check_shapes(q, k, v, g, b, w)
     check_prefill_config(config)
-    B, S, H, DK = q.shape
-    DV = v.shape[-1]
+    B, S, _, DK = q.shape
+    H, DV = v.shape[2], v.shape[3]
     if DK not in _PREFILL_DK or DV % 32:
         raise ValueError(f"hip prefill supports DK in {_PREFILL_DK} and DV % 32 == 0; got DK={DK}, DV={DV}")
     scale = DK ** -0.5 if scale is None else scale

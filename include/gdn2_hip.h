@@ -6,7 +6,11 @@
  * caller; the library never allocates or frees. Sequence tensors are
  * [B, s_alloc, H, D] contiguous with D fastest and a call works on tokens
  * [t0, t0 + n) of that allocation; g is fp32 natural-log decay (<= 0); the
- * state is fp32 [B, H, DK, DV] contiguous. Work is enqueued on `stream`
+ * state is fp32 [B, H, DK, DV] contiguous. Grouped heads: the key-side tensors
+ * q, k, b, g may have HK heads with HK dividing the H heads of v, w, o and the
+ * state; value head h then reads key head h / (H / HK) (HK = H: no grouping;
+ * the reference repeats the key heads instead, gdn2/attention.py:295-297).
+ * Work is enqueued on `stream`
  * (a hipStream_t; NULL = the default stream) with no host synchronisation.
  *
  * Return value: 0 on success, a negative GDN2_ERR_* for a rejected argument
@@ -50,35 +54,39 @@ const char* gdn2_hip_status_string(int status);
  */
 int gdn2_hip_decode(const void* q, const void* k, const void* v, const float* g, const void* b,
                     const void* w, int in_dtype, float* state, void* o, int out_dtype, int B,
-                    int H, int DK, int DV, long s_alloc, long t0, long n, float scale,
+                    int H, int HK, int DK, int DV, long s_alloc, long t0, long n, float scale,
                     void* stream);
 
 /* Bytes of workspace gdn2_hip_chunk_local / gdn2_hip_prefill_chunks need for
- * n_tokens (a multiple of 64) tokens; 0 for an unsupported DK. */
-size_t gdn2_hip_prefill_workspace_bytes(int B, int H, int DK, long n_tokens);
+ * n_tokens (a multiple of 64) tokens of B x HK key heads; 0 for an unsupported
+ * DK. The records depend on q, k, b, g only, so grouped value heads share them. */
+size_t gdn2_hip_prefill_workspace_bytes(int B, int HK, int DK, long n_tokens);
 
 /*
  * Prefill stage 1 (chunk-local, fully parallel): for every 64-token chunk of
  * tokens [t0, t0 + n_tokens) build the log2-space decay cumsum, the Aqk / Akk
  * blocks, Ai = (I + Akk)^-1 and the WY factors, and write one record per chunk
- * into `workspace`. DK in {64, 128}; n_tokens a multiple of 64.
+ * into `workspace`. q, k, b, g are [B, s_alloc, HK, DK] (HK key heads; pass
+ * the head count of those tensors). DK in {64, 128}; n_tokens a multiple of 64.
  * Replaces: wy_stages kernels 1-5 in gdn2/forward.py:801-826
  * (cumsum, intra_diag, inter_blocks, solve, wy).
  */
 int gdn2_hip_chunk_local(const void* q, const void* k, const void* b, const float* g,
-                         int in_dtype, void* workspace, int B, int H, int DK, long s_alloc,
+                         int in_dtype, void* workspace, int B, int HK, int DK, long s_alloc,
                          long t0, long n_tokens, float scale, void* stream);
 
 /*
  * Prefill stage 2 (sequential over chunks, parallel over B*H*DV-tiles): the
  * state scan fused with the output; reads the stage-1 records and v, w.
  * state_in may be NULL (zero state) and may equal state_out. DV a multiple of 16.
+ * v, w, o and the state have H value heads; value head h reads the records of
+ * key head h / (H / HK).
  * Replaces: prefill_scan_kernel(...)(...) in gdn2/inference.py:544-550 and the
  * state_kernel + output_kernel pair in gdn2/forward.py:879-892.
  */
 int gdn2_hip_prefill_scan(const void* v, const void* w, int in_dtype, const void* workspace,
                           const float* state_in, float* state_out, void* o, int out_dtype, int B,
-                          int H, int DK, int DV, long s_alloc, long t0, long n_tokens,
+                          int H, int HK, int DK, int DV, long s_alloc, long t0, long n_tokens,
                           void* stream);
 
 /*
@@ -89,7 +97,7 @@ int gdn2_hip_prefill_scan(const void* v, const void* w, int in_dtype, const void
 int gdn2_hip_prefill_chunks(const void* q, const void* k, const void* v, const float* g,
                             const void* b, const void* w, int in_dtype, const float* state_in,
                             float* state_out, void* o, int out_dtype, void* workspace, int B,
-                            int H, int DK, int DV, long s_alloc, long t0, long n_tokens,
+                            int H, int HK, int DK, int DV, long s_alloc, long t0, long n_tokens,
                             float scale, void* stream);
 
 #ifdef __cplusplus

@@ -120,3 +120,28 @@ def test_gdn2_attention_and_chunk_fwd():
     assert torch.equal(o, o2)
     o16, _ = gdn2_attention(*dev)
     assert o16.dtype == torch.bfloat16 and o16.shape == (B, S, H, D)
+
+
+@pytest.mark.parametrize("DK,H,HK", [(128, 8, 4), (64, 6, 2), (128, 4, 1)])
+def test_grouped_heads_equal_repeated(DK, H, HK):
+    """q, k, b, g on HK key heads with v, w on H value heads must give exactly
+    what the reference's repeat_interleave expansion gives (attention.py:
+    295-297): prefill (whole chunks + ragged tail) and a following decode."""
+    from gdt2_tilelang_amd import gdn2_decode
+
+    print(f"grouped heads DK={DK} H={H} HK={HK}", flush=True)
+    B, S, n = 2, 200, 5
+    _, kd = device_inputs(B, S + n, HK, DK, DK, torch.bfloat16, decay_scale=1.0, seed=5)
+    _, vd = device_inputs(B, S + n, H, DK, DK, torch.bfloat16, decay_scale=1.0, seed=6)
+    q, k, _, g, b, _ = kd
+    v, w = vd[2], vd[5]
+    rep = H // HK
+    qe, ke, ge, be = (t.repeat_interleave(rep, dim=2) for t in (q, k, g, b))
+    s0 = seeded_state(B, H, DK, DK).cuda()
+    o1, s1 = gdn2_prefill(q[:, :S], k[:, :S], v[:, :S], g[:, :S], b[:, :S], w[:, :S], s0.clone(), config=F32)
+    o2, s2 = gdn2_prefill(qe[:, :S], ke[:, :S], v[:, :S], ge[:, :S], be[:, :S], w[:, :S], s0.clone(),
+                          config=F32)
+    d1 = gdn2_decode(q[:, S:], k[:, S:], v[:, S:], g[:, S:], b[:, S:], w[:, S:], s1)
+    d2 = gdn2_decode(qe[:, S:], ke[:, S:], v[:, S:], ge[:, S:], be[:, S:], w[:, S:], s2)
+    torch.cuda.synchronize()
+    assert torch.equal(o1, o2) and torch.equal(s1, s2) and torch.equal(d1, d2)

@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_status_strings():
     lib = _hip.lib()
-    assert lib.gdn2_hip_version() >= 1
+    assert lib.gdn2_hip_version() >= 2
     assert lib.gdn2_hip_status_string(0) == b"success"
     assert b"invalid argument" in lib.gdn2_hip_status_string(-1)
     assert b"unsupported shape" in lib.gdn2_hip_status_string(-2)
@@ -46,7 +46,7 @@ def test_version_and_status_strings():
 
 def test_workspace_size():
     lib = _hip.lib()
-    # one record per (b, h, 64-token chunk); 123392 bytes at DK=128, 73984 at DK=64
+    # one record per (b, key head, 64-token chunk); 123392 bytes at DK=128, 73984 at DK=64
     assert lib.gdn2_hip_prefill_workspace_bytes(2, 16, 128, 4096) == 2 * 16 * 64 * 123392
     assert lib.gdn2_hip_prefill_workspace_bytes(1, 2, 64, 100) == 1 * 2 * 2 * 73984
     assert lib.gdn2_hip_prefill_workspace_bytes(1, 2, 96, 64) == 0
@@ -57,20 +57,24 @@ def test_c_abi_rejects_bad_arguments_before_launch():
     lib = _hip.lib()
     nul = None
     fake = ctypes.c_void_p(16)   # never dereferenced: validation fails first
-    assert lib.gdn2_hip_decode(nul, nul, nul, nul, nul, nul, 1, nul, nul, 1, 1, 1, 128, 128, 1, 0, 1,
+    assert lib.gdn2_hip_decode(nul, nul, nul, nul, nul, nul, 1, nul, nul, 1, 1, 1, 1, 128, 128, 1, 0, 1,
                                0.1, nul) == -1
     args = [fake] * 6
-    assert lib.gdn2_hip_decode(*args, 7, fake, fake, 1, 1, 1, 128, 128, 1, 0, 1, 0.1, nul) == -1
-    assert lib.gdn2_hip_decode(*args, 1, fake, fake, 1, 1, 1, 100, 128, 1, 0, 1, 0.1, nul) == -2
-    assert lib.gdn2_hip_decode(*args, 1, fake, fake, 1, 1, 1, 128, 100, 1, 0, 1, 0.1, nul) == -2
-    assert lib.gdn2_hip_decode(*args, 1, fake, fake, 1, 1, 1, 128, 128, 4, 2, 3, 0.1, nul) == -1
+    assert lib.gdn2_hip_decode(*args, 7, fake, fake, 1, 1, 1, 1, 128, 128, 1, 0, 1, 0.1, nul) == -1
+    assert lib.gdn2_hip_decode(*args, 1, fake, fake, 1, 1, 1, 1, 100, 128, 1, 0, 1, 0.1, nul) == -2
+    assert lib.gdn2_hip_decode(*args, 1, fake, fake, 1, 1, 1, 1, 128, 100, 1, 0, 1, 0.1, nul) == -2
+    assert lib.gdn2_hip_decode(*args, 1, fake, fake, 1, 1, 1, 1, 128, 128, 4, 2, 3, 0.1, nul) == -1
+    # grouped heads: HK must divide H
+    assert lib.gdn2_hip_decode(*args, 1, fake, fake, 1, 1, 6, 4, 128, 128, 1, 0, 1, 0.1, nul) == -1
     assert lib.gdn2_hip_chunk_local(fake, fake, fake, fake, 1, fake, 1, 1, 128, 100, 0, 100, 0.1,
                                     nul) == -2
     assert lib.gdn2_hip_chunk_local(fake, fake, fake, fake, 1, fake, 1, 1, 32, 64, 0, 64, 0.1,
                                     nul) == -2
-    assert lib.gdn2_hip_prefill_scan(fake, fake, 1, fake, nul, fake, fake, 1, 1, 1, 128, 24, 64, 0,
+    assert lib.gdn2_hip_prefill_scan(fake, fake, 1, fake, nul, fake, fake, 1, 1, 1, 1, 128, 24, 64, 0,
                                      64, nul) == -2
-    assert lib.gdn2_hip_prefill_chunks(*args, 1, nul, fake, fake, 1, nul, 1, 1, 128, 128, 64, 0, 64,
+    assert lib.gdn2_hip_prefill_scan(fake, fake, 1, fake, nul, fake, fake, 1, 1, 4, 3, 128, 128, 64, 0,
+                                     64, nul) == -1
+    assert lib.gdn2_hip_prefill_chunks(*args, 1, nul, fake, fake, 1, nul, 1, 1, 1, 128, 128, 64, 0, 64,
                                        0.1, nul) == -1
 
 

@@ -24,10 +24,18 @@ REFERENCE_PARAM_NAMES = {
 
 @pytest.fixture
 def oracle_op(monkeypatch):
-    """Route the layer's op calls to the CPU oracle for host-logic tests."""
+    """Route the layer's op calls to the CPU oracle for host-logic tests. The
+    layer hands the op grouped key heads; the oracle (like the reference's op)
+    takes them repeated up to the value heads."""
+
+    def expand(q, k, v, g, b, w):
+        rep = v.shape[2] // q.shape[2]
+        q, k, g, b = (t.repeat_interleave(rep, dim=2) for t in (q, k, g, b))
+        return q, k, v, g, b, w
 
     def attention(q, k, v, g, b, w, scale=None, initial_state=None, output_final_state=False,
                   config=None, cu_seqlens=None):
+        q, k, v, g, b, w = expand(q, k, v, g, b, w)
         S = q.shape[1]
         pad = (-S) % 64
         if pad:
@@ -37,10 +45,10 @@ def oracle_op(monkeypatch):
         return o[:, :S], st
 
     def prefill(q, k, v, g, b, w, state=None, scale=None, config=None):
-        return oracle.prefill(q, k, v, g, b, w, state, scale)
+        return oracle.prefill(*expand(q, k, v, g, b, w), state, scale)
 
     def decode(q, k, v, g, b, w, state, scale=None):
-        return oracle.decode_loop(q, k, v, g, b, w, state, scale)
+        return oracle.decode_loop(*expand(q, k, v, g, b, w), state, scale)
 
     monkeypatch.setattr(attn_mod, "gdn2_attention", attention)
     monkeypatch.setattr(attn_mod, "gdn2_prefill", prefill)
