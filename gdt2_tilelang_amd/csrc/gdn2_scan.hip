@@ -149,6 +149,9 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
   __shared__ __align__(16) unsigned short sSh[2][DVT * SP], sSl[2][DVT * SP];
   __shared__ __align__(16) unsigned short sZh[2][DVT * TP], sZl[2][DVT * TP];
   __shared__ __align__(16) unsigned short sNh[DVT * TP], sNl[DVT * TP];
+  // output staging: one 16 x 16 tile per output wave, row-major, in OUT_DT
+  constexpr int OSZ = OUT_DT == DT_F32 ? 4 : 2;
+  __shared__ __align__(16) unsigned char sO[4][16 * 16 * OSZ];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -342,15 +345,27 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
       }
     }
     if (!un_role) {
+      // o tile (rows 16m + 4lq + e, columns 16nn + lr in D layout) -> LDS,
+      // then 16 contiguous bytes per lane to global memory
+      unsigned char* so = sO[m];
 #pragma unroll
       for (int nn = 0; nn < NT; ++nn) {
-        const int col = 16 * nn + lr;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const int t = 16 * m + 4 * lq + e;
-          const size_t oi = ((static_cast<size_t>(bi) * s_alloc + tok0 + t) * H + h) * DV + d0 + col;
-          store_elem(o, oi, OUT_DT, X[nn][e]);
+          const int idx = (4 * lq + e) * 16 + lr;
+          if constexpr (OUT_DT == DT_F32) reinterpret_cast<float*>(so)[idx] = X[nn][e];
+          else if constexpr (OUT_DT == DT_BF16) reinterpret_cast<unsigned short*>(so)[idx] = f32_to_bf16_bits(X[nn][e]);
+          else reinterpret_cast<unsigned short*>(so)[idx] = f32_to_f16_bits(X[nn][e]);
         }
+        __builtin_amdgcn_wave_barrier();
+        constexpr int LPR = 16 * OSZ / 16;          // lanes per 16-element row (2 or 4)
+        if (lane < 16 * LPR) {
+          const int r = lane / LPR, c = (lane % LPR) * (16 / OSZ);
+          const uint4 x = *reinterpret_cast<const uint4*>(so + (r * 16 + c) * OSZ);
+          const size_t oi = ((static_cast<size_t>(bi) * s_alloc + tok0 + 16 * m + r) * H + h) * DV + d0 + 16 * nn + c;
+          *reinterpret_cast<uint4*>(static_cast<unsigned char*>(o) + oi * OSZ) = x;
+        }
+        __builtin_amdgcn_wave_barrier();
       }
     }
     put_state(buf ^ 1);
