@@ -24,8 +24,9 @@
 //    exactly with 2^(G_r - G_s) on the VALU.
 //
 // Precision (bf16 MFMA, fp32 accumulate): Aqk, Akk and W use hi+lo split
-// operands (three MFMAs each); the solve is fp32. W, Qg, KG and Aqk are
-// exported as hi/lo pairs, Ai as bf16.
+// operands (three MFMAs each); the solve is fp32. The record holds fp16 values
+// with a power-of-two scale per matrix (layout header), from the chunk maxima
+// of |q|, |k|, |b k| and |Ai|.
 //
 // This kernel serves DK = 64; DK = 128 runs gdn2_chunk_local2.hip.
 #include "gdn2_common.h"
@@ -67,7 +68,8 @@ struct ChunkSmem {
   static constexpr size_t T_OFF = AI_OFF + 64 * AP * 4;              // solve scratch [3][16][17]
   static constexpr size_t REF_OFF = T_OFF + 3 * 16 * 17 * 4;         // [4][DK] per-block reference
   static constexpr size_t TOT_OFF = REF_OFF + 4 * DK * 4;            // cumsum partials [4][DK]
-  static constexpr size_t BYTES = TOT_OFF + 4 * DK * 4;
+  static constexpr size_t MAX_OFF = TOT_OFF + 4 * DK * 4;            // per-wave maxima [4][4]
+  static constexpr size_t BYTES = MAX_OFF + 4 * 4 * 4;
 };
 
 template <int DK, int IN_DT>
@@ -92,6 +94,7 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
   float* sT = reinterpret_cast<float*>(smem + M::T_OFF);
   float* sRef = reinterpret_cast<float*>(smem + M::REF_OFF);
   float* sTot = reinterpret_cast<float*>(smem + M::TOT_OFF);
+  float* sMax = reinterpret_cast<float*>(smem + M::MAX_OFF);
   float* sWf = sK;                                                   // phase D, [64][GP] fp32
 
   const int tid = threadIdx.x;
@@ -144,7 +147,31 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
     dst[0] = make_float4(kv[kk][0], kv[kk][1], kv[kk][2], kv[kk][3]);
     dst[1] = make_float4(kv[kk][4], kv[kk][5], kv[kk][6], kv[kk][7]);
   }
+  {   // chunk maxima of |q|, |k|, |b k| for the fp16 record scales
+    float mq = 0.f, mk = 0.f, mbk = 0.f;
+#pragma unroll
+    for (int kk = 0; kk < KT; ++kk)
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
+        mq = fmaxf(mq, fabsf(qv[kk][j]));
+        mk = fmaxf(mk, fabsf(kv[kk][j]));
+        mbk = fmaxf(mbk, fabsf(bv[kk][j] * kv[kk][j]));
+      }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) {
+      mq = fmaxf(mq, __shfl_xor(mq, off));
+      mk = fmaxf(mk, __shfl_xor(mk, off));
+      mbk = fmaxf(mbk, __shfl_xor(mbk, off));
+    }
+    if (lane == 0) { sMax[4 * wave] = mq; sMax[4 * wave + 1] = mk; sMax[4 * wave + 2] = mbk; }
+  }
   __syncthreads();
+  const float maxq = fmaxf(fmaxf(sMax[0], sMax[4]), fmaxf(sMax[8], sMax[12]));
+  const float maxk = fmaxf(fmaxf(sMax[1], sMax[5]), fmaxf(sMax[9], sMax[13]));
+  const float maxbk = fmaxf(fmaxf(sMax[2], sMax[6]), fmaxf(sMax[10], sMax[14]));
+  const float sc_q = fp16_range_scale(scale * maxq);                 // |Qg| <= scale max|q|
+  const float sc_k = fp16_range_scale(maxk);                         // |KG| <= max|k|
+  const float sc_aqk = fp16_range_scale(scale * DK * maxq * maxk);   // |Aqk| <= scale DK max|q||k|
 
   // ---- phase A.3: per-block references and the fast/exact decision -------
   bool unsafe = false;
@@ -201,10 +228,7 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
       const int t = 32 * kk + 8 * lq + j;
       x[j] = sK[t * GP + c] * fast_exp2(Gl - sG[t * GP + c]);
     }
-    bf16x8 hi, lo;
-    split_bf16x8(x, hi, lo);
-    *reinterpret_cast<bf16x8*>(rec + L::kt_frag(m, kk, 0) + lane * 8) = hi;
-    *reinterpret_cast<bf16x8*>(rec + L::kt_frag(m, kk, 1) + lane * 8) = lo;
+    *reinterpret_cast<uint4*>(rec + L::kt_frag(m, kk) + lane * 8) = pack_f16x8(x, 1.f / sc_k);
   }
 
   // ---- phase B: Aqk / Akk 16x16 blocks, row block i = wave ----------------
@@ -324,20 +348,25 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
   }
 
   // ---- phase D: W = Ai E (split operands); Ai fragments out --------------
-  bf16x8 aih[2], ail[2], aqk_hi[2], aqk_lo[2];
+  {   // max |Ai| over the whole matrix (each thread scans 16 entries)
+    float m = 0.f;
+    for (int e = tid; e < 64 * 64; e += 256) m = fmaxf(m, fabsf(sAI[(e >> 6) * AP + (e & 63)]));
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) m = fmaxf(m, __shfl_xor(m, off));
+    if (lane == 0) sMax[4 * wave + 3] = m;
+  }
+  bf16x8 aih[2], ail[2];
+  float aiw[2][8];
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk) {
     const int s0 = 32 * kk + 8 * lq;
     float x[8];
 #pragma unroll
-    for (int j = 0; j < 8; ++j) x[j] = sAI[my_r * AP + s0 + j];
+    for (int j = 0; j < 8; ++j) x[j] = aiw[kk][j] = sAI[my_r * AP + s0 + j];
     split_bf16x8(x, aih[kk], ail[kk]);
-    *reinterpret_cast<bf16x8*>(rec + L::ai_frag(wave, kk) + lane * 8) = aih[kk];
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] = sA1[my_r * AP + s0 + j];
-    split_bf16x8(x, aqk_hi[kk], aqk_lo[kk]);
-    *reinterpret_cast<bf16x8*>(rec + L::aqk_frag(wave, kk, 0) + lane * 8) = aqk_hi[kk];
-    *reinterpret_cast<bf16x8*>(rec + L::aqk_frag(wave, kk, 1) + lane * 8) = aqk_lo[kk];
+    *reinterpret_cast<uint4*>(rec + L::aqk_frag(wave, kk) + lane * 8) = pack_f16x8(x, 1.f / sc_aqk);
   }
 #pragma unroll
   for (int nn = 0; nn < MT; ++nn) {
@@ -353,23 +382,30 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
     for (int e = 0; e < 4; ++e) sWf[(16 * wave + 4 * lq + e) * GP + c] = acc[e];
   }
   __syncthreads();
+  const float mai = fmaxf(fmaxf(sMax[3], sMax[7]), fmaxf(sMax[11], sMax[15]));
+  const float sc_ai = fp16_range_scale(mai);
+  const float sc_w = fp16_range_scale(64.f * mai * maxbk);   // |W| <= 64 max|Ai| max|b k|
+#pragma unroll
+  for (int kk = 0; kk < 2; ++kk)
+    *reinterpret_cast<uint4*>(rec + L::ai_frag(wave, kk) + lane * 8) = pack_f16x8(aiw[kk], 1.f / sc_ai);
 #pragma unroll
   for (int kk = 0; kk < KT; ++kk) {
     float x[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) x[j] = sWf[my_r * GP + 32 * kk + 8 * lq + j];
-    bf16x8 hi, lo;
-    split_bf16x8(x, hi, lo);
-    *reinterpret_cast<bf16x8*>(rec + L::w_frag(wave, kk, 0) + lane * 8) = hi;
-    *reinterpret_cast<bf16x8*>(rec + L::w_frag(wave, kk, 1) + lane * 8) = lo;
+    *reinterpret_cast<uint4*>(rec + L::w_frag(wave, kk) + lane * 8) = pack_f16x8(x, 1.f / sc_w);
   }
   // Qg = scale * q * gamma, row block `wave`
 #pragma unroll
-  for (int kk = 0; kk < KT; ++kk) {
-    bf16x8 hi, lo;
-    split_bf16x8(qg[kk], hi, lo);
-    *reinterpret_cast<bf16x8*>(rec + L::qg_frag(wave, kk, 0) + lane * 8) = hi;
-    *reinterpret_cast<bf16x8*>(rec + L::qg_frag(wave, kk, 1) + lane * 8) = lo;
+  for (int kk = 0; kk < KT; ++kk)
+    *reinterpret_cast<uint4*>(rec + L::qg_frag(wave, kk) + lane * 8) = pack_f16x8(qg[kk], 1.f / sc_q);
+  if (tid == 0) {
+    float* sc = reinterpret_cast<float*>(rec + L::SC_OFF);
+    sc[SC_W] = sc_w;
+    sc[SC_QG] = sc_q;
+    sc[SC_AI] = sc_ai;
+    sc[SC_KT] = sc_k;
+    sc[SC_AQK] = sc_aqk;
   }
 }
 

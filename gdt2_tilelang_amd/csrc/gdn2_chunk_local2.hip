@@ -25,9 +25,13 @@
 //  C  Ai = (I + Akk)^-1: 16x16 diagonal inverses by forward substitution (one
 //     lane per column), then the off-diagonal blocks by sub-diagonal with
 //     split-bf16 MFMA: X_ij = -X_ii sum_k A_ik X_kj.
-//  D  W = Ai E for the wave's channels (split operands, exported hi + lo).
-//  E  Aqk fragments of row block w (hi + lo). Qg = scale q 2^G is exported in
-//     phase A straight from the lanes that formed it.
+//  D  W = Ai E for the wave's channels (split operands).
+//  E  Aqk fragments of row block w. Qg = scale q 2^G is exported in phase A
+//     straight from the lanes that formed it.
+//
+// Records are fp16 with a power-of-two scale per matrix (layout header): the
+// scales come from the chunk maxima of |q|, |k|, |b k| (phase A) and of |Ai|
+// (phase D, which every wave reads whole).
 //
 // LDS: a 40 KiB shared region (partial-product slabs, then Aqk / Akk / X
 // tiles) and a 9.5 KiB private region per wave for its transposes: < 80 KiB,
@@ -61,6 +65,9 @@ constexpr int SLAB_OFF = AKK_OFF;                   // 12800
 constexpr int SREF_OFF = SLAB_OFF + SLAB_BYTES;     // ref fp32 [wave][4 i][32 c]     2 KiB
 constexpr int SDIAG_OFF = SREF_OFF + 2048;          // exact diag [wave][16][16]      4 KiB
 static_assert(SDIAG_OFF + 4096 <= S_BYTES, "phase B scratch exceeds the shared region");
+// phase A: per-wave maxima of |q|, |k|, |b k| (fp16 record scales)
+constexpr int SMAX_OFF = SDIAG_OFF + 4096;
+static_assert(SMAX_OFF + 64 <= S_BYTES, "max slots exceed the shared region");
 // phase A: each wave stages its KG^T slice [32 c][64 t] fp32 at wave * 8 KiB
 constexpr int SKGT_OFF = 0;
 static_assert(SKGT_OFF + 4 * 8192 <= SREF_OFF, "KG^T staging overlaps the references");
@@ -123,10 +130,6 @@ struct Raw8 {
   }
 };
 
-__device__ __forceinline__ void st_frag(unsigned short* p, const bf16x8& x) {
-  *reinterpret_cast<bf16x8*>(p) = x;
-}
-
 __device__ __forceinline__ void ld8(const float* p, float* x) {
   const float4 a = reinterpret_cast<const float4*>(p)[0];
   const float4 b = reinterpret_cast<const float4*>(p)[1];
@@ -173,6 +176,8 @@ __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
   Raw8<IN_DT> kr[4], br[4];           // k, b of rows 16i + lr (storage format)
   bf16x8 aqh[4], aql[4];              // Aqk row operands, row block i
   bool exact;
+  float maxq, maxk, maxbk;            // chunk maxima of |q|, |k|, |b k| (record scales)
+  float sc_q, sc_k, sc_aqk;           // fp16 scales of Qg, KG^T, Aqk
   {
     // ---- A.1 loads: rows 16i + lr, channels c0..c0+7 -----------------------
     Raw8<IN_DT> qr[4];
@@ -183,6 +188,28 @@ __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
       qr[i].load(qp, idx);
       kr[i].load(kp, idx);
       br[i].load(bp, idx);
+    }
+
+    {   // chunk maxima of |q|, |k|, |b k| -> LDS, combined after the A.3 barrier
+      float mq = 0.f, mk = 0.f, mbk = 0.f;
+#pragma unroll
+      for (int i = 0; i < 4; ++i)
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          mq = fmaxf(mq, fabsf(qr[i][j]));
+          mk = fmaxf(mk, fabsf(kr[i][j]));
+          mbk = fmaxf(mbk, fabsf(br[i][j] * kr[i][j]));
+        }
+#pragma unroll
+      for (int off = 1; off < 64; off <<= 1) {
+        mq = fmaxf(mq, __shfl_xor(mq, off));
+        mk = fmaxf(mk, __shfl_xor(mk, off));
+        mbk = fmaxf(mbk, __shfl_xor(mbk, off));
+      }
+      if (lane == 0) {
+        float* sm = reinterpret_cast<float*>(smem + SMAX_OFF) + 4 * wave;
+        sm[0] = mq; sm[1] = mk; sm[2] = mbk;
+      }
     }
 
     // ---- A.2 cumsum over the 64 rows in log2 units: DPP prefix per 16-lane
@@ -228,6 +255,21 @@ __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
         sref[i * CPW + 8 * lq + j] = 0.5f * (first[i][j] + last);
       }
     exact = __syncthreads_or(unsafe) != 0;
+    {
+      const float* sm = reinterpret_cast<const float*>(smem + SMAX_OFF);
+      maxq = fmaxf(fmaxf(sm[0], sm[4]), fmaxf(sm[8], sm[12]));
+      maxk = fmaxf(fmaxf(sm[1], sm[5]), fmaxf(sm[9], sm[13]));
+      maxbk = fmaxf(fmaxf(sm[2], sm[6]), fmaxf(sm[10], sm[14]));
+      sc_q = fp16_range_scale(scale * maxq);               // |Qg| <= scale max|q|
+      sc_k = fp16_range_scale(maxk);                       // |KG| <= max|k|
+      sc_aqk = fp16_range_scale(scale * DK * maxq * maxk); // |Aqk| <= scale DK max|q| max|k|
+      if (tid == 0) {
+        float* sc = reinterpret_cast<float*>(rec + L::SC_OFF);
+        sc[SC_QG] = sc_q;
+        sc[SC_KT] = sc_k;
+        sc[SC_AQK] = sc_aqk;
+      }
+    }
     if (exact) {
 #pragma unroll
       for (int i = 0; i < 4; ++i)
@@ -263,12 +305,8 @@ __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
         etl[a0] = static_cast<unsigned short>(lo);
         etl[a1] = static_cast<unsigned short>(lo >> 16);
       }
-      {   // Qg fragment (row block i, k step = this wave's channels)
-        bf16x8 hi, lo;
-        split_bf16x8(qg, hi, lo);
-        st_frag(rec + L::qg_frag(i, wave, 0) + lane * 8, hi);
-        st_frag(rec + L::qg_frag(i, wave, 1) + lane * 8, lo);
-      }
+      // Qg fragment (row block i, k step = this wave's channels)
+      *reinterpret_cast<uint4*>(rec + L::qg_frag(i, wave) + lane * 8) = pack_f16x8(qg, 1.f / sc_q);
       split_bf16x8(xq, aqh[i], aql[i]);
     }
     // KG^T fragments m = 2w, 2w+1 (rows = channels), k = t
@@ -278,10 +316,7 @@ __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
       for (int kk = 0; kk < 2; ++kk) {
         float x[8];
         ld8(&kgt[(16 * mm + lr) * 64 + 32 * kk + 8 * lq], x);
-        bf16x8 hi, lo;
-        split_bf16x8(x, hi, lo);
-        st_frag(rec + L::kt_frag(2 * wave + mm, kk, 0) + lane * 8, hi);
-        st_frag(rec + L::kt_frag(2 * wave + mm, kk, 1) + lane * 8, lo);
+        *reinterpret_cast<uint4*>(rec + L::kt_frag(2 * wave + mm, kk) + lane * 8) = pack_f16x8(x, 1.f / sc_k);
       }
     if (lr == 0) {
       float* gl = reinterpret_cast<float*>(rec + L::GL_OFF) + c0;
@@ -483,6 +518,8 @@ __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
   {
     const int half = lq & 1;
     bf16x8 aifh[4][2], aifl[4][2];
+    float xw[2][8];                 // this wave's row block of Ai, for the record
+    float mai = 0.f;                // max |Ai| (every wave reads all of Ai)
 #pragma unroll
     for (int m = 0; m < 4; ++m)
 #pragma unroll
@@ -490,11 +527,25 @@ __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
         const int kt = 2 * kk + (lq >> 1);
         float x[8];
 #pragma unroll
-        for (int jj = 0; jj < 8; ++jj)
+        for (int jj = 0; jj < 8; ++jj) {
           x[jj] = (kt <= m) ? sXT[pair_idx(m, kt) * TF + (8 * half + jj) * TP + lr] : 0.f;
+          mai = fmaxf(mai, fabsf(x[jj]));
+          if (m == wave) xw[kk][jj] = x[jj];
+        }
         split_bf16x8(x, aifh[m][kk], aifl[m][kk]);
-        if (m == wave) st_frag(rec + L::ai_frag(m, kk) + lane * 8, aifh[m][kk]);
       }
+#pragma unroll
+    for (int off = 1; off < 64; off <<= 1) mai = fmaxf(mai, __shfl_xor(mai, off));
+    const float sc_ai = fp16_range_scale(mai);
+    const float sc_w = fp16_range_scale(64.f * mai * maxbk);   // |W| <= 64 max|Ai| max|b k|
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk)
+      *reinterpret_cast<uint4*>(rec + L::ai_frag(wave, kk) + lane * 8) = pack_f16x8(xw[kk], 1.f / sc_ai);
+    if (tid == 0) {
+      float* sc = reinterpret_cast<float*>(rec + L::SC_OFF);
+      sc[SC_W] = sc_w;
+      sc[SC_AI] = sc_ai;
+    }
     bf16x8 ebh[2][2], ebl[2][2];
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
@@ -524,14 +575,11 @@ __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
     for (int m = 0; m < 4; ++m) {
       float x[8];
       ld8(&wsg[(16 * m + lr) * 36 + 8 * lq], x);
-      bf16x8 hi, lo;
-      split_bf16x8(x, hi, lo);
-      st_frag(rec + L::w_frag(m, wave, 0) + lane * 8, hi);
-      st_frag(rec + L::w_frag(m, wave, 1) + lane * 8, lo);
+      *reinterpret_cast<uint4*>(rec + L::w_frag(m, wave) + lane * 8) = pack_f16x8(x, 1.f / sc_w);
     }
   }
 
-  // ---- E: Aqk fragments of row block `wave` (hi / lo) -------------------------
+  // ---- E: Aqk fragments of row block `wave` ---------------------------------
   {
     const int half = lq & 1;
 #pragma unroll
@@ -543,10 +591,7 @@ __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
 #pragma unroll
         for (int jj = 0; jj < 8; ++jj) a[jj] = 0.f;
       }
-      bf16x8 hi, lo;
-      split_bf16x8(a, hi, lo);
-      st_frag(rec + L::aqk_frag(wave, kk, 0) + lane * 8, hi);
-      st_frag(rec + L::aqk_frag(wave, kk, 1) + lane * 8, lo);
+      *reinterpret_cast<uint4*>(rec + L::aqk_frag(wave, kk) + lane * 8) = pack_f16x8(a, 1.f / sc_aqk);
     }
   }
 }

@@ -112,6 +112,48 @@ __device__ __forceinline__ f32x4 mfma3(const bf16x8& ah, const bf16x8& al, const
 
 __device__ __forceinline__ f32x4 zero4() { return f32x4{0.f, 0.f, 0.f, 0.f}; }
 
+// ---- fp16 record fragments ---------------------------------------------------
+
+// Power-of-two scaling for fp16 storage: returns 2^e, e >= 0 the smallest with
+// bound / 2^e < 2^15 (fp16 holds up to 65504). NaN / inf bounds give 2^100.
+__device__ __forceinline__ float fp16_range_scale(float bound) {
+  const uint32_t u = __float_as_uint(fabsf(bound));
+  const int expo = static_cast<int>(u >> 23) - 127;              // floor(log2) for normals
+  int e = expo - 14;
+  e = e < 0 ? 0 : (e > 100 ? 100 : e);
+  if (!(bound == bound)) e = 100;
+  return __uint_as_float(static_cast<uint32_t>(127 + e) << 23);
+}
+
+// Eight floats times `inv` -> eight fp16 (round to nearest even), packed.
+__device__ __forceinline__ uint4 pack_f16x8(const float* x, float inv) {
+  uint32_t r[4];
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const unsigned short a = __builtin_bit_cast(unsigned short, static_cast<_Float16>(x[2 * j] * inv));
+    const unsigned short b = __builtin_bit_cast(unsigned short, static_cast<_Float16>(x[2 * j + 1] * inv));
+    r[j] = static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16);
+  }
+  return make_uint4(r[0], r[1], r[2], r[3]);
+}
+
+// Eight packed fp16 -> exact bf16 hi + lo (hi keeps the top 8 significant bits,
+// lo the remaining 3, both representable in bf16).
+__device__ __forceinline__ void f16x8_to_bf16_hilo(const uint4& raw, bf16x8& hi, bf16x8& lo) {
+  const uint32_t w[4] = {raw.x, raw.y, raw.z, raw.w};
+  u32x4 h, l;
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    const float a = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(w[j] & 0xffffu)));
+    const float b = static_cast<float>(__builtin_bit_cast(_Float16, static_cast<unsigned short>(w[j] >> 16)));
+    const uint32_t ah = __float_as_uint(a) & 0xffff0000u, bh = __float_as_uint(b) & 0xffff0000u;
+    h[j] = (ah >> 16) | bh;
+    l[j] = cvt_pk_bf16(a - __uint_as_float(ah), b - __uint_as_float(bh));
+  }
+  hi = __builtin_bit_cast(bf16x8, h);
+  lo = __builtin_bit_cast(bf16x8, l);
+}
+
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
 
 }  // namespace gdn2

@@ -1,16 +1,20 @@
 // Workspace layout shared by the chunk-local kernel (producer) and the state
 // scan kernel (consumer) of the GDN-2 prefill.
 //
-// One record per chunk of 64 tokens, record index ch = (b*H + h)*NC + n.
-// Every matrix is stored as MFMA A-operand fragments (see gdn2_common.h) so the
-// scan loads each one with a single coalesced 16-byte access per lane:
+// One record per chunk of 64 tokens, record index ch = (b*HK + hk)*NC + n.
+// Every matrix is stored as fp16 MFMA A-operand fragments (see gdn2_common.h):
+// 64 lanes x 8 values = 1 KiB, loaded with one coalesced 16-byte access per
+// lane and expanded in registers to an exact bf16 hi + lo pair (11 significant
+// bits fit in 8 + 8). Each matrix carries a power-of-two scale so that its
+// stored values stay within fp16 range for any input:
 //
-//   W   [4 m][DK/32 kk][hi,lo]   bf16 x2   W   = Ai (b*k*gamma)            64 x DK
-//   QG  [4 m][DK/32 kk][hi,lo]   bf16 x2   Qg  = scale*q*gamma             64 x DK
-//   AI  [4 m][2 kk]              bf16      Ai  = (I + Akk)^-1               64 x 64
-//   KT  [DK/16 m][2 kk][hi,lo]   bf16 x2   KG^T, KG = k*gamma_last/gamma   DK x 64
-//   AQK [4 m][2 kk][hi,lo]       bf16 x2   Aqk (scale and diagonal in)     64 x 64
-//   GL  [DK]                     fp32      gamma_last = exp(G_last)
+//   W   [4 m][DK/32 kk]   fp16   W   = Ai (b*k*gamma)      / SC[0]   64 x DK
+//   QG  [4 m][DK/32 kk]   fp16   Qg  = scale*q*gamma       / SC[1]   64 x DK
+//   AI  [4 m][2 kk]       fp16   Ai  = (I + Akk)^-1        / SC[2]   64 x 64
+//   KT  [DK/16 m][2 kk]   fp16   KG^T, KG = k*gamma_last/gamma / SC[3]  DK x 64
+//   AQK [4 m][2 kk]       fp16   Aqk (scale, diagonal in)  / SC[4]   64 x 64
+//   GL  [DK]              fp32   gamma_last = exp(G_last)
+//   SC  [8]               fp32   the five multipliers (powers of two) above
 //
 // W, QG and AI are what the scan's first phase reads (U = Ai Z, W S, Qg S),
 // KT, AQK and GL what its second phase reads (KG^T Un, Aqk Un).
@@ -22,25 +26,28 @@ namespace gdn2 {
 
 constexpr int kBS = 64;   // chunk length
 constexpr int kBC = 16;   // sub-chunk (MFMA tile) length
-constexpr int kFrag = 64 * 8;  // bf16 elements per fragment
+constexpr int kFrag = 64 * 8;  // 16-bit elements per fragment
+
+enum RecordScale : int { SC_W = 0, SC_QG = 1, SC_AI = 2, SC_KT = 3, SC_AQK = 4 };
 
 template <int DK>
 struct ChunkLayout {
   static constexpr int KT = DK / 32;   // 32-wide k steps over the key dim
   static constexpr int MT = DK / 16;   // 16-row tiles over the key dim
-  static constexpr long W_OFF = 0;
-  static constexpr long QG_OFF = W_OFF + 4L * KT * 2 * kFrag;
-  static constexpr long AI_OFF = QG_OFF + 4L * KT * 2 * kFrag;
+  static constexpr long W_OFF = 0;     // offsets in 16-bit slots
+  static constexpr long QG_OFF = W_OFF + 4L * KT * kFrag;
+  static constexpr long AI_OFF = QG_OFF + 4L * KT * kFrag;
   static constexpr long KT_OFF = AI_OFF + 4L * 2 * kFrag;
-  static constexpr long AQK_OFF = KT_OFF + static_cast<long>(MT) * 2 * 2 * kFrag;
-  static constexpr long GL_OFF = AQK_OFF + 4L * 2 * 2 * kFrag;  // in bf16 slots
-  static constexpr long STRIDE = GL_OFF + 2L * DK;               // bf16 elements per record
+  static constexpr long AQK_OFF = KT_OFF + static_cast<long>(MT) * 2 * kFrag;
+  static constexpr long GL_OFF = AQK_OFF + 4L * 2 * kFrag;
+  static constexpr long SC_OFF = GL_OFF + 2L * DK;
+  static constexpr long STRIDE = ((SC_OFF + 2L * 8) + 127) / 128 * 128;   // 256-byte records
 
-  __host__ __device__ static constexpr long w_frag(int m, int kk, int hl) { return W_OFF + ((m * KT + kk) * 2 + hl) * kFrag; }
-  __host__ __device__ static constexpr long qg_frag(int m, int kk, int hl) { return QG_OFF + ((m * KT + kk) * 2 + hl) * kFrag; }
-  __host__ __device__ static constexpr long kt_frag(int m, int kk, int hl) { return KT_OFF + ((m * 2 + kk) * 2 + hl) * kFrag; }
-  __host__ __device__ static constexpr long aqk_frag(int m, int kk, int hl) { return AQK_OFF + ((m * 2 + kk) * 2 + hl) * kFrag; }
+  __host__ __device__ static constexpr long w_frag(int m, int kk) { return W_OFF + (m * KT + kk) * kFrag; }
+  __host__ __device__ static constexpr long qg_frag(int m, int kk) { return QG_OFF + (m * KT + kk) * kFrag; }
   __host__ __device__ static constexpr long ai_frag(int m, int kk) { return AI_OFF + (m * 2 + kk) * kFrag; }
+  __host__ __device__ static constexpr long kt_frag(int m, int kk) { return KT_OFF + (m * 2 + kk) * kFrag; }
+  __host__ __device__ static constexpr long aqk_frag(int m, int kk) { return AQK_OFF + (m * 2 + kk) * kFrag; }
 };
 
 static_assert((ChunkLayout<128>::STRIDE * 2) % 256 == 0, "record must keep 256-byte alignment");

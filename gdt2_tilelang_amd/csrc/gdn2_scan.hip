@@ -11,9 +11,10 @@
 //   o  = Qg S + Aqk Un                     (Qg = scale * q * gamma)
 //   S  = diag(gamma_last) S + KG^T Un
 //
-// Operands that carry the result's precision are split into bf16 hi + lo
-// (Z, S, Un and the W, Qg, Aqk, KG records) so those products keep ~16
-// mantissa bits; Ai Z uses bf16 Ai. W S needs the split on both sides: with
+// Every product splits both operands into bf16 hi + lo (three MFMAs), so it
+// keeps ~16 mantissa bits. Z, S and Un are split from fp32; the record
+// matrices are stored as fp16 with a power-of-two scale per matrix and split
+// exactly (an fp16 significand is 11 bits). W S needs the precision: with
 // little decay the state is large and Un = U - W S is a small difference of
 // large terms.
 //
@@ -38,17 +39,24 @@ namespace gdn2 {
 constexpr int kScanWaves = 8;
 constexpr int kScanThreads = 64 * kScanWaves;
 
-// Record fragments one wave holds for a chunk. Waves 0-3 ("Un" role) use
-// a1 = Ai and x = W; waves 4-7 ("output" role) use x = Qg and a1/a2 = Aqk
-// hi/lo. Every wave holds the KG^T fragments and gamma_last of its state tile.
+// Record fragments one wave holds for a chunk, as raw fp16 (8 per lane) with
+// the record's power-of-two scale of each matrix. Waves 0-3 ("Un" role) use
+// a = Ai and x = W; waves 4-7 ("output" role) use a = Aqk and x = Qg. Every
+// wave holds the KG^T fragments, their scale and gamma_last of its state tile.
 template <int DK>
 struct ScanFrags {
   static constexpr int KT = DK / 32;
-  bf16x8 a1[2], a2[2];
-  bf16x8 xh[KT], xl[KT];
-  bf16x8 kh[2], kl[2];
+  uint4 a[2];
+  uint4 x[KT];
+  uint4 k[2];
+  float sa, sx, sk;
   float4 gam;
 };
+
+template <int DK>
+__device__ __forceinline__ float rec_scale(const unsigned short* __restrict__ rec, int which) {
+  return reinterpret_cast<const float*>(rec + ChunkLayout<DK>::SC_OFF)[which];
+}
 
 // Fragments of the output / Un phase of a chunk (output row block m = wave & 3).
 template <int DK>
@@ -58,26 +66,15 @@ __device__ __forceinline__ void load_frags_p1(const unsigned short* __restrict__
   constexpr int KT = DK / 32;
   const int o8 = lane * 8;
   const int m = wave & 3;
-  if (wave < 4) {
+  const bool un = wave < 4;
 #pragma unroll
-    for (int kk = 0; kk < 2; ++kk) f.a1[kk] = *reinterpret_cast<const bf16x8*>(rec + L::ai_frag(m, kk) + o8);
+  for (int kk = 0; kk < 2; ++kk)
+    f.a[kk] = *reinterpret_cast<const uint4*>(rec + (un ? L::ai_frag(m, kk) : L::aqk_frag(m, kk)) + o8);
 #pragma unroll
-    for (int kk = 0; kk < KT; ++kk) {
-      f.xh[kk] = *reinterpret_cast<const bf16x8*>(rec + L::w_frag(m, kk, 0) + o8);
-      f.xl[kk] = *reinterpret_cast<const bf16x8*>(rec + L::w_frag(m, kk, 1) + o8);
-    }
-  } else {
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      f.a1[kk] = *reinterpret_cast<const bf16x8*>(rec + L::aqk_frag(m, kk, 0) + o8);
-      f.a2[kk] = *reinterpret_cast<const bf16x8*>(rec + L::aqk_frag(m, kk, 1) + o8);
-    }
-#pragma unroll
-    for (int kk = 0; kk < KT; ++kk) {
-      f.xh[kk] = *reinterpret_cast<const bf16x8*>(rec + L::qg_frag(m, kk, 0) + o8);
-      f.xl[kk] = *reinterpret_cast<const bf16x8*>(rec + L::qg_frag(m, kk, 1) + o8);
-    }
-  }
+  for (int kk = 0; kk < KT; ++kk)
+    f.x[kk] = *reinterpret_cast<const uint4*>(rec + (un ? L::w_frag(m, kk) : L::qg_frag(m, kk)) + o8);
+  f.sa = rec_scale<DK>(rec, un ? SC_AI : SC_AQK);
+  f.sx = rec_scale<DK>(rec, un ? SC_W : SC_QG);
 }
 
 // Fragments of the state-update phase (state tile wave, when DK/16 > wave).
@@ -88,10 +85,8 @@ __device__ __forceinline__ void load_frags_p2(const unsigned short* __restrict__
   if (wave >= DK / 16) return;
   const int o8 = lane * 8;
 #pragma unroll
-  for (int kk = 0; kk < 2; ++kk) {
-    f.kh[kk] = *reinterpret_cast<const bf16x8*>(rec + L::kt_frag(wave, kk, 0) + o8);
-    f.kl[kk] = *reinterpret_cast<const bf16x8*>(rec + L::kt_frag(wave, kk, 1) + o8);
-  }
+  for (int kk = 0; kk < 2; ++kk) f.k[kk] = *reinterpret_cast<const uint4*>(rec + L::kt_frag(wave, kk) + o8);
+  f.sk = rec_scale<DK>(rec, SC_KT);
   f.gam = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(rec + L::GL_OFF) + 16 * wave + 4 * lq);
 }
 
@@ -263,7 +258,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
 
   const int o8 = lane * 8;
   auto frag = [&](const unsigned short* rec, long off) {
-    return *reinterpret_cast<const bf16x8*>(rec + off + o8);
+    return *reinterpret_cast<const uint4*>(rec + off + o8);
   };
 
   auto step = [&](auto parity, ScanFrags<DK>& cur, int nc) {
@@ -277,37 +272,42 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
     f32x4 A[NT], X[NT];
 #pragma unroll
     for (int nn = 0; nn < NT; ++nn) { A[nn] = zero4(); X[nn] = zero4(); }
+    const float sa = cur.sa, sx = cur.sx;
     if (un_role) {
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
+        bf16x8 ah, al;
+        f16x8_to_bf16_hilo(cur.a[kk], ah, al);
+        cur.a[kk] = frag(rp, L::ai_frag(m, kk));
 #pragma unroll
         for (int nn = 0; nn < NT; ++nn) {
           const int col = 16 * nn + lr;
           const bf16x8 zh = *reinterpret_cast<const bf16x8*>(&sZh[buf][col * TP + 32 * kk + 8 * lq]);
           const bf16x8 zl = *reinterpret_cast<const bf16x8*>(&sZl[buf][col * TP + 32 * kk + 8 * lq]);
-          A[nn] = mfma(cur.a1[kk], zh, A[nn]);
-          A[nn] = mfma(cur.a1[kk], zl, A[nn]);
+          A[nn] = mfma3(ah, al, zh, zl, A[nn]);
         }
-        cur.a1[kk] = frag(rp, L::ai_frag(m, kk));
       }
     }
 #pragma unroll
     for (int kk = 0; kk < KT; ++kk) {
+      bf16x8 xh, xl;
+      f16x8_to_bf16_hilo(cur.x[kk], xh, xl);
+      cur.x[kk] = frag(rp, un_role ? L::w_frag(m, kk) : L::qg_frag(m, kk));
 #pragma unroll
       for (int nn = 0; nn < NT; ++nn) {
         const int col = 16 * nn + lr;
         const bf16x8 sh = *reinterpret_cast<const bf16x8*>(&sSh[buf][col * SP + 32 * kk + 8 * lq]);
         const bf16x8 sl = *reinterpret_cast<const bf16x8*>(&sSl[buf][col * SP + 32 * kk + 8 * lq]);
-        X[nn] = mfma3(cur.xh[kk], cur.xl[kk], sh, sl, X[nn]);
+        X[nn] = mfma3(xh, xl, sh, sl, X[nn]);
       }
-      cur.xh[kk] = frag(rp, un_role ? L::w_frag(m, kk, 0) : L::qg_frag(m, kk, 0));
-      cur.xl[kk] = frag(rp, un_role ? L::w_frag(m, kk, 1) : L::qg_frag(m, kk, 1));
     }
+    cur.sx = rec_scale<DK>(rp, un_role ? SC_W : SC_QG);
     if (un_role) {
+      cur.sa = rec_scale<DK>(rp, SC_AI);
 #pragma unroll
       for (int nn = 0; nn < NT; ++nn) {
         const int col = 16 * nn + lr;
-        const f32x4 un = A[nn] - X[nn];
+        const f32x4 un = A[nn] * sa - X[nn] * sx;
         const int t = 16 * m + 4 * lq;
         put_quad(&sNh[col * TP + t], &sNl[col * TP + t], un);
       }
@@ -317,34 +317,53 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
 
     // ---- phase 2: S = diag(gamma_last) S + KG^T Un (state tile = wave);
     //      waves 4-7 finish o = Qg S + Aqk Un for row block m -------------------
+    // The KG^T and Aqk records carry power-of-two scales: S is held divided
+    // by sk across the update (exact) and Qg S is brought to Aqk's scale.
+    const float sk = cur.sk;
     if (owns) {
+      const float ik = 1.f / sk;
+      const float4 gk = make_float4(cur.gam.x * ik, cur.gam.y * ik, cur.gam.z * ik, cur.gam.w * ik);
 #pragma unroll
       for (int nn = 0; nn < NT; ++nn) {
-        S[nn][0] *= cur.gam.x; S[nn][1] *= cur.gam.y;
-        S[nn][2] *= cur.gam.z; S[nn][3] *= cur.gam.w;
+        S[nn][0] *= gk.x; S[nn][1] *= gk.y;
+        S[nn][2] *= gk.z; S[nn][3] *= gk.w;
       }
       cur.gam = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(rp + L::GL_OFF) + 16 * wave + 4 * lq);
+      cur.sk = rec_scale<DK>(rp, SC_KT);
+    }
+    if (!un_role) {
+      const float r = sx / sa;
+#pragma unroll
+      for (int nn = 0; nn < NT; ++nn) X[nn] = X[nn] * r;
+      cur.sa = rec_scale<DK>(rp, SC_AQK);
     }
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk) {
+      bf16x8 kh, kl, ah, al;
+      if (owns) {
+        f16x8_to_bf16_hilo(cur.k[kk], kh, kl);
+        cur.k[kk] = frag(rp, L::kt_frag(wave, kk));
+      }
+      if (!un_role) {
+        f16x8_to_bf16_hilo(cur.a[kk], ah, al);
+        cur.a[kk] = frag(rp, L::aqk_frag(m, kk));
+      }
 #pragma unroll
       for (int nn = 0; nn < NT; ++nn) {
         const int col = 16 * nn + lr;
         const bf16x8 nh = *reinterpret_cast<const bf16x8*>(&sNh[col * TP + 32 * kk + 8 * lq]);
         const bf16x8 nl = *reinterpret_cast<const bf16x8*>(&sNl[col * TP + 32 * kk + 8 * lq]);
-        if (owns) S[nn] = mfma3(cur.kh[kk], cur.kl[kk], nh, nl, S[nn]);
-        if (!un_role) X[nn] = mfma3(cur.a1[kk], cur.a2[kk], nh, nl, X[nn]);
-      }
-      if (owns) {
-        cur.kh[kk] = frag(rp, L::kt_frag(wave, kk, 0));
-        cur.kl[kk] = frag(rp, L::kt_frag(wave, kk, 1));
-      }
-      if (!un_role) {
-        cur.a1[kk] = frag(rp, L::aqk_frag(m, kk, 0));
-        cur.a2[kk] = frag(rp, L::aqk_frag(m, kk, 1));
+        if (owns) S[nn] = mfma3(kh, kl, nh, nl, S[nn]);
+        if (!un_role) X[nn] = mfma3(ah, al, nh, nl, X[nn]);
       }
     }
+    if (owns) {
+#pragma unroll
+      for (int nn = 0; nn < NT; ++nn) S[nn] = S[nn] * sk;
+    }
     if (!un_role) {
+#pragma unroll
+      for (int nn = 0; nn < NT; ++nn) X[nn] = X[nn] * sa;
       // o tile (rows 16m + 4lq + e, columns 16nn + lr in D layout) -> LDS,
       // then 16 contiguous bytes per lane to global memory
       unsigned char* so = sO[m];

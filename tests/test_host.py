@@ -46,9 +46,9 @@ def test_version_and_status_strings():
 
 def test_workspace_size():
     lib = _hip.lib()
-    # one record per (b, key head, 64-token chunk); 123392 bytes at DK=128, 73984 at DK=64
-    assert lib.gdn2_hip_prefill_workspace_bytes(2, 16, 128, 4096) == 2 * 16 * 64 * 123392
-    assert lib.gdn2_hip_prefill_workspace_bytes(1, 2, 64, 100) == 1 * 2 * 2 * 73984
+    # one record per (b, key head, 64-token chunk); 66304 bytes at DK=128, 41472 at DK=64
+    assert lib.gdn2_hip_prefill_workspace_bytes(2, 16, 128, 4096) == 2 * 16 * 64 * 66304
+    assert lib.gdn2_hip_prefill_workspace_bytes(1, 2, 64, 100) == 1 * 2 * 2 * 41472
     assert lib.gdn2_hip_prefill_workspace_bytes(1, 2, 96, 64) == 0
 
 
