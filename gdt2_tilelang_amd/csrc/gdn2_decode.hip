@@ -247,11 +247,22 @@ static hipError_t launch_decode_t(const void* q, const void* k, const void* v, c
   return hipGetLastError();
 }
 
+hipError_t launch_decode_mfma(const void* q, const void* k, const void* v, const float* g,
+                              const void* b, const void* w, float* state, void* o, int B, int H,
+                              int HK, int DK, int DV, long s_alloc, long t0, int n, float scale,
+                              int in_dt, int out_dt, hipStream_t stream);
+
 hipError_t launch_decode(const void* q, const void* k, const void* v, const float* g,
                          const void* b, const void* w, float* state, void* o, int B, int H, int HK,
                          int DK, int DV, long s_alloc, long t0, int n, float scale, int in_dt,
                          int out_dt, hipStream_t stream) {
   if (DV % kDecCols != 0) return hipErrorInvalidValue;
+  // several tokens per call: blocks of 8 on the fp32 matrix cores (DK <= 128)
+  if (n > 1 && DK <= 128) {
+    const hipError_t e = launch_decode_mfma(q, k, v, g, b, w, state, o, B, H, HK, DK, DV, s_alloc, t0,
+                                            n, scale, in_dt, out_dt, stream);
+    if (e != hipErrorNotSupported) return e;
+  }
 #define GDN2_DEC_CASE(DKV, IDT, ODT)                                                          \
   if (DK == DKV && in_dt == IDT && out_dt == ODT)                                             \
     return launch_decode_t<DKV, IDT, ODT>(q, k, v, g, b, w, state, o, B, H, HK, DV, s_alloc, t0, \
