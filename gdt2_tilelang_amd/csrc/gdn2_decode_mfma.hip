@@ -255,6 +255,22 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(
     }
     lds_barrier();
 
+    // ---- P_e = (state columns 2m+e)^T V: 16 projections per column (fp32 MFMA),
+    // issued first so they consume the state rows as they arrive
+    f32x4 P[2][2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) P[e][0] = P[e][1] = zero4();
+    if (active) {
+#pragma unroll
+      for (int s = 0; s < NS; s += 4) {
+        const f32x4 bv = *reinterpret_cast<const f32x4*>(&sm.vec[m][NS * kq + s]);
+#pragma unroll
+        for (int ss = 0; ss < 4; ++ss)
+#pragma unroll
+          for (int e = 0; e < 2; ++e) P[e][ss & 1] = mfma4(T[e][s / 4][ss], bv[ss], P[e][ss & 1]);
+      }
+    }
+
     // ---- Gram coefficients: lane = pair, channels split across the waves
     {
       const int code = gram_code(lane);
@@ -285,18 +301,6 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(
     lds_barrier();
 
     if (active) {
-      // ---- P_e = (state columns 2m+e)^T V: 16 projections per column (fp32 MFMA)
-      f32x4 P[2][2];
-#pragma unroll
-      for (int e = 0; e < 2; ++e) P[e][0] = P[e][1] = zero4();
-#pragma unroll
-      for (int s = 0; s < NS; s += 4) {
-        const f32x4 bv = *reinterpret_cast<const f32x4*>(&sm.vec[m][NS * kq + s]);
-#pragma unroll
-        for (int ss = 0; ss < 4; ++ss)
-#pragma unroll
-          for (int e = 0; e < 2; ++e) P[e][ss & 1] = mfma4(T[e][s / 4][ss], bv[ss], P[e][ss & 1]);
-      }
       // D layout: lane (kq, m) holds P[col 2(4kq + r) + e][vector m]
       float* pst = sm.pst[wave];
 #pragma unroll
