@@ -256,36 +256,41 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(
     lds_barrier();
 
     // ---- P_e = (state columns 2m+e)^T V: 16 projections per column (fp32 MFMA),
-    // issued first so they consume the state rows as they arrive
+    // consuming the state rows as they arrive (a wave past DV works on zeros),
+    // then this wave's share of the Gram coefficients: lane = pair, channel
+    // quads split across the waves. With four waves both sit in one basic block
+    // so the Gram VALU work can issue under the MFMAs.
     f32x4 P[2][2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) P[e][0] = P[e][1] = zero4();
-    if (active) {
 #pragma unroll
-      for (int s = 0; s < NS; s += 4) {
-        const f32x4 bv = *reinterpret_cast<const f32x4*>(&sm.vec[m][NS * kq + s]);
+    for (int s = 0; s < NS; s += 4) {
+      const f32x4 bv = *reinterpret_cast<const f32x4*>(&sm.vec[m][NS * kq + s]);
 #pragma unroll
-        for (int ss = 0; ss < 4; ++ss)
+      for (int ss = 0; ss < 4; ++ss)
 #pragma unroll
-          for (int e = 0; e < 2; ++e) P[e][ss & 1] = mfma4(T[e][s / 4][ss], bv[ss], P[e][ss & 1]);
-      }
+        for (int e = 0; e < 2; ++e) P[e][ss & 1] = mfma4(T[e][s / 4][ss], bv[ss], P[e][ss & 1]);
     }
-
-    // ---- Gram coefficients: lane = pair, channels split across the waves
     {
       const int code = gram_code(lane);
       const int tau = code & 7, t = (code >> 3) & 7;
       const float* xs = (code & 64) ? sm.qs[t] : sm.bk[t];
-      // channel quads [wave * DK/4 / nw, (wave+1) * DK/4 / nw)
-      const int q0 = wave * (DK / 4) / nw, q1 = (wave + 1) * (DK / 4) / nw;
       float acc = 0.f;
-      for (int i = 4 * q0; i < 4 * q1; i += 4) {
+      auto quad = [&](int i) {
         const f32x4 ct = *reinterpret_cast<const f32x4*>(&sm.cl[t][i]);
         const f32x4 cu = *reinterpret_cast<const f32x4*>(&sm.cl[tau][i]);
         const f32x4 kk = *reinterpret_cast<const f32x4*>(&sm.kr[tau][i]);
         const f32x4 xx = *reinterpret_cast<const f32x4*>(&xs[i]);
 #pragma unroll
         for (int e = 0; e < 4; ++e) acc += fast_exp2(ct[e] - cu[e]) * kk[e] * xx[e];
+      };
+      if (nw == MAXW) {
+        constexpr int QW = DK / 4 / MAXW;      // channel quads per wave
+#pragma unroll
+        for (int qq = 0; qq < QW; ++qq) quad(4 * (wave * QW + qq));
+      } else {
+        const int q0 = wave * (DK / 4) / nw, q1 = (wave + 1) * (DK / 4) / nw;
+        for (int qq = q0; qq < q1; ++qq) quad(4 * qq);
       }
       sm.gpart[wave][lane] = acc;
     }
