@@ -114,3 +114,20 @@ def test_decode_baseline_configs(B, n, prompt):
             assert rel_err(o.float(), o1.float()) < 2e-3
     torch.cuda.synchronize()
     assert rel_err(st.cpu(), st_ref) < 2e-3
+
+
+@pytest.mark.parametrize("B,H,DK,DV,n", [(57, 13, 64, 96, 11), (40, 13, 128, 128, 8)])
+def test_decode_many_heads(B, H, DK, DV, n):
+    """Multi-token decode over hundreds of heads (odd head counts), a partial
+    column tile (DV = 96: three waves per workgroup) and a second token block
+    (n = 11)."""
+    print(f"decode many heads B={B} H={H} DK={DK} DV={DV} n={n}", flush=True)
+    cpu, dev = device_inputs(B, n, H, DK, DV, torch.bfloat16)
+    s0 = seeded_state(B, H, DK, DV)
+    st_ref = s0.clone()
+    o_ref = oracle.decode_loop(*cpu, st_ref, None).float()
+    st = s0.cuda()
+    o = gdn2_decode(*dev, st)
+    torch.cuda.synchronize()
+    assert rel_err(st.cpu(), st_ref) < 1e-5
+    assert rel_err(o.float().cpu(), o_ref) < 4e-3
