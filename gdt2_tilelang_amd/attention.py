@@ -17,6 +17,13 @@ Two layer details differ on purpose:
   decode (the reference allocates both in ``dtype`` and a bf16 layer's
   ``conv1d`` then fails on the mixed dtypes);
 * the short-conv decode casts a cached tail to the activation dtype.
+
+On a GPU the layer's work around the op runs as three launches besides the
+op: one GEMM for all seven input projections (their weights concatenated once
+and cached), ``gdn2_hip_layer_prologue`` (short conv + SiLU, L2 norm, gates,
+decay, new conv tail) and ``gdn2_hip_layer_epilogue`` (gated RMSNorm); then
+``o_proj``. CPU tensors take the torch formulas of the reference layer
+(plumbing only: the op itself has no CPU path).
 """
 
 from __future__ import annotations
@@ -27,6 +34,7 @@ import torch
 import torch.nn.functional as F
 from torch import nn
 
+from . import _hip
 from .config import DEFAULT_KERNEL_CONFIG, GDN2Config, GatedDeltaNet2Config
 from .forward import chunk_gdn2_fwd
 from .inference import gdn2_decode, gdn2_prefill
@@ -205,6 +213,83 @@ class GatedDeltaNet2(nn.Module):
         self.scale = DK ** -0.5
         self.erase_scale = config.erase_gate_scale
 
+    # -- fused GPU path ------------------------------------------------------
+    def _cat_cached(self, name, parts):
+        """torch.cat(parts) along dim 0, rebuilt only when a part changes
+        (tracked by storage pointer and version counter)."""
+        key = tuple((t.data_ptr(), t._version, t.dtype, t.device) for t in parts)
+        hit = self.__dict__.get(name)
+        if hit is None or hit[0] != key:
+            hit = (key, torch.cat([t.detach().reshape(t.shape[0], -1) for t in parts], 0).contiguous())
+            self.__dict__[name] = hit
+        return hit[1]
+
+    def _proj_weights(self):
+        # one [4*HK*DK + 3*H*DV, hidden] weight: q | k | v | b | w | f | o_gate
+        return self._cat_cached("_wcat", [self.q_proj.weight, self.k_proj.weight, self.v_proj.weight,
+                                          self.b_proj.weight, self.w_proj.weight, self.f_proj.weight,
+                                          self.o_gate_proj.weight])
+
+    def _project_gpu(self, x, cache, conv_tail=False):
+        """All projections in one GEMM, then the prologue kernel. Returns the op
+        inputs, the projection buffer (its o_gate columns feed _finish_gpu) and
+        the new conv tail (or None)."""
+        B, S, hid = x.shape
+        HK, H, DK, DV = self.num_kv_heads, self.num_heads, self.head_dim_k, self.head_dim_v
+        dqk, dv = HK * DK, H * DV
+        dt = x.dtype
+        proj = F.linear(x.reshape(B * S, hid), self._proj_weights())     # [B*S, 4 dqk + 3 dv]
+        ld = proj.shape[1]
+        es = proj.element_size()
+        base = proj.data_ptr()
+        offs = [0, dqk, 2 * dqk, 2 * dqk + dv, 3 * dqk + dv, 3 * dqk + 2 * dv]   # q k v b w f
+        dev = x.device
+        q = torch.empty(B, S, HK, DK, device=dev, dtype=dt)
+        k = torch.empty_like(q)
+        b = torch.empty_like(q)
+        v = torch.empty(B, S, H, DV, device=dev, dtype=dt)
+        w = torch.empty_like(v)
+        g = torch.empty(B, S, HK, DK, device=dev, dtype=torch.float32)
+        conv_w = conv_b = conv_in = conv_out = None
+        K = 0
+        if self.q_conv is not None:
+            K = self.cfg.conv_size
+            convs = (self.q_conv.conv, self.k_conv.conv, self.v_conv.conv)
+            conv_w = self._cat_cached("_convw", [c.weight for c in convs])
+            if conv_w.dtype != dt:
+                conv_w = conv_w.to(dt)
+            if all(c.bias is not None for c in convs):
+                conv_b = self._cat_cached("_convb", [c.bias for c in convs])
+                conv_b = conv_b.to(dt).reshape(-1) if conv_b.dtype != dt else conv_b.reshape(-1)
+            if cache is not None and cache.conv_state is not None:
+                conv_in = cache.conv_state.to(dt).contiguous()
+            if cache is not None or conv_tail:
+                conv_out = torch.empty(B, 2 * dqk + dv, K - 1, device=dev, dtype=dt)
+        a_log = self.A_log.detach().float().contiguous()
+        dt_bias = self.dt_bias.detach().float().contiguous()
+        P = _hip.ptr
+        _hip.check(_hip.lib().gdn2_hip_layer_prologue(
+            *(base + o * es for o in offs), ld, ld, ld, ld, ld, ld, _hip.dtype_code(dt),
+            P(conv_w), P(conv_b), K, P(conv_in), P(conv_out), P(a_log), P(dt_bias), float(self.erase_scale),
+            P(q), P(k), P(v), P(b), P(w), P(g), B, S, H, HK, DK, DV, _hip.stream_of(dev)),
+            "gdn2_hip_layer_prologue")
+        return (q, k, v, g, b, w), proj, conv_out
+
+    def _finish_gpu(self, x, o, proj):
+        B, S, _ = x.shape
+        H, DV = self.num_heads, self.head_dim_v
+        dqk, dv = self.num_kv_heads * self.head_dim_k, H * DV
+        ld = proj.shape[1]
+        gate_ptr = proj.data_ptr() + (4 * dqk + 2 * dv) * proj.element_size()
+        out = torch.empty(B, S, dv, device=x.device, dtype=x.dtype)
+        o = o.contiguous()
+        weight = self.o_norm.weight.detach().float().contiguous()
+        _hip.check(_hip.lib().gdn2_hip_layer_epilogue(
+            _hip.ptr(o), _hip.dtype_code(o.dtype), gate_ptr, ld, _hip.ptr(weight), float(self.o_norm.eps),
+            _hip.ptr(out), _hip.dtype_code(x.dtype), dv, B, S, H, DV, _hip.stream_of(x.device)),
+            "gdn2_hip_layer_epilogue")
+        return self.o_proj(out)
+
     # -- pieces shared by forward / prefill / decode -----------------------
     def _decay(self, x, lead):
         f = self.f_proj(x).view(*lead, self.num_kv_heads, self.head_dim_k)
@@ -253,6 +338,14 @@ class GatedDeltaNet2(nn.Module):
     def forward(self, hidden_states, cache=None, use_cache=False, cu_seqlens=None):
         """Full-sequence mixer (training form). Returns ``(output, cache or None)``."""
         B, S, _ = hidden_states.shape
+        if hidden_states.is_cuda:
+            (q, k, v, g, b, w), proj, conv_state = self._project_gpu(hidden_states, None, conv_tail=use_cache)
+            o, final_state = gdn2_attention(
+                q, k, v, g, b, w, scale=self.scale,
+                initial_state=cache.recurrent_state if cache is not None else None,
+                output_final_state=use_cache, config=self.cfg.kernel, cu_seqlens=cu_seqlens)
+            out = self._finish_gpu(hidden_states, o, proj)
+            return out, (GDN2Cache(final_state, conv_state) if use_cache else None)
         conv_state = None
         if self.q_conv is not None and use_cache:
             width = self.cfg.conv_size - 1
@@ -273,6 +366,13 @@ class GatedDeltaNet2(nn.Module):
         """Prefill a prompt (or one segment of it); returns ``(output, cache)``."""
         if cache is None:
             cache = self.init_cache(hidden_states.shape[0], device=hidden_states.device)
+        if hidden_states.is_cuda:
+            (q, k, v, g, b, w), proj, conv_out = self._project_gpu(hidden_states, cache)
+            cache.conv_state = conv_out
+            o, state = gdn2_prefill(q, k, v, g, b, w, cache.recurrent_state, scale=self.scale,
+                                    config=self.cfg.kernel)
+            cache.recurrent_state = state
+            return self._finish_gpu(hidden_states, o, proj), cache
         q, k, v, g, b, w = self._project(hidden_states, cache)
         o, state = gdn2_prefill(q, k, v, g, b, w, cache.recurrent_state, scale=self.scale,
                                 config=self.cfg.kernel)
@@ -282,6 +382,11 @@ class GatedDeltaNet2(nn.Module):
     @torch.no_grad()
     def decode(self, hidden_states, cache):
         """Decode ``n`` tokens ``[B, n, hidden]``, updating ``cache`` in place."""
+        if hidden_states.is_cuda:
+            (q, k, v, g, b, w), proj, conv_out = self._project_gpu(hidden_states, cache)
+            cache.conv_state = conv_out
+            o = gdn2_decode(q, k, v, g, b, w, cache.recurrent_state, scale=self.scale)
+            return self._finish_gpu(hidden_states, o, proj), cache
         q, k, v, g, b, w = self._project(hidden_states, cache)
         o = gdn2_decode(q, k, v, g, b, w, cache.recurrent_state, scale=self.scale)
         return self._finish(hidden_states, o), cache

@@ -3,6 +3,7 @@
 #include "../../include/gdn2_hip.h"
 #include "gdn2_common.h"
 #include "gdn2_prefill_layout.h"
+#include "gdn2_layer.h"
 
 namespace gdn2 {
 hipError_t launch_decode(const void*, const void*, const void*, const float*, const void*,
@@ -117,6 +118,46 @@ int gdn2_hip_prefill_chunks(const void* q, const void* k, const void* v, const f
   if (s) return s;
   return gdn2_hip_prefill_scan(v, w, in_dtype, workspace, state_in, state_out, o, out_dtype, B, H,
                                HK, DK, DV, s_alloc, t0, n_tokens, stream);
+}
+
+int gdn2_hip_layer_prologue(const void* xq, const void* xk, const void* xv, const void* xb,
+                            const void* xw, const void* xf, long ld_q, long ld_k, long ld_v,
+                            long ld_b, long ld_w, long ld_f, int act_dtype, const void* conv_w,
+                            const void* conv_b, int conv_k, const void* conv_in, void* conv_out,
+                            const float* a_log, const float* dt_bias, float erase_scale, void* q,
+                            void* k, void* v, void* b, void* w, float* g, int B, long S, int H,
+                            int HK, int DK, int DV, void* stream) {
+  if (!xq || !xk || !xv || !xb || !xw || !xf || !a_log || !dt_bias) return GDN2_ERR_ARG;
+  if (!q || !k || !v || !b || !w || !g) return GDN2_ERR_ARG;
+  if (!dtype_ok(act_dtype) || B < 0 || S < 0 || H < 1 || HK < 1 || H % HK || DV < 1) return GDN2_ERR_ARG;
+  const int dqk = HK * DK, dv = H * DV;
+  if (ld_q < dqk || ld_k < dqk || ld_b < dqk || ld_f < dqk || ld_v < dv || ld_w < dv) return GDN2_ERR_ARG;
+  // DK / 4 lanes per q, k head, a power of two <= 64
+  if (DK < 4 || DK % 4 || DK > 256 || ((DK / 4) & (DK / 4 - 1))) return GDN2_ERR_SHAPE;
+  if (conv_w && (conv_k < 1 || conv_k > 4)) return GDN2_ERR_SHAPE;
+  if (conv_w && conv_out && conv_out == conv_in) return GDN2_ERR_ARG;   // the tail is read while written
+  if (static_cast<long>(B) * S > 0x7fffffffL) return GDN2_ERR_SHAPE;
+  gdn2::lay::ProArgs a;
+  a.x[0] = xq; a.x[1] = xk; a.x[2] = xv; a.x[3] = xb; a.x[4] = xw; a.x[5] = xf;
+  a.ld[0] = ld_q; a.ld[1] = ld_k; a.ld[2] = ld_v; a.ld[3] = ld_b; a.ld[4] = ld_w; a.ld[5] = ld_f;
+  a.conv_w = conv_w; a.conv_b = conv_w ? conv_b : nullptr; a.K = conv_w ? conv_k : 0;
+  a.conv_in = conv_w ? conv_in : nullptr; a.conv_out = conv_w ? conv_out : nullptr;
+  a.a_log = a_log; a.dt_bias = dt_bias; a.erase_scale = erase_scale;
+  a.q = q; a.k = k; a.v = v; a.b = b; a.w = w; a.g = g;
+  a.B = B; a.S = S; a.H = H; a.HK = HK; a.DK = DK; a.DV = DV;
+  return status(gdn2::launch_layer_prologue(a, act_dtype, static_cast<hipStream_t>(stream)));
+}
+
+int gdn2_hip_layer_epilogue(const void* o, int o_dtype, const void* gate, long ld_gate,
+                            const float* weight, float eps, void* out, int out_dtype, long ld_out,
+                            int B, long S, int H, int DV, void* stream) {
+  if (!o || !gate || !weight || !out) return GDN2_ERR_ARG;
+  if (!dtype_ok(o_dtype) || !dtype_ok(out_dtype) || B < 0 || S < 0 || H < 1 || DV < 1) return GDN2_ERR_ARG;
+  if (ld_gate < static_cast<long>(H) * DV || ld_out < static_cast<long>(H) * DV) return GDN2_ERR_ARG;
+  const long rows = static_cast<long>(B) * S * H;
+  if ((rows + 3) / 4 > 0x7fffffffL) return GDN2_ERR_SHAPE;
+  return status(gdn2::launch_layer_epilogue(o, o_dtype, gate, ld_gate, weight, eps, out, out_dtype, ld_out,
+                                            rows, H, DV, static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

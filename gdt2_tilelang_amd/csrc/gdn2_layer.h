@@ -1,0 +1,32 @@
+// Arguments of the GatedDeltaNet2 layer prologue kernel (gdn2_layer.hip),
+// shared with the C ABI that validates and forwards them.
+#pragma once
+
+#include <hip/hip_runtime.h>
+
+namespace gdn2 {
+namespace lay {
+
+struct ProArgs {
+  const void* x[6];        // raw q, k, v, b, w, f projections (rows of B*S tokens)
+  long ld[6];              // their row strides, in elements
+  const void* conv_w;      // [C, K] (C = 2*HK*DK + H*DV), or null: no conv
+  const void* conv_b;      // [C] or null
+  int K;
+  const void* conv_in;     // [B, C, K-1] or null (zeros)
+  void* conv_out;          // [B, C, K-1] or null
+  const float* a_log;      // [HK]
+  const float* dt_bias;    // [HK, DK]
+  float erase_scale;
+  void* q; void* k; void* v; void* b; void* w; float* g;   // outputs, contiguous
+  int B; long S; int H, HK, DK, DV;
+};
+
+}  // namespace lay
+
+hipError_t launch_layer_prologue(const lay::ProArgs& a, int act_dt, hipStream_t stream);
+hipError_t launch_layer_epilogue(const void* o, int o_dt, const void* gate, long ld_gate, const float* weight,
+                                 float eps, void* out, int out_dt, long ld_out, long rows, int H, int DV,
+                                 hipStream_t stream);
+
+}  // namespace gdn2

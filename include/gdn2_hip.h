@@ -100,6 +100,45 @@ int gdn2_hip_prefill_chunks(const void* q, const void* k, const void* v, const f
                             int H, int HK, int DK, int DV, long s_alloc, long t0, long n_tokens,
                             float scale, void* stream);
 
+/*
+ * GatedDeltaNet2 layer prologue (one launch per prefill segment or decode
+ * block): for the B x S tokens of the raw projections xq, xk [.., HK*DK],
+ * xv, xw [.., H*DV], xb, xf [.., HK*DK] (row strides ld_* in elements, all in
+ * act_dtype), compute
+ *   q, k = L2-normalised (per DK-channel head) SiLU(causal depthwise conv(x))
+ *   v    = SiLU(causal depthwise conv(xv))
+ *   b    = sigmoid(xb) * erase_scale,  w = sigmoid(xw)
+ *   g    = -exp(a_log[hk]) * softplus(xf + dt_bias[hk, :])        (fp32)
+ * into contiguous q, k, b [B, S, HK, DK], v, w [B, S, H, DV] (act_dtype) and
+ * g [B, S, HK, DK] (fp32). The conv (width conv_k <= 4, weights conv_w
+ * [C, conv_k] and bias conv_b [C] in act_dtype, C = 2*HK*DK + H*DV, channel
+ * order q | k | v) continues from conv_in [B, C, conv_k - 1] (NULL: zeros) and
+ * writes the last conv_k - 1 conv inputs to conv_out (same layout, distinct
+ * buffer; NULL: not written). conv_w NULL: no conv (and no SiLU).
+ * DK/4 must be a power of two <= 64.
+ * Replaces: the layer's q/k/v conv, F.normalize and gate/decay ops in
+ * gdn2/attention.py (_ShortConv.decode :206-215, _gates :290-293, the
+ * normalisation in prefill/decode :360-402).
+ */
+int gdn2_hip_layer_prologue(const void* xq, const void* xk, const void* xv, const void* xb,
+                            const void* xw, const void* xf, long ld_q, long ld_k, long ld_v,
+                            long ld_b, long ld_w, long ld_f, int act_dtype, const void* conv_w,
+                            const void* conv_b, int conv_k, const void* conv_in, void* conv_out,
+                            const float* a_log, const float* dt_bias, float erase_scale, void* q,
+                            void* k, void* v, void* b, void* w, float* g, int B, long S, int H,
+                            int HK, int DK, int DV, void* stream);
+
+/*
+ * GatedDeltaNet2 layer epilogue: per token and value head,
+ *   out = o * rsqrt(mean(o^2) + eps) * weight * silu(gate)
+ * o [B, S, H, DV] contiguous in o_dtype; gate and out rows of H*DV in
+ * out_dtype with row strides ld_gate / ld_out; weight [DV] fp32.
+ * Replaces: _GatedRMSNorm.forward (gdn2/attention.py:218-229).
+ */
+int gdn2_hip_layer_epilogue(const void* o, int o_dtype, const void* gate, long ld_gate,
+                            const float* weight, float eps, void* out, int out_dtype, long ld_out,
+                            int B, long S, int H, int DV, void* stream);
+
 #ifdef __cplusplus
 }
 #endif

@@ -72,3 +72,38 @@ def test_config4_segmented_prefill_then_decode():
     print(f"  segmented vs one-shot: prefill {e_pre:.2e} decode {e_dec:.2e} state {e_st:.2e}", flush=True)
     assert e_st < 2e-3
     assert e_pre < 1e-2 and e_dec < 1e-2
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 2e-5), (torch.bfloat16, 1.6e-2)])
+@pytest.mark.parametrize("S,with_cache", [(37, False), (37, True), (2, True), (1, True)])
+def test_fused_prologue_epilogue_match_torch_formulas(dtype, tol, S, with_cache):
+    """gdn2_hip_layer_prologue / _epilogue against the layer's torch formulas
+    (GatedDeltaNet2._project / _finish run on the same GPU tensors): the conv
+    continuing from a non-zero cached tail (including S < conv_size - 1, where
+    the new tail keeps part of the old one), L2 norm, gates, decay, the new
+    conv tail, and the gated RMSNorm + o_proj. fp32 is held to fp32 round-off;
+    bf16 to the rounding of bf16 intermediates the torch formulas keep."""
+    torch.manual_seed(0)
+    cfg = GatedDeltaNet2Config(hidden_size=256, num_heads=4, num_kv_heads=2, head_dim_k=64, head_dim_v=32)
+    layer = GatedDeltaNet2(cfg).cuda().to(dtype).eval()
+    gen = torch.Generator(device="cuda").manual_seed(3)
+    x = torch.randn(2, S, 256, device="cuda", generator=gen).to(dtype)
+    cache_a = cache_b = None
+    if with_cache:
+        cache_a = layer.init_cache(2, device="cuda")
+        cache_a.conv_state = torch.randn(cache_a.conv_state.shape, device="cuda", generator=gen).to(dtype)
+        cache_b = layer.init_cache(2, device="cuda")
+        cache_b.conv_state = cache_a.conv_state.clone()
+    with torch.no_grad():
+        got, proj, tail = layer._project_gpu(x, cache_b)
+        want = layer._project(x, cache_a)
+        for name, a, b in zip("qkvgbw", got, want):
+            assert a.shape == b.shape, name
+            assert rel_err(a.float(), b.float()) < tol, name
+        if with_cache:   # raw projections: one fused GEMM vs three, so not bit-equal
+            assert tail.shape == cache_a.conv_state.shape
+            assert rel_err(tail.float(), cache_a.conv_state.float()) < tol
+        o = torch.randn(2, S, 4, 32, device="cuda", generator=gen).to(dtype)
+        out_gpu = layer._finish_gpu(x, o, proj)
+        out_ref = layer._finish(x, o)
+        assert rel_err(out_gpu.float(), out_ref.float()) < tol
