@@ -132,8 +132,16 @@ int gdn2_hip_layer_prologue(const void* xq, const void* xk, const void* xv, cons
   if (!dtype_ok(act_dtype) || B < 0 || S < 0 || H < 1 || HK < 1 || H % HK || DV < 1) return GDN2_ERR_ARG;
   const int dqk = HK * DK, dv = H * DV;
   if (ld_q < dqk || ld_k < dqk || ld_b < dqk || ld_f < dqk || ld_v < dv || ld_w < dv) return GDN2_ERR_ARG;
-  // DK / 4 lanes per q, k head, a power of two <= 64
-  if (DK < 4 || DK % 4 || DK > 256 || ((DK / 4) & (DK / 4 - 1))) return GDN2_ERR_SHAPE;
+  // 8-channel lane items: DK / 8 lanes per q, k head, a power of two <= 64
+  if (DK < 8 || DK % 8 || DK > 512 || ((DK / 8) & (DK / 8 - 1)) || DV % 8) return GDN2_ERR_SHAPE;
+  // 16-byte vector accesses: rows and bases aligned
+  const long lds[6] = {ld_q, ld_k, ld_v, ld_b, ld_w, ld_f};
+  const void* xs[6] = {xq, xk, xv, xb, xw, xf};
+  for (int i = 0; i < 6; ++i)
+    if (lds[i] % 8 || reinterpret_cast<uintptr_t>(xs[i]) % 16) return GDN2_ERR_ARG;
+  const void* outs[6] = {q, k, v, b, w, g};
+  for (int i = 0; i < 6; ++i)
+    if (reinterpret_cast<uintptr_t>(outs[i]) % 16) return GDN2_ERR_ARG;
   if (conv_w && (conv_k < 1 || conv_k > 4)) return GDN2_ERR_SHAPE;
   if (conv_w && conv_out && conv_out == conv_in) return GDN2_ERR_ARG;   // the tail is read while written
   if (static_cast<long>(B) * S > 0x7fffffffL) return GDN2_ERR_SHAPE;

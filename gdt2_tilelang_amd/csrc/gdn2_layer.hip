@@ -51,90 +51,181 @@ __device__ __forceinline__ float group_sum(float x, int group) {
 }
 
 
-// Conv (+ SiLU) of channel c (global conv channel index) at token t of batch
-// bi, reading raw input channel cx of tensor x (row stride ldx).
+constexpr int TT = 4;            // tokens per prologue workgroup
+constexpr int kProThreads = 128;
+
+// Eight consecutive elements of a row (16 bytes for 16-bit types, 32 for fp32).
 template <int DT>
-__device__ __forceinline__ float conv_at(const ProArgs& a, int bi, long t, const void* x, long ldx, int cx,
-                                         int c, long C) {
-  const int K = a.K;
-  float y = a.conv_b ? ld<DT>(a.conv_b, c) : 0.f;
+__device__ __forceinline__ void ld8(const void* p, long i, float* x) {
+  if constexpr (DT == DT_F32) {
+    const float4 a = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i);
+    const float4 b = *reinterpret_cast<const float4*>(static_cast<const float*>(p) + i + 4);
+    x[0] = a.x; x[1] = a.y; x[2] = a.z; x[3] = a.w; x[4] = b.x; x[5] = b.y; x[6] = b.z; x[7] = b.w;
+  } else {
+    const uint4 r = *reinterpret_cast<const uint4*>(static_cast<const unsigned short*>(p) + i);
+    const uint32_t u[4] = {r.x, r.y, r.z, r.w};
 #pragma unroll
-  for (int j = 0; j < kMaxConv; ++j) {
-    if (j >= K) break;
-    const long p = t - (K - 1) + j;   // input position within the segment
-    float in;
-    if (p >= 0) in = ld<DT>(x, (static_cast<long>(bi) * a.S + p) * ldx + cx);
-    else in = a.conv_in ? ld<DT>(a.conv_in, (static_cast<long>(bi) * C + c) * (K - 1) + (p + K - 1)) : 0.f;
-    y += ld<DT>(a.conv_w, static_cast<long>(c) * K + j) * in;
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (DT == DT_BF16) { x[2 * j] = bf16_lo_f32(u[j]); x[2 * j + 1] = bf16_hi_f32(u[j]); }
+      else { x[2 * j] = f16_bits_to_f32(u[j] & 0xffff); x[2 * j + 1] = f16_bits_to_f32(u[j] >> 16); }
+    }
   }
-  return silu(y);
 }
 
 template <int DT>
-__global__ __launch_bounds__(kThreads) void prologue_kernel(ProArgs a) {
-  const long tok = blockIdx.x;                 // token row b * S + t
-  const int bi = static_cast<int>(tok / a.S);
-  const long t = tok % a.S;
+__device__ __forceinline__ void st8(void* p, long i, const float* x) {
+  if constexpr (DT == DT_F32) {
+    *reinterpret_cast<float4*>(static_cast<float*>(p) + i) = make_float4(x[0], x[1], x[2], x[3]);
+    *reinterpret_cast<float4*>(static_cast<float*>(p) + i + 4) = make_float4(x[4], x[5], x[6], x[7]);
+  } else {
+    uint32_t u[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      if constexpr (DT == DT_BF16) u[j] = cvt_pk_bf16(x[2 * j], x[2 * j + 1]);
+      else u[j] = static_cast<uint32_t>(f32_to_f16_bits(x[2 * j])) | (static_cast<uint32_t>(f32_to_f16_bits(x[2 * j + 1])) << 16);
+    }
+    *reinterpret_cast<uint4*>(static_cast<unsigned short*>(p) + i) = make_uint4(u[0], u[1], u[2], u[3]);
+  }
+}
+
+// Grid (token blocks of TT, item blocks of kProThreads, batch). A lane item
+// is a group of 8 channels: first the conv items (q | k | v), then the gate
+// items (b | w | f). A conv item reads the raw rows t0-(K-1) .. t0+TT-1 of
+// its 8 channels once and its weights once for all TT tokens. A q / k head is
+// DK/8 consecutive lanes of one wave, whose squared sums are combined with
+// lane shuffles. Small token counts (decode) still spread over
+// (C + 2*HK*DK + H*DV) / 8 / kProThreads workgroups.
+template <int DT>
+__global__ __launch_bounds__(kProThreads) void prologue_kernel(ProArgs a) {
+  const int bi = blockIdx.z;
+  const long t0 = static_cast<long>(blockIdx.x) * TT;
+  const int nt = static_cast<int>(min(static_cast<long>(TT), a.S - t0));
   const int tid = threadIdx.x;
   const int dqk = a.HK * a.DK, dv = a.H * a.DV;
   const long C = 2L * dqk + dv;
+  const int K = a.K;
   const bool conv = a.conv_w != nullptr;
-  const int group = a.DK / 4;                  // lanes per q / k head (4 channels each)
+  const int group = a.DK / 8;                   // lanes per q / k head
+  const int nconv = static_cast<int>(C / 8);
+  const long row0 = static_cast<long>(bi) * a.S;
 
-  // q and k: conv + SiLU, then L2 norm per head (x / max(||x||, 1e-12))
-#pragma unroll
-  for (int which = 0; which < 2; ++which) {
+  const int nb = dqk / 8, nw = dv / 8;
+  const int item = blockIdx.y * kProThreads + tid;
+  if (item < nconv) {
+    const int c0 = 8 * item;                    // global conv channel
+    const int which = c0 < dqk ? 0 : (c0 < 2 * dqk ? 1 : 2);
+    const int cx = c0 - which * dqk;            // channel within its tensor
     const void* x = a.x[which];
     const long ldx = a.ld[which];
-    void* out = which == 0 ? a.q : a.k;
-    for (int c4 = 4 * tid; c4 < dqk; c4 += 4 * kThreads) {
-      float y[4];
-      float ss = 0.f;
+    float y[TT][8];
+    if (conv) {
+      float wt[kMaxConv][8], bias[8];
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int c = c4 + e;
-        y[e] = conv ? conv_at<DT>(a, bi, t, x, ldx, c, which * dqk + c, C) : ld<DT>(x, tok * ldx + c);
-        ss += y[e] * y[e];
+      for (int e = 0; e < 8; ++e) {
+        bias[e] = a.conv_b ? ld<DT>(a.conv_b, c0 + e) : 0.f;
+#pragma unroll
+        for (int j = 0; j < kMaxConv; ++j) wt[j][e] = j < K ? ld<DT>(a.conv_w, static_cast<long>(c0 + e) * K + j) : 0.f;
       }
-      ss = group_sum(ss, group);
-      const float inv = 1.f / fmaxf(sqrtf(ss), 1e-12f);
 #pragma unroll
-      for (int e = 0; e < 4; ++e) st<DT>(out, tok * dqk + c4 + e, y[e] * inv);
-    }
-  }
-  // v: conv + SiLU
-  for (int c = tid; c < dv; c += kThreads) {
-    const float y = conv ? conv_at<DT>(a, bi, t, a.x[2], a.ld[2], c, 2 * dqk + c, C) : ld<DT>(a.x[2], tok * a.ld[2] + c);
-    st<DT>(a.v, tok * dv + c, y);
-  }
-  // gates
-  for (int c = tid; c < dqk; c += kThreads) {
-    st<DT>(a.b, tok * dqk + c, sigmoid(ld<DT>(a.x[3], tok * a.ld[3] + c)) * a.erase_scale);
-    const int hk = c / a.DK;
-    const float f = ld<DT>(a.x[5], tok * a.ld[5] + c) + a.dt_bias[c];
-    a.g[tok * dqk + c] = -__expf(a.a_log[hk]) * softplus(f);
-  }
-  for (int c = tid; c < dv; c += kThreads) st<DT>(a.w, tok * dv + c, sigmoid(ld<DT>(a.x[4], tok * a.ld[4] + c)));
-
-  // new conv tail: entry i holds the input at position S - (K-1) + i
-  if (conv && a.conv_out) {
-    const int K1 = a.K - 1;
-    for (int i = 0; i < K1; ++i) {
-      const long p = a.S - K1 + i;
-      if (p >= 0 ? p != t : t != 0) continue;   // the token at p writes it; token 0 copies old entries
-      for (long c = tid; c < C; c += kThreads) {
-        float xin;
+      for (int t = 0; t < TT; ++t)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[t][e] = bias[e];
+      // input row r = t0 - (K-1) + r, r < TT + K - 1; each feeds the outputs t with j = r - t
+#pragma unroll
+      for (int r = 0; r < TT + kMaxConv - 1; ++r) {
+        if (r >= nt + K - 1) break;
+        const long p = t0 - (K - 1) + r;
+        float in[8];
         if (p >= 0) {
-          const int which = c < dqk ? 0 : (c < 2 * dqk ? 1 : 2);
-          const long cx = which == 0 ? c : (which == 1 ? c - dqk : c - 2 * dqk);
-          xin = ld<DT>(a.x[which], (static_cast<long>(bi) * a.S + p) * a.ld[which] + cx);
+          ld8<DT>(x, (row0 + p) * ldx + cx, in);
         } else {
-          xin = a.conv_in ? ld<DT>(a.conv_in, (static_cast<long>(bi) * C + c) * K1 + (p + K1)) : 0.f;
+#pragma unroll
+          for (int e = 0; e < 8; ++e)
+            in[e] = a.conv_in ? ld<DT>(a.conv_in, (static_cast<long>(bi) * C + c0 + e) * (K - 1) + (p + K - 1)) : 0.f;
         }
-        st<DT>(a.conv_out, (static_cast<long>(bi) * C + c) * K1 + i, xin);
+#pragma unroll
+        for (int t = 0; t < TT; ++t) {
+          const int j = r - t;
+          if (j < 0 || j >= K) continue;
+#pragma unroll
+          for (int e = 0; e < 8; ++e) y[t][e] += wt[j][e] * in[e];
+        }
+      }
+#pragma unroll
+      for (int t = 0; t < TT; ++t)
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[t][e] = silu(y[t][e]);
+    } else {
+#pragma unroll
+      for (int t = 0; t < TT; ++t) {
+        if (t < nt) ld8<DT>(x, (row0 + t0 + t) * ldx + cx, y[t]);
+      }
+    }
+    void* out = which == 0 ? a.q : (which == 1 ? a.k : a.v);
+    const int width = which == 2 ? dv : dqk;
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      if (which < 2) {   // L2 norm over the head (wave-uniform: heads never straddle q | k | v)
+        float ss = 0.f;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) ss += y[t][e] * y[t][e];
+        ss = group_sum(ss, group);
+        const float inv = 1.f / fmaxf(sqrtf(ss), 1e-12f);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[t][e] *= inv;
+      }
+      if (t < nt) st8<DT>(out, (row0 + t0 + t) * width + cx, y[t]);
+    }
+    // new conv tail of these 8 channels: entry i holds the input at position
+    // S - (K-1) + i; written by the workgroup holding that token, or
+    // (position < 0, a segment shorter than K-1) copied from the old tail by
+    // the first token block
+    if (conv && a.conv_out) {
+      const int K1 = K - 1;
+      for (int i = 0; i < K1; ++i) {
+        const long p = a.S - K1 + i;
+        if (p >= 0 ? (p < t0 || p >= t0 + nt) : t0 != 0) continue;
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          const long c = c0 + e;
+          const float xin = p >= 0 ? ld<DT>(x, (row0 + p) * ldx + cx + e)
+                                   : (a.conv_in ? ld<DT>(a.conv_in, (static_cast<long>(bi) * C + c) * K1 + (p + K1)) : 0.f);
+          st<DT>(a.conv_out, (static_cast<long>(bi) * C + c) * K1 + i, xin);
+        }
+      }
+    }
+  } else if (item < nconv + 2 * nb + nw) {
+    const int it = item - nconv;
+    const int kind = it < nb ? 0 : (it < nb + nw ? 1 : 2);
+    const int c0 = 8 * (kind == 0 ? it : (kind == 1 ? it - nb : it - nb - nw));
+    float dtb[8], al = 0.f;
+    if (kind == 2) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) dtb[e] = a.dt_bias[c0 + e];
+      al = -__expf(a.a_log[c0 / a.DK]);
+    }
+    for (int t = 0; t < nt; ++t) {
+      const long tok = row0 + t0 + t;
+      float xv[8];
+      if (kind == 0) {
+        ld8<DT>(a.x[3], tok * a.ld[3] + c0, xv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[e] = sigmoid(xv[e]) * a.erase_scale;
+        st8<DT>(a.b, tok * dqk + c0, xv);
+      } else if (kind == 1) {
+        ld8<DT>(a.x[4], tok * a.ld[4] + c0, xv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[e] = sigmoid(xv[e]);
+        st8<DT>(a.w, tok * dv + c0, xv);
+      } else {
+        ld8<DT>(a.x[5], tok * a.ld[5] + c0, xv);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) xv[e] = al * softplus(xv[e] + dtb[e]);
+        st8<DT_F32>(a.g, tok * dqk + c0, xv);
       }
     }
   }
+
 }
 
 // gated RMSNorm: one wave per (token, value head)
@@ -167,12 +258,14 @@ __global__ __launch_bounds__(kThreads) void epilogue_kernel(const void* __restri
 }  // namespace lay
 
 hipError_t launch_layer_prologue(const lay::ProArgs& a, int act_dt, hipStream_t stream) {
-  const long rows = static_cast<long>(a.B) * a.S;
-  if (rows == 0) return hipSuccess;
-  const dim3 grid(static_cast<unsigned>(rows));
-  if (act_dt == DT_BF16) hipLaunchKernelGGL(lay::prologue_kernel<DT_BF16>, grid, dim3(lay::kThreads), 0, stream, a);
-  else if (act_dt == DT_F16) hipLaunchKernelGGL(lay::prologue_kernel<DT_F16>, grid, dim3(lay::kThreads), 0, stream, a);
-  else if (act_dt == DT_F32) hipLaunchKernelGGL(lay::prologue_kernel<DT_F32>, grid, dim3(lay::kThreads), 0, stream, a);
+  if (a.B == 0 || a.S == 0) return hipSuccess;
+  // conv items (q, k, v channels) plus gate items (b, w, f channels), both 2*HK*DK + H*DV wide
+  const long items = 2 * ((2L * a.HK * a.DK + a.H * a.DV) / 8);
+  const dim3 grid(static_cast<unsigned>((a.S + lay::TT - 1) / lay::TT),
+                  static_cast<unsigned>((items + lay::kProThreads - 1) / lay::kProThreads), static_cast<unsigned>(a.B));
+  if (act_dt == DT_BF16) hipLaunchKernelGGL(lay::prologue_kernel<DT_BF16>, grid, dim3(lay::kProThreads), 0, stream, a);
+  else if (act_dt == DT_F16) hipLaunchKernelGGL(lay::prologue_kernel<DT_F16>, grid, dim3(lay::kProThreads), 0, stream, a);
+  else if (act_dt == DT_F32) hipLaunchKernelGGL(lay::prologue_kernel<DT_F32>, grid, dim3(lay::kProThreads), 0, stream, a);
   else return hipErrorInvalidValue;
   return hipGetLastError();
 }
