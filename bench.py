@@ -1,6 +1,6 @@
 """Benchmark of the GDN-2 hip backend on one MI355X; prints ONE JSON line.
 
-    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode]
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--no-cpu] [--no-decode] [--no-layer]
 
 Headline (BASELINE.json ``metric``): prefill tokens/s at BASELINE config 1
 (B=2 S=4096 H=16 DK=DV=128, bf16 q,k,v,b,w, fp32 g, synthetic data with the
@@ -12,7 +12,8 @@ cannot hold a step's working set.
 Also reported: decode state GB/s for BASELINE configs 2 (decode_step, B=64,
 64 calls) and 3 (decode_multi n=8, B=32), rotating enough independent states
 (> 256 MB in total) that every call streams its state from HBM, and the CPU
-baseline: the oracle's chunkwise torch path on the host cores.
+baseline: the oracle's chunkwise torch path on the host cores, and the
+GatedDeltaNet2 layer at BASELINE config 4 (segmented prefill + 128 steps).
 """
 
 from __future__ import annotations
@@ -173,6 +174,45 @@ def bench_decode(B, n, calls, steps_per_buf_min, H=16, D=128):
                 tokens_per_s=round(B * n / (us * 1e-6), 1))
 
 
+def bench_layer(reps=3):
+    """a GatedDeltaNet2 layer (hidden 2048, 16 value / 8 key
+    heads, head dims 128, random-init bf16 weights, x ~ N(0,1), B=1) prefills a
+    ragged 32700-token prompt in 4 segments, passing the cache back between
+    them, then decodes 128 steps through ``GatedDeltaNet2.step``. Eager calls,
+    as a user of the layer makes them; best of ``reps`` runs."""
+    from gdt2_tilelang_amd import GatedDeltaNet2, GatedDeltaNet2Config
+
+    torch.manual_seed(0)
+    cfg = GatedDeltaNet2Config(hidden_size=2048, num_heads=16, num_kv_heads=8, head_dim_k=128,
+                               head_dim_v=128)
+    layer = GatedDeltaNet2(cfg).cuda().to(torch.bfloat16).eval()
+    S, steps = 32700, 128
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    x = torch.randn(1, S + steps, 2048, device="cuda", generator=gen).to(torch.bfloat16)
+    bounds = [0, 8175, 16350, 24525, S]
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(3)]
+
+    def run():
+        cache = None
+        ev[0].record()
+        for lo, hi in zip(bounds[:-1], bounds[1:]):
+            _, cache = layer.prefill(x[:, lo:hi], cache)
+        ev[1].record()
+        for t in range(steps):
+            layer.step(x[:, S + t], cache)
+        ev[2].record()
+        torch.cuda.synchronize()
+        return ev[0].elapsed_time(ev[1]), ev[1].elapsed_time(ev[2])
+
+    run()
+    pf, dc = min(run() for _ in range(reps))
+    return dict(workload="GatedDeltaNet2 layer, BASELINE config 4: hidden 2048, H=16 HK=8 DK=DV=128, "
+                         "bf16, B=1, 32700-token prompt in 4 segments then 128 step() calls",
+                prefill_ms=round(pf, 3), prefill_tokens_per_s=round(S / (pf * 1e-3), 1),
+                decode_ms_128_steps=round(dc, 3), decode_steps_per_s=round(steps / (dc * 1e-3), 1),
+                timing="eager Python calls, HIP events, best of %d" % reps)
+
+
 def cpu_baseline(budget_s=12.0):
     """The oracle's chunkwise torch path (reference gdn2/reference.py:168-261)
     on the host cores, over repeated full config-1 prefills."""
@@ -219,6 +259,8 @@ def main():
     ap.add_argument("--no-decode", action="store_true", help="skip the decode configs")
     ap.add_argument("--prefill-only", action="store_true", help="prefill steps only (for profilers)")
     ap.add_argument("--decode-only", action="store_true", help="decode configs only (for profilers)")
+    ap.add_argument("--no-layer", action="store_true", help="skip the config-4 layer run")
+    ap.add_argument("--layer-only", action="store_true", help="config-4 layer run only (for profilers)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="three plain 1 GiB device copies (scales rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -242,6 +284,9 @@ def main():
     if args.decode_only:
         log(json.dumps({"config2_decode_step": bench_decode(64, 1, calls=64, steps_per_buf_min=1),
                         "config3_decode_multi_n8": bench_decode(32, 8, calls=64, steps_per_buf_min=1)}))
+        return
+    if args.layer_only:
+        log(json.dumps(bench_layer()))
         return
     ms_step, cl_ms, sc_ms = bench_prefill(args.steps, args.warmup)
     if args.prefill_only:
@@ -288,6 +333,8 @@ def main():
             "config2_decode_step": bench_decode(64, 1, calls=64, steps_per_buf_min=1),
             "config3_decode_multi_n8": bench_decode(32, 8, calls=64, steps_per_buf_min=1),
         }
+    if not args.no_layer:
+        out["layer"] = bench_layer()
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)

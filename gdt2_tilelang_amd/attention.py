@@ -224,6 +224,15 @@ class GatedDeltaNet2(nn.Module):
             self.__dict__[name] = hit
         return hit[1]
 
+    def _f32_cached(self, name, t):
+        """Contiguous fp32 copy of parameter ``t``, rebuilt only when it changes."""
+        key = (t.data_ptr(), t._version, t.dtype, t.device)
+        hit = self.__dict__.get(name)
+        if hit is None or hit[0] != key:
+            hit = (key, t.detach().float().contiguous())
+            self.__dict__[name] = hit
+        return hit[1]
+
     def _proj_weights(self):
         # one [4*HK*DK + 3*H*DV, hidden] weight: q | k | v | b | w | f | o_gate
         return self._cat_cached("_wcat", [self.q_proj.weight, self.k_proj.weight, self.v_proj.weight,
@@ -265,8 +274,8 @@ class GatedDeltaNet2(nn.Module):
                 conv_in = cache.conv_state.to(dt).contiguous()
             if cache is not None or conv_tail:
                 conv_out = torch.empty(B, 2 * dqk + dv, K - 1, device=dev, dtype=dt)
-        a_log = self.A_log.detach().float().contiguous()
-        dt_bias = self.dt_bias.detach().float().contiguous()
+        a_log = self._f32_cached("_alog32", self.A_log)
+        dt_bias = self._f32_cached("_dtb32", self.dt_bias)
         P = _hip.ptr
         _hip.check(_hip.lib().gdn2_hip_layer_prologue(
             *(base + o * es for o in offs), ld, ld, ld, ld, ld, ld, _hip.dtype_code(dt),
@@ -283,7 +292,7 @@ class GatedDeltaNet2(nn.Module):
         gate_ptr = proj.data_ptr() + (4 * dqk + 2 * dv) * proj.element_size()
         out = torch.empty(B, S, dv, device=x.device, dtype=x.dtype)
         o = o.contiguous()
-        weight = self.o_norm.weight.detach().float().contiguous()
+        weight = self._f32_cached("_onw32", self.o_norm.weight)
         _hip.check(_hip.lib().gdn2_hip_layer_epilogue(
             _hip.ptr(o), _hip.dtype_code(o.dtype), gate_ptr, ld, _hip.ptr(weight), float(self.o_norm.eps),
             _hip.ptr(out), _hip.dtype_code(x.dtype), dv, B, S, H, DV, _hip.stream_of(x.device)),
