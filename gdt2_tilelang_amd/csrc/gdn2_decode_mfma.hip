@@ -233,7 +233,11 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(
   float wv[TB];
   col_wv(L0, c0, wv);
 
-  for (int tb = 0; tb < n; tb += TB) {
+  // One block of up to TB tokens. The first block is applied outside the loop
+  // so that the state registers flow into it straight from their loads: inside
+  // the loop they are loop-carried, and the register copies that entering the
+  // loop needs would wait for every state load before the staging below.
+  auto block = [&](const int tb) __attribute__((always_inline)) {
     const int L = min(TB, n - tb);
     const bool last = tb + TB >= n;
     if (tb == 0) {
@@ -255,22 +259,8 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(
     }
     lds_barrier();
 
-    // ---- P_e = (state columns 2m+e)^T V: 16 projections per column (fp32 MFMA),
-    // consuming the state rows as they arrive (a wave past DV works on zeros),
-    // then this wave's share of the Gram coefficients: lane = pair, channel
-    // quads split across the waves. With four waves both sit in one basic block
-    // so the Gram VALU work can issue under the MFMAs.
-    f32x4 P[2][2];
-#pragma unroll
-    for (int e = 0; e < 2; ++e) P[e][0] = P[e][1] = zero4();
-#pragma unroll
-    for (int s = 0; s < NS; s += 4) {
-      const f32x4 bv = *reinterpret_cast<const f32x4*>(&sm.vec[m][NS * kq + s]);
-#pragma unroll
-      for (int ss = 0; ss < 4; ++ss)
-#pragma unroll
-        for (int e = 0; e < 2; ++e) P[e][ss & 1] = mfma4(T[e][s / 4][ss], bv[ss], P[e][ss & 1]);
-    }
+    // ---- this wave's share of the Gram coefficients: lane = pair, channel quads
+    // split across the waves (LDS only: no wait on the state loads)
     {
       const int code = gram_code(lane);
       const int tau = code & 7, t = (code >> 3) & 7;
@@ -305,6 +295,20 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(
     }
     lds_barrier();
 
+    // ---- P_e = (state columns 2m+e)^T V: 16 projections per column (fp32 MFMA),
+    // consuming the state rows as they arrive (a wave past DV works on zeros).
+    // In the first block the Gram work above runs while the state is in flight.
+    f32x4 P[2][2];
+#pragma unroll
+    for (int e = 0; e < 2; ++e) P[e][0] = P[e][1] = zero4();
+#pragma unroll
+    for (int s = 0; s < NS; s += 4) {
+      const f32x4 bv = *reinterpret_cast<const f32x4*>(&sm.vec[m][NS * kq + s]);
+#pragma unroll
+      for (int ss = 0; ss < 4; ++ss)
+#pragma unroll
+        for (int e = 0; e < 2; ++e) P[e][ss & 1] = mfma4(T[e][s / 4][ss], bv[ss], P[e][ss & 1]);
+    }
     if (active) {
       // D layout: lane (kq, m) holds P[col 2(4kq + r) + e][vector m]
       float* pst = sm.pst[wave];
@@ -382,7 +386,9 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(
       }
     }
     lds_barrier();   // the block's staging is read by every wave before it is replaced
-  }
+  };
+  block(0);
+  for (int tb = TB; tb < n; tb += TB) block(tb);
 }
 
 template <int DK, int IN_DT, int OUT_DT>
