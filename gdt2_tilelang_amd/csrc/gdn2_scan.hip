@@ -11,17 +11,23 @@
 //   o  = Qg S + Aqk Un                     (Qg = scale * q * gamma)
 //   S  = diag(gamma_last) S + KG^T Un
 //
-// Every product splits both operands into bf16 hi + lo (three MFMAs), so it
-// keeps ~16 mantissa bits. Z, S and Un are split from fp32; the record
-// matrices are stored as fp16 with a power-of-two scale per matrix and split
-// exactly (an fp16 significand is 11 bits). W S needs the precision: with
-// little decay the state is large and Un = U - W S is a small difference of
-// large terms.
+// Precision. The record matrices are fp16 with a power-of-two scale per
+// matrix (11-bit significands, exact). The four products with the state or Un
+// (W S, Qg S, KG^T Un, Aqk Un) run on fp16 MFMAs straight from the record
+// fragments: S and Un are split into fp16 hi + lo (~22 bits) after scaling
+// each value column by a power of two that puts the column's largest entry in
+// [2^14, 2^15), so the split is exact up to fp32 round-off and cannot
+// overflow; the scale is undone on the fp32 accumulator. U = Ai Z splits both
+// operands into bf16 hi + lo (three MFMAs, ~16 bits; Ai's fp16 values split
+// exactly). W S needs the precision: with little decay the state is large and
+// Un = U - W S is a small difference of large terms.
 //
 // Eight waves. Phase 1: waves 0-3 form Un for output row block m = w (U and
-// W S), waves 4-7 form Qg S for the same blocks. A barrier hands Un over
-// through LDS. Phase 2: wave w updates state rows 16w..16w+15 with KG^T Un and
-// waves 4-7 finish o with Aqk Un. A second barrier hands the new state over.
+// W S), waves 4-7 form Qg S for the same blocks. The column maxima of Un meet
+// in LDS (barrier), then Un is split at the common column scales and handed
+// over (barrier). Phase 2: wave w updates state rows 16w..16w+15 with KG^T Un
+// and waves 4-7 finish o with Aqk Un; the new state is handed over the same
+// way as Un (column maxima, barrier, split, barrier).
 // LDS holds S^T, Z and Un in B-operand order ([column][k], k contiguous); Z is
 // double-buffered so the next chunk's Z is staged while the current one is in
 // use. Record fragments are double-buffered in registers by chunk parity and
@@ -77,12 +83,12 @@ __device__ __forceinline__ void load_frags_p1(const unsigned short* __restrict__
   f.sx = rec_scale<DK>(rec, un ? SC_W : SC_QG);
 }
 
-// Fragments of the state-update phase (state tile wave, when DK/16 > wave).
+// Fragments of the state-update phase (state tile wave).
 template <int DK>
 __device__ __forceinline__ void load_frags_p2(const unsigned short* __restrict__ rec, int wave,
                                               int lane, int lq, ScanFrags<DK>& f) {
   using L = ChunkLayout<DK>;
-  if (wave >= DK / 16) return;
+  wave = wave < DK / 16 ? wave : DK / 16 - 1;   // a wave without a tile holds the last one's (unused)
   const int o8 = lane * 8;
 #pragma unroll
   for (int kk = 0; kk < 2; ++kk) f.k[kk] = *reinterpret_cast<const uint4*>(rec + L::kt_frag(wave, kk) + o8);
@@ -118,13 +124,52 @@ struct Raw4 {
   }
 };
 
-// packed pair store of a D-layout quad (4 consecutive k for one column) as hi/lo
-__device__ __forceinline__ void put_quad(unsigned short* hi, unsigned short* lo, const f32x4& x) {
-  uint32_t h0, l0, h1, l1;
-  split_pk(x[0], x[1], h0, l0);
-  split_pk(x[2], x[3], h1, l1);
-  *reinterpret_cast<uint2*>(hi) = make_uint2(h0, h1);
-  *reinterpret_cast<uint2*>(lo) = make_uint2(l0, l1);
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+// A (fp16 record fragment) times B (fp16): v_mfma_f32_16x16x32_f16, whose
+// operand layout is that of the bf16 instruction.
+__device__ __forceinline__ f32x4 mfma_f16(const uint4& a, const uint4& b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                0, 0, 0);
+}
+// exact fp16 A times a B operand split into fp16 hi + lo
+__device__ __forceinline__ f32x4 mfma2(const uint4& a, const uint4& bh, const uint4& bl, f32x4 c) {
+  c = mfma_f16(a, bh, c);
+  return mfma_f16(a, bl, c);
+}
+
+// max |x| over the column of a D-layout 16 x 16 tile (lane (lq, lr) holds rows
+// 4lq .. 4lq+3 of column lr); every lane of the column gets it. Lanes 32 and 16
+// apart are combined with the permlane swaps (VALU, no LDS).
+__device__ __forceinline__ float tile_col_max(const f32x4& x) {
+  float m = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+  uint32_t u = __float_as_uint(m);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  m = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+  u = __float_as_uint(m);
+  const auto r16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+}
+
+// Power-of-two scale 2^s putting mx in [2^14, 2^15) (s clamped to +-126, so a
+// zero column gets 2^126 and stays zero); *inv = 2^-s exactly.
+__device__ __forceinline__ float col_scale(float mx, float* inv) {
+  const int ex = static_cast<int>((__float_as_uint(mx) >> 23) & 0xffu);   // biased exponent
+  int se = 141 - ex;                                                       // 14 - unbiased exponent
+  se = se < -126 ? -126 : (se > 126 ? 126 : se);
+  *inv = __uint_as_float(static_cast<uint32_t>(127 - se) << 23);
+  return __uint_as_float(static_cast<uint32_t>(127 + se) << 23);
+}
+
+// A D-layout quad (4 consecutive k of one column) times sc as fp16 hi + lo:
+// hi rounds toward zero, lo is the exact fp32 remainder rounded to fp16.
+__device__ __forceinline__ void put_quad_f16(unsigned short* hi, unsigned short* lo, const f32x4& x, float sc) {
+  const float a = x[0] * sc, b = x[1] * sc, c = x[2] * sc, d = x[3] * sc;
+  const auto h01 = __builtin_amdgcn_cvt_pkrtz(a, b), h23 = __builtin_amdgcn_cvt_pkrtz(c, d);
+  const auto l01 = __builtin_amdgcn_cvt_pkrtz(a - static_cast<float>(h01[0]), b - static_cast<float>(h01[1]));
+  const auto l23 = __builtin_amdgcn_cvt_pkrtz(c - static_cast<float>(h23[0]), d - static_cast<float>(h23[1]));
+  *reinterpret_cast<uint2*>(hi) = make_uint2(__builtin_bit_cast(uint32_t, h01), __builtin_bit_cast(uint32_t, h23));
+  *reinterpret_cast<uint2*>(lo) = make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23));
 }
 
 template <int DK, int NT, int IN_DT, int OUT_DT>
@@ -144,6 +189,10 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
   __shared__ __align__(16) unsigned short sSh[2][DVT * SP], sSl[2][DVT * SP];
   __shared__ __align__(16) unsigned short sZh[2][DVT * TP], sZl[2][DVT * TP];
   __shared__ __align__(16) unsigned short sNh[DVT * TP], sNl[DVT * TP];
+  // S^T and Un are fp16 hi / lo at per-column power-of-two scales: the column
+  // maxima of each producing wave, and the inverse scales the consumers apply
+  __shared__ float sSmx[MT][DVT], sSinv[2][DVT];
+  __shared__ float sNmx[4][DVT], sNinv[DVT];
   // output staging: one 16 x 16 tile per output wave, row-major, in OUT_DT
   constexpr int OSZ = OUT_DT == DT_F32 ? 4 : 2;
   __shared__ __align__(16) unsigned char sO[4][16 * 16 * OSZ];
@@ -228,13 +277,30 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
       const int c = 16 * wave + 4 * lq + e;
       S[nn][e] = (s_in && owns) ? s_in[(static_cast<size_t>(bh) * DK + c) * DV + d0 + 16 * nn + lr] : 0.f;
     }
+  // Hand the state to the B-operand buffer `buf` (every wave calls it: it
+  // contains a barrier): column maxima of each owner's rows, then the split at
+  // the common column scale.
   auto put_state = [&](int buf) {
+    if (owns) {
+#pragma unroll
+      for (int nn = 0; nn < NT; ++nn) {
+        const float mx = tile_col_max(S[nn]);      // all lanes: the permlanes read every lane
+        if (lq == 0) sSmx[wave][16 * nn + lr] = mx;
+      }
+    }
+    __syncthreads();
     if (!owns) return;
 #pragma unroll
     for (int nn = 0; nn < NT; ++nn) {
       const int col = 16 * nn + lr;
+      float mx = sSmx[0][col];
+#pragma unroll
+      for (int ww = 1; ww < MT; ++ww) mx = fmaxf(mx, sSmx[ww][col]);
+      float inv;
+      const float sc = col_scale(mx, &inv);
       const int c = 16 * wave + 4 * lq;
-      put_quad(&sSh[buf][col * SP + c], &sSl[buf][col * SP + c], S[nn]);
+      put_quad_f16(&sSh[buf][col * SP + c], &sSl[buf][col * SP + c], S[nn], sc);
+      if (wave == 0 && lq == 0) sSinv[buf][col] = inv;
     }
   };
 
@@ -277,8 +343,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
 #pragma unroll
       for (int kk = 0; kk < 2; ++kk) {
         bf16x8 ah, al;
-        f16x8_to_bf16_hilo(cur.a[kk], ah, al);
-        cur.a[kk] = frag(rp, L::ai_frag(m, kk));
+        f16x8_to_bf16_hilo(cur.a[kk], ah, al);     // refilled in phase 2
 #pragma unroll
         for (int nn = 0; nn < NT; ++nn) {
           const int col = 16 * nn + lr;
@@ -290,80 +355,93 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
     }
 #pragma unroll
     for (int kk = 0; kk < KT; ++kk) {
-      bf16x8 xh, xl;
-      f16x8_to_bf16_hilo(cur.x[kk], xh, xl);
-      cur.x[kk] = frag(rp, un_role ? L::w_frag(m, kk) : L::qg_frag(m, kk));
 #pragma unroll
       for (int nn = 0; nn < NT; ++nn) {
         const int col = 16 * nn + lr;
-        const bf16x8 sh = *reinterpret_cast<const bf16x8*>(&sSh[buf][col * SP + 32 * kk + 8 * lq]);
-        const bf16x8 sl = *reinterpret_cast<const bf16x8*>(&sSl[buf][col * SP + 32 * kk + 8 * lq]);
-        X[nn] = mfma3(xh, xl, sh, sl, X[nn]);
+        const uint4 sh = *reinterpret_cast<const uint4*>(&sSh[buf][col * SP + 32 * kk + 8 * lq]);
+        const uint4 sl = *reinterpret_cast<const uint4*>(&sSl[buf][col * SP + 32 * kk + 8 * lq]);
+        X[nn] = mfma2(cur.x[kk], sh, sl, X[nn]);
       }
+      // refilled after its last use, into the same registers
+      cur.x[kk] = frag(rp, un_role ? L::w_frag(m, kk) : L::qg_frag(m, kk));
     }
+    // X is W S (or Qg S) at the record scale times the state's column scale
+    float xs[NT];
+#pragma unroll
+    for (int nn = 0; nn < NT; ++nn) xs[nn] = sx * sSinv[buf][16 * nn + lr];
     cur.sx = rec_scale<DK>(rp, un_role ? SC_W : SC_QG);
+    f32x4 un[NT];
     if (un_role) {
       cur.sa = rec_scale<DK>(rp, SC_AI);
 #pragma unroll
       for (int nn = 0; nn < NT; ++nn) {
-        const int col = 16 * nn + lr;
-        const f32x4 un = A[nn] * sa - X[nn] * sx;
-        const int t = 16 * m + 4 * lq;
-        put_quad(&sNh[col * TP + t], &sNl[col * TP + t], un);
+        un[nn] = A[nn] * sa - X[nn] * xs[nn];
+        const float mx = tile_col_max(un[nn]);
+        if (lq == 0) sNmx[m][16 * nn + lr] = mx;
       }
     }
     put_z(Other{});     // that LDS buffer was last read in chunk nc-1 (a clamped copy at the end)
     __syncthreads();
-
-    // ---- phase 2: S = diag(gamma_last) S + KG^T Un (state tile = wave);
-    //      waves 4-7 finish o = Qg S + Aqk Un for row block m -------------------
-    // The KG^T and Aqk records carry power-of-two scales: S is held divided
-    // by sk across the update (exact) and Qg S is brought to Aqk's scale.
-    const float sk = cur.sk;
-    if (owns) {
-      const float ik = 1.f / sk;
-      const float4 gk = make_float4(cur.gam.x * ik, cur.gam.y * ik, cur.gam.z * ik, cur.gam.w * ik);
-#pragma unroll
-      for (int nn = 0; nn < NT; ++nn) {
-        S[nn][0] *= gk.x; S[nn][1] *= gk.y;
-        S[nn][2] *= gk.z; S[nn][3] *= gk.w;
-      }
-      cur.gam = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(rp + L::GL_OFF) + 16 * wave + 4 * lq);
-      cur.sk = rec_scale<DK>(rp, SC_KT);
-    }
-    if (!un_role) {
-      const float r = sx / sa;
-#pragma unroll
-      for (int nn = 0; nn < NT; ++nn) X[nn] = X[nn] * r;
-      cur.sa = rec_scale<DK>(rp, SC_AQK);
-    }
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-      bf16x8 kh, kl, ah, al;
-      if (owns) {
-        f16x8_to_bf16_hilo(cur.k[kk], kh, kl);
-        cur.k[kk] = frag(rp, L::kt_frag(wave, kk));
-      }
-      if (!un_role) {
-        f16x8_to_bf16_hilo(cur.a[kk], ah, al);
-        cur.a[kk] = frag(rp, L::aqk_frag(m, kk));
-      }
+    if (un_role) {      // Un at the common column scales of the four row blocks
 #pragma unroll
       for (int nn = 0; nn < NT; ++nn) {
         const int col = 16 * nn + lr;
-        const bf16x8 nh = *reinterpret_cast<const bf16x8*>(&sNh[col * TP + 32 * kk + 8 * lq]);
-        const bf16x8 nl = *reinterpret_cast<const bf16x8*>(&sNl[col * TP + 32 * kk + 8 * lq]);
-        if (owns) S[nn] = mfma3(kh, kl, nh, nl, S[nn]);
-        if (!un_role) X[nn] = mfma3(ah, al, nh, nl, X[nn]);
+        const float mx = fmaxf(fmaxf(sNmx[0][col], sNmx[1][col]), fmaxf(sNmx[2][col], sNmx[3][col]));
+        float inv;
+        const float sc = col_scale(mx, &inv);
+        const int t = 16 * m + 4 * lq;
+        put_quad_f16(&sNh[col * TP + t], &sNl[col * TP + t], un[nn], sc);
+        if (m == 0 && lq == 0) sNinv[col] = inv;
       }
     }
+    __syncthreads();
+
+    // ---- phase 2: S = diag(gamma_last) S + KG^T Un (state tile = wave);
+    //      waves 4-7 finish o = Qg S + Aqk Un for row block m -------------------
+    // The KG^T and Aqk records carry power-of-two scales, Un its column
+    // scales: both are undone on the fresh accumulators T (KG^T Un) and Y
+    // (Aqk Un).
+    const float sk = cur.sk;
+    // Refills are unconditional (a wave without a state tile re-reads the last
+    // tile's fragments), so every path through the loop has the same loads and
+    // the compiler's wait counts never fall back to waiting for all of them.
+    const int kt_tile = owns ? wave : MT - 1;
+    const float4 gk = cur.gam;
+    cur.gam = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(rp + L::GL_OFF) + 16 * kt_tile + 4 * lq);
+    cur.sk = rec_scale<DK>(rp, SC_KT);
+    if (!un_role) cur.sa = rec_scale<DK>(rp, SC_AQK);
+    f32x4 T[NT], Y[NT];
+#pragma unroll
+    for (int nn = 0; nn < NT; ++nn) { T[nn] = zero4(); Y[nn] = zero4(); }
+#pragma unroll
+    for (int kk = 0; kk < 2; ++kk) {
+#pragma unroll
+      for (int nn = 0; nn < NT; ++nn) {
+        const int col = 16 * nn + lr;
+        const uint4 nh = *reinterpret_cast<const uint4*>(&sNh[col * TP + 32 * kk + 8 * lq]);
+        const uint4 nl = *reinterpret_cast<const uint4*>(&sNl[col * TP + 32 * kk + 8 * lq]);
+        if (owns) T[nn] = mfma2(cur.k[kk], nh, nl, T[nn]);
+        if (!un_role) Y[nn] = mfma2(cur.a[kk], nh, nl, Y[nn]);
+      }
+      cur.k[kk] = frag(rp, L::kt_frag(kt_tile, kk));
+      cur.a[kk] = frag(rp, un_role ? L::ai_frag(m, kk) : L::aqk_frag(m, kk));
+    }
+    float ni[NT];
+#pragma unroll
+    for (int nn = 0; nn < NT; ++nn) ni[nn] = sNinv[16 * nn + lr];
     if (owns) {
 #pragma unroll
-      for (int nn = 0; nn < NT; ++nn) S[nn] = S[nn] * sk;
+      for (int nn = 0; nn < NT; ++nn) {
+        const float f = sk * ni[nn];
+        S[nn][0] = S[nn][0] * gk.x + T[nn][0] * f;
+        S[nn][1] = S[nn][1] * gk.y + T[nn][1] * f;
+        S[nn][2] = S[nn][2] * gk.z + T[nn][2] * f;
+        S[nn][3] = S[nn][3] * gk.w + T[nn][3] * f;
+      }
     }
     if (!un_role) {
 #pragma unroll
-      for (int nn = 0; nn < NT; ++nn) X[nn] = X[nn] * sa;
+      for (int nn = 0; nn < NT; ++nn) X[nn] = X[nn] * xs[nn] + Y[nn] * (sa * ni[nn]);
       // o tile (rows 16m + 4lq + e, columns 16nn + lr in D layout) -> LDS,
       // then 16 contiguous bytes per lane to global memory
       unsigned char* so = sO[m];
