@@ -185,14 +185,18 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
   constexpr int TP = kBS + 8;          // bf16 pitch of [DVT][64] arrays
   constexpr int ZQ = kBS * DVT / 4;    // Z quads per chunk tile
   constexpr int ZIT = (ZQ + kScanThreads - 1) / kScanThreads;
+  // With fewer Z quads than threads the output waves (the upper threads) stage
+  // Z: the Un waves carry the longer phase 1.
+  constexpr int ZOFF = ZQ < kScanThreads ? kScanThreads - ZQ : 0;
 
   __shared__ __align__(16) unsigned short sSh[2][DVT * SP], sSl[2][DVT * SP];
   __shared__ __align__(16) unsigned short sZh[2][DVT * TP], sZl[2][DVT * TP];
   __shared__ __align__(16) unsigned short sNh[DVT * TP], sNl[DVT * TP];
   // S^T and Un are fp16 hi / lo at per-column power-of-two scales: the column
   // maxima of each producing wave, and the inverse scales the consumers apply
-  __shared__ float sSmx[MT][DVT], sSinv[2][DVT];
-  __shared__ float sNmx[4][DVT], sNinv[DVT];
+  __shared__ __align__(16) float sSmx[DVT][MT];
+  __shared__ __align__(16) float sNmx[DVT][4];
+  __shared__ float sSinv[2][DVT], sNinv[DVT];
   // output staging: one 16 x 16 tile per output wave, row-major, in OUT_DT
   constexpr int OSZ = OUT_DT == DT_F32 ? 4 : 2;
   __shared__ __align__(16) unsigned char sO[4][16 * 16 * OSZ];
@@ -238,8 +242,8 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
     constexpr int p = decltype(parity)::value;
 #pragma unroll
     for (int it = 0; it < ZIT; ++it) {
-      const int e = tid + kScanThreads * it;
-      if (e >= ZQ) break;
+      const int e = tid - ZOFF + kScanThreads * it;
+      if (e < 0 || e >= ZQ) break;
       const int t = e / (DVT / 4), cq = e % (DVT / 4);
       const size_t idx = ((static_cast<size_t>(bi) * s_alloc + t0 + static_cast<long>(nc) * kBS + t) * H + h) * DV + d0 + 4 * cq;
       zv[p][it].load(v, idx);
@@ -250,8 +254,8 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
     constexpr int buf = decltype(parity)::value;
 #pragma unroll
     for (int it = 0; it < ZIT; ++it) {
-      const int e = tid + kScanThreads * it;
-      if (e >= ZQ) break;
+      const int e = tid - ZOFF + kScanThreads * it;
+      if (e < 0 || e >= ZQ) break;
       const int t = e / (DVT / 4), cq = e % (DVT / 4);
       float a[4], b[4];
       zv[buf][it].get(a);
@@ -285,7 +289,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
 #pragma unroll
       for (int nn = 0; nn < NT; ++nn) {
         const float mx = tile_col_max(S[nn]);      // all lanes: the permlanes read every lane
-        if (lq == 0) sSmx[wave][16 * nn + lr] = mx;
+        if (lq == 0) sSmx[16 * nn + lr][wave] = mx;
       }
     }
     __syncthreads();
@@ -293,9 +297,12 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
 #pragma unroll
     for (int nn = 0; nn < NT; ++nn) {
       const int col = 16 * nn + lr;
-      float mx = sSmx[0][col];
+      float mx = 0.f;
 #pragma unroll
-      for (int ww = 1; ww < MT; ++ww) mx = fmaxf(mx, sSmx[ww][col]);
+      for (int ww = 0; ww < MT; ww += 4) {
+        const float4 x = *reinterpret_cast<const float4*>(&sSmx[col][ww]);
+        mx = fmaxf(mx, fmaxf(fmaxf(x.x, x.y), fmaxf(x.z, x.w)));
+      }
       float inv;
       const float sc = col_scale(mx, &inv);
       const int c = 16 * wave + 4 * lq;
@@ -327,10 +334,36 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
     return *reinterpret_cast<const uint4*>(rec + off + o8);
   };
 
+  // o tile of chunk nc (rows 16m + 4lq + e, columns 16nn + lr in D layout) ->
+  // LDS, then 16 contiguous bytes per lane to global memory (output waves)
+  f32x4 Opend[NT];
+  auto store_o = [&](int nc) {
+    const long tok0 = t0 + static_cast<long>(nc) * kBS;
+    unsigned char* so = sO[m];
+#pragma unroll
+    for (int nn = 0; nn < NT; ++nn) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int idx = (4 * lq + e) * 16 + lr;
+        if constexpr (OUT_DT == DT_F32) reinterpret_cast<float*>(so)[idx] = Opend[nn][e];
+        else if constexpr (OUT_DT == DT_BF16) reinterpret_cast<unsigned short*>(so)[idx] = f32_to_bf16_bits(Opend[nn][e]);
+        else reinterpret_cast<unsigned short*>(so)[idx] = f32_to_f16_bits(Opend[nn][e]);
+      }
+      __builtin_amdgcn_wave_barrier();
+      constexpr int LPR = 16 * OSZ / 16;          // lanes per 16-element row (2 or 4)
+      if (lane < 16 * LPR) {
+        const int r = lane / LPR, c = (lane % LPR) * (16 / OSZ);
+        const uint4 x = *reinterpret_cast<const uint4*>(so + (r * 16 + c) * OSZ);
+        const size_t oi = ((static_cast<size_t>(bi) * s_alloc + tok0 + 16 * m + r) * H + h) * DV + d0 + 16 * nn + c;
+        *reinterpret_cast<uint4*>(static_cast<unsigned char*>(o) + oi * OSZ) = x;
+      }
+      __builtin_amdgcn_wave_barrier();
+    }
+  };
+
   auto step = [&](auto parity, ScanFrags<DK>& cur, int nc) {
     constexpr int buf = decltype(parity)::value;   // == nc & 1
     using Other = std::integral_constant<int, buf ^ 1>;
-    const long tok0 = t0 + static_cast<long>(nc) * kBS;
     const int pre = min(nc + 2, last);
     const unsigned short* rp = rec0 + static_cast<size_t>(pre) * L::STRIDE;
 
@@ -365,6 +398,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
       // refilled after its last use, into the same registers
       cur.x[kk] = frag(rp, un_role ? L::w_frag(m, kk) : L::qg_frag(m, kk));
     }
+    if (!un_role && nc > 0) store_o(nc - 1);
     // X is W S (or Qg S) at the record scale times the state's column scale
     float xs[NT];
 #pragma unroll
@@ -377,7 +411,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
       for (int nn = 0; nn < NT; ++nn) {
         un[nn] = A[nn] * sa - X[nn] * xs[nn];
         const float mx = tile_col_max(un[nn]);
-        if (lq == 0) sNmx[m][16 * nn + lr] = mx;
+        if (lq == 0) sNmx[16 * nn + lr][m] = mx;
       }
     }
     put_z(Other{});     // that LDS buffer was last read in chunk nc-1 (a clamped copy at the end)
@@ -386,7 +420,8 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
 #pragma unroll
       for (int nn = 0; nn < NT; ++nn) {
         const int col = 16 * nn + lr;
-        const float mx = fmaxf(fmaxf(sNmx[0][col], sNmx[1][col]), fmaxf(sNmx[2][col], sNmx[3][col]));
+        const float4 x4 = *reinterpret_cast<const float4*>(&sNmx[col][0]);
+        const float mx = fmaxf(fmaxf(x4.x, x4.y), fmaxf(x4.z, x4.w));
         float inv;
         const float sc = col_scale(mx, &inv);
         const int t = 16 * m + 4 * lq;
@@ -441,29 +476,8 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
     }
     if (!un_role) {
 #pragma unroll
-      for (int nn = 0; nn < NT; ++nn) X[nn] = X[nn] * xs[nn] + Y[nn] * (sa * ni[nn]);
-      // o tile (rows 16m + 4lq + e, columns 16nn + lr in D layout) -> LDS,
-      // then 16 contiguous bytes per lane to global memory
-      unsigned char* so = sO[m];
-#pragma unroll
-      for (int nn = 0; nn < NT; ++nn) {
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const int idx = (4 * lq + e) * 16 + lr;
-          if constexpr (OUT_DT == DT_F32) reinterpret_cast<float*>(so)[idx] = X[nn][e];
-          else if constexpr (OUT_DT == DT_BF16) reinterpret_cast<unsigned short*>(so)[idx] = f32_to_bf16_bits(X[nn][e]);
-          else reinterpret_cast<unsigned short*>(so)[idx] = f32_to_f16_bits(X[nn][e]);
-        }
-        __builtin_amdgcn_wave_barrier();
-        constexpr int LPR = 16 * OSZ / 16;          // lanes per 16-element row (2 or 4)
-        if (lane < 16 * LPR) {
-          const int r = lane / LPR, c = (lane % LPR) * (16 / OSZ);
-          const uint4 x = *reinterpret_cast<const uint4*>(so + (r * 16 + c) * OSZ);
-          const size_t oi = ((static_cast<size_t>(bi) * s_alloc + tok0 + 16 * m + r) * H + h) * DV + d0 + 16 * nn + c;
-          *reinterpret_cast<uint4*>(static_cast<unsigned char*>(o) + oi * OSZ) = x;
-        }
-        __builtin_amdgcn_wave_barrier();
-      }
+      // stored in the next chunk's phase 1, where these waves have slack
+      for (int nn = 0; nn < NT; ++nn) Opend[nn] = X[nn] * xs[nn] + Y[nn] * (sa * ni[nn]);
     }
     put_state(buf ^ 1);
     fetch_z(parity, pre);
@@ -476,6 +490,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
     step(P1{}, fr[1], nc + 1);
   }
   if (nc < NC) step(P0{}, fr[0], nc);
+  if (!un_role && NC > 0) store_o(NC - 1);
 
   if (!owns) return;
 #pragma unroll
