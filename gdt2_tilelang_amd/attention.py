@@ -272,6 +272,8 @@ class GatedDeltaNet2(nn.Module):
                 conv_b = conv_b.to(dt).reshape(-1) if conv_b.dtype != dt else conv_b.reshape(-1)
             if cache is not None and cache.conv_state is not None:
                 conv_in = cache.conv_state.to(dt).contiguous()
+                if conv_in.data_ptr() % 16:          # the kernel reads 16-byte vectors
+                    conv_in = conv_in.clone()
             if cache is not None or conv_tail:
                 conv_out = torch.empty(B, 2 * dqk + dv, K - 1, device=dev, dtype=dt)
         a_log = self._f32_cached("_alog32", self.A_log)

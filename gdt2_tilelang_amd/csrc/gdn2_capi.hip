@@ -143,6 +143,9 @@ int gdn2_hip_layer_prologue(const void* xq, const void* xk, const void* xv, cons
   for (int i = 0; i < 6; ++i)
     if (reinterpret_cast<uintptr_t>(outs[i]) % 16) return GDN2_ERR_ARG;
   if (conv_w && (conv_k < 1 || conv_k > 4)) return GDN2_ERR_SHAPE;
+  const void* cv[4] = {conv_w, conv_b, conv_in, conv_out};   // read / written as 16-byte vectors
+  for (int i = 0; i < 4; ++i)
+    if (conv_w && reinterpret_cast<uintptr_t>(cv[i]) % 16) return GDN2_ERR_ARG;
   if (conv_w && conv_out && conv_out == conv_in) return GDN2_ERR_ARG;   // the tail is read while written
   if (static_cast<long>(B) * S > 0x7fffffffL) return GDN2_ERR_SHAPE;
   gdn2::lay::ProArgs a;

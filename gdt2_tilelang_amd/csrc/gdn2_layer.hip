@@ -95,16 +95,19 @@ __device__ __forceinline__ void st8(void* p, long i, const float* x) {
 // DK/8 consecutive lanes of one wave, whose squared sums are combined with
 // lane shuffles. Small token counts (decode) still spread over
 // (C + 2*HK*DK + H*DV) / 8 / kProThreads workgroups.
-template <int DT>
+// KC: conv width (0: no conv), a template argument so that every register
+// array below is indexed at compile time.
+template <int DT, int KC>
 __global__ __launch_bounds__(kProThreads) void prologue_kernel(ProArgs a) {
+  static_assert(TT >= kMaxConv - 1, "a window reaching before the segment must start at token 0");
   const int bi = blockIdx.z;
   const long t0 = static_cast<long>(blockIdx.x) * TT;
   const int nt = static_cast<int>(min(static_cast<long>(TT), a.S - t0));
   const int tid = threadIdx.x;
   const int dqk = a.HK * a.DK, dv = a.H * a.DV;
   const long C = 2L * dqk + dv;
-  const int K = a.K;
-  const bool conv = a.conv_w != nullptr;
+  constexpr int K = KC;
+  constexpr bool conv = KC > 0;
   const int group = a.DK / 8;                   // lanes per q / k head
   const int nconv = static_cast<int>(C / 8);
   const long row0 = static_cast<long>(bi) * a.S;
@@ -118,43 +121,70 @@ __global__ __launch_bounds__(kProThreads) void prologue_kernel(ProArgs a) {
     const void* x = a.x[which];
     const long ldx = a.ld[which];
     float y[TT][8];
-    if (conv) {
-      float wt[kMaxConv][8], bias[8];
+    if constexpr (conv) {
+      // Every load of the item is issued up front as 16-byte vectors (this
+      // kernel also runs for a single decode token, where it is latency-bound):
+      // the item's weights [8 channels][K], bias, cached conv tail
+      // [8 channels][K-1] and its window of input rows t0-(K-1) .. t0+nt-1.
+      constexpr int K1 = K - 1;
+      float wflat[8 * K], cin[8 * K1 + 1], bias[8];
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        bias[e] = a.conv_b ? ld<DT>(a.conv_b, c0 + e) : 0.f;
+      for (int c = 0; c < K; ++c) ld8<DT>(a.conv_w, static_cast<long>(c0) * K + 8 * c, wflat + 8 * c);
+      if (a.conv_b) ld8<DT>(a.conv_b, c0, bias);
+      else {
 #pragma unroll
-        for (int j = 0; j < kMaxConv; ++j) wt[j][e] = j < K ? ld<DT>(a.conv_w, static_cast<long>(c0 + e) * K + j) : 0.f;
+        for (int e = 0; e < 8; ++e) bias[e] = 0.f;
       }
+      const bool need_cin = t0 < K1;                   // window reaches before the segment
 #pragma unroll
-      for (int t = 0; t < TT; ++t)
+      for (int c = 0; c < K1; ++c) {
+        if (need_cin && a.conv_in) ld8<DT>(a.conv_in, (static_cast<long>(bi) * C + c0) * K1 + 8 * c, cin + 8 * c);
+        else {
 #pragma unroll
-        for (int e = 0; e < 8; ++e) y[t][e] = bias[e];
-      // input row r = t0 - (K-1) + r, r < TT + K - 1; each feeds the outputs t with j = r - t
+          for (int e = 0; e < 8; ++e) cin[8 * c + e] = 0.f;
+        }
+      }
+      // window row r is the input at position t0 - K1 + r, r < nt + K1; a
+      // position before the segment (then t0 = 0, so row r < K1) is tail entry r
+      float win[TT + K1][8];
 #pragma unroll
-      for (int r = 0; r < TT + kMaxConv - 1; ++r) {
-        if (r >= nt + K - 1) break;
-        const long p = t0 - (K - 1) + r;
-        float in[8];
-        if (p >= 0) {
-          ld8<DT>(x, (row0 + p) * ldx + cx, in);
+      for (int r = 0; r < TT + K1; ++r) {
+        const long p = t0 - K1 + r;
+        if (r < nt + K1 && p >= 0) ld8<DT>(x, (row0 + p) * ldx + cx, win[r]);
+        else if (r < K1 && p < 0) {
+#pragma unroll
+          for (int e = 0; e < 8; ++e) win[r][e] = cin[e * K1 + r];
         } else {
 #pragma unroll
-          for (int e = 0; e < 8; ++e)
-            in[e] = a.conv_in ? ld<DT>(a.conv_in, (static_cast<long>(bi) * C + c0 + e) * (K - 1) + (p + K - 1)) : 0.f;
-        }
-#pragma unroll
-        for (int t = 0; t < TT; ++t) {
-          const int j = r - t;
-          if (j < 0 || j >= K) continue;
-#pragma unroll
-          for (int e = 0; e < 8; ++e) y[t][e] += wt[j][e] * in[e];
+          for (int e = 0; e < 8; ++e) win[r][e] = 0.f;
         }
       }
 #pragma unroll
       for (int t = 0; t < TT; ++t)
 #pragma unroll
-        for (int e = 0; e < 8; ++e) y[t][e] = silu(y[t][e]);
+        for (int e = 0; e < 8; ++e) {
+          float acc = bias[e];
+#pragma unroll
+          for (int jj = 0; jj < K; ++jj) acc += wflat[e * K + jj] * win[t + jj][e];
+          y[t][e] = silu(acc);
+        }
+      // new conv tail (entry i = the input at position S - K1 + i = window row
+      // nt + i of the last token block), 8*K1 contiguous values
+      if constexpr (K1 > 0) if (a.conv_out && t0 + nt == a.S) {
+#pragma unroll
+        for (int c = 0; c < K1; ++c) {
+          float z[8];
+#pragma unroll
+          for (int f = 0; f < 8; ++f) {
+            const int flat = 8 * c + f, e = flat / K1, i2 = flat % K1;
+            float zz = 0.f;                    // window row nt + i2 (nt is not a constant)
+#pragma unroll
+            for (int r = 0; r < TT + K1; ++r) zz = r == nt + i2 ? win[r][e] : zz;
+            z[f] = zz;
+          }
+          st8<DT>(a.conv_out, (static_cast<long>(bi) * C + c0) * K1 + 8 * c, z);
+        }
+      }
     } else {
 #pragma unroll
       for (int t = 0; t < TT; ++t) {
@@ -175,24 +205,6 @@ __global__ __launch_bounds__(kProThreads) void prologue_kernel(ProArgs a) {
         for (int e = 0; e < 8; ++e) y[t][e] *= inv;
       }
       if (t < nt) st8<DT>(out, (row0 + t0 + t) * width + cx, y[t]);
-    }
-    // new conv tail of these 8 channels: entry i holds the input at position
-    // S - (K-1) + i; written by the workgroup holding that token, or
-    // (position < 0, a segment shorter than K-1) copied from the old tail by
-    // the first token block
-    if (conv && a.conv_out) {
-      const int K1 = K - 1;
-      for (int i = 0; i < K1; ++i) {
-        const long p = a.S - K1 + i;
-        if (p >= 0 ? (p < t0 || p >= t0 + nt) : t0 != 0) continue;
-#pragma unroll
-        for (int e = 0; e < 8; ++e) {
-          const long c = c0 + e;
-          const float xin = p >= 0 ? ld<DT>(x, (row0 + p) * ldx + cx + e)
-                                   : (a.conv_in ? ld<DT>(a.conv_in, (static_cast<long>(bi) * C + c) * K1 + (p + K1)) : 0.f);
-          st<DT>(a.conv_out, (static_cast<long>(bi) * C + c) * K1 + i, xin);
-        }
-      }
     }
   } else if (item < nconv + 2 * nb + nw) {
     const int it = item - nconv;
@@ -263,11 +275,22 @@ hipError_t launch_layer_prologue(const lay::ProArgs& a, int act_dt, hipStream_t 
   const long items = 2 * ((2L * a.HK * a.DK + a.H * a.DV) / 8);
   const dim3 grid(static_cast<unsigned>((a.S + lay::TT - 1) / lay::TT),
                   static_cast<unsigned>((items + lay::kProThreads - 1) / lay::kProThreads), static_cast<unsigned>(a.B));
-  if (act_dt == DT_BF16) hipLaunchKernelGGL(lay::prologue_kernel<DT_BF16>, grid, dim3(lay::kProThreads), 0, stream, a);
-  else if (act_dt == DT_F16) hipLaunchKernelGGL(lay::prologue_kernel<DT_F16>, grid, dim3(lay::kProThreads), 0, stream, a);
-  else if (act_dt == DT_F32) hipLaunchKernelGGL(lay::prologue_kernel<DT_F32>, grid, dim3(lay::kProThreads), 0, stream, a);
-  else return hipErrorInvalidValue;
-  return hipGetLastError();
+  const int kc = a.conv_w ? a.K : 0;
+  if (kc < 0 || kc > lay::kMaxConv) return hipErrorInvalidValue;
+#define GDN2_PRO(DTV)                                                                                   \
+  if (act_dt == DTV) {                                                                                  \
+    switch (kc) {                                                                                       \
+      case 0: hipLaunchKernelGGL((lay::prologue_kernel<DTV, 0>), grid, dim3(lay::kProThreads), 0, stream, a); break; \
+      case 1: hipLaunchKernelGGL((lay::prologue_kernel<DTV, 1>), grid, dim3(lay::kProThreads), 0, stream, a); break; \
+      case 2: hipLaunchKernelGGL((lay::prologue_kernel<DTV, 2>), grid, dim3(lay::kProThreads), 0, stream, a); break; \
+      case 3: hipLaunchKernelGGL((lay::prologue_kernel<DTV, 3>), grid, dim3(lay::kProThreads), 0, stream, a); break; \
+      default: hipLaunchKernelGGL((lay::prologue_kernel<DTV, 4>), grid, dim3(lay::kProThreads), 0, stream, a); break; \
+    }                                                                                                   \
+    return hipGetLastError();                                                                           \
+  }
+  GDN2_PRO(DT_BF16) GDN2_PRO(DT_F16) GDN2_PRO(DT_F32)
+#undef GDN2_PRO
+  return hipErrorInvalidValue;
 }
 
 hipError_t launch_layer_epilogue(const void* o, int o_dt, const void* gate, long ld_gate, const float* weight,

@@ -116,7 +116,7 @@ int gdn2_hip_prefill_chunks(const void* q, const void* k, const void* v, const f
  * writes the last conv_k - 1 conv inputs to conv_out (same layout, distinct
  * buffer; NULL: not written). conv_w NULL: no conv (and no SiLU).
  * DK/8 must be a power of two <= 64 and DV a multiple of 8; the row strides
- * multiples of 8 and every x / output pointer 16-byte aligned.
+ * multiples of 8 and every x / output / conv pointer 16-byte aligned.
  * Replaces: the layer's q/k/v conv, F.normalize and gate/decay ops in
  * gdn2/attention.py (_ShortConv.decode :206-215, _gates :290-293, the
  * normalisation in prefill/decode :360-402).
