@@ -313,7 +313,7 @@ def main():
         "config": {"workload": "gdn2 prefill, BASELINE config 1: B=2 S=4096 H=16 DK=DV=128, "
                                "bf16 q,k,v,b,w + fp32 g in, bf16 o + fp32 state out, chunk 64",
                    "global_batch": B1, "seq_len": S1, "heads": H1, "head_dim": D1,
-                   "arithmetic": "bf16 MFMA (hi/lo split where precision needs it), fp32 accumulate"},
+                   "arithmetic": "bf16 and fp16 MFMA (hi/lo splits where precision needs it), fp32 accumulate"},
         "roofline": {
             "bound": "hbm",
             "kernel": "prefill step = gdn2 chunk_local_kernel + scan_kernel",

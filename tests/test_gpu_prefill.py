@@ -46,6 +46,14 @@ def test_prefill_matches_oracle(B, S, H, DK, DV):
     _check(B, S, H, DK, DV)
 
 
+@pytest.mark.parametrize("B,H,DK,DV", [(1, 66, 128, 128), (2, 34, 64, 128), (1, 130, 64, 64)])
+def test_prefill_two_value_tiles_per_workgroup(B, H, DK, DV):
+    """Enough heads (B*H*DV/16 > 512) that the scan gives each workgroup two
+    16-column value tiles, where every thread stages Z."""
+    assert B * H * DV // 16 > 512
+    _check(B, 192, H, DK, DV)
+
+
 @pytest.mark.parametrize("decay_scale", [0.0, 1.0, 8.0, 30.0])
 def test_prefill_decay_scales(decay_scale):
     """Covers both block-rescaling paths: 8 and 30 force the exact path
