@@ -4,8 +4,8 @@
 // 252-258).
 //
 // One 512-thread workgroup per (b, h, DVT-wide value tile); the fp32 state
-// tile S[DK, DVT] stays in MFMA accumulators for the whole sequence. Per chunk,
-// from the chunk record (gdn2_prefill_layout.h) and v, w:
+// tile S[DK, DVT] stays in registers for the whole sequence. Per chunk, from
+// the chunk record (gdn2_prefill_layout.h) and v, w:
 //
 //   Z  = w * v          U = Ai Z          Un = U - W S
 //   o  = Qg S + Aqk Un                     (Qg = scale * q * gamma)
@@ -14,24 +14,27 @@
 // Precision. The record matrices are fp16 with a power-of-two scale per
 // matrix (11-bit significands, exact). The four products with the state or Un
 // (W S, Qg S, KG^T Un, Aqk Un) run on fp16 MFMAs straight from the record
-// fragments: S and Un are split into fp16 hi + lo (~22 bits) after scaling
-// each value column by a power of two that puts the column's largest entry in
-// [2^14, 2^15), so the split is exact up to fp32 round-off and cannot
-// overflow; the scale is undone on the fp32 accumulator. U = Ai Z splits both
-// operands into bf16 hi + lo (three MFMAs, ~16 bits; Ai's fp16 values split
-// exactly). W S needs the precision: with little decay the state is large and
-// Un = U - W S is a small difference of large terms.
+// fragments. S and Un are split into fp16 hi + lo (~22 bits) after scaling
+// each 32-row block of a value column by a power of two that puts the block's
+// largest entry in [2^14, 2^15), so the split cannot overflow; a 32-row block
+// is one MFMA k step, and its scale is undone on that step's fp32 product.
+// U = Ai Z splits both operands into bf16 hi + lo (three MFMAs, ~16 bits; Ai's
+// fp16 values split exactly). W S needs the precision: with little decay the
+// state is large and Un = U - W S is a small difference of large terms.
 //
-// Eight waves. Phase 1: waves 0-3 form Un for output row block m = w (U and
-// W S), waves 4-7 form Qg S for the same blocks. The column maxima of Un meet
-// in LDS (barrier), then Un is split at the common column scales and handed
-// over (barrier). Phase 2: wave w updates state rows 16w..16w+15 with KG^T Un
-// and waves 4-7 finish o with Aqk Un; the new state is handed over the same
-// way as Un (column maxima, barrier, split, barrier).
-// LDS holds S^T, Z and Un in B-operand order ([column][k], k contiguous); Z is
-// double-buffered so the next chunk's Z is staged while the current one is in
-// use. Record fragments are double-buffered in registers by chunk parity and
-// each one is refilled with chunk n+2's copy right after its last MFMA.
+// Roles (fixed per wave, so each role's loop issues a fixed set of loads):
+//   waves 0-3   output row block m = w: Qg S (phase 1), o = Qg S + Aqk Un
+//               (phase 2, stored during the next phase 1); waves w < DK/32
+//               also own state rows 32w .. 32w+31 (phase 2 update, then the
+//               split hand-off of those rows).
+//   waves 4-5   Un for token rows 32u .. 32u+31 (u = w - 4): W S, then
+//               Un = U - W S, split at the wave's own scales (phase 1).
+//   waves 6-7   stage the next chunk's Z (phase 1) and form its U = Ai Z for
+//               token rows 32u .. 32u+31 (u = w - 6, phase 2).
+// Two barriers per chunk: after phase 1 (Un, Z) and after phase 2 (S, U).
+// LDS holds S^T, Un^T and Z^T in B-operand order ([column][k], k contiguous).
+// Record fragments are double-buffered in registers by chunk parity and each
+// one is refilled with its next copy right after its last use.
 //
 // Workgroup -> (head, tile) is XCD-aware: the tiles of one head land on the
 // same XCD so its chunk records come from HBM once into that XCD's L2.
@@ -45,62 +48,9 @@ namespace gdn2 {
 constexpr int kScanWaves = 8;
 constexpr int kScanThreads = 64 * kScanWaves;
 
-// Record fragments one wave holds for a chunk, as raw fp16 (8 per lane) with
-// the record's power-of-two scale of each matrix. Waves 0-3 ("Un" role) use
-// a = Ai and x = W; waves 4-7 ("output" role) use a = Aqk and x = Qg. Every
-// wave holds the KG^T fragments, their scale and gamma_last of its state tile.
-template <int DK>
-struct ScanFrags {
-  static constexpr int KT = DK / 32;
-  uint4 a[2];
-  uint4 x[KT];
-  uint4 k[2];
-  float sa, sx, sk;
-  float4 gam;
-};
-
 template <int DK>
 __device__ __forceinline__ float rec_scale(const unsigned short* __restrict__ rec, int which) {
   return reinterpret_cast<const float*>(rec + ChunkLayout<DK>::SC_OFF)[which];
-}
-
-// Fragments of the output / Un phase of a chunk (output row block m = wave & 3).
-template <int DK>
-__device__ __forceinline__ void load_frags_p1(const unsigned short* __restrict__ rec, int wave,
-                                              int lane, ScanFrags<DK>& f) {
-  using L = ChunkLayout<DK>;
-  constexpr int KT = DK / 32;
-  const int o8 = lane * 8;
-  const int m = wave & 3;
-  const bool un = wave < 4;
-#pragma unroll
-  for (int kk = 0; kk < 2; ++kk)
-    f.a[kk] = *reinterpret_cast<const uint4*>(rec + (un ? L::ai_frag(m, kk) : L::aqk_frag(m, kk)) + o8);
-#pragma unroll
-  for (int kk = 0; kk < KT; ++kk)
-    f.x[kk] = *reinterpret_cast<const uint4*>(rec + (un ? L::w_frag(m, kk) : L::qg_frag(m, kk)) + o8);
-  f.sa = rec_scale<DK>(rec, un ? SC_AI : SC_AQK);
-  f.sx = rec_scale<DK>(rec, un ? SC_W : SC_QG);
-}
-
-// Fragments of the state-update phase (state tile wave).
-template <int DK>
-__device__ __forceinline__ void load_frags_p2(const unsigned short* __restrict__ rec, int wave,
-                                              int lane, int lq, ScanFrags<DK>& f) {
-  using L = ChunkLayout<DK>;
-  wave = wave < DK / 16 ? wave : DK / 16 - 1;   // a wave without a tile holds the last one's (unused)
-  const int o8 = lane * 8;
-#pragma unroll
-  for (int kk = 0; kk < 2; ++kk) f.k[kk] = *reinterpret_cast<const uint4*>(rec + L::kt_frag(wave, kk) + o8);
-  f.sk = rec_scale<DK>(rec, SC_KT);
-  f.gam = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(rec + L::GL_OFF) + 16 * wave + 4 * lq);
-}
-
-template <int DK>
-__device__ __forceinline__ void load_frags(const unsigned short* __restrict__ rec, int wave, int lane,
-                                           int lq, ScanFrags<DK>& f) {
-  load_frags_p1<DK>(rec, wave, lane, f);
-  load_frags_p2<DK>(rec, wave, lane, lq, f);
 }
 
 // Four consecutive v (or w) elements as floats, raw register form per dtype.
@@ -172,43 +122,38 @@ __device__ __forceinline__ void put_quad_f16(unsigned short* hi, unsigned short*
   *reinterpret_cast<uint2*>(lo) = make_uint2(__builtin_bit_cast(uint32_t, l01), __builtin_bit_cast(uint32_t, l23));
 }
 
+// role bits of a wave
+constexpr int kRoleOut = 1, kRoleState = 2, kRoleUn = 4, kRoleZU = 8;
+
 template <int DK, int NT, int IN_DT, int OUT_DT>
 __global__ __launch_bounds__(kScanThreads) void scan_kernel(
     const void* __restrict__ v, const void* __restrict__ w, const unsigned short* __restrict__ ws,
     const float* __restrict__ s_in, float* __restrict__ s_out, void* __restrict__ o,
     int BH, int H, int HK, int DV, long s_alloc, long t0, int NC) {
   using L = ChunkLayout<DK>;
-  constexpr int KT = DK / 32;
-  constexpr int MT = DK / 16;          // 16-row state tiles; wave w < MT owns tile w
+  constexpr int KT = DK / 32;          // 32-row k blocks of S = state-owning waves
   constexpr int DVT = 16 * NT;
-  constexpr int SP = DK + 8;           // bf16 pitch of S^T [DVT][DK]
-  constexpr int TP = kBS + 8;          // bf16 pitch of [DVT][64] arrays
-  constexpr int ZQ = kBS * DVT / 4;    // Z quads per chunk tile
-  constexpr int ZIT = (ZQ + kScanThreads - 1) / kScanThreads;
-  // With fewer Z quads than threads the output waves (the upper threads) stage
-  // Z: the Un waves carry the longer phase 1.
-  constexpr int ZOFF = ZQ < kScanThreads ? kScanThreads - ZQ : 0;
+  constexpr int SP = DK + 8;           // 16-bit pitch of S^T [DVT][DK]
+  constexpr int TP = kBS + 8;          // 16-bit pitch of [DVT][64] arrays
+  constexpr int ZQ = kBS * DVT / 4;    // Z quads per chunk tile, staged by 128 threads
+  constexpr int ZIT = ZQ / 128;
+  static_assert(ZQ % 128 == 0, "Z staging assumes whole quads per thread");
 
   __shared__ __align__(16) unsigned short sSh[2][DVT * SP], sSl[2][DVT * SP];
   __shared__ __align__(16) unsigned short sZh[2][DVT * TP], sZl[2][DVT * TP];
   __shared__ __align__(16) unsigned short sNh[DVT * TP], sNl[DVT * TP];
-  // S^T and Un are fp16 hi / lo at per-column power-of-two scales: the column
-  // maxima of each producing wave, and the inverse scales the consumers apply
-  __shared__ __align__(16) float sSmx[DVT][MT];
-  __shared__ __align__(16) float sNmx[DVT][4];
-  __shared__ float sSinv[2][DVT], sNinv[DVT];
-  // output staging: one 16 x 16 tile per output wave, row-major, in OUT_DT
+  __shared__ __align__(16) float sSinv[2][DVT][KT];     // inverse block scales of S^T
+  __shared__ __align__(16) float sNinv[DVT][2];         // of Un^T
+  __shared__ __align__(16) f32x4 sU[4][NT][64];         // U of the next chunk, D layout
   constexpr int OSZ = OUT_DT == DT_F32 ? 4 : 2;
   __shared__ __align__(16) unsigned char sO[4][16 * 16 * OSZ];
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);   // wave-uniform: scalar branches
-  const bool un_role = wave < 4;
-  const bool owns = wave < MT;
-  const int m = wave & 3;              // output row block of the chunk
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15;
   const int lq = lane >> 4;
+  const int o8 = lane * 8;
 
   // XCD-aware block -> (head, tile) map (workgroups are dealt round-robin to 8
   // XCDs): all tiles of the value heads that share a key head, hence a record
@@ -233,273 +178,350 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
   const int bh = bi * H + h;
   const int d0 = tile * DVT;
   const unsigned short* rec0 = ws + static_cast<size_t>(bhk) * NC * L::STRIDE;   // key head's records
-
-  // Z staging: quad e -> token t = e / (DVT/4), columns 4*cq .. 4*cq+3
-  Raw4<IN_DT> zv[2][ZIT], zw[2][ZIT];    // [chunk parity]
-  // parity P (= chunk index & 1) is a compile-time constant so the two register
-  // copies stay in registers
-  auto fetch_z = [&](auto parity, int nc) {
-    constexpr int p = decltype(parity)::value;
-#pragma unroll
-    for (int it = 0; it < ZIT; ++it) {
-      const int e = tid - ZOFF + kScanThreads * it;
-      if (e < 0 || e >= ZQ) break;
-      const int t = e / (DVT / 4), cq = e % (DVT / 4);
-      const size_t idx = ((static_cast<size_t>(bi) * s_alloc + t0 + static_cast<long>(nc) * kBS + t) * H + h) * DV + d0 + 4 * cq;
-      zv[p][it].load(v, idx);
-      zw[p][it].load(w, idx);
-    }
-  };
-  auto put_z = [&](auto parity) {     // stage Z of the chunk with this parity into LDS buffer P
-    constexpr int buf = decltype(parity)::value;
-#pragma unroll
-    for (int it = 0; it < ZIT; ++it) {
-      const int e = tid - ZOFF + kScanThreads * it;
-      if (e < 0 || e >= ZQ) break;
-      const int t = e / (DVT / 4), cq = e % (DVT / 4);
-      float a[4], b[4];
-      zv[buf][it].get(a);
-      zw[buf][it].get(b);
-#pragma unroll
-      for (int u = 0; u < 4; u += 2) {
-        uint32_t hi, lo;
-        split_pk(a[u] * b[u], a[u + 1] * b[u + 1], hi, lo);
-        sZh[buf][(4 * cq + u) * TP + t] = static_cast<unsigned short>(hi);
-        sZl[buf][(4 * cq + u) * TP + t] = static_cast<unsigned short>(lo);
-        sZh[buf][(4 * cq + u + 1) * TP + t] = static_cast<unsigned short>(hi >> 16);
-        sZl[buf][(4 * cq + u + 1) * TP + t] = static_cast<unsigned short>(lo >> 16);
-      }
-    }
-  };
-
-  // ---- state in: rows c = 16*wave + 4*lq + e, column d0 + 16*nn + lr
-  f32x4 S[NT];
-#pragma unroll
-  for (int nn = 0; nn < NT; ++nn)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int c = 16 * wave + 4 * lq + e;
-      S[nn][e] = (s_in && owns) ? s_in[(static_cast<size_t>(bh) * DK + c) * DV + d0 + 16 * nn + lr] : 0.f;
-    }
-  // Hand the state to the B-operand buffer `buf` (every wave calls it: it
-  // contains a barrier): column maxima of each owner's rows, then the split at
-  // the common column scale.
-  auto put_state = [&](int buf) {
-    if (owns) {
-#pragma unroll
-      for (int nn = 0; nn < NT; ++nn) {
-        const float mx = tile_col_max(S[nn]);      // all lanes: the permlanes read every lane
-        if (lq == 0) sSmx[16 * nn + lr][wave] = mx;
-      }
-    }
-    __syncthreads();
-    if (!owns) return;
-#pragma unroll
-    for (int nn = 0; nn < NT; ++nn) {
-      const int col = 16 * nn + lr;
-      float mx = 0.f;
-#pragma unroll
-      for (int ww = 0; ww < MT; ww += 4) {
-        const float4 x = *reinterpret_cast<const float4*>(&sSmx[col][ww]);
-        mx = fmaxf(mx, fmaxf(fmaxf(x.x, x.y), fmaxf(x.z, x.w)));
-      }
-      float inv;
-      const float sc = col_scale(mx, &inv);
-      const int c = 16 * wave + 4 * lq;
-      put_quad_f16(&sSh[buf][col * SP + c], &sSl[buf][col * SP + c], S[nn], sc);
-      if (wave == 0 && lq == 0) sSinv[buf][col] = inv;
-    }
-  };
-
-  // Record fragments are double-buffered in registers by chunk parity: chunk
-  // n's buffer is refilled with chunk n+2's fragments one fragment at a time,
-  // right after that fragment's last MFMA, so the loads are spread over both
-  // phases and the memory pipe stays busy while the matrix cores run.
-  using P0 = std::integral_constant<int, 0>;
-  using P1 = std::integral_constant<int, 1>;
-  ScanFrags<DK> fr[2];
-  // Every step issues the same loads (the chunk index is clamped at the end)
-  // so the compiler's wait counts are identical on every path through the loop.
   const int last = NC - 1;
-  fetch_z(P0{}, 0);
-  load_frags<DK>(rec0, wave, lane, lq, fr[0]);
-  put_state(0);
-  put_z(P0{});
-  fetch_z(P1{}, min(1, last));
-  load_frags<DK>(rec0 + static_cast<size_t>(min(1, last)) * L::STRIDE, wave, lane, lq, fr[1]);
-  __syncthreads();
-
-  const int o8 = lane * 8;
+  auto recp = [&](int c) { return rec0 + static_cast<size_t>(min(c, last)) * L::STRIDE; };
   auto frag = [&](const unsigned short* rec, long off) {
     return *reinterpret_cast<const uint4*>(rec + off + o8);
   };
-
-  // o tile of chunk nc (rows 16m + 4lq + e, columns 16nn + lr in D layout) ->
-  // LDS, then 16 contiguous bytes per lane to global memory (output waves)
-  f32x4 Opend[NT];
-  auto store_o = [&](int nc) {
-    const long tok0 = t0 + static_cast<long>(nc) * kBS;
-    unsigned char* so = sO[m];
-#pragma unroll
-    for (int nn = 0; nn < NT; ++nn) {
-#pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        const int idx = (4 * lq + e) * 16 + lr;
-        if constexpr (OUT_DT == DT_F32) reinterpret_cast<float*>(so)[idx] = Opend[nn][e];
-        else if constexpr (OUT_DT == DT_BF16) reinterpret_cast<unsigned short*>(so)[idx] = f32_to_bf16_bits(Opend[nn][e]);
-        else reinterpret_cast<unsigned short*>(so)[idx] = f32_to_f16_bits(Opend[nn][e]);
-      }
-      __builtin_amdgcn_wave_barrier();
-      constexpr int LPR = 16 * OSZ / 16;          // lanes per 16-element row (2 or 4)
-      if (lane < 16 * LPR) {
-        const int r = lane / LPR, c = (lane % LPR) * (16 / OSZ);
-        const uint4 x = *reinterpret_cast<const uint4*>(so + (r * 16 + c) * OSZ);
-        const size_t oi = ((static_cast<size_t>(bi) * s_alloc + tok0 + 16 * m + r) * H + h) * DV + d0 + 16 * nn + c;
-        *reinterpret_cast<uint4*>(static_cast<unsigned char*>(o) + oi * OSZ) = x;
-      }
-      __builtin_amdgcn_wave_barrier();
-    }
+  // B operand (8 consecutive k of column 16nn + lr) of a [column][k] array
+  auto bop = [&](const unsigned short* a, int pitch, int nn, int k0) {
+    return *reinterpret_cast<const uint4*>(&a[(16 * nn + lr) * pitch + k0 + 8 * lq]);
   };
 
-  auto step = [&](auto parity, ScanFrags<DK>& cur, int nc) {
-    constexpr int buf = decltype(parity)::value;   // == nc & 1
-    using Other = std::integral_constant<int, buf ^ 1>;
-    const int pre = min(nc + 2, last);
-    const unsigned short* rp = rec0 + static_cast<size_t>(pre) * L::STRIDE;
+  auto run = [&](auto role_tag) {
+    constexpr int R = decltype(role_tag)::value;
+    constexpr bool OUT = R & kRoleOut, STATE = R & kRoleState, UN = R & kRoleUn, ZU = R & kRoleZU;
+    const int m = wave & 3;              // output row block (OUT)
+    const int u = (wave - 4) & 1;        // token-row pair (UN, ZU)
 
-    // ---- phase 1, row block m: Un = Ai Z - W S (waves 0-3), Qg S (waves 4-7)
-    f32x4 A[NT], X[NT];
+    // ---- record fragments, double-buffered by chunk parity -------------------
+    uint4 fq[2][OUT ? KT : 1], fa[2][OUT ? 2 : 1];            // Qg_m, Aqk_m
+    uint4 fk[2][STATE ? 2 : 1][2];                              // KG^T tiles 2w, 2w+1
+    float4 gam[2][STATE ? 2 : 1];
+    uint4 fw[2][UN ? 2 : 1][UN ? KT : 1];                       // W blocks 2u, 2u+1
+    uint4 fi[2][ZU ? 2 : 1][2];                                 // Ai blocks 2u, 2u+1
+    float sc[2][5];
+    auto load_all = [&](int p, const unsigned short* rec) {
+      if constexpr (OUT) {
 #pragma unroll
-    for (int nn = 0; nn < NT; ++nn) { A[nn] = zero4(); X[nn] = zero4(); }
-    const float sa = cur.sa, sx = cur.sx;
-    if (un_role) {
+        for (int kk = 0; kk < KT; ++kk) fq[p][kk] = frag(rec, L::qg_frag(m, kk));
 #pragma unroll
-      for (int kk = 0; kk < 2; ++kk) {
-        bf16x8 ah, al;
-        f16x8_to_bf16_hilo(cur.a[kk], ah, al);     // refilled in phase 2
+        for (int kk = 0; kk < 2; ++kk) fa[p][kk] = frag(rec, L::aqk_frag(m, kk));
+      }
+      if constexpr (STATE) {
 #pragma unroll
-        for (int nn = 0; nn < NT; ++nn) {
-          const int col = 16 * nn + lr;
-          const bf16x8 zh = *reinterpret_cast<const bf16x8*>(&sZh[buf][col * TP + 32 * kk + 8 * lq]);
-          const bf16x8 zl = *reinterpret_cast<const bf16x8*>(&sZl[buf][col * TP + 32 * kk + 8 * lq]);
-          A[nn] = mfma3(ah, al, zh, zl, A[nn]);
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk) fk[p][t][kk] = frag(rec, L::kt_frag(2 * wave + t, kk));
+          gam[p][t] = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(rec + L::GL_OFF) +
+                                                        32 * wave + 16 * t + 4 * lq);
         }
       }
-    }
+      if constexpr (UN) {
 #pragma unroll
-    for (int kk = 0; kk < KT; ++kk) {
+        for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-      for (int nn = 0; nn < NT; ++nn) {
-        const int col = 16 * nn + lr;
-        const uint4 sh = *reinterpret_cast<const uint4*>(&sSh[buf][col * SP + 32 * kk + 8 * lq]);
-        const uint4 sl = *reinterpret_cast<const uint4*>(&sSl[buf][col * SP + 32 * kk + 8 * lq]);
-        X[nn] = mfma2(cur.x[kk], sh, sl, X[nn]);
+          for (int kk = 0; kk < KT; ++kk) fw[p][bb][kk] = frag(rec, L::w_frag(2 * u + bb, kk));
       }
-      // refilled after its last use, into the same registers
-      cur.x[kk] = frag(rp, un_role ? L::w_frag(m, kk) : L::qg_frag(m, kk));
-    }
-    if (!un_role && nc > 0) store_o(nc - 1);
-    // X is W S (or Qg S) at the record scale times the state's column scale
-    float xs[NT];
+      if constexpr (ZU) {
 #pragma unroll
-    for (int nn = 0; nn < NT; ++nn) xs[nn] = sx * sSinv[buf][16 * nn + lr];
-    cur.sx = rec_scale<DK>(rp, un_role ? SC_W : SC_QG);
-    f32x4 un[NT];
-    if (un_role) {
-      cur.sa = rec_scale<DK>(rp, SC_AI);
+        for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-      for (int nn = 0; nn < NT; ++nn) {
-        un[nn] = A[nn] * sa - X[nn] * xs[nn];
-        const float mx = tile_col_max(un[nn]);
-        if (lq == 0) sNmx[16 * nn + lr][m] = mx;
+          for (int kk = 0; kk < 2; ++kk) fi[p][bb][kk] = frag(rec, L::ai_frag(2 * u + bb, kk));
       }
-    }
-    put_z(Other{});     // that LDS buffer was last read in chunk nc-1 (a clamped copy at the end)
-    __syncthreads();
-    if (un_role) {      // Un at the common column scales of the four row blocks
+#pragma unroll
+      for (int j = 0; j < 5; ++j) sc[p][j] = rec_scale<DK>(rec, j);
+    };
+
+    // ---- Z staging (ZU waves: 128 threads, ZIT quads each) ----------------------
+    const int zt = tid - 384;
+    Raw4<IN_DT> zv[ZIT], zw[ZIT];
+    auto fetch_z = [&](int nc) {
+#pragma unroll
+      for (int it = 0; it < ZIT; ++it) {
+        const int e = zt + 128 * it;
+        const int t = e / (DVT / 4), cq = e % (DVT / 4);
+        const size_t idx = ((static_cast<size_t>(bi) * s_alloc + t0 + static_cast<long>(min(nc, last)) * kBS + t) * H + h) * DV + d0 + 4 * cq;
+        zv[it].load(v, idx);
+        zw[it].load(w, idx);
+      }
+    };
+    auto put_z = [&](int buf) {
+#pragma unroll
+      for (int it = 0; it < ZIT; ++it) {
+        const int e = zt + 128 * it;
+        const int t = e / (DVT / 4), cq = e % (DVT / 4);
+        float a[4], b[4];
+        zv[it].get(a);
+        zw[it].get(b);
+#pragma unroll
+        for (int q = 0; q < 4; q += 2) {
+          uint32_t hi, lo;
+          split_pk(a[q] * b[q], a[q + 1] * b[q + 1], hi, lo);
+          sZh[buf][(4 * cq + q) * TP + t] = static_cast<unsigned short>(hi);
+          sZl[buf][(4 * cq + q) * TP + t] = static_cast<unsigned short>(lo);
+          sZh[buf][(4 * cq + q + 1) * TP + t] = static_cast<unsigned short>(hi >> 16);
+          sZl[buf][(4 * cq + q + 1) * TP + t] = static_cast<unsigned short>(lo >> 16);
+        }
+      }
+    };
+    // U = Ai Z of token rows 32u + 16bb (record units) for the chunk whose Ai
+    // fragments are in buffer p and whose Z is in LDS buffer zb
+    auto form_u = [&](int p, int zb) {
+#pragma unroll
+      for (int bb = 0; bb < 2; ++bb) {
+        f32x4 acc[NT];
+#pragma unroll
+        for (int nn = 0; nn < NT; ++nn) acc[nn] = zero4();
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) {
+          bf16x8 ah, al;
+          f16x8_to_bf16_hilo(fi[p][bb][kk], ah, al);
+#pragma unroll
+          for (int nn = 0; nn < NT; ++nn) {
+            const bf16x8 zh = __builtin_bit_cast(bf16x8, bop(sZh[zb], TP, nn, 32 * kk));
+            const bf16x8 zl = __builtin_bit_cast(bf16x8, bop(sZl[zb], TP, nn, 32 * kk));
+            acc[nn] = mfma3(ah, al, zh, zl, acc[nn]);
+          }
+        }
+#pragma unroll
+        for (int nn = 0; nn < NT; ++nn) sU[2 * u + bb][nn][lane] = acc[nn];
+      }
+    };
+
+    // ---- state (STATE waves: rows 32w + 16t + 4lq + e, column d0 + 16nn + lr) --
+    f32x4 S[STATE ? 2 : 1][NT];
+    // split hand-off of the wave's 32 rows into S^T buffer b at the wave's
+    // own per-column scale
+    auto put_state = [&](int b) {
 #pragma unroll
       for (int nn = 0; nn < NT; ++nn) {
-        const int col = 16 * nn + lr;
-        const float4 x4 = *reinterpret_cast<const float4*>(&sNmx[col][0]);
-        const float mx = fmaxf(fmaxf(x4.x, x4.y), fmaxf(x4.z, x4.w));
+        const float mx = fmaxf(tile_col_max(S[0][nn]), tile_col_max(S[1][nn]));
         float inv;
-        const float sc = col_scale(mx, &inv);
-        const int t = 16 * m + 4 * lq;
-        put_quad_f16(&sNh[col * TP + t], &sNl[col * TP + t], un[nn], sc);
-        if (m == 0 && lq == 0) sNinv[col] = inv;
+        const float scl = col_scale(mx, &inv);
+        const int col = 16 * nn + lr;
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          const int c = 32 * wave + 16 * t + 4 * lq;
+          put_quad_f16(&sSh[b][col * SP + c], &sSl[b][col * SP + c], S[t][nn], scl);
+        }
+        if (lq == 0) sSinv[b][col][wave] = inv;
       }
+    };
+
+    // W S or Qg S for one row block: sum over the k blocks of the state of the
+    // fp16 products, each un-scaled by its block's column scale
+    auto times_state = [&](const uint4* fr, int b, f32x4* X) {
+#pragma unroll
+      for (int nn = 0; nn < NT; ++nn) X[nn] = zero4();
+#pragma unroll
+      for (int nn = 0; nn < NT; ++nn) {
+        float inv[KT];
+        if constexpr (KT == 4) {
+          const float4 x = *reinterpret_cast<const float4*>(&sSinv[b][16 * nn + lr][0]);
+          inv[0] = x.x; inv[1] = x.y; inv[2] = x.z; inv[3] = x.w;
+        } else {
+          const float2 x = *reinterpret_cast<const float2*>(&sSinv[b][16 * nn + lr][0]);
+          inv[0] = x.x; inv[1] = x.y;
+        }
+#pragma unroll
+        for (int kk = 0; kk < KT; ++kk) {
+          f32x4 p = mfma_f16(fr[kk], bop(sSh[b], SP, nn, 32 * kk), zero4());
+          p = mfma_f16(fr[kk], bop(sSl[b], SP, nn, 32 * kk), p);
+          X[nn] += p * inv[kk];
+        }
+      }
+    };
+    // KG^T Un or Aqk Un for one 16-row tile: two token blocks, each un-scaled
+    auto times_un = [&](const uint4* fr, f32x4* Y) {
+#pragma unroll
+      for (int nn = 0; nn < NT; ++nn) {
+        const float2 inv = *reinterpret_cast<const float2*>(&sNinv[16 * nn + lr][0]);
+        f32x4 p0 = mfma_f16(fr[0], bop(sNh, TP, nn, 0), zero4());
+        p0 = mfma_f16(fr[0], bop(sNl, TP, nn, 0), p0);
+        f32x4 p1 = mfma_f16(fr[1], bop(sNh, TP, nn, 32), zero4());
+        p1 = mfma_f16(fr[1], bop(sNl, TP, nn, 32), p1);
+        Y[nn] = p0 * inv.x + p1 * inv.y;
+      }
+    };
+
+    // o tile of chunk nc (rows 16m + 4lq + e, columns 16nn + lr in D layout) ->
+    // LDS, then 16 contiguous bytes per lane to global memory
+    f32x4 Opend[OUT ? NT : 1];
+    auto store_o = [&](int nc) {
+      const long tok0 = t0 + static_cast<long>(nc) * kBS;
+      unsigned char* so = sO[m];
+#pragma unroll
+      for (int nn = 0; nn < NT; ++nn) {
+#pragma unroll
+        for (int e = 0; e < 4; ++e) {
+          const int idx = (4 * lq + e) * 16 + lr;
+          if constexpr (OUT_DT == DT_F32) reinterpret_cast<float*>(so)[idx] = Opend[nn][e];
+          else if constexpr (OUT_DT == DT_BF16) reinterpret_cast<unsigned short*>(so)[idx] = f32_to_bf16_bits(Opend[nn][e]);
+          else reinterpret_cast<unsigned short*>(so)[idx] = f32_to_f16_bits(Opend[nn][e]);
+        }
+        __builtin_amdgcn_wave_barrier();
+        constexpr int LPR = 16 * OSZ / 16;          // lanes per 16-element row (2 or 4)
+        if (lane < 16 * LPR) {
+          const int rr = lane / LPR, c = (lane % LPR) * (16 / OSZ);
+          const uint4 x = *reinterpret_cast<const uint4*>(so + (rr * 16 + c) * OSZ);
+          const size_t oi = ((static_cast<size_t>(bi) * s_alloc + tok0 + 16 * m + rr) * H + h) * DV + d0 + 16 * nn + c;
+          *reinterpret_cast<uint4*>(static_cast<unsigned char*>(o) + oi * OSZ) = x;
+        }
+        __builtin_amdgcn_wave_barrier();
+      }
+    };
+
+    // ---- set-up: records of chunks 0 and 1, Z_0 and U_0, S_0 ------------------
+    load_all(0, recp(0));
+    load_all(1, recp(1));
+    if constexpr (ZU) {
+      fetch_z(0);
+      put_z(0);
+      fetch_z(1);
+    }
+    if constexpr (STATE) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int nn = 0; nn < NT; ++nn)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int c = 32 * wave + 16 * t + 4 * lq + e;
+            S[t][nn][e] = s_in ? s_in[(static_cast<size_t>(bh) * DK + c) * DV + d0 + 16 * nn + lr] : 0.f;
+          }
+      put_state(0);
+    }
+    __syncthreads();
+    if constexpr (ZU) {
+      form_u(0, 0);
+      // buffer 0 (chunk 0's Ai) now serves chunk 2 (ZU waves read chunk n+1's
+      // Ai in step n)
+#pragma unroll
+      for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) fi[0][bb][kk] = frag(recp(2), L::ai_frag(2 * u + bb, kk));
     }
     __syncthreads();
 
-    // ---- phase 2: S = diag(gamma_last) S + KG^T Un (state tile = wave);
-    //      waves 4-7 finish o = Qg S + Aqk Un for row block m -------------------
-    // The KG^T and Aqk records carry power-of-two scales, Un its column
-    // scales: both are undone on the fresh accumulators T (KG^T Un) and Y
-    // (Aqk Un).
-    const float sk = cur.sk;
-    // Refills are unconditional (a wave without a state tile re-reads the last
-    // tile's fragments), so every path through the loop has the same loads and
-    // the compiler's wait counts never fall back to waiting for all of them.
-    const int kt_tile = owns ? wave : MT - 1;
-    const float4 gk = cur.gam;
-    cur.gam = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(rp + L::GL_OFF) + 16 * kt_tile + 4 * lq);
-    cur.sk = rec_scale<DK>(rp, SC_KT);
-    if (!un_role) cur.sa = rec_scale<DK>(rp, SC_AQK);
-    f32x4 T[NT], Y[NT];
+    // ---- the chunk loop --------------------------------------------------------
+    auto step = [&](auto parity, int nc) {
+      constexpr int p = decltype(parity)::value;   // == nc & 1
+      const unsigned short* rp = recp(nc + 2);      // refills: chunk nc + 2 into buffer p
+
+      // phase 1
+      f32x4 X[OUT ? NT : 1];
+      if constexpr (OUT) {
+        times_state(fq[p], p, X);
 #pragma unroll
-    for (int nn = 0; nn < NT; ++nn) { T[nn] = zero4(); Y[nn] = zero4(); }
-#pragma unroll
-    for (int kk = 0; kk < 2; ++kk) {
-#pragma unroll
-      for (int nn = 0; nn < NT; ++nn) {
-        const int col = 16 * nn + lr;
-        const uint4 nh = *reinterpret_cast<const uint4*>(&sNh[col * TP + 32 * kk + 8 * lq]);
-        const uint4 nl = *reinterpret_cast<const uint4*>(&sNl[col * TP + 32 * kk + 8 * lq]);
-        if (owns) T[nn] = mfma2(cur.k[kk], nh, nl, T[nn]);
-        if (!un_role) Y[nn] = mfma2(cur.a[kk], nh, nl, Y[nn]);
+        for (int kk = 0; kk < KT; ++kk) fq[p][kk] = frag(rp, L::qg_frag(m, kk));
+        if (nc > 0) store_o(nc - 1);
       }
-      cur.k[kk] = frag(rp, L::kt_frag(kt_tile, kk));
-      cur.a[kk] = frag(rp, un_role ? L::ai_frag(m, kk) : L::aqk_frag(m, kk));
-    }
-    float ni[NT];
+      if constexpr (UN) {
+        f32x4 un[2][NT];
 #pragma unroll
-    for (int nn = 0; nn < NT; ++nn) ni[nn] = sNinv[16 * nn + lr];
-    if (owns) {
+        for (int bb = 0; bb < 2; ++bb) {
+          f32x4 WS[NT];
+          times_state(fw[p][bb], p, WS);
 #pragma unroll
-      for (int nn = 0; nn < NT; ++nn) {
-        const float f = sk * ni[nn];
-        S[nn][0] = S[nn][0] * gk.x + T[nn][0] * f;
-        S[nn][1] = S[nn][1] * gk.y + T[nn][1] * f;
-        S[nn][2] = S[nn][2] * gk.z + T[nn][2] * f;
-        S[nn][3] = S[nn][3] * gk.w + T[nn][3] * f;
+          for (int kk = 0; kk < KT; ++kk) fw[p][bb][kk] = frag(rp, L::w_frag(2 * u + bb, kk));
+#pragma unroll
+          for (int nn = 0; nn < NT; ++nn) un[bb][nn] = sU[2 * u + bb][nn][lane] * sc[p][SC_AI] - WS[nn] * sc[p][SC_W];
+        }
+#pragma unroll
+        for (int nn = 0; nn < NT; ++nn) {
+          const float mx = fmaxf(tile_col_max(un[0][nn]), tile_col_max(un[1][nn]));
+          float inv;
+          const float scl = col_scale(mx, &inv);
+          const int col = 16 * nn + lr;
+#pragma unroll
+          for (int bb = 0; bb < 2; ++bb) {
+            const int t = 32 * u + 16 * bb + 4 * lq;
+            put_quad_f16(&sNh[col * TP + t], &sNl[col * TP + t], un[bb][nn], scl);
+          }
+          if (lq == 0) sNinv[col][u] = inv;
+        }
       }
-    }
-    if (!un_role) {
+      if constexpr (ZU) put_z(p ^ 1);          // Z of chunk nc + 1
+      __syncthreads();
+
+      // phase 2
+      if constexpr (STATE) {
 #pragma unroll
-      // stored in the next chunk's phase 1, where these waves have slack
-      for (int nn = 0; nn < NT; ++nn) Opend[nn] = X[nn] * xs[nn] + Y[nn] * (sa * ni[nn]);
+        for (int t = 0; t < 2; ++t) {
+          f32x4 T[NT];
+          times_un(fk[p][t], T);
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk) fk[p][t][kk] = frag(rp, L::kt_frag(2 * wave + t, kk));
+          const float4 g4 = gam[p][t];
+          const float sk = sc[p][SC_KT];
+#pragma unroll
+          for (int nn = 0; nn < NT; ++nn) {
+            S[t][nn][0] = S[t][nn][0] * g4.x + T[nn][0] * sk;
+            S[t][nn][1] = S[t][nn][1] * g4.y + T[nn][1] * sk;
+            S[t][nn][2] = S[t][nn][2] * g4.z + T[nn][2] * sk;
+            S[t][nn][3] = S[t][nn][3] * g4.w + T[nn][3] * sk;
+          }
+          gam[p][t] = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(rp + L::GL_OFF) +
+                                                        32 * wave + 16 * t + 4 * lq);
+        }
+        put_state(p ^ 1);
+      }
+      if constexpr (OUT) {
+        f32x4 Y[NT];
+        times_un(fa[p], Y);
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) fa[p][kk] = frag(rp, L::aqk_frag(m, kk));
+#pragma unroll
+        for (int nn = 0; nn < NT; ++nn) Opend[nn] = X[nn] * sc[p][SC_QG] + Y[nn] * sc[p][SC_AQK];
+      }
+      if constexpr (ZU) {
+        form_u(p ^ 1, p ^ 1);                  // U of chunk nc + 1
+        const unsigned short* r3 = recp(nc + 3);
+#pragma unroll
+        for (int bb = 0; bb < 2; ++bb)
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk) fi[p ^ 1][bb][kk] = frag(r3, L::ai_frag(2 * u + bb, kk));
+        fetch_z(nc + 2);
+      }
+#pragma unroll
+      for (int j = 0; j < 5; ++j) sc[p][j] = rec_scale<DK>(rp, j);
+      __syncthreads();
+    };
+
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    int nc = 0;
+    for (; nc + 1 < NC; nc += 2) {
+      step(P0{}, nc);
+      step(P1{}, nc + 1);
     }
-    put_state(buf ^ 1);
-    fetch_z(parity, pre);
-    __syncthreads();
+    if (nc < NC) step(P0{}, nc);
+
+    if constexpr (OUT) {
+      if (NC > 0) store_o(NC - 1);
+    }
+    if constexpr (STATE) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int nn = 0; nn < NT; ++nn)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int c = 32 * wave + 16 * t + 4 * lq + e;
+            s_out[(static_cast<size_t>(bh) * DK + c) * DV + d0 + 16 * nn + lr] = S[t][nn][e];
+          }
+    }
   };
 
-  int nc = 0;
-  for (; nc + 1 < NC; nc += 2) {
-    step(P0{}, fr[0], nc);
-    step(P1{}, fr[1], nc + 1);
+  if (wave < 4) {
+    if (wave < KT) run(std::integral_constant<int, kRoleOut | kRoleState>{});
+    else run(std::integral_constant<int, kRoleOut>{});
+  } else if (wave < 6) {
+    run(std::integral_constant<int, kRoleUn>{});
+  } else {
+    run(std::integral_constant<int, kRoleZU>{});
   }
-  if (nc < NC) step(P0{}, fr[0], nc);
-  if (!un_role && NC > 0) store_o(NC - 1);
-
-  if (!owns) return;
-#pragma unroll
-  for (int nn = 0; nn < NT; ++nn)
-#pragma unroll
-    for (int e = 0; e < 4; ++e) {
-      const int c = 16 * wave + 4 * lq + e;
-      s_out[(static_cast<size_t>(bh) * DK + c) * DV + d0 + 16 * nn + lr] = S[nn][e];
-    }
 }
 
 template <int DK, int NT, int IN_DT, int OUT_DT>
