@@ -4,9 +4,10 @@
 // One record per chunk of 64 tokens, record index ch = (b*HK + hk)*NC + n.
 // Every matrix is stored as fp16 MFMA A-operand fragments (see gdn2_common.h):
 // 64 lanes x 8 values = 1 KiB, loaded with one coalesced 16-byte access per
-// lane and expanded in registers to an exact bf16 hi + lo pair (11 significant
-// bits fit in 8 + 8). Each matrix carries a power-of-two scale so that its
-// stored values stay within fp16 range for any input:
+// lane. The scan feeds W, QG, KT and AQK to fp16 MFMAs as they are and expands
+// AI in registers to an exact bf16 hi + lo pair (11 significant bits fit in
+// 8 + 8). Each matrix carries a power-of-two scale so that its stored values
+// stay within fp16 range for any input:
 //
 //   W   [4 m][DK/32 kk]   fp16   W   = Ai (b*k*gamma)      / SC[0]   64 x DK
 //   QG  [4 m][DK/32 kk]   fp16   Qg  = scale*q*gamma       / SC[1]   64 x DK
