@@ -250,6 +250,21 @@ def read_traffic():
     return None
 
 
+def read_mfma_busy():
+    """MFMA busy fraction per prefill kernel from the committed rocprofv3 --pmc summary, if any."""
+    path = os.path.join(os.path.dirname(os.path.abspath(__file__)), "profiles", "mfma_busy_pmc.txt")
+    if not os.path.exists(path):
+        return None
+    out = {}
+    with open(path) as f:
+        for line in f:
+            if "(prefill, config 1)" in line and "%" in line:
+                name = "chunk_local" if "chunk_local" in line else "scan"
+                pct = [t for t in line.split() if t.endswith("%")][0]
+                out[name] = round(float(pct[:-1]) / 100, 4)
+    return out or None
+
+
 def main():
     ap = argparse.ArgumentParser()
     ap.add_argument("--gpus", type=int, default=1)
@@ -326,6 +341,7 @@ def main():
             "kernel_us": {"chunk_local": round(cl_ms * 1e3, 2), "scan": round(sc_ms * 1e3, 2)},
             "gemm_tflops": round(ALG_FLOPS_PREFILL / kern_s / 1e12, 1),
             "gemm_frac_of_bf16_peak": round(ALG_FLOPS_PREFILL / kern_s / 1e12 / BF16_DENSE_TFLOPS, 4),
+            "mfma_busy_pmc": read_mfma_busy(),
         },
     }
     if not args.no_decode:
