@@ -82,11 +82,6 @@ __device__ __forceinline__ f32x4 mfma_f16(const uint4& a, const uint4& b, f32x4 
   return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
                                                 0, 0, 0);
 }
-// exact fp16 A times a B operand split into fp16 hi + lo
-__device__ __forceinline__ f32x4 mfma2(const uint4& a, const uint4& bh, const uint4& bl, f32x4 c) {
-  c = mfma_f16(a, bh, c);
-  return mfma_f16(a, bl, c);
-}
 
 // max |x| over the column of a D-layout 16 x 16 tile (lane (lq, lr) holds rows
 // 4lq .. 4lq+3 of column lr); every lane of the column gets it. Lanes 32 and 16
