@@ -10,9 +10,9 @@ hipError_t launch_decode(const void*, const void*, const void*, const float*, co
                          const void*, float*, void*, int, int, int, int, int, long, long, int,
                          float, int, int, hipStream_t);
 hipError_t launch_chunk_local(const void*, const void*, const void*, const float*, int, int, int,
-                              int, long, long, int, float, unsigned short*, hipStream_t);
+                              int, long, long, int, long, float, unsigned short*, hipStream_t);
 hipError_t launch_scan(const void*, const void*, int, const unsigned short*, const float*, float*,
-                       void*, int, int, int, int, int, int, long, long, int, hipStream_t);
+                       void*, int, int, int, int, int, int, long, long, int, long, hipStream_t);
 }  // namespace gdn2
 
 namespace {
@@ -33,8 +33,8 @@ int status(hipError_t e) { return e == hipSuccess ? 0 : static_cast<int>(e); }
 int check_prefill(int B, int H, int DK, long s_alloc, long t0, long n_tokens) {
   if (B < 1 || H < 1 || t0 < 0 || n_tokens < 0 || s_alloc < t0 + n_tokens) return GDN2_ERR_ARG;
   if (DK != 64 && DK != 128) return GDN2_ERR_SHAPE;
-  if (n_tokens % gdn2::kBS) return GDN2_ERR_SHAPE;
-  if (static_cast<long>(B) * H * (n_tokens / gdn2::kBS) > 0x7fffffffL) return GDN2_ERR_SHAPE;
+  // a ragged last chunk is allowed: its rows past n_tokens are read as zeros
+  if (static_cast<long>(B) * H * ((n_tokens + gdn2::kBS - 1) / gdn2::kBS) > 0x7fffffffL) return GDN2_ERR_SHAPE;
   return 0;
 }
 
@@ -81,7 +81,8 @@ int gdn2_hip_chunk_local(const void* q, const void* k, const void* b, const floa
   if (int e = check_prefill(B, HK, DK, s_alloc, t0, n_tokens)) return e;
   if (n_tokens == 0) return 0;
   return status(gdn2::launch_chunk_local(q, k, b, g, in_dtype, B, HK, DK, s_alloc, t0,
-                                         static_cast<int>(n_tokens / gdn2::kBS), scale,
+                                         static_cast<int>((n_tokens + gdn2::kBS - 1) / gdn2::kBS),
+                                         n_tokens, scale,
                                          static_cast<unsigned short*>(workspace),
                                          static_cast<hipStream_t>(stream)));
 }
@@ -98,7 +99,7 @@ int gdn2_hip_prefill_scan(const void* v, const void* w, int in_dtype, const void
   if (n_tokens == 0) return GDN2_ERR_SHAPE;
   return status(gdn2::launch_scan(v, w, in_dtype, static_cast<const unsigned short*>(workspace),
                                   state_in, state_out, o, out_dtype, B, H, HK, DK, DV, s_alloc, t0,
-                                  static_cast<int>(n_tokens / gdn2::kBS),
+                                  static_cast<int>((n_tokens + gdn2::kBS - 1) / gdn2::kBS), n_tokens,
                                   static_cast<hipStream_t>(stream)));
 }
 

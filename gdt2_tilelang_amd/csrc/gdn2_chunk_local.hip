@@ -75,7 +75,7 @@ struct ChunkSmem {
 template <int DK, int IN_DT>
 __global__ __launch_bounds__(256) void chunk_local_kernel(
     const void* __restrict__ qp, const void* __restrict__ kp, const void* __restrict__ bp,
-    const float* __restrict__ g, int H, long s_alloc, long t0, int NC, float scale,
+    const float* __restrict__ g, int H, long s_alloc, long t0, int NC, long n_tok, float scale,
     unsigned short* __restrict__ ws) {
   using L = ChunkLayout<DK>;
   using M = ChunkSmem<DK>;
@@ -109,8 +109,11 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
   const int h = bh % H;
   const long tok0 = t0 + static_cast<long>(n) * kBS;
   unsigned short* rec = ws + static_cast<size_t>(ch) * L::STRIDE;
+  // rows past the call's last token (a ragged last chunk) read as zeros, which
+  // the chunkwise form treats as inert; their loads re-read the last valid row
+  const int nvalid = static_cast<int>(min(static_cast<long>(kBS), n_tok - static_cast<long>(n) * kBS));
   auto row_base = [&](int r) -> size_t {
-    return ((static_cast<size_t>(bi) * s_alloc + tok0 + r) * H + h) * DK;
+    return ((static_cast<size_t>(bi) * s_alloc + tok0 + min(r, nvalid - 1)) * H + h) * DK;
   };
 
   // ---- phase A.1: chunk-local cumsum of g in log2 units -> sG ------------
@@ -121,7 +124,10 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
     const int part = tid / DK;
     float run[RPP];
 #pragma unroll
-    for (int r = 0; r < RPP; ++r) run[r] = g[row_base(part * RPP + r) + c];
+    for (int r = 0; r < RPP; ++r) {
+      const float x = g[row_base(part * RPP + r) + c];
+      run[r] = part * RPP + r < nvalid ? x : 0.f;
+    }
 #pragma unroll
     for (int r = 1; r < RPP; ++r) run[r] += run[r - 1];
     sTot[part * DK + c] = run[RPP - 1];
@@ -143,6 +149,10 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
     load8<IN_DT>(qp, idx, qv[kk]);
     load8<IN_DT>(kp, idx, kv[kk]);
     load8<IN_DT>(bp, idx, bv[kk]);
+    if (my_r >= nvalid) {
+#pragma unroll
+      for (int j = 0; j < 8; ++j) qv[kk][j] = kv[kk][j] = bv[kk][j] = 0.f;
+    }
     float4* dst = reinterpret_cast<float4*>(&sK[my_r * GP + c0]);
     dst[0] = make_float4(kv[kk][0], kv[kk][1], kv[kk][2], kv[kk][3]);
     dst[1] = make_float4(kv[kk][4], kv[kk][5], kv[kk][6], kv[kk][7]);
@@ -411,8 +421,8 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
 
 template <int DK, int IN_DT>
 static hipError_t launch_chunk_local_t(const void* q, const void* k, const void* b, const float* g,
-                                       int B, int H, long s_alloc, long t0, int NC, float scale,
-                                       unsigned short* ws, hipStream_t stream) {
+                                       int B, int H, long s_alloc, long t0, int NC, long n_tok,
+                                       float scale, unsigned short* ws, hipStream_t stream) {
   constexpr size_t smem = ChunkSmem<DK>::BYTES;
   static bool configured = false;   // attribute set once per process (same value always)
   if (!configured) {
@@ -424,22 +434,22 @@ static hipError_t launch_chunk_local_t(const void* q, const void* k, const void*
   }
   const unsigned grid = static_cast<unsigned>(B) * H * NC;
   hipLaunchKernelGGL((chunk_local_kernel<DK, IN_DT>), dim3(grid), dim3(256), smem, stream, q, k,
-                     b, g, H, s_alloc, t0, NC, scale, ws);
+                     b, g, H, s_alloc, t0, NC, n_tok, scale, ws);
   return hipGetLastError();
 }
 
 hipError_t launch_chunk_local2(const void* q, const void* k, const void* b, const float* g,
-                               int in_dt, int B, int H, long s_alloc, long t0, int NC,
+                               int in_dt, int B, int H, long s_alloc, long t0, int NC, long n_tok,
                                float scale, unsigned short* ws, hipStream_t stream);
 
 hipError_t launch_chunk_local(const void* q, const void* k, const void* b, const float* g,
                               int in_dt, int B, int H, int DK, long s_alloc, long t0, int NC,
-                              float scale, unsigned short* ws, hipStream_t stream) {
+                              long n_tok, float scale, unsigned short* ws, hipStream_t stream) {
   // DK = 128 runs the channel-sliced kernel (gdn2_chunk_local2.hip); DK = 64 this one.
-  if (DK == 128) return launch_chunk_local2(q, k, b, g, in_dt, B, H, s_alloc, t0, NC, scale, ws, stream);
+  if (DK == 128) return launch_chunk_local2(q, k, b, g, in_dt, B, H, s_alloc, t0, NC, n_tok, scale, ws, stream);
 #define GDN2_CL_CASE(DKV, DTV)                                                             \
   if (DK == DKV && in_dt == DTV)                                                           \
-    return launch_chunk_local_t<DKV, DTV>(q, k, b, g, B, H, s_alloc, t0, NC, scale, ws, stream);
+    return launch_chunk_local_t<DKV, DTV>(q, k, b, g, B, H, s_alloc, t0, NC, n_tok, scale, ws, stream);
   GDN2_CL_CASE(64, DT_BF16) GDN2_CL_CASE(64, DT_F16) GDN2_CL_CASE(64, DT_F32)
 #undef GDN2_CL_CASE
   return hipErrorInvalidValue;

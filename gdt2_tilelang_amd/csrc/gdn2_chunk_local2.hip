@@ -123,6 +123,10 @@ struct Raw8 {
       a = *reinterpret_cast<const u32x4*>(static_cast<const unsigned short*>(base) + idx);
     }
   }
+  __device__ __forceinline__ void zero() {   // +0.0 in every storage format
+    a = u32x4{0, 0, 0, 0};
+    b = u32x4{0, 0, 0, 0};
+  }
   __device__ __forceinline__ float operator[](int j) const {
     if constexpr (IN_DT == DT_F32) return __uint_as_float(j < 4 ? a[j] : b[j - 4]);
     else if constexpr (IN_DT == DT_BF16) return (j & 1) ? bf16_hi_f32(a[j >> 1]) : bf16_lo_f32(a[j >> 1]);
@@ -142,7 +146,7 @@ __device__ __forceinline__ void ld8(const float* p, float* x) {
 template <int IN_DT>
 __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
     const void* __restrict__ qp, const void* __restrict__ kp, const void* __restrict__ bp,
-    const float* __restrict__ g, int H, long s_alloc, long t0, int NC, float scale,
+    const float* __restrict__ g, int H, long s_alloc, long t0, int NC, long n_tok, float scale,
     unsigned short* __restrict__ ws) {
   using namespace cl2;
   using L = ChunkLayout<DK>;
@@ -168,8 +172,11 @@ __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
   const long tok0 = t0 + static_cast<long>(n) * kBS;
   unsigned short* rec = ws + static_cast<size_t>(ch) * L::STRIDE;
   const int c0 = CPW * wave + 8 * lq;        // first of this lane's 8 channels
+  // rows past the call's last token (a ragged last chunk) read as zeros, which
+  // the chunkwise form treats as inert; their loads re-read the last valid row
+  const int nvalid = static_cast<int>(min(static_cast<long>(kBS), n_tok - static_cast<long>(n) * kBS));
   auto gidx = [&](int r) -> size_t {
-    return ((static_cast<size_t>(bi) * s_alloc + tok0 + r) * H + h) * DK + c0;
+    return ((static_cast<size_t>(bi) * s_alloc + tok0 + min(r, nvalid - 1)) * H + h) * DK + c0;
   };
 
   float G[4][8];                      // live through phase B
@@ -188,6 +195,13 @@ __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
       qr[i].load(qp, idx);
       kr[i].load(kp, idx);
       br[i].load(bp, idx);
+      if (16 * i + lr >= nvalid) {
+#pragma unroll
+        for (int j = 0; j < 8; ++j) G[i][j] = 0.f;
+        qr[i].zero();
+        kr[i].zero();
+        br[i].zero();
+      }
     }
 
     {   // chunk maxima of |q|, |k|, |b k| -> LDS, combined after the A.3 barrier
@@ -374,6 +388,10 @@ __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
         const size_t idx = gidx(16 * i + lr);
         float xr[8];
         load8<IN_DT>(round == 0 ? qp : bp, idx, xr);
+        if (16 * i + lr >= nvalid) {
+#pragma unroll
+          for (int j = 0; j < 8; ++j) xr[j] = 0.f;
+        }
         if (round == 1) {
 #pragma unroll
           for (int j = 0; j < 8; ++j) xr[j] *= kr[i][j];
@@ -598,8 +616,8 @@ __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
 
 template <int IN_DT>
 static hipError_t launch_chunk_local2_t(const void* q, const void* k, const void* b, const float* g,
-                                        int B, int H, long s_alloc, long t0, int NC, float scale,
-                                        unsigned short* ws, hipStream_t stream) {
+                                        int B, int H, long s_alloc, long t0, int NC, long n_tok,
+                                        float scale, unsigned short* ws, hipStream_t stream) {
   constexpr int smem = cl2::LDS_BYTES;
   static bool configured = false;   // attribute set once per process (same value always)
   if (!configured) {
@@ -610,19 +628,19 @@ static hipError_t launch_chunk_local2_t(const void* q, const void* k, const void
   }
   const unsigned grid = static_cast<unsigned>(B) * H * NC;
   hipLaunchKernelGGL((chunk_local2_kernel<IN_DT>), dim3(grid), dim3(256), smem, stream, q, k, b, g,
-                     H, s_alloc, t0, NC, scale, ws);
+                     H, s_alloc, t0, NC, n_tok, scale, ws);
   return hipGetLastError();
 }
 
 hipError_t launch_chunk_local2(const void* q, const void* k, const void* b, const float* g,
-                               int in_dt, int B, int H, long s_alloc, long t0, int NC,
+                               int in_dt, int B, int H, long s_alloc, long t0, int NC, long n_tok,
                                float scale, unsigned short* ws, hipStream_t stream) {
   if (in_dt == DT_BF16)
-    return launch_chunk_local2_t<DT_BF16>(q, k, b, g, B, H, s_alloc, t0, NC, scale, ws, stream);
+    return launch_chunk_local2_t<DT_BF16>(q, k, b, g, B, H, s_alloc, t0, NC, n_tok, scale, ws, stream);
   if (in_dt == DT_F16)
-    return launch_chunk_local2_t<DT_F16>(q, k, b, g, B, H, s_alloc, t0, NC, scale, ws, stream);
+    return launch_chunk_local2_t<DT_F16>(q, k, b, g, B, H, s_alloc, t0, NC, n_tok, scale, ws, stream);
   if (in_dt == DT_F32)
-    return launch_chunk_local2_t<DT_F32>(q, k, b, g, B, H, s_alloc, t0, NC, scale, ws, stream);
+    return launch_chunk_local2_t<DT_F32>(q, k, b, g, B, H, s_alloc, t0, NC, n_tok, scale, ws, stream);
   return hipErrorInvalidValue;
 }
 

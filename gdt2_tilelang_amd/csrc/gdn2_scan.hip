@@ -62,6 +62,10 @@ struct Raw4 {
     if constexpr (IN_DT == DT_F32) v = *reinterpret_cast<const float4*>(static_cast<const float*>(base) + idx);
     else v = *reinterpret_cast<const uint2*>(static_cast<const unsigned short*>(base) + idx);
   }
+  __device__ __forceinline__ void zero() {   // +0.0 in every storage format
+    if constexpr (IN_DT == DT_F32) v = make_float4(0.f, 0.f, 0.f, 0.f);
+    else v = make_uint2(0u, 0u);
+  }
   __device__ __forceinline__ void get(float* x) const {
     if constexpr (IN_DT == DT_F32) {
       x[0] = v.x; x[1] = v.y; x[2] = v.z; x[3] = v.w;
@@ -124,7 +128,7 @@ template <int DK, int NT, int IN_DT, int OUT_DT>
 __global__ __launch_bounds__(kScanThreads) void scan_kernel(
     const void* __restrict__ v, const void* __restrict__ w, const unsigned short* __restrict__ ws,
     const float* __restrict__ s_in, float* __restrict__ s_out, void* __restrict__ o,
-    int BH, int H, int HK, int DV, long s_alloc, long t0, int NC) {
+    int BH, int H, int HK, int DV, long s_alloc, long t0, int NC, long n_tok) {
   using L = ChunkLayout<DK>;
   constexpr int KT = DK / 32;          // 32-row k blocks of S = state-owning waves
   constexpr int DVT = 16 * NT;
@@ -174,6 +178,9 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
   const int d0 = tile * DVT;
   const unsigned short* rec0 = ws + static_cast<size_t>(bhk) * NC * L::STRIDE;   // key head's records
   const int last = NC - 1;
+  // tokens of the last chunk (64 unless the call ends in a ragged chunk, whose
+  // missing rows read as zeros and whose o rows past the end are not stored)
+  const int nlast = static_cast<int>(n_tok - static_cast<long>(last) * kBS);
   auto recp = [&](int c) { return rec0 + static_cast<size_t>(min(c, last)) * L::STRIDE; };
   auto frag = [&](const unsigned short* rec, long off) {
     return *reinterpret_cast<const uint4*>(rec + off + o8);
@@ -236,9 +243,16 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
       for (int it = 0; it < ZIT; ++it) {
         const int e = zt + 128 * it;
         const int t = e / (DVT / 4), cq = e % (DVT / 4);
-        const size_t idx = ((static_cast<size_t>(bi) * s_alloc + t0 + static_cast<long>(min(nc, last)) * kBS + t) * H + h) * DV + d0 + 4 * cq;
+        const int cz = min(nc, last);
+        const bool ok = cz < last || t < nlast;
+        const int tl = ok ? t : nlast - 1;     // the load stays inside the call's tokens
+        const size_t idx = ((static_cast<size_t>(bi) * s_alloc + t0 + static_cast<long>(cz) * kBS + tl) * H + h) * DV + d0 + 4 * cq;
         zv[it].load(v, idx);
         zw[it].load(w, idx);
+        if (!ok) {
+          zv[it].zero();
+          zw[it].zero();
+        }
       }
     };
     auto put_z = [&](int buf) {
@@ -357,8 +371,9 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
         }
         __builtin_amdgcn_wave_barrier();
         constexpr int LPR = 16 * OSZ / 16;          // lanes per 16-element row (2 or 4)
-        if (lane < 16 * LPR) {
-          const int rr = lane / LPR, c = (lane % LPR) * (16 / OSZ);
+        const int rr = lane / LPR;
+        if (lane < 16 * LPR && (nc < last || 16 * m + rr < nlast)) {
+          const int c = (lane % LPR) * (16 / OSZ);
           const uint4 x = *reinterpret_cast<const uint4*>(so + (rr * 16 + c) * OSZ);
           const size_t oi = ((static_cast<size_t>(bi) * s_alloc + tok0 + 16 * m + rr) * H + h) * DV + d0 + 16 * nn + c;
           *reinterpret_cast<uint4*>(static_cast<unsigned char*>(o) + oi * OSZ) = x;
@@ -522,11 +537,11 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
 template <int DK, int NT, int IN_DT, int OUT_DT>
 static hipError_t launch_scan_t(const void* v, const void* w, const unsigned short* ws,
                                 const float* s_in, float* s_out, void* o, int B, int H, int HK,
-                                int DV, long s_alloc, long t0, int NC, hipStream_t stream) {
+                                int DV, long s_alloc, long t0, int NC, long n_tok, hipStream_t stream) {
   const int BH = B * H;
   const unsigned grid = static_cast<unsigned>(BH) * (DV / (16 * NT));
   hipLaunchKernelGGL((scan_kernel<DK, NT, IN_DT, OUT_DT>), dim3(grid), dim3(kScanThreads), 0, stream, v, w,
-                     ws, s_in, s_out, o, BH, H, HK, DV, s_alloc, t0, NC);
+                     ws, s_in, s_out, o, BH, H, HK, DV, s_alloc, t0, NC, n_tok);
   return hipGetLastError();
 }
 
@@ -539,12 +554,12 @@ int scan_nt_for(int B, int H, int DV) {
 
 hipError_t launch_scan(const void* v, const void* w, int in_dt, const unsigned short* ws,
                        const float* s_in, float* s_out, void* o, int out_dt, int B, int H, int HK, int DK,
-                       int DV, long s_alloc, long t0, int NC, hipStream_t stream) {
+                       int DV, long s_alloc, long t0, int NC, long n_tok, hipStream_t stream) {
   const int nt = scan_nt_for(B, H, DV);
 #define GDN2_SCAN_CASE(DKV, NTV, DTV, ODV)                                                     \
   if (DK == DKV && nt == NTV && in_dt == DTV && out_dt == ODV)                                 \
     return launch_scan_t<DKV, NTV, DTV, ODV>(v, w, ws, s_in, s_out, o, B, H, HK, DV, s_alloc, t0, \
-                                             NC, stream);
+                                             NC, n_tok, stream);
 #define GDN2_SCAN_OUT(DKV, NTV, DTV) \
   GDN2_SCAN_CASE(DKV, NTV, DTV, DT_BF16) GDN2_SCAN_CASE(DKV, NTV, DTV, DT_F16) GDN2_SCAN_CASE(DKV, NTV, DTV, DT_F32)
 #define GDN2_SCAN_DT(DKV, NTV) \

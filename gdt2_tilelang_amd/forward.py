@@ -4,9 +4,11 @@
 but runs the serving pipeline: the chunk-local kernel then the fused
 scan + output kernel, so the per-chunk states ``h`` are never materialised
 (the reference's ``state_kernel`` / ``output_kernel`` pair stores them only
-for its backward, which this backend does not provide). Sequences that are
-not a chunk multiple are zero-padded; the padding is inert because g = 0
-keeps the decay at 1 and b = w = 0 removes both erase and write.
+for its backward, which this backend does not provide). A sequence that is
+not a chunk multiple needs no padded copy (the reference zero-pads,
+``gdn2/forward.py:748-753``): the kernels read the missing rows of the last
+chunk as zeros, which are inert because g = 0 keeps the decay at 1 and
+b = w = 0 removes both erase and write.
 """
 
 from __future__ import annotations
@@ -14,17 +16,9 @@ from __future__ import annotations
 import torch
 
 from .config import DEFAULT_KERNEL_CONFIG, GDN2Config
-from .inference import _check_shapes, _prefill_chunks, _require_device, check_prefill_config
+from .inference import _check_shapes, _prefill_chunks, _require_device, _token_layout, check_prefill_config
 
 __all__ = ["chunk_gdn2_fwd", "chunk_gdn2_bwd"]
-
-
-def _pad_to_chunk(x: torch.Tensor, total: int) -> torch.Tensor:
-    """Right-pad the sequence axis of ``[B, S, H, D]`` with zeros to ``total``."""
-    if x.shape[1] == total:
-        return x.contiguous()
-    pad = x.new_zeros(x.shape[0], total - x.shape[1], *x.shape[2:])
-    return torch.cat([x, pad], dim=1)
 
 
 @torch.no_grad()
@@ -44,22 +38,19 @@ def chunk_gdn2_fwd(q, k, v, g, b, w, scale, initial_state=None, output_final_sta
     H, DV = v.shape[2], v.shape[3]
     if DK not in (64, 128) or DV % 32:
         raise ValueError(f"hip prefill supports DK in (64, 128) and DV % 32 == 0; got DK={DK}, DV={DV}")
-    BS = config.chunk_size
-    S_pad = ((S + BS - 1) // BS) * BS
-    q, k, v, b, w = (_pad_to_chunk(t, S_pad) for t in (q, k, v, b, w))
-    g = _pad_to_chunk(g.float(), S_pad)
+    (q, k, v, g, b, w), s_alloc = _token_layout((q, k, v, g.float(), b, w))
     if initial_state is not None:
         _require_device(q, initial_state)
         initial_state = initial_state.to(torch.float32).contiguous()
     final = torch.empty(B, H, DK, DV, dtype=torch.float32, device=dev)
-    o = torch.empty(B, S_pad, H, DV, dtype=config.output_dtype or q.dtype, device=dev)
-    if S_pad:
-        _prefill_chunks(q, k, v, g, b, w, initial_state, final, o, S_pad, 0, S_pad, scale)
+    o = torch.empty(B, S, H, DV, dtype=config.output_dtype or q.dtype, device=dev)
+    if S:
+        _prefill_chunks(q, k, v, g, b, w, initial_state, final, o, s_alloc, 0, S, scale)
     elif initial_state is not None:
         final.copy_(initial_state)
     else:
         final.zero_()
-    return o[:, :S], (final if output_final_state else None)
+    return o, (final if output_final_state else None)
 
 
 def chunk_gdn2_bwd(*args, **kwargs):

@@ -6,11 +6,14 @@ Mirrors the reference's ``gdn2/inference.py`` API:
     gdn2_decode(q, k, v, g, b, w, state, scale=None)                  -> o  (state in place)
     gdn2_decode_step(q, k, v, g, b, w, state, scale=None)             -> o  ([B, H, D] layout)
 
-Prefill runs whole 64-token chunks through the two prefill kernels (chunk-local
-WY stage, then the fused state scan + output that never materialises the
-per-chunk states) and a ragged tail through the decode kernel, exactly as the
-reference routes it (``gdn2/inference.py:517-555``). Decode keeps the state
-resident across the ``n`` tokens of a call.
+Prefill runs the prompt's 64-token chunks through the two prefill kernels
+(chunk-local WY stage, then the fused state scan + output that never
+materialises the per-chunk states); a ragged tail rides along as a last, partly
+filled chunk whose missing rows the kernels read as zeros. The reference sends
+that tail through its decode kernel instead (``gdn2/inference.py:517-555``);
+both compute the same recurrence, and a prompt shorter than one chunk still
+goes through decode with the state updated in place, as in the reference.
+Decode keeps the state resident across the ``n`` tokens of a call.
 
 Grouped heads: q, k, b, g may carry HK key heads where v, w (and the state)
 carry H value heads, HK dividing H; value head h then reads key head
@@ -162,8 +165,11 @@ def check_prefill_config(config: GDN2Config) -> None:
 def gdn2_prefill(q, k, v, g, b, w, state=None, scale=None, config: GDN2Config = DEFAULT_KERNEL_CONFIG):
     """Prefill a prompt; returns ``(o, state)`` to decode from.
 
-    Whole chunks go through the chunk-local kernel and the fused scan + output
-    kernel; a ragged tail goes through the decode kernel rather than padding.
+    The prompt goes through the chunk-local kernel and the fused scan + output
+    kernel, a ragged tail as a last, partly filled chunk (the reference runs
+    the tail through its decode kernel, ``inference.py:537-553``; both compute
+    the same recurrence). A prompt shorter than one chunk goes through the
+    decode kernel.
     Call repeatedly, passing the state back, to prefill in segments.
 
     Args:
@@ -200,9 +206,13 @@ def gdn2_prefill(q, k, v, g, b, w, state=None, scale=None, config: GDN2Config = 
     (q, k, v, g, b, w), s_alloc = _token_layout((q, k, v, g, b, w))
     o = torch.empty(B, s_alloc, H, DV, dtype=out_dtype, device=dev)
     if n_full:
+        # the ragged tail rides along as a last, partly filled chunk (its missing
+        # rows read as zeros, which the chunkwise form treats as inert)
         new_state = torch.empty_like(state)
-        _prefill_chunks(q, k, v, g, b, w, state, new_state, o, s_alloc, 0, n_full, scale)
+        _prefill_chunks(q, k, v, g, b, w, state, new_state, o, s_alloc, 0, S, scale)
         state = new_state
-    if S > n_full:
-        _decode_into(q, k, v, g, b, w, state, o, s_alloc, n_full, S - n_full, scale)
+    elif S:
+        # shorter than one chunk: the recurrence, updating state in place as the
+        # reference's decode path does
+        _decode_into(q, k, v, g, b, w, state, o, s_alloc, 0, S, scale)
     return o, state

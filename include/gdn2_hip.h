@@ -58,7 +58,7 @@ int gdn2_hip_decode(const void* q, const void* k, const void* v, const float* g,
                     void* stream);
 
 /* Bytes of workspace gdn2_hip_chunk_local / gdn2_hip_prefill_chunks need for
- * n_tokens (a multiple of 64) tokens of B x HK key heads; 0 for an unsupported
+ * n_tokens tokens (rounded up to whole 64-token chunks) of B x HK key heads; 0 for an unsupported
  * DK. The records depend on q, k, b, g only, so grouped value heads share them. */
 size_t gdn2_hip_prefill_workspace_bytes(int B, int HK, int DK, long n_tokens);
 
@@ -67,7 +67,9 @@ size_t gdn2_hip_prefill_workspace_bytes(int B, int HK, int DK, long n_tokens);
  * tokens [t0, t0 + n_tokens) build the log2-space decay cumsum, the Aqk / Akk
  * blocks, Ai = (I + Akk)^-1 and the WY factors, and write one record per chunk
  * into `workspace`. q, k, b, g are [B, s_alloc, HK, DK] (HK key heads; pass
- * the head count of those tensors). DK in {64, 128}; n_tokens a multiple of 64.
+ * the head count of those tensors). DK in {64, 128}. n_tokens need not be a
+ * multiple of 64: the last chunk's rows past n_tokens are read as zeros (they
+ * are never loaded), which leaves the state and the other outputs unchanged.
  * Replaces: wy_stages kernels 1-5 in gdn2/forward.py:801-826
  * (cumsum, intra_diag, inter_blocks, solve, wy).
  */
@@ -91,7 +93,8 @@ int gdn2_hip_prefill_scan(const void* v, const void* w, int in_dtype, const void
 
 /*
  * Both prefill stages back to back on one stream: o[t0 : t0+n_tokens] and the
- * state after the last token. Replaces the device branch of gdn2_prefill
+ * state after the last token (n_tokens any count >= 1; o rows past it are not
+ * written). Replaces the device branch of gdn2_prefill
  * (gdn2/inference.py:542-550) and of chunk_gdn2_fwd (gdn2/forward.py:870-895).
  */
 int gdn2_hip_prefill_chunks(const void* q, const void* k, const void* v, const float* g,

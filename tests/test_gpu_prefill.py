@@ -153,3 +153,34 @@ def test_grouped_heads_equal_repeated(DK, H, HK):
     d2 = gdn2_decode(qe[:, S:], ke[:, S:], v[:, S:], ge[:, S:], be[:, S:], w[:, S:], s2)
     torch.cuda.synchronize()
     assert torch.equal(o1, o2) and torch.equal(s1, s2) and torch.equal(d1, d2)
+
+
+@pytest.mark.parametrize("DK", [64, 128])
+def test_c_abi_ragged_window(DK):
+    """The C ABI on a window [t0, t0 + n) of a larger allocation with n not a
+    chunk multiple: the last chunk's missing rows are read as zeros, o rows
+    outside the window are left alone, and the result equals the recurrence on
+    the window alone."""
+    from gdt2_tilelang_amd import _hip
+
+    B, S_alloc, H, DV, t0, n = 2, 230, 2, 64, 10, 150
+    print(f"ragged window DK={DK} t0={t0} n={n} s_alloc={S_alloc}", flush=True)
+    cpu, dev = device_inputs(B, S_alloc, H, DK, DV, torch.bfloat16)
+    s0 = seeded_state(B, H, DK, DV)
+    win = tuple(t[:, t0:t0 + n] for t in cpu)
+    o_ref, s_ref = oracle.recurrent_gdn2(*win, None, s0.clone(), True)
+    q, k, v, g, b, w = dev
+    lib = _hip.lib()
+    ws = torch.empty(lib.gdn2_hip_prefill_workspace_bytes(B, H, DK, n), dtype=torch.uint8, device="cuda")
+    o = torch.full((B, S_alloc, H, DV), 7.0, device="cuda")
+    s_in, s_out = s0.cuda(), torch.empty(B, H, DK, DV, device="cuda")
+    P = _hip.ptr
+    _hip.check(lib.gdn2_hip_prefill_chunks(P(q), P(k), P(v), P(g), P(b), P(w), _hip.dtype_code(q.dtype),
+                                           P(s_in), P(s_out), P(o), 0, P(ws), B, H, H, DK, DV, S_alloc,
+                                           t0, n, DK ** -0.5, _hip.stream_of(q.device)), "prefill_chunks")
+    torch.cuda.synchronize()
+    oc = o.cpu()
+    assert (oc[:, :t0] == 7.0).all() and (oc[:, t0 + n:] == 7.0).all()
+    eo, es = rel_err(oc[:, t0:t0 + n], o_ref), rel_err(s_out.cpu(), s_ref)
+    print(f"  rel_err o={eo:.2e} state={es:.2e}", flush=True)
+    assert eo < TOL and es < TOL

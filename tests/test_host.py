@@ -66,8 +66,10 @@ def test_c_abi_rejects_bad_arguments_before_launch():
     assert lib.gdn2_hip_decode(*args, 1, fake, fake, 1, 1, 1, 1, 128, 128, 4, 2, 3, 0.1, nul) == -1
     # grouped heads: HK must divide H
     assert lib.gdn2_hip_decode(*args, 1, fake, fake, 1, 1, 6, 4, 128, 128, 1, 0, 1, 0.1, nul) == -1
-    assert lib.gdn2_hip_chunk_local(fake, fake, fake, fake, 1, fake, 1, 1, 128, 100, 0, 100, 0.1,
-                                    nul) == -2
+    # a ragged token count is accepted (the last chunk is partly filled), but the
+    # tokens must lie inside the allocation
+    assert lib.gdn2_hip_chunk_local(fake, fake, fake, fake, 1, fake, 1, 1, 128, 100, 0, 101, 0.1,
+                                    nul) == -1
     assert lib.gdn2_hip_chunk_local(fake, fake, fake, fake, 1, fake, 1, 1, 32, 64, 0, 64, 0.1,
                                     nul) == -2
     assert lib.gdn2_hip_prefill_scan(fake, fake, 1, fake, nul, fake, fake, 1, 1, 1, 1, 128, 24, 64, 0,
