@@ -233,6 +233,21 @@ class GatedDeltaNet2(nn.Module):
             self.__dict__[name] = hit
         return hit[1]
 
+    def _linear(self, x2, weight):
+        """x2 [M, K] @ weight^T. A few rows (decode) go through the library's
+        GEMV, which streams the weight once; more rows through torch."""
+        M, K = x2.shape
+        if (M <= 8 and K % 8 == 0 and x2.dtype == weight.dtype and weight.is_contiguous()
+                and not (torch.is_grad_enabled() and (weight.requires_grad or x2.requires_grad))
+                and x2.stride(1) == 1 and x2.stride(0) % 8 == 0 and x2.data_ptr() % 16 == 0
+                and weight.data_ptr() % 16 == 0):
+            y = torch.empty(M, weight.shape[0], device=x2.device, dtype=x2.dtype)
+            _hip.check(_hip.lib().gdn2_hip_gemv(
+                x2.data_ptr(), x2.stride(0), weight.data_ptr(), y.data_ptr(), y.stride(0),
+                _hip.dtype_code(x2.dtype), M, weight.shape[0], K, _hip.stream_of(x2.device)), "gdn2_hip_gemv")
+            return y
+        return F.linear(x2, weight)
+
     def _proj_weights(self):
         # one [4*HK*DK + 3*H*DV, hidden] weight: q | k | v | b | w | f | o_gate
         return self._cat_cached("_wcat", [self.q_proj.weight, self.k_proj.weight, self.v_proj.weight,
@@ -247,7 +262,7 @@ class GatedDeltaNet2(nn.Module):
         HK, H, DK, DV = self.num_kv_heads, self.num_heads, self.head_dim_k, self.head_dim_v
         dqk, dv = HK * DK, H * DV
         dt = x.dtype
-        proj = F.linear(x.reshape(B * S, hid), self._proj_weights())     # [B*S, 4 dqk + 3 dv]
+        proj = self._linear(x.reshape(B * S, hid), self._proj_weights())     # [B*S, 4 dqk + 3 dv]
         ld = proj.shape[1]
         es = proj.element_size()
         base = proj.data_ptr()
@@ -299,7 +314,7 @@ class GatedDeltaNet2(nn.Module):
             _hip.ptr(o), _hip.dtype_code(o.dtype), gate_ptr, ld, _hip.ptr(weight), float(self.o_norm.eps),
             _hip.ptr(out), _hip.dtype_code(x.dtype), dv, B, S, H, DV, _hip.stream_of(x.device)),
             "gdn2_hip_layer_epilogue")
-        return self.o_proj(out)
+        return self._linear(out.reshape(B * S, dv), self.o_proj.weight).view(B, S, -1)
 
     # -- pieces shared by forward / prefill / decode -----------------------
     def _decay(self, x, lead):

@@ -13,6 +13,7 @@ hipError_t launch_chunk_local(const void*, const void*, const void*, const float
                               int, long, long, int, long, float, unsigned short*, hipStream_t);
 hipError_t launch_scan(const void*, const void*, int, const unsigned short*, const float*, float*,
                        void*, int, int, int, int, int, int, long, long, int, long, hipStream_t);
+hipError_t launch_gemv(const void*, const void*, void*, int, int, int, int, long, long, hipStream_t);
 }  // namespace gdn2
 
 namespace {
@@ -158,6 +159,16 @@ int gdn2_hip_layer_prologue(const void* xq, const void* xk, const void* xv, cons
   a.q = q; a.k = k; a.v = v; a.b = b; a.w = w; a.g = g;
   a.B = B; a.S = S; a.H = H; a.HK = HK; a.DK = DK; a.DV = DV;
   return status(gdn2::launch_layer_prologue(a, act_dtype, static_cast<hipStream_t>(stream)));
+}
+
+int gdn2_hip_gemv(const void* x, long ldx, const void* W, void* y, long ldy, int dtype, int M, int N,
+                  int K, void* stream) {
+  if (!x || !W || !y) return GDN2_ERR_ARG;
+  if (!dtype_ok(dtype) || M < 1 || N < 1 || K < 1 || ldx < K || ldy < N) return GDN2_ERR_ARG;
+  if (M > 8 || K % 8) return GDN2_ERR_SHAPE;
+  // 16-byte vector reads of x and W rows
+  if (ldx % 8 || reinterpret_cast<uintptr_t>(x) % 16 || reinterpret_cast<uintptr_t>(W) % 16) return GDN2_ERR_ARG;
+  return status(gdn2::launch_gemv(x, W, y, dtype, M, N, K, ldx, ldy, static_cast<hipStream_t>(stream)));
 }
 
 int gdn2_hip_layer_epilogue(const void* o, int o_dtype, const void* gate, long ld_gate,

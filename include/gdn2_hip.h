@@ -133,6 +133,17 @@ int gdn2_hip_layer_prologue(const void* xq, const void* xk, const void* xv, cons
                             int HK, int DK, int DV, void* stream);
 
 /*
+ * Few-row linear layer y = x W^T: x [M, K] (row stride ldx), W [N, K] (the
+ * nn.Linear weight, contiguous), y [M, N] (row stride ldy), all in dtype, fp32
+ * accumulation. M <= 8, K and ldx multiples of 8, x and W 16-byte aligned.
+ * Bound by reading W once; for decode steps of a few tokens it replaces the
+ * layer's projection GEMMs (gdn2/attention.py:440-454 and o_proj :268, :414,
+ * which torch runs through hipBLASLt).
+ */
+int gdn2_hip_gemv(const void* x, long ldx, const void* W, void* y, long ldy, int dtype, int M, int N,
+                  int K, void* stream);
+
+/*
  * GatedDeltaNet2 layer epilogue: per token and value head,
  *   out = o * rsqrt(mean(o^2) + eps) * weight * silu(gate)
  * o [B, S, H, DV] contiguous in o_dtype; gate and out rows of H*DV in

@@ -107,3 +107,22 @@ def test_fused_prologue_epilogue_match_torch_formulas(dtype, tol, S, with_cache)
         out_gpu = layer._finish_gpu(x, o, proj)
         out_ref = layer._finish(x, o)
         assert rel_err(out_gpu.float(), out_ref.float()) < tol
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-5), (torch.bfloat16, 8e-3)])
+@pytest.mark.parametrize("M,N,K", [(1, 10240, 2048), (3, 2048, 2048), (8, 100, 64), (5, 37, 8)])
+def test_gemv_matches_linear(dtype, tol, M, N, K):
+    """The few-row linear layer (C ABI) against torch's fp32 product, at one
+    rounding of the output dtype."""
+    from gdt2_tilelang_amd import _hip
+    print(f"gemv M={M} N={N} K={K} {dtype}", flush=True)
+    gen = torch.Generator().manual_seed(M * 7 + N)
+    x = torch.randn(M, K, generator=gen).to(dtype).cuda()
+    W = (torch.randn(N, K, generator=gen) * K ** -0.5).to(dtype).cuda()
+    y = torch.empty(M, N, dtype=dtype, device="cuda")
+    _hip.check(_hip.lib().gdn2_hip_gemv(x.data_ptr(), K, W.data_ptr(), y.data_ptr(), N, _hip.dtype_code(dtype),
+                                        M, N, K, _hip.stream_of(x.device)), "gemv")
+    ref = x.float() @ W.float().t()
+    err = ((y.float() - ref).abs().max() / ref.abs().max()).item()
+    print(f"  rel err {err:.2e}", flush=True)
+    assert err < tol
