@@ -316,6 +316,64 @@ class GatedDeltaNet2(nn.Module):
             "gdn2_hip_layer_epilogue")
         return self._linear(out.reshape(B * S, dv), self.o_proj.weight).view(B, S, -1)
 
+    def _decode_fused(self, x, cache):
+        """A decode call of B*n <= 8 tokens as one library call
+        (gdn2_hip_layer_decode: projections, prologue, recurrence, gated norm,
+        o_proj). Returns the output, or None when the shapes or the cache do not
+        qualify (the caller then takes the per-stage path)."""
+        B, n, hid = x.shape
+        st = cache.recurrent_state
+        HK, H, DK, DV = self.num_kv_heads, self.num_heads, self.head_dim_k, self.head_dim_v
+        dt = x.dtype
+        if (B * n > 8 or hid % 8 or (H * DV) % 8 or DK % 8 or (DK // 8) & (DK // 8 - 1) or DK > 512
+                or DV % 32 or DK not in (32, 64, 128, 256) or st is None or st.dtype != torch.float32
+                or not st.is_contiguous() or tuple(st.shape) != (B, H, DK, DV) or st.device != x.device
+                or self.o_proj.weight.dtype != dt):
+            return None
+        lib = _hip.lib()
+        code = _hip.dtype_code(dt)
+        key = (B, n, dt, x.device)
+        hit = self.__dict__.get("_dec_ws")
+        if hit is None or hit[0] != key:
+            nbytes = lib.gdn2_hip_layer_decode_workspace_bytes(B, n, H, HK, DK, DV, code)
+            hit = (key, torch.empty(nbytes + 256, dtype=torch.uint8, device=x.device))
+            self.__dict__["_dec_ws"] = hit
+        ws_ptr = (hit[1].data_ptr() + 255) // 256 * 256
+        x2 = x.reshape(B * n, hid).contiguous()
+        if x2.data_ptr() % 16:
+            x2 = x2.clone()
+        w_proj = self._proj_weights()
+        w_out = self.o_proj.weight.detach()
+        if not w_out.is_contiguous():
+            return None
+        conv_w = conv_b = conv_in = conv_out = None
+        K = 0
+        if self.q_conv is not None:
+            K = self.cfg.conv_size
+            convs = (self.q_conv.conv, self.k_conv.conv, self.v_conv.conv)
+            conv_w = self._cat_cached("_convw", [c.weight for c in convs])
+            if conv_w.dtype != dt:
+                conv_w = conv_w.to(dt)
+            if all(c.bias is not None for c in convs):
+                conv_b = self._cat_cached("_convb", [c.bias for c in convs])
+                conv_b = conv_b.to(dt).reshape(-1) if conv_b.dtype != dt else conv_b.reshape(-1)
+            if cache.conv_state is not None:
+                conv_in = cache.conv_state.to(dt).contiguous()
+                if conv_in.data_ptr() % 16:
+                    conv_in = conv_in.clone()
+            conv_out = torch.empty(B, 2 * HK * DK + H * DV, K - 1, device=x.device, dtype=dt)
+        out = torch.empty(B, n, hid, device=x.device, dtype=dt)
+        P = _hip.ptr
+        _hip.check(lib.gdn2_hip_layer_decode(
+            P(x2), P(w_proj), P(conv_w), P(conv_b), K, P(conv_in), P(conv_out),
+            P(self._f32_cached("_alog32", self.A_log)), P(self._f32_cached("_dtb32", self.dt_bias)),
+            float(self.erase_scale), P(st), P(self._f32_cached("_onw32", self.o_norm.weight)),
+            float(self.o_norm.eps), P(w_out), P(out), ws_ptr, code, B, n, hid, H, HK, DK, DV,
+            float(self.scale), _hip.stream_of(x.device)), "gdn2_hip_layer_decode")
+        if self.q_conv is not None:
+            cache.conv_state = conv_out
+        return out
+
     # -- pieces shared by forward / prefill / decode -----------------------
     def _decay(self, x, lead):
         f = self.f_proj(x).view(*lead, self.num_kv_heads, self.head_dim_k)
@@ -409,6 +467,9 @@ class GatedDeltaNet2(nn.Module):
     def decode(self, hidden_states, cache):
         """Decode ``n`` tokens ``[B, n, hidden]``, updating ``cache`` in place."""
         if hidden_states.is_cuda:
+            out = self._decode_fused(hidden_states, cache)
+            if out is not None:
+                return out, cache
             (q, k, v, g, b, w), proj, conv_out = self._project_gpu(hidden_states, cache)
             cache.conv_state = conv_out
             o = gdn2_decode(q, k, v, g, b, w, cache.recurrent_state, scale=self.scale)

@@ -183,4 +183,66 @@ int gdn2_hip_layer_epilogue(const void* o, int o_dtype, const void* gate, long l
                                             rows, H, DV, static_cast<hipStream_t>(stream)));
 }
 
+// Workspace of gdn2_hip_layer_decode: segments of M rows, each 256-byte aligned.
+struct DecodeWs {
+  size_t proj, q, k, b, v, w, g, o, normed, bytes;
+};
+
+static DecodeWs decode_ws(long M, int H, int HK, int DK, int DV, int dtype) {
+  const size_t es = dtype == gdn2::DT_F32 ? 4 : 2;
+  const long dqk = static_cast<long>(HK) * DK, dv = static_cast<long>(H) * DV;
+  auto up = [](size_t x) { return (x + 255) / 256 * 256; };
+  DecodeWs s;
+  size_t at = 0;
+  s.proj = at; at += up(M * (4 * dqk + 3 * dv) * es);
+  s.q = at; at += up(M * dqk * es);
+  s.k = at; at += up(M * dqk * es);
+  s.b = at; at += up(M * dqk * es);
+  s.v = at; at += up(M * dv * es);
+  s.w = at; at += up(M * dv * es);
+  s.g = at; at += up(M * dqk * 4);
+  s.o = at; at += up(M * dv * es);
+  s.normed = at; at += up(M * dv * es);
+  s.bytes = at;
+  return s;
+}
+
+size_t gdn2_hip_layer_decode_workspace_bytes(int B, int n, int H, int HK, int DK, int DV, int dtype) {
+  if (B < 1 || n < 1 || H < 1 || HK < 1 || DK < 1 || DV < 1 || !dtype_ok(dtype)) return 0;
+  return decode_ws(static_cast<long>(B) * n, H, HK, DK, DV, dtype).bytes;
+}
+
+int gdn2_hip_layer_decode(const void* x, const void* w_proj, const void* conv_w, const void* conv_b,
+                          int conv_k, const void* conv_in, void* conv_out, const float* a_log,
+                          const float* dt_bias, float erase_scale, float* state, const float* norm_w,
+                          float norm_eps, const void* w_out, void* out, void* workspace, int dtype, int B,
+                          int n, int hidden, int H, int HK, int DK, int DV, float scale, void* stream) {
+  if (!x || !w_proj || !w_out || !out || !workspace || !state || !norm_w) return GDN2_ERR_ARG;
+  if (B < 1 || n < 1 || hidden < 1 || H < 1 || HK < 1 || H % HK || !dtype_ok(dtype)) return GDN2_ERR_ARG;
+  if (reinterpret_cast<uintptr_t>(workspace) % 256) return GDN2_ERR_ARG;
+  const int M = B * n;
+  const long dqk = static_cast<long>(HK) * DK, dv = static_cast<long>(H) * DV;
+  const long ldp = 4 * dqk + 3 * dv;
+  const DecodeWs s = decode_ws(M, H, HK, DK, DV, dtype);
+  char* ws = static_cast<char*>(workspace);
+  const size_t es = dtype == gdn2::DT_F32 ? 4 : 2;
+  char* proj = ws + s.proj;
+  // projections: one [M, 4 dqk + 3 dv] product (q | k | v | b | w | f | o_gate)
+  if (int e = gdn2_hip_gemv(x, hidden, w_proj, proj, ldp, dtype, M, static_cast<int>(ldp), hidden, stream)) return e;
+  const long offs[6] = {0, dqk, 2 * dqk, 2 * dqk + dv, 3 * dqk + dv, 3 * dqk + 2 * dv};   // q k v b w f
+  if (int e = gdn2_hip_layer_prologue(proj + offs[0] * es, proj + offs[1] * es, proj + offs[2] * es,
+                                      proj + offs[3] * es, proj + offs[4] * es, proj + offs[5] * es, ldp, ldp,
+                                      ldp, ldp, ldp, ldp, dtype, conv_w, conv_b, conv_k, conv_in, conv_out,
+                                      a_log, dt_bias, erase_scale, ws + s.q, ws + s.k, ws + s.v, ws + s.b,
+                                      ws + s.w, reinterpret_cast<float*>(ws + s.g), B, n, H, HK, DK, DV, stream))
+    return e;
+  if (int e = gdn2_hip_decode(ws + s.q, ws + s.k, ws + s.v, reinterpret_cast<const float*>(ws + s.g), ws + s.b,
+                              ws + s.w, dtype, state, ws + s.o, dtype, B, H, HK, DK, DV, n, 0, n, scale, stream))
+    return e;
+  if (int e = gdn2_hip_layer_epilogue(ws + s.o, dtype, proj + (4 * dqk + 2 * dv) * es, ldp, norm_w, norm_eps,
+                                      ws + s.normed, dtype, dv, B, n, H, DV, stream))
+    return e;
+  return gdn2_hip_gemv(ws + s.normed, dv, w_out, out, hidden, dtype, M, hidden, static_cast<int>(dv), stream);
+}
+
 }  // extern "C"

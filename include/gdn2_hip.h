@@ -144,6 +144,24 @@ int gdn2_hip_gemv(const void* x, long ldx, const void* W, void* y, long ldy, int
                   int K, void* stream);
 
 /*
+ * One GatedDeltaNet2 decode call of n tokens for B sequences (B*n <= 8), as
+ * the five launches above on one stream: projections (gdn2_hip_gemv with the
+ * fused weight w_proj [4*HK*DK + 3*H*DV, hidden], rows q | k | v | b | w | f |
+ * o_gate), the layer prologue (conv with conv_in -> conv_out, L2 norm, gates,
+ * decay), the recurrence on `state` (fp32 [B, H, DK, DV], updated in place),
+ * the gated RMSNorm (norm_w fp32 [DV]) and o_proj (w_out [hidden, H*DV]).
+ * x [B*n, hidden] and out [B*n, hidden] in dtype. Intermediates live in
+ * `workspace` (256-byte aligned, gdn2_hip_layer_decode_workspace_bytes).
+ * Replaces: GatedDeltaNet2.decode / step (gdn2/attention.py:417-478).
+ */
+size_t gdn2_hip_layer_decode_workspace_bytes(int B, int n, int H, int HK, int DK, int DV, int dtype);
+int gdn2_hip_layer_decode(const void* x, const void* w_proj, const void* conv_w, const void* conv_b,
+                          int conv_k, const void* conv_in, void* conv_out, const float* a_log,
+                          const float* dt_bias, float erase_scale, float* state, const float* norm_w,
+                          float norm_eps, const void* w_out, void* out, void* workspace, int dtype, int B,
+                          int n, int hidden, int H, int HK, int DK, int DV, float scale, void* stream);
+
+/*
  * GatedDeltaNet2 layer epilogue: per token and value head,
  *   out = o * rsqrt(mean(o^2) + eps) * weight * silu(gate)
  * o [B, S, H, DV] contiguous in o_dtype; gate and out rows of H*DV in

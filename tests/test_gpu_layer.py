@@ -126,3 +126,29 @@ def test_gemv_matches_linear(dtype, tol, M, N, K):
     err = ((y.float() - ref).abs().max() / ref.abs().max()).item()
     print(f"  rel err {err:.2e}", flush=True)
     assert err < tol
+
+
+@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
+def test_fused_decode_call_matches_stagewise(dtype, tol):
+    """GatedDeltaNet2.decode for B*n <= 8 runs as one library call
+    (gdn2_hip_layer_decode); it must agree with the per-stage GPU path
+    (hipBLASLt projections, the same prologue / decode / epilogue kernels)."""
+    from gdt2_tilelang_amd.inference import gdn2_decode
+    torch.manual_seed(0)
+    cfg = GatedDeltaNet2Config(hidden_size=256, num_heads=4, num_kv_heads=2, head_dim_k=64, head_dim_v=64)
+    layer = GatedDeltaNet2(cfg).cuda().to(dtype).eval()
+    B, n = 2, 3
+    print(f"fused decode {dtype} B={B} n={n}", flush=True)
+    x0 = torch.randn(B, 70, 256, device="cuda").to(dtype)
+    xs = torch.randn(B, n, 256, device="cuda").to(dtype)
+    _, cache = layer.prefill(x0, None)
+    c2 = type(cache)(cache.recurrent_state.clone(), cache.conv_state.clone())
+    out1, cache = layer.decode(xs, cache)
+    with torch.no_grad():
+        (q, k, v, g, b, w), proj, conv_out = layer._project_gpu(xs, c2)
+        o = gdn2_decode(q, k, v, g, b, w, c2.recurrent_state, scale=layer.scale)
+        out2 = layer._finish_gpu(xs, o, proj)
+    torch.cuda.synchronize()
+    assert rel_err(out1.float().cpu(), out2.float().cpu()) < tol
+    assert rel_err(cache.recurrent_state.cpu(), c2.recurrent_state.cpu()) < tol
+    assert rel_err(cache.conv_state.float().cpu(), conv_out.float().cpu()) < tol
