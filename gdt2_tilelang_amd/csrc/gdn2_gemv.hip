@@ -17,7 +17,7 @@ namespace gdn2 {
 namespace gv {
 
 constexpr int kThreads = 256;
-constexpr int RW = 4;            // output rows per wave
+constexpr int RW = 2;            // output rows per wave (measured best of 1, 2, 4, 8, 16)
 constexpr int kMaxM = 8;         // x rows handled per launch
 
 template <int DT>
@@ -56,6 +56,7 @@ __global__ __launch_bounds__(kThreads) void gemv_kernel(const void* __restrict__
   long wrow[RW];
 #pragma unroll
   for (int r = 0; r < RW; ++r) wrow[r] = static_cast<long>(min(n0 + r, N - 1)) * K;
+#pragma unroll 4
   for (int k0 = 8 * lane; k0 < K; k0 += 512) {
     Vec8<DT> wv[RW], xv[M];
 #pragma unroll
