@@ -128,21 +128,27 @@ def test_gemv_matches_linear(dtype, tol, M, N, K):
     assert err < tol
 
 
-@pytest.mark.parametrize("dtype,tol", [(torch.float32, 1e-4), (torch.bfloat16, 2e-2)])
-def test_fused_decode_call_matches_stagewise(dtype, tol):
+@pytest.mark.parametrize("dtype,tol,B,n,conv", [
+    (torch.float32, 1e-4, 2, 3, 4), (torch.bfloat16, 2e-2, 2, 3, 4), (torch.float16, 1e-2, 1, 8, 4),
+    (torch.bfloat16, 2e-2, 1, 1, 2), (torch.float32, 1e-4, 4, 2, 0), (torch.bfloat16, 2e-2, 3, 3, 4),
+])
+def test_fused_decode_call_matches_stagewise(dtype, tol, B, n, conv):
     """GatedDeltaNet2.decode for B*n <= 8 runs as one library call
     (gdn2_hip_layer_decode); it must agree with the per-stage GPU path
-    (hipBLASLt projections, the same prologue / decode / epilogue kernels)."""
+    (hipBLASLt projections, the same prologue / decode / epilogue kernels).
+    B*n = 9 takes the per-stage path itself; conv 0 is a layer without the
+    short convolution."""
     from gdt2_tilelang_amd.inference import gdn2_decode
     torch.manual_seed(0)
-    cfg = GatedDeltaNet2Config(hidden_size=256, num_heads=4, num_kv_heads=2, head_dim_k=64, head_dim_v=64)
+    cfg = GatedDeltaNet2Config(hidden_size=256, num_heads=4, num_kv_heads=2, head_dim_k=64, head_dim_v=64,
+                               conv_size=conv)
     layer = GatedDeltaNet2(cfg).cuda().to(dtype).eval()
-    B, n = 2, 3
-    print(f"fused decode {dtype} B={B} n={n}", flush=True)
+    print(f"fused decode {dtype} B={B} n={n} conv={conv}", flush=True)
     x0 = torch.randn(B, 70, 256, device="cuda").to(dtype)
     xs = torch.randn(B, n, 256, device="cuda").to(dtype)
     _, cache = layer.prefill(x0, None)
-    c2 = type(cache)(cache.recurrent_state.clone(), cache.conv_state.clone())
+    c2 = type(cache)(cache.recurrent_state.clone(),
+                     None if cache.conv_state is None else cache.conv_state.clone())
     out1, cache = layer.decode(xs, cache)
     with torch.no_grad():
         (q, k, v, g, b, w), proj, conv_out = layer._project_gpu(xs, c2)
@@ -151,4 +157,7 @@ def test_fused_decode_call_matches_stagewise(dtype, tol):
     torch.cuda.synchronize()
     assert rel_err(out1.float().cpu(), out2.float().cpu()) < tol
     assert rel_err(cache.recurrent_state.cpu(), c2.recurrent_state.cpu()) < tol
-    assert rel_err(cache.conv_state.float().cpu(), conv_out.float().cpu()) < tol
+    if conv:
+        assert rel_err(cache.conv_state.float().cpu(), conv_out.float().cpu()) < tol
+    else:
+        assert cache.conv_state is None and conv_out is None
