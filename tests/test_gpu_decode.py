@@ -116,11 +116,14 @@ def test_decode_baseline_configs(B, n, prompt):
     assert rel_err(st.cpu(), st_ref) < 2e-3
 
 
-@pytest.mark.parametrize("B,H,DK,DV,n", [(57, 13, 64, 96, 11), (40, 13, 128, 128, 8)])
+@pytest.mark.parametrize("B,H,DK,DV,n", [
+    (57, 13, 64, 96, 11), (40, 13, 128, 128, 8),
+    (64, 8, 64, 64, 5), (128, 4, 32, 32, 3), (32, 8, 128, 256, 8), (48, 11, 128, 96, 2),
+])
 def test_decode_many_heads(B, H, DK, DV, n):
     """Multi-token decode over hundreds of heads (odd head counts), a partial
-    column tile (DV = 96: three waves per workgroup) and a second token block
-    (n = 11)."""
+    column tile (DV = 96: three waves per workgroup), a second token block
+    (n = 11), one-wave workgroups (DV = 32) and two column tiles per head."""
     print(f"decode many heads B={B} H={H} DK={DK} DV={DV} n={n}", flush=True)
     cpu, dev = device_inputs(B, n, H, DK, DV, torch.bfloat16)
     s0 = seeded_state(B, H, DK, DV)
