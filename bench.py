@@ -281,7 +281,7 @@ def main():
     args = ap.parse_args()
     if args.gpus != 1:
         print(json.dumps({"error": "this build runs on one GPU only; the GDN-2 path shards by "
-                                   "batch/head with no exchange (see DESIGN.md), --gpus must be 1"}))
+                                   "batch/head with no exchange between GPUs, so one GPU's share is the same kernels at a smaller shape; --gpus must be 1"}))
         sys.exit(2)
     if not torch.cuda.is_available():
         print(json.dumps({"error": "no GPU visible"}))
