@@ -184,3 +184,39 @@ def test_c_abi_ragged_window(DK):
     eo, es = rel_err(oc[:, t0:t0 + n], o_ref), rel_err(s_out.cpu(), s_ref)
     print(f"  rel_err o={eo:.2e} state={es:.2e}", flush=True)
     assert eo < TOL and es < TOL
+
+
+def test_prefill_random_shapes():
+    """Seeded random shapes against the oracle: ragged lengths (including under
+    one chunk), grouped heads, DK 64 / 128, DV from 32 to 256, three input
+    dtypes, with and without an initial state."""
+    gen = torch.Generator().manual_seed(1234)
+
+    def pick(xs):
+        return xs[int(torch.randint(len(xs), (1,), generator=gen))]
+
+    for case in range(14):
+        B = pick([1, 2, 3])
+        S = int(torch.randint(1, 700, (1,), generator=gen))
+        HK = pick([1, 2, 3])
+        H = HK * pick([1, 2])
+        DK = pick([64, 128])
+        DV = pick([32, 64, 96, 128, 160, 256])
+        dtype = pick([torch.bfloat16, torch.float16, torch.float32])
+        with_state = bool(torch.randint(2, (1,), generator=gen))
+        print(f"case {case}: B={B} S={S} H={H} HK={HK} DK={DK} DV={DV} {dtype} state={with_state}", flush=True)
+        cpu, dev = device_inputs(B, S, H, DK, DV, dtype, seed=case)
+        # grouped heads: the key-side tensors keep the first HK heads
+        cpu = (cpu[0][:, :, :HK], cpu[1][:, :, :HK], cpu[2], cpu[3][:, :, :HK], cpu[4][:, :, :HK], cpu[5])
+        dev = tuple(t.contiguous() for t in (dev[0][:, :, :HK], dev[1][:, :, :HK], dev[2], dev[3][:, :, :HK],
+                                             dev[4][:, :, :HK], dev[5]))
+        rep = H // HK
+        exp = lambda t: t.repeat_interleave(rep, dim=2)
+        s0 = seeded_state(B, H, DK, DV, seed=case) if with_state else None
+        o_ref, s_ref = oracle.prefill(exp(cpu[0]), exp(cpu[1]), cpu[2], exp(cpu[3]), exp(cpu[4]), cpu[5],
+                                      None if s0 is None else s0.clone())
+        o, st = gdn2_prefill(*dev, None if s0 is None else s0.cuda(), config=F32)
+        torch.cuda.synchronize()
+        eo, es = rel_err(o.cpu(), o_ref), rel_err(st.cpu(), s_ref)
+        print(f"  rel_err o={eo:.2e} state={es:.2e}", flush=True)
+        assert eo < TOL and es < TOL
