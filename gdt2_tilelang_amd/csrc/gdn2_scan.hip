@@ -46,6 +46,12 @@
 namespace gdn2 {
 
 constexpr int kScanWaves = 8;
+// record-fragment register buffers: 2 refills two chunks ahead (hides more
+// latency), 1 refills one chunk ahead; NT = 2 takes 1, which keeps it out of
+// scratch (226 VGPRs instead of 256 plus spills; B=8 headline scan 381 -> 343 us),
+// NT = 1 keeps 2 (118 vs 127 us at B=2).
+template <int NT>
+constexpr int kScanRecordBuffers = NT == 2 ? 1 : 2;
 constexpr int kScanThreads = 64 * kScanWaves;
 
 template <int DK>
@@ -197,12 +203,13 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
     const int u = (wave - 4) & 1;        // token-row pair (UN, ZU)
 
     // ---- record fragments, double-buffered by chunk parity -------------------
-    uint4 fq[2][OUT ? KT : 1], fa[2][OUT ? 2 : 1];            // Qg_m, Aqk_m
-    uint4 fk[2][STATE ? 2 : 1][2];                              // KG^T tiles 2w, 2w+1
-    float4 gam[2][STATE ? 2 : 1];
-    uint4 fw[2][UN ? 2 : 1][UN ? KT : 1];                       // W blocks 2u, 2u+1
-    uint4 fi[2][ZU ? 2 : 1][2];                                 // Ai blocks 2u, 2u+1
-    float sc[2][5];
+    constexpr int NB = kScanRecordBuffers<NT>;
+    uint4 fq[NB][OUT ? KT : 1], fa[NB][OUT ? 2 : 1];          // Qg_m, Aqk_m
+    uint4 fk[NB][STATE ? 2 : 1][2];                             // KG^T tiles 2w, 2w+1
+    float4 gam[NB][STATE ? 2 : 1];
+    uint4 fw[NB][UN ? 2 : 1][UN ? KT : 1];                      // W blocks 2u, 2u+1
+    uint4 fi[NB][ZU ? 2 : 1][2];                                // Ai blocks 2u, 2u+1
+    float sc[NB][5];
     auto load_all = [&](int p, const unsigned short* rec) {
       if constexpr (OUT) {
 #pragma unroll
@@ -384,7 +391,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
 
     // ---- set-up: records of chunks 0 and 1, Z_0 and U_0, S_0 ------------------
     load_all(0, recp(0));
-    load_all(1, recp(1));
+    if constexpr (NB == 2) load_all(1, recp(1));
     if constexpr (ZU) {
       fetch_z(0);
       put_z(0);
@@ -410,19 +417,20 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
 #pragma unroll
       for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) fi[0][bb][kk] = frag(recp(2), L::ai_frag(2 * u + bb, kk));
+        for (int kk = 0; kk < 2; ++kk) fi[0][bb][kk] = frag(recp(NB), L::ai_frag(2 * u + bb, kk));
     }
     __syncthreads();
 
     // ---- the chunk loop --------------------------------------------------------
     auto step = [&](auto parity, int nc) {
-      constexpr int p = decltype(parity)::value;   // == nc & 1
-      const unsigned short* rp = recp(nc + 2);      // refills: chunk nc + 2 into buffer p
+      constexpr int ph = decltype(parity)::value;  // == nc & 1 (LDS buffers)
+      constexpr int p = ph % NB;                    // record-fragment buffer
+      const unsigned short* rp = recp(nc + NB);     // refills: chunk nc + NB into buffer p
 
       // phase 1
       f32x4 X[OUT ? NT : 1];
       if constexpr (OUT) {
-        times_state(fq[p], p, X);
+        times_state(fq[p], ph, X);
 #pragma unroll
         for (int kk = 0; kk < KT; ++kk) fq[p][kk] = frag(rp, L::qg_frag(m, kk));
         if (nc > 0) store_o(nc - 1);
@@ -432,7 +440,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
 #pragma unroll
         for (int bb = 0; bb < 2; ++bb) {
           f32x4 WS[NT];
-          times_state(fw[p][bb], p, WS);
+          times_state(fw[p][bb], ph, WS);
 #pragma unroll
           for (int kk = 0; kk < KT; ++kk) fw[p][bb][kk] = frag(rp, L::w_frag(2 * u + bb, kk));
 #pragma unroll
@@ -452,7 +460,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
           if (lq == 0) sNinv[col][u] = inv;
         }
       }
-      if constexpr (ZU) put_z(p ^ 1);          // Z of chunk nc + 1
+      if constexpr (ZU) put_z(ph ^ 1);         // Z of chunk nc + 1
       __syncthreads();
 
       // phase 2
@@ -475,7 +483,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
           gam[p][t] = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(rp + L::GL_OFF) +
                                                         32 * wave + 16 * t + 4 * lq);
         }
-        put_state(p ^ 1);
+        put_state(ph ^ 1);
       }
       if constexpr (OUT) {
         f32x4 Y[NT];
@@ -486,12 +494,13 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
         for (int nn = 0; nn < NT; ++nn) Opend[nn] = X[nn] * sc[p][SC_QG] + Y[nn] * sc[p][SC_AQK];
       }
       if constexpr (ZU) {
-        form_u(p ^ 1, p ^ 1);                  // U of chunk nc + 1
-        const unsigned short* r3 = recp(nc + 3);
+        constexpr int pn = (ph ^ 1) % NB;     // fragments of chunk nc + 1
+        form_u(pn, ph ^ 1);                    // U of chunk nc + 1
+        const unsigned short* r3 = recp(nc + 1 + NB);
 #pragma unroll
         for (int bb = 0; bb < 2; ++bb)
 #pragma unroll
-          for (int kk = 0; kk < 2; ++kk) fi[p ^ 1][bb][kk] = frag(r3, L::ai_frag(2 * u + bb, kk));
+          for (int kk = 0; kk < 2; ++kk) fi[pn][bb][kk] = frag(r3, L::ai_frag(2 * u + bb, kk));
         fetch_z(nc + 2);
       }
 #pragma unroll
