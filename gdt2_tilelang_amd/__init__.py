@@ -21,7 +21,7 @@ not part of this package; the backward is not provided.
 
 from .attention import GDN2Cache, GatedDeltaNet2, gdn2_attention, resolve_backend
 from .config import DEFAULT_KERNEL_CONFIG, GDN2Config, GatedDeltaNet2Config
-from .forward import chunk_gdn2_bwd, chunk_gdn2_fwd
+from .forward import chunk_gdn2_bwd, chunk_gdn2_fwd, chunk_gdn2_varlen_fwd
 from .inference import gdn2_decode, gdn2_decode_step, gdn2_prefill
 
 __all__ = [
@@ -35,6 +35,7 @@ __all__ = [
     "GDN2Config",
     "DEFAULT_KERNEL_CONFIG",
     "chunk_gdn2_fwd",
+    "chunk_gdn2_varlen_fwd",
     "chunk_gdn2_bwd",
     "resolve_backend",
 ]

@@ -36,7 +36,7 @@ from torch import nn
 
 from . import _hip
 from .config import DEFAULT_KERNEL_CONFIG, GDN2Config, GatedDeltaNet2Config
-from .forward import chunk_gdn2_fwd
+from .forward import chunk_gdn2_fwd, chunk_gdn2_varlen_fwd
 from .inference import gdn2_decode, gdn2_prefill
 
 __all__ = ["gdn2_attention", "GatedDeltaNet2", "GDN2Cache", "resolve_backend"]
@@ -84,7 +84,11 @@ def gdn2_attention(q, k, v, g, b, w, scale=None, initial_state=None, output_fina
         initial_state: ``[B, H, DK, DV]`` or ``None``; never modified.
         output_final_state: also return the state after the last token.
         config: execution configuration.
-        cu_seqlens: packed-sequence offsets; not implemented, raises.
+        cu_seqlens: ``[N + 1]`` int offsets of N sequences packed in one batch
+            row (B = 1); each runs its own recurrence, ``initial_state`` and
+            the final state are then ``[N, H, DK, DV]``. The reference rejects
+            packed batches (``gdn2/attention.py:142-145``); this backend runs
+            them in one pass (forward only).
 
     Returns:
         ``(o [B, S, H, DV], final_state or None)``.
@@ -93,13 +97,15 @@ def gdn2_attention(q, k, v, g, b, w, scale=None, initial_state=None, output_fina
     needs_grad = torch.is_grad_enabled() and any(
         t is not None and t.requires_grad for t in (q, k, v, g, b, w, initial_state))
     backend = resolve_backend(config.backend, q.device.type == "cuda", needs_grad)
-    if cu_seqlens is not None:
-        raise NotImplementedError(
-            "packed variable-length batches are not implemented yet; pad the batch instead")
     if backend == "torch":
         raise NotImplementedError(
             "the 'torch' backend is the reference package's CPU path (gdn2.reference); "
             "this package provides the 'hip' backend only")
+    if cu_seqlens is not None:
+        if needs_grad:
+            raise NotImplementedError("packed sequences (cu_seqlens) are forward-only on the hip backend")
+        return chunk_gdn2_varlen_fwd(q, k, v, g, b, w, scale, cu_seqlens, initial_state, output_final_state,
+                                     config)
     if needs_grad:
         return _GDN2Function.apply(q, k, v, g, b, w, scale, initial_state, output_final_state, config)
     return chunk_gdn2_fwd(q, k, v, g, b, w, scale, initial_state, output_final_state, config)
@@ -422,6 +428,9 @@ class GatedDeltaNet2(nn.Module):
     def forward(self, hidden_states, cache=None, use_cache=False, cu_seqlens=None):
         """Full-sequence mixer (training form). Returns ``(output, cache or None)``."""
         B, S, _ = hidden_states.shape
+        if cu_seqlens is not None and self.q_conv is not None:
+            raise NotImplementedError("packed sequences (cu_seqlens) through the layer's short convolution "
+                                      "are not supported; pass a padded batch")
         if hidden_states.is_cuda:
             (q, k, v, g, b, w), proj, conv_state = self._project_gpu(hidden_states, None, conv_tail=use_cache)
             o, final_state = gdn2_attention(

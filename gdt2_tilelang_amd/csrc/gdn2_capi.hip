@@ -10,15 +10,15 @@ hipError_t launch_decode(const void*, const void*, const void*, const float*, co
                          const void*, float*, void*, int, int, int, int, int, long, long, int,
                          float, int, int, hipStream_t);
 hipError_t launch_chunk_local(const void*, const void*, const void*, const float*, int, int, int,
-                              int, long, long, int, long, float, unsigned short*, hipStream_t);
+                              int, long, long, int, long, float, unsigned short*, Varlen, hipStream_t);
 hipError_t launch_scan(const void*, const void*, int, const unsigned short*, const float*, float*,
-                       void*, int, int, int, int, int, int, long, long, int, long, hipStream_t);
+                       void*, int, int, int, int, int, int, long, long, int, long, Varlen, hipStream_t);
 hipError_t launch_gemv(const void*, const void*, void*, int, int, int, int, long, long, hipStream_t);
 }  // namespace gdn2
 
 namespace {
 
-constexpr int kAbiVersion = 2;   // 2: grouped key heads (HK)
+constexpr int kAbiVersion = 3;   // 2: grouped key heads (HK); 3: packed sequences
 
 bool dtype_ok(int dt) { return dt == GDN2_DTYPE_F32 || dt == GDN2_DTYPE_BF16 || dt == GDN2_DTYPE_F16; }
 
@@ -38,6 +38,10 @@ int check_prefill(int B, int H, int DK, long s_alloc, long t0, long n_tokens) {
   if (static_cast<long>(B) * H * ((n_tokens + gdn2::kBS - 1) / gdn2::kBS) > 0x7fffffffL) return GDN2_ERR_SHAPE;
   return 0;
 }
+
+// record slots per key head of a packed batch: sequence s's chunk c sits at
+// slot s + floor(cu[s] / 64) + c, which stays below ceil(T / 64) + nseq
+long varlen_slots(int nseq, long T) { return (T + gdn2::kBS - 1) / gdn2::kBS + nseq; }
 
 }  // namespace
 
@@ -84,7 +88,7 @@ int gdn2_hip_chunk_local(const void* q, const void* k, const void* b, const floa
   return status(gdn2::launch_chunk_local(q, k, b, g, in_dtype, B, HK, DK, s_alloc, t0,
                                          static_cast<int>((n_tokens + gdn2::kBS - 1) / gdn2::kBS),
                                          n_tokens, scale,
-                                         static_cast<unsigned short*>(workspace),
+                                         static_cast<unsigned short*>(workspace), gdn2::Varlen{nullptr, 0},
                                          static_cast<hipStream_t>(stream)));
 }
 
@@ -101,7 +105,7 @@ int gdn2_hip_prefill_scan(const void* v, const void* w, int in_dtype, const void
   return status(gdn2::launch_scan(v, w, in_dtype, static_cast<const unsigned short*>(workspace),
                                   state_in, state_out, o, out_dtype, B, H, HK, DK, DV, s_alloc, t0,
                                   static_cast<int>((n_tokens + gdn2::kBS - 1) / gdn2::kBS), n_tokens,
-                                  static_cast<hipStream_t>(stream)));
+                                  gdn2::Varlen{nullptr, 0}, static_cast<hipStream_t>(stream)));
 }
 
 int gdn2_hip_prefill_chunks(const void* q, const void* k, const void* v, const float* g,
@@ -120,6 +124,35 @@ int gdn2_hip_prefill_chunks(const void* q, const void* k, const void* v, const f
   if (s) return s;
   return gdn2_hip_prefill_scan(v, w, in_dtype, workspace, state_in, state_out, o, out_dtype, B, H,
                                HK, DK, DV, s_alloc, t0, n_tokens, stream);
+}
+
+size_t gdn2_hip_prefill_varlen_workspace_bytes(int nseq, int HK, int DK, long T) {
+  if (nseq < 1 || T < 0) return 0;
+  return gdn2_hip_prefill_workspace_bytes(1, HK, DK, varlen_slots(nseq, T) * gdn2::kBS);
+}
+
+int gdn2_hip_prefill_varlen(const void* q, const void* k, const void* v, const float* g,
+                            const void* b, const void* w, int in_dtype, const int* cu_seqlens, int nseq,
+                            const float* state_in, float* state_out, void* o, int out_dtype,
+                            void* workspace, int H, int HK, int DK, int DV, long T, float scale,
+                            void* stream) {
+  if (!q || !k || !v || !g || !b || !w || !cu_seqlens) return GDN2_ERR_ARG;
+  if (!workspace || !state_out || !o) return GDN2_ERR_ARG;
+  if (!dtype_ok(in_dtype) || !dtype_ok(out_dtype)) return GDN2_ERR_ARG;
+  if (nseq < 1 || T < 0 || H < 1 || HK < 1 || H % HK) return GDN2_ERR_ARG;
+  if (DK != 64 && DK != 128) return GDN2_ERR_SHAPE;
+  if (DV < 16 || DV % 16 || DV > 4096) return GDN2_ERR_SHAPE;
+  const long slots = varlen_slots(nseq, T);
+  if (static_cast<long>(HK) * slots > 0x7fffffffL || static_cast<long>(nseq) * H * (DV / 16) > 0x7fffffffL)
+    return GDN2_ERR_SHAPE;
+  const gdn2::Varlen vl{cu_seqlens, nseq};
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  unsigned short* ws = static_cast<unsigned short*>(workspace);
+  hipError_t e = gdn2::launch_chunk_local(q, k, b, g, in_dtype, 1, HK, DK, T, 0, static_cast<int>(slots),
+                                          T, scale, ws, vl, st);
+  if (e != hipSuccess) return status(e);
+  return status(gdn2::launch_scan(v, w, in_dtype, ws, state_in, state_out, o, out_dtype, nseq, H, HK, DK,
+                                  DV, T, 0, static_cast<int>(slots), T, vl, st));
 }
 
 int gdn2_hip_layer_prologue(const void* xq, const void* xk, const void* xv, const void* xb,

@@ -76,7 +76,7 @@ template <int DK, int IN_DT>
 __global__ __launch_bounds__(256) void chunk_local_kernel(
     const void* __restrict__ qp, const void* __restrict__ kp, const void* __restrict__ bp,
     const float* __restrict__ g, int H, long s_alloc, long t0, int NC, long n_tok, float scale,
-    unsigned short* __restrict__ ws) {
+    unsigned short* __restrict__ ws, Varlen vl) {
   using L = ChunkLayout<DK>;
   using M = ChunkSmem<DK>;
   constexpr int KT = DK / 32;
@@ -107,11 +107,13 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
   const int n = ch % NC;
   const int bi = bh / H;
   const int h = bh % H;
-  const long tok0 = t0 + static_cast<long>(n) * kBS;
+  long tok0 = t0 + static_cast<long>(n) * kBS;
   unsigned short* rec = ws + static_cast<size_t>(ch) * L::STRIDE;
   // rows past the call's last token (a ragged last chunk) read as zeros, which
   // the chunkwise form treats as inert; their loads re-read the last valid row
-  const int nvalid = static_cast<int>(min(static_cast<long>(kBS), n_tok - static_cast<long>(n) * kBS));
+  int nvalid = static_cast<int>(min(static_cast<long>(kBS), n_tok - static_cast<long>(n) * kBS));
+  // a packed batch (B = 1, s_alloc = T): slot n of the key head -> (sequence, chunk)
+  if (vl.cu && !varlen_chunk(vl, s_alloc, n, tok0, nvalid)) return;
   auto row_base = [&](int r) -> size_t {
     return ((static_cast<size_t>(bi) * s_alloc + tok0 + min(r, nvalid - 1)) * H + h) * DK;
   };
@@ -422,7 +424,7 @@ __global__ __launch_bounds__(256) void chunk_local_kernel(
 template <int DK, int IN_DT>
 static hipError_t launch_chunk_local_t(const void* q, const void* k, const void* b, const float* g,
                                        int B, int H, long s_alloc, long t0, int NC, long n_tok,
-                                       float scale, unsigned short* ws, hipStream_t stream) {
+                                       float scale, unsigned short* ws, Varlen vl, hipStream_t stream) {
   constexpr size_t smem = ChunkSmem<DK>::BYTES;
   static bool configured = false;   // attribute set once per process (same value always)
   if (!configured) {
@@ -434,22 +436,22 @@ static hipError_t launch_chunk_local_t(const void* q, const void* k, const void*
   }
   const unsigned grid = static_cast<unsigned>(B) * H * NC;
   hipLaunchKernelGGL((chunk_local_kernel<DK, IN_DT>), dim3(grid), dim3(256), smem, stream, q, k,
-                     b, g, H, s_alloc, t0, NC, n_tok, scale, ws);
+                     b, g, H, s_alloc, t0, NC, n_tok, scale, ws, vl);
   return hipGetLastError();
 }
 
 hipError_t launch_chunk_local2(const void* q, const void* k, const void* b, const float* g,
                                int in_dt, int B, int H, long s_alloc, long t0, int NC, long n_tok,
-                               float scale, unsigned short* ws, hipStream_t stream);
+                               float scale, unsigned short* ws, Varlen vl, hipStream_t stream);
 
 hipError_t launch_chunk_local(const void* q, const void* k, const void* b, const float* g,
                               int in_dt, int B, int H, int DK, long s_alloc, long t0, int NC,
-                              long n_tok, float scale, unsigned short* ws, hipStream_t stream) {
+                              long n_tok, float scale, unsigned short* ws, Varlen vl, hipStream_t stream) {
   // DK = 128 runs the channel-sliced kernel (gdn2_chunk_local2.hip); DK = 64 this one.
-  if (DK == 128) return launch_chunk_local2(q, k, b, g, in_dt, B, H, s_alloc, t0, NC, n_tok, scale, ws, stream);
+  if (DK == 128) return launch_chunk_local2(q, k, b, g, in_dt, B, H, s_alloc, t0, NC, n_tok, scale, ws, vl, stream);
 #define GDN2_CL_CASE(DKV, DTV)                                                             \
   if (DK == DKV && in_dt == DTV)                                                           \
-    return launch_chunk_local_t<DKV, DTV>(q, k, b, g, B, H, s_alloc, t0, NC, n_tok, scale, ws, stream);
+    return launch_chunk_local_t<DKV, DTV>(q, k, b, g, B, H, s_alloc, t0, NC, n_tok, scale, ws, vl, stream);
   GDN2_CL_CASE(64, DT_BF16) GDN2_CL_CASE(64, DT_F16) GDN2_CL_CASE(64, DT_F32)
 #undef GDN2_CL_CASE
   return hipErrorInvalidValue;

@@ -147,7 +147,7 @@ template <int IN_DT>
 __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
     const void* __restrict__ qp, const void* __restrict__ kp, const void* __restrict__ bp,
     const float* __restrict__ g, int H, long s_alloc, long t0, int NC, long n_tok, float scale,
-    unsigned short* __restrict__ ws) {
+    unsigned short* __restrict__ ws, Varlen vl) {
   using namespace cl2;
   using L = ChunkLayout<DK>;
   extern __shared__ __align__(16) unsigned char smem[];
@@ -169,12 +169,14 @@ __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
   const int n = ch % NC;
   const int bi = bh / H;
   const int h = bh % H;
-  const long tok0 = t0 + static_cast<long>(n) * kBS;
+  long tok0 = t0 + static_cast<long>(n) * kBS;
   unsigned short* rec = ws + static_cast<size_t>(ch) * L::STRIDE;
   const int c0 = CPW * wave + 8 * lq;        // first of this lane's 8 channels
   // rows past the call's last token (a ragged last chunk) read as zeros, which
   // the chunkwise form treats as inert; their loads re-read the last valid row
-  const int nvalid = static_cast<int>(min(static_cast<long>(kBS), n_tok - static_cast<long>(n) * kBS));
+  int nvalid = static_cast<int>(min(static_cast<long>(kBS), n_tok - static_cast<long>(n) * kBS));
+  // a packed batch (B = 1, s_alloc = T): slot n of the key head -> (sequence, chunk)
+  if (vl.cu && !varlen_chunk(vl, s_alloc, n, tok0, nvalid)) return;
   auto gidx = [&](int r) -> size_t {
     return ((static_cast<size_t>(bi) * s_alloc + tok0 + min(r, nvalid - 1)) * H + h) * DK + c0;
   };
@@ -617,7 +619,7 @@ __global__ __launch_bounds__(256, 2) void chunk_local2_kernel(
 template <int IN_DT>
 static hipError_t launch_chunk_local2_t(const void* q, const void* k, const void* b, const float* g,
                                         int B, int H, long s_alloc, long t0, int NC, long n_tok,
-                                        float scale, unsigned short* ws, hipStream_t stream) {
+                                        float scale, unsigned short* ws, Varlen vl, hipStream_t stream) {
   constexpr int smem = cl2::LDS_BYTES;
   static bool configured = false;   // attribute set once per process (same value always)
   if (!configured) {
@@ -628,19 +630,19 @@ static hipError_t launch_chunk_local2_t(const void* q, const void* k, const void
   }
   const unsigned grid = static_cast<unsigned>(B) * H * NC;
   hipLaunchKernelGGL((chunk_local2_kernel<IN_DT>), dim3(grid), dim3(256), smem, stream, q, k, b, g,
-                     H, s_alloc, t0, NC, n_tok, scale, ws);
+                     H, s_alloc, t0, NC, n_tok, scale, ws, vl);
   return hipGetLastError();
 }
 
 hipError_t launch_chunk_local2(const void* q, const void* k, const void* b, const float* g,
                                int in_dt, int B, int H, long s_alloc, long t0, int NC, long n_tok,
-                               float scale, unsigned short* ws, hipStream_t stream) {
+                               float scale, unsigned short* ws, Varlen vl, hipStream_t stream) {
   if (in_dt == DT_BF16)
-    return launch_chunk_local2_t<DT_BF16>(q, k, b, g, B, H, s_alloc, t0, NC, n_tok, scale, ws, stream);
+    return launch_chunk_local2_t<DT_BF16>(q, k, b, g, B, H, s_alloc, t0, NC, n_tok, scale, ws, vl, stream);
   if (in_dt == DT_F16)
-    return launch_chunk_local2_t<DT_F16>(q, k, b, g, B, H, s_alloc, t0, NC, n_tok, scale, ws, stream);
+    return launch_chunk_local2_t<DT_F16>(q, k, b, g, B, H, s_alloc, t0, NC, n_tok, scale, ws, vl, stream);
   if (in_dt == DT_F32)
-    return launch_chunk_local2_t<DT_F32>(q, k, b, g, B, H, s_alloc, t0, NC, n_tok, scale, ws, stream);
+    return launch_chunk_local2_t<DT_F32>(q, k, b, g, B, H, s_alloc, t0, NC, n_tok, scale, ws, vl, stream);
   return hipErrorInvalidValue;
 }
 

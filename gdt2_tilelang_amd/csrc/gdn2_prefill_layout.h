@@ -54,4 +54,51 @@ struct ChunkLayout {
 static_assert((ChunkLayout<128>::STRIDE * 2) % 256 == 0, "record must keep 256-byte alignment");
 static_assert((ChunkLayout<64>::STRIDE * 2) % 256 == 0, "record must keep 256-byte alignment");
 
+// Packed variable-length batches (cu_seqlens). Sequence s holds tokens
+// [cu[s], cu[s+1]) of one [T, H, D] allocation and its chunk c (64 tokens, the
+// last one possibly ragged) has the record slot  s + floor(cu[s] / 64) + c.
+// Slots are distinct (sequence s ends at or before slot s + 1 + floor(cu[s+1] / 64),
+// where sequence s + 1 starts) and number at most ceil(T / 64) + nseq per key
+// head; a slot between two sequences holds no chunk. Offsets are clamped into
+// [0, T], so a malformed array cannot move an access outside the buffers.
+struct Varlen {
+  const int* cu;   // nseq + 1 offsets in device memory; nullptr: a dense batch
+  int nseq;
+};
+
+__device__ __forceinline__ long varlen_off(const int* cu, int s, long T) {
+  return min(max(static_cast<long>(cu[s]), 0L), T);
+}
+
+// The sequence whose slot range holds `slot` (the last s with
+// s + floor(cu[s] / 64) <= slot), by a 64-way search across the wave: every
+// round each lane tests one candidate, so ceil(log64(nseq)) dependent loads.
+__device__ __forceinline__ int varlen_seq(const int* cu, int nseq, long T, long slot) {
+  const int lane = threadIdx.x & 63;
+  int lo = 0, len = nseq;
+  while (len > 1) {
+    const int step = (len + 63) >> 6;
+    const int s = lo + lane * step;
+    const bool ok = s < lo + len && s + varlen_off(cu, s, T) / kBS <= slot;
+    const int cnt = __popcll(__ballot(ok));   // the passing lanes form a prefix; lane 0 passes
+    const int nlo = lo + (cnt - 1) * step;
+    len = min(step, lo + len - nlo);
+    lo = nlo;
+  }
+  return lo;
+}
+
+// First token and valid rows of chunk slot `slot` of a packed batch of T
+// tokens; false for a slot that holds no chunk.
+__device__ __forceinline__ bool varlen_chunk(const Varlen& vl, long T, long slot, long& tok0, int& nvalid) {
+  const int s = varlen_seq(vl.cu, vl.nseq, T, slot);
+  const long a = varlen_off(vl.cu, s, T);
+  const long e = max(varlen_off(vl.cu, s + 1, T), a);
+  const long c = slot - s - a / kBS;
+  if (c < 0 || c * kBS >= e - a) return false;
+  tok0 = a + c * kBS;
+  nvalid = static_cast<int>(min(static_cast<long>(kBS), e - tok0));
+  return true;
+}
+
 }  // namespace gdn2

@@ -134,7 +134,7 @@ template <int DK, int NT, int IN_DT, int OUT_DT>
 __global__ __launch_bounds__(kScanThreads) void scan_kernel(
     const void* __restrict__ v, const void* __restrict__ w, const unsigned short* __restrict__ ws,
     const float* __restrict__ s_in, float* __restrict__ s_out, void* __restrict__ o,
-    int BH, int H, int HK, int DV, long s_alloc, long t0, int NC, long n_tok) {
+    int BH, int H, int HK, int DV, long s_alloc, long t0, int NC, long n_tok, Varlen vl) {
   using L = ChunkLayout<DK>;
   constexpr int KT = DK / 32;          // 32-row k blocks of S = state-owning waves
   constexpr int DVT = 16 * NT;
@@ -182,7 +182,28 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
   const int tile = r % ntile;
   const int bh = bi * H + h;
   const int d0 = tile * DVT;
-  const unsigned short* rec0 = ws + static_cast<size_t>(bhk) * NC * L::STRIDE;   // key head's records
+  // A packed batch (vl.cu set, one [T, H, D] allocation, NC = record slots per
+  // key head): batch row bi is sequence bi, tokens [cu[bi], cu[bi+1]), whose
+  // chunks sit at slots bi + floor(cu[bi] / 64) + c of its key head.
+  size_t slot0 = static_cast<size_t>(bhk) * NC;
+  int bt = bi;                           // batch row of the token tensors
+  if (vl.cu) {
+    const long a = varlen_off(vl.cu, bi, s_alloc);
+    const long e = max(varlen_off(vl.cu, bi + 1, s_alloc), a);
+    slot0 = static_cast<size_t>(bhk % HK) * NC + bi + a / kBS;
+    t0 = a;
+    n_tok = e - a;
+    NC = static_cast<int>((n_tok + kBS - 1) / kBS);
+    bt = 0;
+    if (n_tok == 0) {                    // an empty sequence passes its state through
+      for (int i = threadIdx.x; i < DK * DVT; i += kScanThreads) {
+        const size_t si = (static_cast<size_t>(bh) * DK + i / DVT) * DV + d0 + i % DVT;
+        s_out[si] = s_in ? s_in[si] : 0.f;
+      }
+      return;
+    }
+  }
+  const unsigned short* rec0 = ws + slot0 * L::STRIDE;   // key head's records
   const int last = NC - 1;
   // tokens of the last chunk (64 unless the call ends in a ragged chunk, whose
   // missing rows read as zeros and whose o rows past the end are not stored)
@@ -253,7 +274,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
         const int cz = min(nc, last);
         const bool ok = cz < last || t < nlast;
         const int tl = ok ? t : nlast - 1;     // the load stays inside the call's tokens
-        const size_t idx = ((static_cast<size_t>(bi) * s_alloc + t0 + static_cast<long>(cz) * kBS + tl) * H + h) * DV + d0 + 4 * cq;
+        const size_t idx = ((static_cast<size_t>(bt) * s_alloc + t0 + static_cast<long>(cz) * kBS + tl) * H + h) * DV + d0 + 4 * cq;
         zv[it].load(v, idx);
         zw[it].load(w, idx);
         if (!ok) {
@@ -382,7 +403,7 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
         if (lane < 16 * LPR && (nc < last || 16 * m + rr < nlast)) {
           const int c = (lane % LPR) * (16 / OSZ);
           const uint4 x = *reinterpret_cast<const uint4*>(so + (rr * 16 + c) * OSZ);
-          const size_t oi = ((static_cast<size_t>(bi) * s_alloc + tok0 + 16 * m + rr) * H + h) * DV + d0 + 16 * nn + c;
+          const size_t oi = ((static_cast<size_t>(bt) * s_alloc + tok0 + 16 * m + rr) * H + h) * DV + d0 + 16 * nn + c;
           *reinterpret_cast<uint4*>(static_cast<unsigned char*>(o) + oi * OSZ) = x;
         }
         __builtin_amdgcn_wave_barrier();
@@ -546,11 +567,12 @@ __global__ __launch_bounds__(kScanThreads) void scan_kernel(
 template <int DK, int NT, int IN_DT, int OUT_DT>
 static hipError_t launch_scan_t(const void* v, const void* w, const unsigned short* ws,
                                 const float* s_in, float* s_out, void* o, int B, int H, int HK,
-                                int DV, long s_alloc, long t0, int NC, long n_tok, hipStream_t stream) {
+                                int DV, long s_alloc, long t0, int NC, long n_tok, Varlen vl,
+                                hipStream_t stream) {
   const int BH = B * H;
   const unsigned grid = static_cast<unsigned>(BH) * (DV / (16 * NT));
   hipLaunchKernelGGL((scan_kernel<DK, NT, IN_DT, OUT_DT>), dim3(grid), dim3(kScanThreads), 0, stream, v, w,
-                     ws, s_in, s_out, o, BH, H, HK, DV, s_alloc, t0, NC, n_tok);
+                     ws, s_in, s_out, o, BH, H, HK, DV, s_alloc, t0, NC, n_tok, vl);
   return hipGetLastError();
 }
 
@@ -563,12 +585,12 @@ int scan_nt_for(int B, int H, int DV) {
 
 hipError_t launch_scan(const void* v, const void* w, int in_dt, const unsigned short* ws,
                        const float* s_in, float* s_out, void* o, int out_dt, int B, int H, int HK, int DK,
-                       int DV, long s_alloc, long t0, int NC, long n_tok, hipStream_t stream) {
+                       int DV, long s_alloc, long t0, int NC, long n_tok, Varlen vl, hipStream_t stream) {
   const int nt = scan_nt_for(B, H, DV);
 #define GDN2_SCAN_CASE(DKV, NTV, DTV, ODV)                                                     \
   if (DK == DKV && nt == NTV && in_dt == DTV && out_dt == ODV)                                 \
     return launch_scan_t<DKV, NTV, DTV, ODV>(v, w, ws, s_in, s_out, o, B, H, HK, DV, s_alloc, t0, \
-                                             NC, n_tok, stream);
+                                             NC, n_tok, vl, stream);
 #define GDN2_SCAN_OUT(DKV, NTV, DTV) \
   GDN2_SCAN_CASE(DKV, NTV, DTV, DT_BF16) GDN2_SCAN_CASE(DKV, NTV, DTV, DT_F16) GDN2_SCAN_CASE(DKV, NTV, DTV, DT_F32)
 #define GDN2_SCAN_DT(DKV, NTV) \

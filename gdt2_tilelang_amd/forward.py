@@ -15,10 +15,11 @@ from __future__ import annotations
 
 import torch
 
+from . import _hip
 from .config import DEFAULT_KERNEL_CONFIG, GDN2Config
 from .inference import _check_shapes, _prefill_chunks, _require_device, _token_layout, check_prefill_config
 
-__all__ = ["chunk_gdn2_fwd", "chunk_gdn2_bwd"]
+__all__ = ["chunk_gdn2_fwd", "chunk_gdn2_varlen_fwd", "chunk_gdn2_bwd"]
 
 
 @torch.no_grad()
@@ -50,6 +51,70 @@ def chunk_gdn2_fwd(q, k, v, g, b, w, scale, initial_state=None, output_final_sta
         final.copy_(initial_state)
     else:
         final.zero_()
+    return o, (final if output_final_state else None)
+
+
+def check_cu_seqlens(cu_seqlens, T: int) -> torch.Tensor:
+    """Validate packed-sequence offsets on the host; returns them as int32 on
+    the host. ``cu_seqlens`` is a 1-D integer tensor ``[N + 1]`` with
+    ``cu[0] == 0``, ``cu[N] == T`` and non-decreasing entries (empty sequences
+    allowed), the convention of packed-batch kernels (FLA ``cu_seqlens``)."""
+    if not isinstance(cu_seqlens, torch.Tensor) or cu_seqlens.dim() != 1 or cu_seqlens.numel() < 2:
+        raise ValueError("cu_seqlens must be a 1-D tensor of N + 1 offsets (N >= 1)")
+    if cu_seqlens.dtype not in (torch.int32, torch.int64):
+        raise TypeError(f"cu_seqlens must be int32 or int64; got {cu_seqlens.dtype}")
+    cu = cu_seqlens.detach().to("cpu", torch.int64)
+    if int(cu[0]) != 0 or int(cu[-1]) != T:
+        raise ValueError(f"cu_seqlens must start at 0 and end at the packed length {T}; "
+                         f"got {int(cu[0])} .. {int(cu[-1])}")
+    if bool((cu[1:] < cu[:-1]).any()):
+        raise ValueError("cu_seqlens must be non-decreasing")
+    return cu.to(torch.int32)
+
+
+@torch.no_grad()
+def chunk_gdn2_varlen_fwd(q, k, v, g, b, w, scale, cu_seqlens, initial_state=None, output_final_state=False,
+                          config: GDN2Config = DEFAULT_KERNEL_CONFIG):
+    """Packed variable-length forward: N sequences concatenated along one
+    ``[1, T, H, D]`` batch row, sequence i holding tokens
+    ``cu_seqlens[i] : cu_seqlens[i + 1]``, each an independent recurrence.
+
+    Args:
+        q, k, b, g: ``[1, T, HK, DK]``; v, w: ``[1, T, H, DV]``.
+        cu_seqlens: ``[N + 1]`` int32 / int64 offsets (see ``check_cu_seqlens``).
+        initial_state: ``[N, H, DK, DV]`` or ``None`` (zeros); never modified.
+
+    Returns:
+        ``(o [1, T, H, DV], final_state [N, H, DK, DV] fp32 or None)``. Both
+        kernels run once for the whole batch; sequence i's result equals a
+        separate call on its tokens alone.
+    """
+    dev = _require_device(q, k, v, g, b, w)
+    _check_shapes(q, k, v, g, b, w)
+    check_prefill_config(config)
+    B, T, HK, DK = q.shape
+    H, DV = v.shape[2], v.shape[3]
+    if B != 1:
+        raise ValueError(f"packed sequences (cu_seqlens) need batch size 1; got {B}")
+    if DK not in (64, 128) or DV % 32:
+        raise ValueError(f"hip prefill supports DK in (64, 128) and DV % 32 == 0; got DK={DK}, DV={DV}")
+    cu = check_cu_seqlens(cu_seqlens, T).to(dev, non_blocking=False)
+    N = cu.numel() - 1
+    (q, k, v, g, b, w), _ = _token_layout((q, k, v, g.float(), b, w))
+    if initial_state is not None:
+        _require_device(q, initial_state)
+        if tuple(initial_state.shape) != (N, H, DK, DV):
+            raise ValueError(f"initial_state has shape {tuple(initial_state.shape)}, expected {(N, H, DK, DV)}")
+        initial_state = initial_state.to(torch.float32).contiguous()
+    final = torch.empty(N, H, DK, DV, dtype=torch.float32, device=dev)
+    o = torch.empty(1, T, H, DV, dtype=config.output_dtype or q.dtype, device=dev)
+    lib = _hip.lib()
+    ws = torch.empty(lib.gdn2_hip_prefill_varlen_workspace_bytes(N, HK, DK, T), dtype=torch.uint8, device=dev)
+    _hip.check(lib.gdn2_hip_prefill_varlen(
+        _hip.ptr(q), _hip.ptr(k), _hip.ptr(v), _hip.ptr(g), _hip.ptr(b), _hip.ptr(w),
+        _hip.dtype_code(q.dtype), _hip.ptr(cu), N, _hip.ptr(initial_state), _hip.ptr(final), _hip.ptr(o),
+        _hip.dtype_code(o.dtype), _hip.ptr(ws), H, HK, DK, DV, T, float(scale),
+        _hip.stream_of(dev)), "gdn2_hip_prefill_varlen")
     return o, (final if output_final_state else None)
 
 

@@ -104,6 +104,30 @@ int gdn2_hip_prefill_chunks(const void* q, const void* k, const void* v, const f
                             float scale, void* stream);
 
 /*
+ * Both prefill stages over a packed variable-length batch: nseq sequences
+ * concatenated in one [T, H, D] allocation (q, k, b, g with HK heads; v, w, o
+ * with H), sequence i holding tokens [cu_seqlens[i], cu_seqlens[i+1]) and
+ * running its own recurrence from state_in[i] (state_in NULL: zeros) to
+ * state_out[i] (both fp32 [nseq, H, DK, DV]; they may be equal). cu_seqlens is
+ * int32 in device memory, nseq + 1 entries, 0 = cu[0] <= cu[1] <= ... <= cu[nseq]
+ * = T (empty sequences allowed: their state is copied through). The library
+ * cannot check the offsets without a host sync; it clamps them into [0, T],
+ * so malformed offsets give wrong results but no access outside the buffers.
+ * One chunk-local launch covers every sequence's chunks, one scan launch every
+ * (sequence, value head, tile). DK in {64, 128}; DV a multiple of 16.
+ * Workspace: gdn2_hip_prefill_varlen_workspace_bytes (ceil(T/64) + nseq
+ * record slots per key head).
+ * Replaces: gdn2_attention(..., cu_seqlens=...) (gdn2/attention.py:142-145),
+ * which the reference rejects with NotImplementedError.
+ */
+size_t gdn2_hip_prefill_varlen_workspace_bytes(int nseq, int HK, int DK, long T);
+int gdn2_hip_prefill_varlen(const void* q, const void* k, const void* v, const float* g,
+                            const void* b, const void* w, int in_dtype, const int* cu_seqlens, int nseq,
+                            const float* state_in, float* state_out, void* o, int out_dtype,
+                            void* workspace, int H, int HK, int DK, int DV, long T, float scale,
+                            void* stream);
+
+/*
  * GatedDeltaNet2 layer prologue (one launch per prefill segment or decode
  * block): for the B x S tokens of the raw projections xq, xk [.., HK*DK],
  * xv, xw [.., H*DV], xb, xf [.., HK*DK] (row strides ld_* in elements, all in

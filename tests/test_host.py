@@ -102,10 +102,48 @@ def test_cpu_tensors_fail_loudly():
         gdn2_decode(*ins, torch.zeros(1, 2, 64, 64))
 
 
-def test_varlen_is_rejected():
+def test_varlen_host_validation():
+    """Packed sequences: the torch backend and CPU tensors are refused as for a
+    dense batch; the offsets are checked on the host before any launch."""
+    from gdt2_tilelang_amd.forward import check_cu_seqlens
     ins = make_inputs(1, 128, 2, 16, 16)
-    with pytest.raises(NotImplementedError, match="variable-length"):
-        gdn2_attention(*ins, config=GDN2Config(backend="torch"), cu_seqlens=torch.tensor([0, 64, 128]))
+    cu = torch.tensor([0, 64, 128])
+    with pytest.raises(NotImplementedError, match="'hip' backend only"):
+        gdn2_attention(*ins, config=GDN2Config(backend="torch"), cu_seqlens=cu)
+    with pytest.raises(ValueError, match="requires a CUDA device"):
+        gdn2_attention(*ins, config=GDN2Config(backend="hip"), cu_seqlens=cu)
+    assert check_cu_seqlens(torch.tensor([0, 0, 5, 5, 9]), 9).tolist() == [0, 0, 5, 5, 9]
+    assert check_cu_seqlens(torch.tensor([0, 7], dtype=torch.int32), 7).dtype == torch.int32
+    with pytest.raises(ValueError, match="start at 0"):
+        check_cu_seqlens(torch.tensor([1, 9]), 9)
+    with pytest.raises(ValueError, match="end at the packed length"):
+        check_cu_seqlens(torch.tensor([0, 8]), 9)
+    with pytest.raises(ValueError, match="non-decreasing"):
+        check_cu_seqlens(torch.tensor([0, 6, 4, 9]), 9)
+    with pytest.raises(ValueError, match="1-D"):
+        check_cu_seqlens(torch.tensor([0]), 0)
+    with pytest.raises(TypeError, match="int32 or int64"):
+        check_cu_seqlens(torch.tensor([0.0, 9.0]), 9)
+
+
+def test_varlen_slot_map_is_injective():
+    """The record-slot map the packed kernels use (sequence s's chunk c at
+    s + floor(cu[s] / 64) + c) gives distinct slots below ceil(T / 64) + N,
+    checked by brute force over random offsets (empty and ragged sequences)."""
+    g = torch.Generator().manual_seed(7)
+    for _ in range(200):
+        N = int(torch.randint(1, 12, (1,), generator=g))
+        lens = torch.randint(0, 200, (N,), generator=g) * (torch.rand(N, generator=g) > 0.2)
+        cu = [0] + torch.cumsum(lens, 0).tolist()
+        T = cu[-1]
+        slots = [s + cu[s] // 64 + c for s in range(N) for c in range(-(-(cu[s + 1] - cu[s]) // 64))]
+        assert len(set(slots)) == len(slots)
+        assert all(0 <= x < -(-T // 64) + N for x in slots)
+        # slot -> sequence: the last s with s + cu[s] // 64 <= slot
+        for x in slots:
+            s = max(i for i in range(N) if i + cu[i] // 64 <= x)
+            c = x - s - cu[s] // 64
+            assert 0 <= c * 64 < cu[s + 1] - cu[s]
 
 
 def test_tiling_and_dtype_validation():

@@ -71,6 +71,13 @@ def test_grouped_heads_rejects_bad_ratio():
         GatedDeltaNet2(GatedDeltaNet2Config(hidden_size=64, num_heads=6, num_kv_heads=4))
 
 
+def test_packed_sequences_rejected_through_short_conv():
+    """The layer's causal conv would mix tokens across packed sequences."""
+    layer = small_layer()
+    with pytest.raises(NotImplementedError, match="cu_seqlens"):
+        layer(torch.randn(1, 8, 64), cu_seqlens=torch.tensor([0, 3, 8]))
+
+
 @pytest.mark.parametrize("draft", [1, 2, 5])
 def test_decode_matches_forward(oracle_op, draft):
     layer = small_layer()
