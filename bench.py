@@ -112,6 +112,57 @@ def bench_prefill(steps, warmup):
     return ms_step, cl, sc
 
 
+def bench_varlen(reps=20, nseq=16):
+    """Config 1's 8192 tokens packed as nseq sequences of seeded random lengths
+    (one gdn2_hip_prefill_varlen call: one chunk-local and one scan launch),
+    against the same sequences as separate prefill calls."""
+    from gdt2_tilelang_amd import _hip
+
+    lib = _hip.lib()
+    dev = torch.device("cuda")
+    stream = torch.cuda.current_stream()
+    sp = _hip.stream_of(dev)
+    T = B1 * S1
+    gen = torch.Generator().manual_seed(21)
+    cuts = sorted((torch.randperm(T - 1, generator=gen)[:nseq - 1] + 1).tolist())
+    cu = [0] + cuts + [T]
+    lens = [cu[i + 1] - cu[i] for i in range(nseq)]
+    q, k, v, g, b, w = cfg_inputs(1, T, H1, D1, D1, seed=13)
+    cu_dev = torch.tensor(cu, dtype=torch.int32, device=dev)
+    ws = torch.empty(lib.gdn2_hip_prefill_varlen_workspace_bytes(nseq, H1, D1, T), dtype=torch.uint8, device=dev)
+    ws1 = torch.empty(lib.gdn2_hip_prefill_workspace_bytes(1, H1, D1, max(lens)), dtype=torch.uint8, device=dev)
+    o = torch.empty(1, T, H1, D1, dtype=torch.bfloat16, device=dev)
+    st = torch.empty(nseq, H1, D1, D1, dtype=torch.float32, device=dev)
+    P = _hip.ptr
+    scale = D1 ** -0.5
+
+    def packed():
+        _hip.check(lib.gdn2_hip_prefill_varlen(P(q), P(k), P(v), P(g), P(b), P(w), 1, P(cu_dev), nseq, None,
+                                               P(st), P(o), 1, P(ws), H1, H1, D1, D1, T, scale, sp), "varlen")
+
+    def separate():
+        for i in range(nseq):
+            _hip.check(lib.gdn2_hip_prefill_chunks(
+                P(q), P(k), P(v), P(g), P(b), P(w), 1, None, P(st[i]), P(o), 1, P(ws1), 1, H1, H1, D1, D1,
+                T, cu[i], lens[i], scale, sp), "prefill_chunks")
+
+    res = {}
+    for name, fn in (("packed", packed), ("separate_calls", separate)):
+        for _ in range(3):
+            fn()
+        e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        e0.record(stream)
+        for _ in range(reps):
+            fn()
+        e1.record(stream)
+        torch.cuda.synchronize()
+        res[name] = e0.elapsed_time(e1) / reps * 1e3
+    return {"sequences": nseq, "tokens": T, "min_len": min(lens), "max_len": max(lens),
+            "heads": H1, "head_dim": D1,
+            "packed_us": round(res["packed"], 1), "packed_tokens_per_s": round(T / (res["packed"] * 1e-6), 1),
+            "separate_calls_us": round(res["separate_calls"], 1)}
+
+
 def bench_decode(B, n, calls, steps_per_buf_min, H=16, D=128):
     """Average µs per decode call with rotating states (> MALL) for config 2/3.
 
@@ -275,6 +326,7 @@ def main():
     ap.add_argument("--prefill-only", action="store_true", help="prefill steps only (for profilers)")
     ap.add_argument("--decode-only", action="store_true", help="decode configs only (for profilers)")
     ap.add_argument("--no-layer", action="store_true", help="skip the config-4 layer run")
+    ap.add_argument("--no-varlen", action="store_true", help="skip the packed-sequence prefill run")
     ap.add_argument("--layer-only", action="store_true", help="config-4 layer run only (for profilers)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="three plain 1 GiB device copies (scales rocprofv3 byte counters)")
@@ -349,6 +401,8 @@ def main():
             "config2_decode_step": bench_decode(64, 1, calls=64, steps_per_buf_min=1),
             "config3_decode_multi_n8": bench_decode(32, 8, calls=64, steps_per_buf_min=1),
         }
+    if not args.no_varlen:
+        out["varlen"] = bench_varlen()
     if not args.no_layer:
         out["layer"] = bench_layer()
     if not args.no_cpu:
