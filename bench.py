@@ -327,6 +327,7 @@ def main():
     ap.add_argument("--decode-only", action="store_true", help="decode configs only (for profilers)")
     ap.add_argument("--no-layer", action="store_true", help="skip the config-4 layer run")
     ap.add_argument("--no-varlen", action="store_true", help="skip the packed-sequence prefill run")
+    ap.add_argument("--varlen-only", action="store_true", help="packed-sequence prefill run only (for profilers)")
     ap.add_argument("--layer-only", action="store_true", help="config-4 layer run only (for profilers)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="three plain 1 GiB device copies (scales rocprofv3 byte counters)")
@@ -354,6 +355,9 @@ def main():
         return
     if args.layer_only:
         log(json.dumps(bench_layer()))
+        return
+    if args.varlen_only:
+        log(json.dumps(bench_varlen()))
         return
     ms_step, cl_ms, sc_ms = bench_prefill(args.steps, args.warmup)
     if args.prefill_only:
