@@ -51,7 +51,7 @@ __device__ __forceinline__ float group_sum(float x, int group) {
 }
 
 
-constexpr int TT = 4;            // tokens per prologue workgroup
+constexpr int TT = 4;            // tokens per prologue workgroup (8 measured slower: fewer waves per SIMD)
 constexpr int kProThreads = 128;
 
 // Eight consecutive elements of a row (16 bytes for 16-bit types, 32 for fp32).
@@ -216,24 +216,29 @@ __global__ __launch_bounds__(kProThreads) void prologue_kernel(ProArgs a) {
       for (int e = 0; e < 8; ++e) dtb[e] = a.dt_bias[c0 + e];
       al = -__expf(a.a_log[c0 / a.DK]);
     }
-    for (int t = 0; t < nt; ++t) {
+    // all TT rows are requested before any is used (rows past the segment
+    // re-read its last row and are not stored)
+    const void* src = a.x[3 + kind];
+    const long lds = a.ld[3 + kind];
+    float xv[TT][8];
+#pragma unroll
+    for (int t = 0; t < TT; ++t) ld8<DT>(src, (row0 + t0 + min(t, nt - 1)) * lds + c0, xv[t]);
+#pragma unroll
+    for (int t = 0; t < TT; ++t) {
+      if (t >= nt) break;
       const long tok = row0 + t0 + t;
-      float xv[8];
       if (kind == 0) {
-        ld8<DT>(a.x[3], tok * a.ld[3] + c0, xv);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xv[e] = sigmoid(xv[e]) * a.erase_scale;
-        st8<DT>(a.b, tok * dqk + c0, xv);
+        for (int e = 0; e < 8; ++e) xv[t][e] = sigmoid(xv[t][e]) * a.erase_scale;
+        st8<DT>(a.b, tok * dqk + c0, xv[t]);
       } else if (kind == 1) {
-        ld8<DT>(a.x[4], tok * a.ld[4] + c0, xv);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xv[e] = sigmoid(xv[e]);
-        st8<DT>(a.w, tok * dv + c0, xv);
+        for (int e = 0; e < 8; ++e) xv[t][e] = sigmoid(xv[t][e]);
+        st8<DT>(a.w, tok * dv + c0, xv[t]);
       } else {
-        ld8<DT>(a.x[5], tok * a.ld[5] + c0, xv);
 #pragma unroll
-        for (int e = 0; e < 8; ++e) xv[e] = al * softplus(xv[e] + dtb[e]);
-        st8<DT_F32>(a.g, tok * dqk + c0, xv);
+        for (int e = 0; e < 8; ++e) xv[t][e] = al * softplus(xv[t][e] + dtb[e]);
+        st8<DT_F32>(a.g, tok * dqk + c0, xv[t]);
       }
     }
   }
@@ -267,6 +272,43 @@ __global__ __launch_bounds__(kThreads) void epilogue_kernel(const void* __restri
   }
 }
 
+// gated RMSNorm, vector form (DV % 8 == 0, DV <= 512, 16-byte aligned rows):
+// G lanes per (token, value head) row, G the power of two >= DV / 8, each lane
+// holding 8 consecutive elements; o is read once and kept in registers between
+// the sum of squares and the store, and the gate is requested before the sum.
+template <int ODT, int GDT>
+__global__ __launch_bounds__(kThreads) void epilogue8_kernel(const void* __restrict__ o, const void* __restrict__ gate,
+                                                             long ld_gate, const float* __restrict__ weight, float eps,
+                                                             void* __restrict__ out, long ld_out, long rows, int H,
+                                                             int DV, int G) {
+  const int lane = threadIdx.x & 63;
+  const long row = (static_cast<long>(blockIdx.x) * (kThreads / 64) + (threadIdx.x >> 6)) * (64 / G) + lane / G;
+  const int c = (lane % G) * 8;
+  const bool act = row < rows && c < DV;
+  const long tok = row / H;
+  const int h = static_cast<int>(row % H);
+  float x[8], gt[8];
+  if (act) {
+    ld8<ODT>(o, row * DV + c, x);
+    ld8<GDT>(gate, tok * ld_gate + static_cast<long>(h) * DV + c, gt);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) x[e] = gt[e] = 0.f;
+  }
+  float ss = 0.f;
+#pragma unroll
+  for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
+  ss = group_sum(ss, G);                       // every lane takes part in the shuffles
+  if (!act) return;
+  const float r = rsqrtf(ss / DV + eps);
+  const float4 w0 = *reinterpret_cast<const float4*>(weight + c);
+  const float4 w1 = *reinterpret_cast<const float4*>(weight + c + 4);
+  const float w[8] = {w0.x, w0.y, w0.z, w0.w, w1.x, w1.y, w1.z, w1.w};
+#pragma unroll
+  for (int e = 0; e < 8; ++e) x[e] = x[e] * r * w[e] * silu(gt[e]);
+  st8<GDT>(out, tok * ld_out + static_cast<long>(h) * DV + c, x);
+}
+
 }  // namespace lay
 
 hipError_t launch_layer_prologue(const lay::ProArgs& a, int act_dt, hipStream_t stream) {
@@ -297,6 +339,26 @@ hipError_t launch_layer_epilogue(const void* o, int o_dt, const void* gate, long
                                  float eps, void* out, int out_dt, long ld_out, long rows, int H, int DV,
                                  hipStream_t stream) {
   if (rows == 0) return hipSuccess;
+  const auto al16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) == 0; };
+  if (DV % 8 == 0 && DV <= 512 && ld_gate % 8 == 0 && ld_out % 8 == 0 && al16(o) && al16(gate) && al16(out) &&
+      al16(weight)) {
+    int G = 1;
+    while (G < DV / 8) G <<= 1;
+    const long rows_per_block = (lay::kThreads / 64) * (64 / G);
+    const dim3 grid8(static_cast<unsigned>((rows + rows_per_block - 1) / rows_per_block));
+#define GDN2_EPI8(ODV, GDV)                                                                                  \
+    if (o_dt == ODV && out_dt == GDV) {                                                                      \
+      hipLaunchKernelGGL((lay::epilogue8_kernel<ODV, GDV>), grid8, dim3(lay::kThreads), 0, stream, o, gate,  \
+                         ld_gate, weight, eps, out, ld_out, rows, H, DV, G);                                 \
+      return hipGetLastError();                                                                              \
+    }
+#define GDN2_EPI8_O(GDV) GDN2_EPI8(DT_F32, GDV) GDN2_EPI8(DT_BF16, GDV) GDN2_EPI8(DT_F16, GDV)
+    GDN2_EPI8_O(DT_F32) GDN2_EPI8_O(DT_BF16) GDN2_EPI8_O(DT_F16)
+#undef GDN2_EPI8_O
+#undef GDN2_EPI8
+    return hipErrorInvalidValue;
+  }
+  // scalar form: one wave per (token, value head)
   const dim3 grid(static_cast<unsigned>((rows + 3) / 4));
 #define GDN2_EPI(ODV, GDV)                                                                                  \
   if (o_dt == ODV && out_dt == GDV) {                                                                       \

@@ -74,6 +74,33 @@ def test_config4_segmented_prefill_then_decode():
     assert e_pre < 1e-2 and e_dec < 1e-2
 
 
+@pytest.mark.parametrize("DV,ld_pad", [(32, 0), (128, 0), (512, 0), (96, 8), (36, 0), (520, 0), (128, 3)])
+@pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
+def test_epilogue_c_abi(DV, ld_pad, dtype):
+    """gdn2_hip_layer_epilogue (gated RMSNorm) against its formula in fp32:
+    the vector form (DV % 8 == 0, DV <= 512, row strides multiples of 8) and
+    the scalar form (DV = 36, DV = 520, an odd gate row stride)."""
+    from gdt2_tilelang_amd import _hip
+    print(f"epilogue DV={DV} ld_pad={ld_pad} {dtype}", flush=True)
+    B, S, H, eps = 2, 37, 3, 1e-6
+    gen = torch.Generator(device="cuda").manual_seed(DV + ld_pad)
+    o = torch.randn(B, S, H, DV, device="cuda", generator=gen).to(dtype)
+    ldg = H * DV + ld_pad
+    gate_buf = torch.randn(B * S, ldg, device="cuda", generator=gen).to(dtype)
+    gate = gate_buf[:, :H * DV]
+    weight = torch.rand(DV, device="cuda", generator=gen) + 0.5
+    out = torch.empty(B * S, H * DV, device="cuda", dtype=dtype)
+    code = _hip.dtype_code(dtype)
+    _hip.check(_hip.lib().gdn2_hip_layer_epilogue(
+        _hip.ptr(o), code, _hip.ptr(gate_buf), ldg, _hip.ptr(weight), eps, _hip.ptr(out), code, H * DV,
+        B, S, H, DV, _hip.stream_of(o.device)), "epilogue")
+    of = o.float().reshape(B * S, H, DV)
+    ref = of * torch.rsqrt(of.pow(2).mean(-1, keepdim=True) + eps) * weight
+    ref = (ref * torch.nn.functional.silu(gate.float().reshape(B * S, H, DV))).reshape(B * S, H * DV)
+    torch.cuda.synchronize()
+    assert rel_err(out.float(), ref) < (2e-6 if dtype == torch.float32 else 8e-3)
+
+
 @pytest.mark.parametrize("dtype,tol", [(torch.float32, 2e-5), (torch.bfloat16, 1.6e-2)])
 @pytest.mark.parametrize("S,with_cache", [(37, False), (37, True), (2, True), (1, True)])
 def test_fused_prologue_epilogue_match_torch_formulas(dtype, tol, S, with_cache):
