@@ -108,6 +108,12 @@ def chunk_gdn2_varlen_fwd(q, k, v, g, b, w, scale, cu_seqlens, initial_state=Non
         initial_state = initial_state.to(torch.float32).contiguous()
     final = torch.empty(N, H, DK, DV, dtype=torch.float32, device=dev)
     o = torch.empty(1, T, H, DV, dtype=config.output_dtype or q.dtype, device=dev)
+    if T == 0:                          # every sequence empty: the states pass through
+        if initial_state is not None:
+            final.copy_(initial_state)
+        else:
+            final.zero_()
+        return o, (final if output_final_state else None)
     lib = _hip.lib()
     ws = torch.empty(lib.gdn2_hip_prefill_varlen_workspace_bytes(N, HK, DK, T), dtype=torch.uint8, device=dev)
     _hip.check(lib.gdn2_hip_prefill_varlen(

@@ -110,6 +110,15 @@ def test_varlen_no_initial_state_and_no_final():
     assert rel_err(o[:, 70:].cpu(), o_ref) < TOL and rel_err(st2[2:].cpu(), s_ref) < TOL
 
 
+def test_varlen_all_empty():
+    H, DK, DV = 2, 64, 64
+    _, dev, cu = _packed([0, 0, 0], H, H, DK, DV)
+    s0 = seeded_state(3, H, DK, DV).cuda()
+    o, st = gdn2_attention(*dev, initial_state=s0, output_final_state=True, config=F32, cu_seqlens=cu)
+    torch.cuda.synchronize()
+    assert o.shape == (1, 0, H, DV) and torch.equal(st, s0)
+
+
 @pytest.mark.parametrize("N", [100, 5000])
 def test_varlen_many_short_sequences(N):
     """Thousands of short sequences (N = 5000 takes three rounds of the
