@@ -155,16 +155,17 @@ def test_grouped_heads_equal_repeated(DK, H, HK):
     assert torch.equal(o1, o2) and torch.equal(s1, s2) and torch.equal(d1, d2)
 
 
-@pytest.mark.parametrize("DK", [64, 128])
-def test_c_abi_ragged_window(DK):
+@pytest.mark.parametrize("DK,DV", [(64, 64), (128, 64), (128, 16), (64, 48)])
+def test_c_abi_ragged_window(DK, DV):
     """The C ABI on a window [t0, t0 + n) of a larger allocation with n not a
     chunk multiple: the last chunk's missing rows are read as zeros, o rows
     outside the window are left alone, and the result equals the recurrence on
-    the window alone."""
+    the window alone. DV 16 and 48: value widths the C ABI takes (multiples of
+    16) below the Python API's multiples of 32."""
     from gdt2_tilelang_amd import _hip
 
-    B, S_alloc, H, DV, t0, n = 2, 230, 2, 64, 10, 150
-    print(f"ragged window DK={DK} t0={t0} n={n} s_alloc={S_alloc}", flush=True)
+    B, S_alloc, H, t0, n = 2, 230, 2, 10, 150
+    print(f"ragged window DK={DK} DV={DV} t0={t0} n={n} s_alloc={S_alloc}", flush=True)
     cpu, dev = device_inputs(B, S_alloc, H, DK, DV, torch.bfloat16)
     s0 = seeded_state(B, H, DK, DV)
     win = tuple(t[:, t0:t0 + n] for t in cpu)
