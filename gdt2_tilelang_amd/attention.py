@@ -36,7 +36,7 @@ from torch import nn
 
 from . import _hip
 from .config import DEFAULT_KERNEL_CONFIG, GDN2Config, GatedDeltaNet2Config
-from .forward import chunk_gdn2_fwd, chunk_gdn2_varlen_fwd
+from .forward import check_cu_seqlens, chunk_gdn2_fwd, chunk_gdn2_varlen_fwd
 from .inference import gdn2_decode, gdn2_prefill
 
 __all__ = ["gdn2_attention", "GatedDeltaNet2", "GDN2Cache", "resolve_backend"]
@@ -260,10 +260,12 @@ class GatedDeltaNet2(nn.Module):
                                           self.b_proj.weight, self.w_proj.weight, self.f_proj.weight,
                                           self.o_gate_proj.weight])
 
-    def _project_gpu(self, x, cache, conv_tail=False):
+    def _project_gpu(self, x, cache, conv_tail=False, cu=None):
         """All projections in one GEMM, then the prologue kernel. Returns the op
         inputs, the projection buffer (its o_gate columns feed _finish_gpu) and
-        the new conv tail (or None)."""
+        the new conv tail (or None). ``cu``: int32 device offsets of packed
+        sequences (B = 1, no cache): each token's conv window starts at its
+        own sequence's first token."""
         B, S, hid = x.shape
         HK, H, DK, DV = self.num_kv_heads, self.num_heads, self.head_dim_k, self.head_dim_v
         dqk, dv = HK * DK, H * DV
@@ -300,6 +302,13 @@ class GatedDeltaNet2(nn.Module):
         a_log = self._f32_cached("_alog32", self.A_log)
         dt_bias = self._f32_cached("_dtb32", self.dt_bias)
         P = _hip.ptr
+        if cu is not None:
+            _hip.check(_hip.lib().gdn2_hip_layer_prologue_varlen(
+                *(base + o * es for o in offs), ld, ld, ld, ld, ld, ld, _hip.dtype_code(dt),
+                P(conv_w), P(conv_b), K, P(a_log), P(dt_bias), float(self.erase_scale),
+                P(q), P(k), P(v), P(b), P(w), P(g), P(cu), cu.numel() - 1, S, H, HK, DK, DV,
+                _hip.stream_of(dev)), "gdn2_hip_layer_prologue_varlen")
+            return (q, k, v, g, b, w), proj, None
         _hip.check(_hip.lib().gdn2_hip_layer_prologue(
             *(base + o * es for o in offs), ld, ld, ld, ld, ld, ld, _hip.dtype_code(dt),
             P(conv_w), P(conv_b), K, P(conv_in), P(conv_out), P(a_log), P(dt_bias), float(self.erase_scale),
@@ -428,9 +437,21 @@ class GatedDeltaNet2(nn.Module):
     def forward(self, hidden_states, cache=None, use_cache=False, cu_seqlens=None):
         """Full-sequence mixer (training form). Returns ``(output, cache or None)``."""
         B, S, _ = hidden_states.shape
+        if cu_seqlens is not None and hidden_states.is_cuda:
+            # packed sequences: per-sequence conv windows in the prologue, the
+            # packed op; per-sequence conv tails are not kept, so no cache
+            if cache is not None or use_cache:
+                raise NotImplementedError("packed sequences (cu_seqlens) through the layer take no cache "
+                                          "and return none")
+            if B != 1:
+                raise ValueError(f"packed sequences (cu_seqlens) need batch size 1; got {B}")
+            cu = check_cu_seqlens(cu_seqlens, S).to(hidden_states.device)
+            (q, k, v, g, b, w), proj, _ = self._project_gpu(hidden_states, None, cu=cu)
+            o, _ = gdn2_attention(q, k, v, g, b, w, scale=self.scale, config=self.cfg.kernel, cu_seqlens=cu)
+            return self._finish_gpu(hidden_states, o, proj), None
         if cu_seqlens is not None and self.q_conv is not None:
             raise NotImplementedError("packed sequences (cu_seqlens) through the layer's short convolution "
-                                      "are not supported; pass a padded batch")
+                                      "run on the GPU only")
         if hidden_states.is_cuda:
             (q, k, v, g, b, w), proj, conv_state = self._project_gpu(hidden_states, None, conv_tail=use_cache)
             o, final_state = gdn2_attention(

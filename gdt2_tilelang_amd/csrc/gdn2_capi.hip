@@ -155,13 +155,13 @@ int gdn2_hip_prefill_varlen(const void* q, const void* k, const void* v, const f
                                   DV, T, 0, static_cast<int>(slots), T, vl, st));
 }
 
-int gdn2_hip_layer_prologue(const void* xq, const void* xk, const void* xv, const void* xb,
-                            const void* xw, const void* xf, long ld_q, long ld_k, long ld_v,
-                            long ld_b, long ld_w, long ld_f, int act_dtype, const void* conv_w,
-                            const void* conv_b, int conv_k, const void* conv_in, void* conv_out,
-                            const float* a_log, const float* dt_bias, float erase_scale, void* q,
-                            void* k, void* v, void* b, void* w, float* g, int B, long S, int H,
-                            int HK, int DK, int DV, void* stream) {
+static int layer_prologue(const void* xq, const void* xk, const void* xv, const void* xb,
+                          const void* xw, const void* xf, long ld_q, long ld_k, long ld_v,
+                          long ld_b, long ld_w, long ld_f, int act_dtype, const void* conv_w,
+                          const void* conv_b, int conv_k, const void* conv_in, void* conv_out,
+                          const float* a_log, const float* dt_bias, float erase_scale, void* q,
+                          void* k, void* v, void* b, void* w, float* g, int B, long S, int H,
+                          int HK, int DK, int DV, const int* cu_seqlens, int nseq, void* stream) {
   if (!xq || !xk || !xv || !xb || !xw || !xf || !a_log || !dt_bias) return GDN2_ERR_ARG;
   if (!q || !k || !v || !b || !w || !g) return GDN2_ERR_ARG;
   if (!dtype_ok(act_dtype) || B < 0 || S < 0 || H < 1 || HK < 1 || H % HK || DV < 1) return GDN2_ERR_ARG;
@@ -191,7 +191,33 @@ int gdn2_hip_layer_prologue(const void* xq, const void* xk, const void* xv, cons
   a.a_log = a_log; a.dt_bias = dt_bias; a.erase_scale = erase_scale;
   a.q = q; a.k = k; a.v = v; a.b = b; a.w = w; a.g = g;
   a.B = B; a.S = S; a.H = H; a.HK = HK; a.DK = DK; a.DV = DV;
+  a.cu = conv_w ? cu_seqlens : nullptr; a.nseq = nseq;
   return status(gdn2::launch_layer_prologue(a, act_dtype, static_cast<hipStream_t>(stream)));
+}
+
+int gdn2_hip_layer_prologue(const void* xq, const void* xk, const void* xv, const void* xb,
+                            const void* xw, const void* xf, long ld_q, long ld_k, long ld_v,
+                            long ld_b, long ld_w, long ld_f, int act_dtype, const void* conv_w,
+                            const void* conv_b, int conv_k, const void* conv_in, void* conv_out,
+                            const float* a_log, const float* dt_bias, float erase_scale, void* q,
+                            void* k, void* v, void* b, void* w, float* g, int B, long S, int H,
+                            int HK, int DK, int DV, void* stream) {
+  return layer_prologue(xq, xk, xv, xb, xw, xf, ld_q, ld_k, ld_v, ld_b, ld_w, ld_f, act_dtype, conv_w, conv_b,
+                        conv_k, conv_in, conv_out, a_log, dt_bias, erase_scale, q, k, v, b, w, g, B, S, H, HK, DK,
+                        DV, nullptr, 0, stream);
+}
+
+int gdn2_hip_layer_prologue_varlen(const void* xq, const void* xk, const void* xv, const void* xb,
+                                   const void* xw, const void* xf, long ld_q, long ld_k, long ld_v,
+                                   long ld_b, long ld_w, long ld_f, int act_dtype, const void* conv_w,
+                                   const void* conv_b, int conv_k, const float* a_log, const float* dt_bias,
+                                   float erase_scale, void* q, void* k, void* v, void* b, void* w, float* g,
+                                   const int* cu_seqlens, int nseq, long T, int H, int HK, int DK, int DV,
+                                   void* stream) {
+  if (!cu_seqlens || nseq < 1) return GDN2_ERR_ARG;
+  return layer_prologue(xq, xk, xv, xb, xw, xf, ld_q, ld_k, ld_v, ld_b, ld_w, ld_f, act_dtype, conv_w, conv_b,
+                        conv_k, nullptr, nullptr, a_log, dt_bias, erase_scale, q, k, v, b, w, g, 1, T, H, HK, DK,
+                        DV, cu_seqlens, nseq, stream);
 }
 
 int gdn2_hip_gemv(const void* x, long ldx, const void* W, void* y, long ldy, int dtype, int M, int N,

@@ -20,6 +20,8 @@ struct ProArgs {
   float erase_scale;
   void* q; void* k; void* v; void* b; void* w; float* g;   // outputs, contiguous
   int B; long S; int H, HK, DK, DV;
+  const int* cu = nullptr; // packed sequences (B = 1): nseq + 1 offsets; the conv
+  int nseq = 0;            // window of a token starts at its sequence's first token
 };
 
 }  // namespace lay

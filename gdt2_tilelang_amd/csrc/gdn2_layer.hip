@@ -16,6 +16,7 @@
 // Everything is computed in fp32 and rounded once on store.
 #include "gdn2_common.h"
 #include "gdn2_layer.h"
+#include "gdn2_prefill_layout.h"
 
 namespace gdn2 {
 
@@ -112,6 +113,17 @@ __global__ __launch_bounds__(kProThreads) void prologue_kernel(ProArgs a) {
   const int nconv = static_cast<int>(C / 8);
   const long row0 = static_cast<long>(bi) * a.S;
 
+  // packed sequences: the first token of the sequence holding each token of
+  // the block (found by all lanes together, before the per-lane item branch);
+  // conv window rows before it are zeros. Dense: no row of a window is cut.
+  long sstart[TT];
+#pragma unroll
+  for (int t = 0; t < TT; ++t) sstart[t] = t0 - TT - kMaxConv;
+  if (conv && a.cu) {
+#pragma unroll
+    for (int t = 0; t < TT; ++t) sstart[t] = varlen_token_start(a.cu, a.nseq, a.S, t0 + min(t, nt - 1));
+  }
+
   const int nb = dqk / 8, nw = dv / 8;
   const int item = blockIdx.y * kProThreads + tid;
   if (item < nconv) {
@@ -165,7 +177,8 @@ __global__ __launch_bounds__(kProThreads) void prologue_kernel(ProArgs a) {
         for (int e = 0; e < 8; ++e) {
           float acc = bias[e];
 #pragma unroll
-          for (int jj = 0; jj < K; ++jj) acc += wflat[e * K + jj] * win[t + jj][e];
+          for (int jj = 0; jj < K; ++jj)
+            acc += wflat[e * K + jj] * (t0 - K1 + t + jj >= sstart[t] ? win[t + jj][e] : 0.f);
           y[t][e] = silu(acc);
         }
       // new conv tail (entry i = the input at position S - K1 + i = window row

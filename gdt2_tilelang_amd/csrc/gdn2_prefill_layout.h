@@ -80,12 +80,31 @@ __device__ __forceinline__ int varlen_seq(const int* cu, int nseq, long T, long 
     const int step = (len + 63) >> 6;
     const int s = lo + lane * step;
     const bool ok = s < lo + len && s + varlen_off(cu, s, T) / kBS <= slot;
-    const int cnt = __popcll(__ballot(ok));   // the passing lanes form a prefix; lane 0 passes
+    // the passing lanes form a prefix and lane 0 passes for well-formed
+    // offsets (cu[0] = 0); the max keeps a malformed array inside [0, nseq)
+    const int cnt = max(__popcll(__ballot(ok)), 1);
     const int nlo = lo + (cnt - 1) * step;
     len = min(step, lo + len - nlo);
     lo = nlo;
   }
   return lo;
+}
+
+// First token of the packed sequence that holds token p: the largest cu[s] <= p
+// (the last such s, so empty sequences are skipped), by the same 64-way search.
+__device__ __forceinline__ long varlen_token_start(const int* cu, int nseq, long T, long p) {
+  const int lane = threadIdx.x & 63;
+  int lo = 0, len = nseq;
+  while (len > 1) {
+    const int step = (len + 63) >> 6;
+    const int s = lo + lane * step;
+    const bool ok = s < lo + len && varlen_off(cu, s, T) <= p;
+    const int cnt = max(__popcll(__ballot(ok)), 1);
+    const int nlo = lo + (cnt - 1) * step;
+    len = min(step, lo + len - nlo);
+    lo = nlo;
+  }
+  return varlen_off(cu, lo, T);
 }
 
 // First token and valid rows of chunk slot `slot` of a packed batch of T

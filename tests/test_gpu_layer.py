@@ -74,6 +74,41 @@ def test_config4_segmented_prefill_then_decode():
     assert e_pre < 1e-2 and e_dec < 1e-2
 
 
+@pytest.mark.parametrize("dtype,tol,ptol", [(torch.float32, 2e-3, 1e-5), (torch.bfloat16, 2e-2, 1.6e-2)])
+@pytest.mark.parametrize("DK,H,HK,conv", [(64, 4, 2, 4), (128, 2, 2, 3), (64, 4, 4, 0)])
+def test_layer_forward_packed_sequences(dtype, tol, ptol, DK, H, HK, conv):
+    """GatedDeltaNet2.forward(x [1, T, hidden], cu_seqlens) equals the layer run
+    on each sequence alone. The prologue outputs (conv windows cut at each
+    sequence's start, also for sequences shorter than the window) are compared
+    to fp32 GEMM round-off; the layer output to the op's parity bar, since the
+    packed and per-sequence projection GEMMs round differently and the op's
+    fp16 records then round differently too."""
+    torch.manual_seed(0)
+    cfg = GatedDeltaNet2Config(hidden_size=256, num_heads=H, num_kv_heads=HK, head_dim_k=DK, head_dim_v=64,
+                               conv_size=conv)
+    layer = GatedDeltaNet2(cfg).cuda().to(dtype).eval()
+    lens = [5, 0, 70, 1, 130, 2, 64]
+    print(f"layer packed {dtype} DK={DK} H={H} HK={HK} conv={conv} lens={lens}", flush=True)
+    cu = torch.tensor([0] + torch.cumsum(torch.tensor(lens), 0).tolist(), dtype=torch.int32)
+    x = torch.randn(1, int(cu[-1]), 256, device="cuda").to(dtype)
+    with torch.no_grad():
+        out, cache = layer(x, cu_seqlens=cu)
+        assert cache is None and out.shape == x.shape
+        packed, _, _ = layer._project_gpu(x, None, cu=cu.cuda())
+        for i in range(len(lens)):
+            a, e = int(cu[i]), int(cu[i + 1])
+            if e == a:
+                continue
+            xi = x[:, a:e].contiguous()
+            alone, _, _ = layer._project_gpu(xi, None)
+            for name, tp, ta in zip("qkvgbw", packed, alone):
+                assert rel_err(tp[:, a:e].float().cpu(), ta.float().cpu()) < ptol, (i, name)
+            ref, _ = layer(xi)
+            assert rel_err(out[:, a:e].float().cpu(), ref.float().cpu()) < tol, i
+    with pytest.raises(NotImplementedError, match="cache"):
+        layer(x, cu_seqlens=cu, use_cache=True)
+
+
 @pytest.mark.parametrize("DV,ld_pad", [(32, 0), (128, 0), (512, 0), (96, 8), (36, 0), (520, 0), (128, 3)])
 @pytest.mark.parametrize("dtype", [torch.float32, torch.bfloat16])
 def test_epilogue_c_abi(DV, ld_pad, dtype):
