@@ -35,7 +35,8 @@ SIGNATURES = {
     "gdn2_hip_layer_prologue": (_I, [_P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _L, _I, _P, _P, _I, _P, _P,
                                      _P, _P, _F, _P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _I, _I, _P]),
     "gdn2_hip_layer_prologue_varlen": (_I, [_P, _P, _P, _P, _P, _P, _L, _L, _L, _L, _L, _L, _I, _P, _P, _I, _P,
-                                            _P, _F, _P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _I, _I, _P]),
+                                            _P, _P, _P, _F, _P, _P, _P, _P, _P, _P, _P, _I, _L, _I, _I, _I, _I,
+                                            _P]),
     "gdn2_hip_layer_epilogue": (_I, [_P, _I, _P, _L, _P, _F, _P, _I, _L, _I, _L, _I, _I, _P]),
     "gdn2_hip_gemv": (_I, [_P, _L, _P, _P, _L, _I, _I, _I, _I, _P]),
     "gdn2_hip_layer_decode_workspace_bytes": (_S, [_I, _I, _I, _I, _I, _I, _I]),

@@ -243,7 +243,7 @@ class GatedDeltaNet2(nn.Module):
         """x2 [M, K] @ weight^T. A few rows (decode) go through the library's
         GEMV, which streams the weight once; more rows through torch."""
         M, K = x2.shape
-        if (M <= 8 and K % 8 == 0 and x2.dtype == weight.dtype and weight.is_contiguous()
+        if (1 <= M <= 8 and K % 8 == 0 and x2.dtype == weight.dtype and weight.is_contiguous()
                 and not (torch.is_grad_enabled() and (weight.requires_grad or x2.requires_grad))
                 and x2.stride(1) == 1 and x2.stride(0) % 8 == 0 and x2.data_ptr() % 16 == 0
                 and weight.data_ptr() % 16 == 0):
@@ -263,9 +263,10 @@ class GatedDeltaNet2(nn.Module):
     def _project_gpu(self, x, cache, conv_tail=False, cu=None):
         """All projections in one GEMM, then the prologue kernel. Returns the op
         inputs, the projection buffer (its o_gate columns feed _finish_gpu) and
-        the new conv tail (or None). ``cu``: int32 device offsets of packed
-        sequences (B = 1, no cache): each token's conv window starts at its
-        own sequence's first token."""
+        the new conv tail (or None). ``cu``: int32 device offsets of N packed
+        sequences (B = 1): each token's conv window starts at its own
+        sequence's first token, continuing from that sequence's cached tail
+        (``cache.conv_state`` [N, C, K-1]); the new tails are [N, C, K-1]."""
         B, S, hid = x.shape
         HK, H, DK, DV = self.num_kv_heads, self.num_heads, self.head_dim_k, self.head_dim_v
         dqk, dv = HK * DK, H * DV
@@ -298,17 +299,18 @@ class GatedDeltaNet2(nn.Module):
                 if conv_in.data_ptr() % 16:          # the kernel reads 16-byte vectors
                     conv_in = conv_in.clone()
             if cache is not None or conv_tail:
-                conv_out = torch.empty(B, 2 * dqk + dv, K - 1, device=dev, dtype=dt)
+                nrow = B if cu is None else cu.numel() - 1
+                conv_out = torch.empty(nrow, 2 * dqk + dv, K - 1, device=dev, dtype=dt)
         a_log = self._f32_cached("_alog32", self.A_log)
         dt_bias = self._f32_cached("_dtb32", self.dt_bias)
         P = _hip.ptr
         if cu is not None:
             _hip.check(_hip.lib().gdn2_hip_layer_prologue_varlen(
                 *(base + o * es for o in offs), ld, ld, ld, ld, ld, ld, _hip.dtype_code(dt),
-                P(conv_w), P(conv_b), K, P(a_log), P(dt_bias), float(self.erase_scale),
+                P(conv_w), P(conv_b), K, P(conv_in), P(conv_out), P(a_log), P(dt_bias), float(self.erase_scale),
                 P(q), P(k), P(v), P(b), P(w), P(g), P(cu), cu.numel() - 1, S, H, HK, DK, DV,
                 _hip.stream_of(dev)), "gdn2_hip_layer_prologue_varlen")
-            return (q, k, v, g, b, w), proj, None
+            return (q, k, v, g, b, w), proj, conv_out
         _hip.check(_hip.lib().gdn2_hip_layer_prologue(
             *(base + o * es for o in offs), ld, ld, ld, ld, ld, ld, _hip.dtype_code(dt),
             P(conv_w), P(conv_b), K, P(conv_in), P(conv_out), P(a_log), P(dt_bias), float(self.erase_scale),
@@ -438,20 +440,29 @@ class GatedDeltaNet2(nn.Module):
         """Full-sequence mixer (training form). Returns ``(output, cache or None)``."""
         B, S, _ = hidden_states.shape
         if cu_seqlens is not None and hidden_states.is_cuda:
-            # packed sequences: per-sequence conv windows in the prologue, the
-            # packed op; per-sequence conv tails are not kept, so no cache
-            if cache is not None or use_cache:
-                raise NotImplementedError("packed sequences (cu_seqlens) through the layer take no cache "
-                                          "and return none")
+            # packed sequences: per-sequence conv windows in the prologue and the
+            # packed op; as for a dense batch, the conv starts fresh (the
+            # cache's conv tails are not read) and the recurrent state carries on
             if B != 1:
                 raise ValueError(f"packed sequences (cu_seqlens) need batch size 1; got {B}")
             cu = check_cu_seqlens(cu_seqlens, S).to(hidden_states.device)
-            (q, k, v, g, b, w), proj, _ = self._project_gpu(hidden_states, None, cu=cu)
-            o, _ = gdn2_attention(q, k, v, g, b, w, scale=self.scale, config=self.cfg.kernel, cu_seqlens=cu)
-            return self._finish_gpu(hidden_states, o, proj), None
+            N = cu.numel() - 1
+            if cache is not None and cache.recurrent_state.shape[0] != N:
+                raise ValueError(f"a packed batch of {N} sequences needs a cache of {N} rows; "
+                                 f"got {cache.recurrent_state.shape[0]}")
+            (q, k, v, g, b, w), proj, conv_state = self._project_gpu(hidden_states, None, conv_tail=use_cache,
+                                                                     cu=cu)
+            o, final_state = gdn2_attention(
+                q, k, v, g, b, w, scale=self.scale,
+                initial_state=cache.recurrent_state if cache is not None else None,
+                output_final_state=use_cache, config=self.cfg.kernel, cu_seqlens=cu)
+            out = self._finish_gpu(hidden_states, o, proj)
+            return out, (GDN2Cache(final_state, conv_state) if use_cache else None)
         if cu_seqlens is not None and self.q_conv is not None:
             raise NotImplementedError("packed sequences (cu_seqlens) through the layer's short convolution "
                                       "run on the GPU only")
+        if hidden_states.is_cuda and S == 0:             # nothing to run: the state carries over
+            return self._empty_call(hidden_states, cache, use_cache, fresh_conv=True)
         if hidden_states.is_cuda:
             (q, k, v, g, b, w), proj, conv_state = self._project_gpu(hidden_states, None, conv_tail=use_cache)
             o, final_state = gdn2_attention(
@@ -476,10 +487,19 @@ class GatedDeltaNet2(nn.Module):
         return out, (GDN2Cache(final_state, conv_state) if use_cache else None)
 
     @torch.no_grad()
-    def prefill(self, hidden_states, cache=None):
-        """Prefill a prompt (or one segment of it); returns ``(output, cache)``."""
+    def prefill(self, hidden_states, cache=None, *, cu_seqlens=None):
+        """Prefill a prompt (or one segment of it); returns ``(output, cache)``.
+
+        ``cu_seqlens`` (an extension; GPU only): ``hidden_states`` is ``[1, T,
+        hidden]`` holding N packed prompts, and the cache (``None``: fresh)
+        has N rows; each sequence continues from its own recurrent state and
+        conv tail, and the returned cache has one of each per sequence."""
+        if cu_seqlens is not None:
+            return self._prefill_packed(hidden_states, cache, cu_seqlens)
         if cache is None:
             cache = self.init_cache(hidden_states.shape[0], device=hidden_states.device)
+        if hidden_states.is_cuda and hidden_states.shape[1] == 0:
+            return self._empty_call(hidden_states, cache, True, fresh_conv=False)
         if hidden_states.is_cuda:
             (q, k, v, g, b, w), proj, conv_out = self._project_gpu(hidden_states, cache)
             cache.conv_state = conv_out
@@ -492,6 +512,42 @@ class GatedDeltaNet2(nn.Module):
                                 config=self.cfg.kernel)
         cache.recurrent_state = state
         return self._finish(hidden_states, o), cache
+
+    def _empty_call(self, x, cache, use_cache, fresh_conv):
+        """A call of zero tokens: empty output; the recurrent state carries over
+        and the conv tail is zeros (forward: a fresh conv) or the cached one."""
+        B = x.shape[0]
+        out = x.new_empty(B, 0, self.cfg.hidden_size)
+        if not use_cache:
+            return out, None
+        state = (cache.recurrent_state.clone() if cache is not None
+                 else self.init_cache(B, device=x.device).recurrent_state)
+        conv = None
+        if self.q_conv is not None:
+            C = 2 * self.num_kv_heads * self.head_dim_k + self.num_heads * self.head_dim_v
+            if fresh_conv or cache is None or cache.conv_state is None:
+                conv = torch.zeros(B, C, self.cfg.conv_size - 1, device=x.device, dtype=x.dtype)
+            else:
+                conv = cache.conv_state
+        return out, GDN2Cache(state, conv)
+
+    def _prefill_packed(self, x, cache, cu_seqlens):
+        if not x.is_cuda:
+            raise ValueError("packed prefill (cu_seqlens) requires a CUDA device (a ROCm GPU)")
+        B, S, _ = x.shape
+        if B != 1:
+            raise ValueError(f"packed sequences (cu_seqlens) need batch size 1; got {B}")
+        cu = check_cu_seqlens(cu_seqlens, S).to(x.device)
+        N = cu.numel() - 1
+        if cache is None:
+            cache = self.init_cache(N, device=x.device)
+        elif cache.recurrent_state.shape[0] != N:
+            raise ValueError(f"a packed batch of {N} sequences needs a cache of {N} rows; "
+                             f"got {cache.recurrent_state.shape[0]}")
+        (q, k, v, g, b, w), proj, conv_out = self._project_gpu(x, cache, cu=cu)
+        o, state = gdn2_attention(q, k, v, g, b, w, scale=self.scale, initial_state=cache.recurrent_state,
+                                  output_final_state=True, config=self.cfg.kernel, cu_seqlens=cu)
+        return self._finish_gpu(x, o, proj), GDN2Cache(state, conv_out)
 
     @torch.no_grad()
     def decode(self, hidden_states, cache):

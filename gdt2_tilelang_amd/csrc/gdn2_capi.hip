@@ -210,13 +210,13 @@ int gdn2_hip_layer_prologue(const void* xq, const void* xk, const void* xv, cons
 int gdn2_hip_layer_prologue_varlen(const void* xq, const void* xk, const void* xv, const void* xb,
                                    const void* xw, const void* xf, long ld_q, long ld_k, long ld_v,
                                    long ld_b, long ld_w, long ld_f, int act_dtype, const void* conv_w,
-                                   const void* conv_b, int conv_k, const float* a_log, const float* dt_bias,
-                                   float erase_scale, void* q, void* k, void* v, void* b, void* w, float* g,
-                                   const int* cu_seqlens, int nseq, long T, int H, int HK, int DK, int DV,
-                                   void* stream) {
+                                   const void* conv_b, int conv_k, const void* conv_in, void* conv_out,
+                                   const float* a_log, const float* dt_bias, float erase_scale, void* q, void* k,
+                                   void* v, void* b, void* w, float* g, const int* cu_seqlens, int nseq, long T,
+                                   int H, int HK, int DK, int DV, void* stream) {
   if (!cu_seqlens || nseq < 1) return GDN2_ERR_ARG;
   return layer_prologue(xq, xk, xv, xb, xw, xf, ld_q, ld_k, ld_v, ld_b, ld_w, ld_f, act_dtype, conv_w, conv_b,
-                        conv_k, nullptr, nullptr, a_log, dt_bias, erase_scale, q, k, v, b, w, g, 1, T, H, HK, DK,
+                        conv_k, conv_in, conv_out, a_log, dt_bias, erase_scale, q, k, v, b, w, g, 1, T, H, HK, DK,
                         DV, cu_seqlens, nseq, stream);
 }
 

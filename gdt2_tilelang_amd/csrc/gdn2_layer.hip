@@ -98,7 +98,11 @@ __device__ __forceinline__ void st8(void* p, long i, const float* x) {
 // (C + 2*HK*DK + H*DV) / 8 / kProThreads workgroups.
 // KC: conv width (0: no conv), a template argument so that every register
 // array below is indexed at compile time.
-template <int DT, int KC>
+// VL: a packed batch (B = 1, a.cu set, with a conv): each token's conv window
+// starts at its own sequence's first token, the rows before it coming from
+// that sequence's cached conv tail (a.conv_in [nseq, C, K-1]) or zeros; the
+// new tails are written by conv_tail_varlen_kernel.
+template <int DT, int KC, bool VL>
 __global__ __launch_bounds__(kProThreads) void prologue_kernel(ProArgs a) {
   static_assert(TT >= kMaxConv - 1, "a window reaching before the segment must start at token 0");
   const int bi = blockIdx.z;
@@ -113,15 +117,16 @@ __global__ __launch_bounds__(kProThreads) void prologue_kernel(ProArgs a) {
   const int nconv = static_cast<int>(C / 8);
   const long row0 = static_cast<long>(bi) * a.S;
 
-  // packed sequences: the first token of the sequence holding each token of
-  // the block (found by all lanes together, before the per-lane item branch);
-  // conv window rows before it are zeros. Dense: no row of a window is cut.
+  // packed sequences: the sequence holding each token of the block and its
+  // first token (found by all lanes together, before the per-lane item branch)
+  int sseq[TT];
   long sstart[TT];
+  if constexpr (VL) {
 #pragma unroll
-  for (int t = 0; t < TT; ++t) sstart[t] = t0 - TT - kMaxConv;
-  if (conv && a.cu) {
-#pragma unroll
-    for (int t = 0; t < TT; ++t) sstart[t] = varlen_token_start(a.cu, a.nseq, a.S, t0 + min(t, nt - 1));
+    for (int t = 0; t < TT; ++t) {
+      sseq[t] = varlen_token_seq(a.cu, a.nseq, a.S, t0 + min(t, nt - 1));
+      sstart[t] = varlen_off(a.cu, sseq[t], a.S);
+    }
   }
 
   const int nb = dqk / 8, nw = dv / 8;
@@ -147,7 +152,7 @@ __global__ __launch_bounds__(kProThreads) void prologue_kernel(ProArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) bias[e] = 0.f;
       }
-      const bool need_cin = t0 < K1;                   // window reaches before the segment
+      const bool need_cin = !VL && t0 < K1;            // window reaches before the segment
 #pragma unroll
       for (int c = 0; c < K1; ++c) {
         if (need_cin && a.conv_in) ld8<DT>(a.conv_in, (static_cast<long>(bi) * C + c0) * K1 + 8 * c, cin + 8 * c);
@@ -177,13 +182,21 @@ __global__ __launch_bounds__(kProThreads) void prologue_kernel(ProArgs a) {
         for (int e = 0; e < 8; ++e) {
           float acc = bias[e];
 #pragma unroll
-          for (int jj = 0; jj < K; ++jj)
-            acc += wflat[e * K + jj] * (t0 - K1 + t + jj >= sstart[t] ? win[t + jj][e] : 0.f);
+          for (int jj = 0; jj < K; ++jj) {
+            float xin = win[t + jj][e];
+            if constexpr (VL) {
+              const long p = t0 - K1 + t + jj;       // before its sequence: cached tail entry or zero
+              if (p < sstart[t])
+                xin = a.conv_in ? ld<DT>(a.conv_in, (static_cast<long>(sseq[t]) * C + c0 + e) * K1 + (p - sstart[t] + K1))
+                                : 0.f;
+            }
+            acc += wflat[e * K + jj] * xin;
+          }
           y[t][e] = silu(acc);
         }
       // new conv tail (entry i = the input at position S - K1 + i = window row
       // nt + i of the last token block), 8*K1 contiguous values
-      if constexpr (K1 > 0) if (a.conv_out && t0 + nt == a.S) {
+      if constexpr (K1 > 0 && !VL) if (a.conv_out && t0 + nt == a.S) {
 #pragma unroll
         for (int c = 0; c < K1; ++c) {
           float z[8];
@@ -256,6 +269,48 @@ __global__ __launch_bounds__(kProThreads) void prologue_kernel(ProArgs a) {
     }
   }
 
+}
+
+// New conv tails of a packed batch: per sequence s and 8-channel item, the
+// conv inputs at positions cu[s+1] - K1 .. cu[s+1] - 1; a position before the
+// sequence's first token takes the entry of the sequence's previous tail
+// (conv_in) or zero, so an empty sequence passes its tail through.
+template <int DT, int K1>
+__global__ __launch_bounds__(kThreads) void conv_tail_varlen_kernel(ProArgs a) {
+  const int dqk = a.HK * a.DK, dv = a.H * a.DV;
+  const long C = 2L * dqk + dv;
+  const long nconv = C / 8;
+  const long idx = static_cast<long>(blockIdx.x) * kThreads + threadIdx.x;
+  const int s = static_cast<int>(idx / nconv);
+  if (s >= a.nseq) return;
+  const int c0 = static_cast<int>(idx % nconv) * 8;
+  const int which = c0 < dqk ? 0 : (c0 < 2 * dqk ? 1 : 2);
+  const int cx = c0 - which * dqk;
+  const long st = varlen_off(a.cu, s, a.S);
+  const long en = max(varlen_off(a.cu, s + 1, a.S), st);
+  float z[K1][8];
+#pragma unroll
+  for (int i = 0; i < K1; ++i) {
+    const long p = en - K1 + i;
+    if (p >= st) {
+      ld8<DT>(a.x[which], p * a.ld[which] + cx, z[i]);
+    } else {
+#pragma unroll
+      for (int e = 0; e < 8; ++e)
+        z[i][e] = a.conv_in ? ld<DT>(a.conv_in, (static_cast<long>(s) * C + c0 + e) * K1 + (p - st + K1)) : 0.f;
+    }
+  }
+  // layout [C][K1] per sequence: the item's 8 * K1 values are contiguous
+#pragma unroll
+  for (int c = 0; c < K1; ++c) {
+    float o[8];
+#pragma unroll
+    for (int f = 0; f < 8; ++f) {
+      const int flat = 8 * c + f;
+      o[f] = z[flat % K1][flat / K1];
+    }
+    st8<DT>(a.conv_out, (static_cast<long>(s) * C + c0) * K1 + 8 * c, o);
+  }
 }
 
 // gated RMSNorm: one wave per (token, value head)
@@ -332,19 +387,34 @@ hipError_t launch_layer_prologue(const lay::ProArgs& a, int act_dt, hipStream_t 
                   static_cast<unsigned>((items + lay::kProThreads - 1) / lay::kProThreads), static_cast<unsigned>(a.B));
   const int kc = a.conv_w ? a.K : 0;
   if (kc < 0 || kc > lay::kMaxConv) return hipErrorInvalidValue;
+  const bool vl = a.cu != nullptr && kc > 0;
+  // packed batch with a cache: the new per-sequence conv tails
+  const long tail_items = static_cast<long>(a.nseq) * ((2L * a.HK * a.DK + a.H * a.DV) / 8);
+  const dim3 tail_grid(static_cast<unsigned>((tail_items + lay::kThreads - 1) / lay::kThreads));
+#define GDN2_PRO_K(DTV, KV)                                                                             \
+  if (vl) {                                                                                             \
+    hipLaunchKernelGGL((lay::prologue_kernel<DTV, KV, true>), grid, dim3(lay::kProThreads), 0, stream, a); \
+    if (KV > 1 && a.conv_out)                                                                           \
+      hipLaunchKernelGGL((lay::conv_tail_varlen_kernel<DTV, (KV > 1 ? KV - 1 : 1)>), tail_grid,         \
+                         dim3(lay::kThreads), 0, stream, a);                                             \
+  } else {                                                                                              \
+    hipLaunchKernelGGL((lay::prologue_kernel<DTV, KV, false>), grid, dim3(lay::kProThreads), 0, stream, a); \
+  }                                                                                                     \
+  break;
 #define GDN2_PRO(DTV)                                                                                   \
   if (act_dt == DTV) {                                                                                  \
     switch (kc) {                                                                                       \
-      case 0: hipLaunchKernelGGL((lay::prologue_kernel<DTV, 0>), grid, dim3(lay::kProThreads), 0, stream, a); break; \
-      case 1: hipLaunchKernelGGL((lay::prologue_kernel<DTV, 1>), grid, dim3(lay::kProThreads), 0, stream, a); break; \
-      case 2: hipLaunchKernelGGL((lay::prologue_kernel<DTV, 2>), grid, dim3(lay::kProThreads), 0, stream, a); break; \
-      case 3: hipLaunchKernelGGL((lay::prologue_kernel<DTV, 3>), grid, dim3(lay::kProThreads), 0, stream, a); break; \
-      default: hipLaunchKernelGGL((lay::prologue_kernel<DTV, 4>), grid, dim3(lay::kProThreads), 0, stream, a); break; \
+      case 0: hipLaunchKernelGGL((lay::prologue_kernel<DTV, 0, false>), grid, dim3(lay::kProThreads), 0, stream, a); break; \
+      case 1: GDN2_PRO_K(DTV, 1)                                                                        \
+      case 2: GDN2_PRO_K(DTV, 2)                                                                        \
+      case 3: GDN2_PRO_K(DTV, 3)                                                                        \
+      default: GDN2_PRO_K(DTV, 4)                                                                       \
     }                                                                                                   \
     return hipGetLastError();                                                                           \
   }
   GDN2_PRO(DT_BF16) GDN2_PRO(DT_F16) GDN2_PRO(DT_F32)
 #undef GDN2_PRO
+#undef GDN2_PRO_K
   return hipErrorInvalidValue;
 }
 

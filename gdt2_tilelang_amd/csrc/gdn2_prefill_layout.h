@@ -90,9 +90,9 @@ __device__ __forceinline__ int varlen_seq(const int* cu, int nseq, long T, long 
   return lo;
 }
 
-// First token of the packed sequence that holds token p: the largest cu[s] <= p
-// (the last such s, so empty sequences are skipped), by the same 64-way search.
-__device__ __forceinline__ long varlen_token_start(const int* cu, int nseq, long T, long p) {
+// The packed sequence that holds token p: the last s with cu[s] <= p (so
+// empty sequences are skipped), by the same 64-way search.
+__device__ __forceinline__ int varlen_token_seq(const int* cu, int nseq, long T, long p) {
   const int lane = threadIdx.x & 63;
   int lo = 0, len = nseq;
   while (len > 1) {
@@ -104,7 +104,7 @@ __device__ __forceinline__ long varlen_token_start(const int* cu, int nseq, long
     len = min(step, lo + len - nlo);
     lo = nlo;
   }
-  return varlen_off(cu, lo, T);
+  return lo;
 }
 
 // First token and valid rows of chunk slot `slot` of a packed batch of T

@@ -160,9 +160,12 @@ int gdn2_hip_layer_prologue(const void* xq, const void* xk, const void* xv, cons
  * The layer prologue over a packed variable-length batch: T tokens of nseq
  * sequences in one row (cu_seqlens as for gdn2_hip_prefill_varlen, int32 in
  * device memory). Each token's conv window starts at its own sequence's first
- * token (rows before it read as zeros, as at the start of a fresh sequence);
- * the L2 norms, gates and decay are per token as in gdn2_hip_layer_prologue.
- * No cached conv tails are read or written.
+ * token; the rows before it come from that sequence's cached conv tail,
+ * conv_in [nseq, C, conv_k - 1] (NULL: zeros, a fresh sequence). conv_out
+ * [nseq, C, conv_k - 1] (NULL: not written; distinct from conv_in) receives
+ * every sequence's new tail, the last conv_k - 1 conv inputs, earlier entries
+ * coming from its old tail (an empty sequence keeps its tail). The L2 norms,
+ * gates and decay are per token as in gdn2_hip_layer_prologue.
  * Replaces: the same ops as gdn2_hip_layer_prologue for
  * GatedDeltaNet2.forward(..., cu_seqlens=...) (gdn2/attention.py:299-358), whose
  * cu_seqlens the reference's op rejects.
@@ -170,10 +173,10 @@ int gdn2_hip_layer_prologue(const void* xq, const void* xk, const void* xv, cons
 int gdn2_hip_layer_prologue_varlen(const void* xq, const void* xk, const void* xv, const void* xb,
                                    const void* xw, const void* xf, long ld_q, long ld_k, long ld_v,
                                    long ld_b, long ld_w, long ld_f, int act_dtype, const void* conv_w,
-                                   const void* conv_b, int conv_k, const float* a_log, const float* dt_bias,
-                                   float erase_scale, void* q, void* k, void* v, void* b, void* w, float* g,
-                                   const int* cu_seqlens, int nseq, long T, int H, int HK, int DK, int DV,
-                                   void* stream);
+                                   const void* conv_b, int conv_k, const void* conv_in, void* conv_out,
+                                   const float* a_log, const float* dt_bias, float erase_scale, void* q, void* k,
+                                   void* v, void* b, void* w, float* g, const int* cu_seqlens, int nseq, long T,
+                                   int H, int HK, int DK, int DV, void* stream);
 
 /*
  * Few-row linear layer y = x W^T: x [M, K] (row stride ldx), W [N, K] (the

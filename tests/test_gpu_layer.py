@@ -105,8 +105,59 @@ def test_layer_forward_packed_sequences(dtype, tol, ptol, DK, H, HK, conv):
                 assert rel_err(tp[:, a:e].float().cpu(), ta.float().cpu()) < ptol, (i, name)
             ref, _ = layer(xi)
             assert rel_err(out[:, a:e].float().cpu(), ref.float().cpu()) < tol, i
-    with pytest.raises(NotImplementedError, match="cache"):
-        layer(x, cu_seqlens=cu, use_cache=True)
+
+
+@pytest.mark.parametrize("conv", [4, 2, 0])
+@pytest.mark.parametrize("mode", ["prefill", "forward"])
+def test_layer_packed_prefill_cache_then_decode(conv, mode):
+    """Packed prompts with a cache, against each sequence run alone:
+    prefill(x, cache, cu_seqlens=...) continues every sequence from its own
+    cached state and conv tail (an empty sequence keeps both);
+    forward(x, cache, use_cache=True, cu_seqlens=...) continues the states with
+    a fresh conv, as the dense forward does. Both return one state and one conv
+    tail per sequence, and a batched decode from that cache equals the
+    per-sequence decodes. fp32, so the comparison is at the op's parity bar."""
+    torch.manual_seed(0)
+    cfg = GatedDeltaNet2Config(hidden_size=256, num_heads=4, num_kv_heads=2, head_dim_k=64, head_dim_v=64,
+                               conv_size=conv)
+    layer = GatedDeltaNet2(cfg).cuda().eval()
+    pre = [9, 70, 2, 30]                     # earlier segments, one per sequence
+    lens = [5, 0, 67, 1]                     # the packed segment (one empty, one shorter than the window)
+    N = len(lens)
+    print(f"layer packed cache conv={conv} pre={pre} lens={lens}", flush=True)
+    cu = torch.tensor([0] + torch.cumsum(torch.tensor(lens), 0).tolist(), dtype=torch.int32)
+    xs_pre = [torch.randn(1, n, 256, device="cuda") for n in pre]
+    x = torch.randn(1, int(cu[-1]), 256, device="cuda")
+    x_dec = torch.randn(N, 3, 256, device="cuda")
+    with torch.no_grad():
+        caches = [layer.prefill(xp)[1] for xp in xs_pre]
+        cache = type(caches[0])(torch.cat([c.recurrent_state for c in caches]),
+                                None if conv == 0 else torch.cat([c.conv_state for c in caches]))
+        if mode == "prefill":
+            out, cache2 = layer.prefill(x, cache, cu_seqlens=cu)
+        else:
+            out, cache2 = layer(x, cache, use_cache=True, cu_seqlens=cu)
+        assert cache2.recurrent_state.shape[0] == N
+        st2 = cache2.recurrent_state.clone()           # decode advances the cache
+        cv2 = None if cache2.conv_state is None else cache2.conv_state.clone()
+        dec, _ = layer.decode(x_dec, cache2)
+        for i in range(N):
+            a, e = int(cu[i]), int(cu[i + 1])
+            ci = caches[i]
+            if mode == "prefill":
+                ci = type(ci)(ci.recurrent_state.clone(), None if ci.conv_state is None else ci.conv_state.clone())
+                if e > a:
+                    oi, ci = layer.prefill(x[:, a:e].contiguous(), ci)
+                    assert rel_err(out[:, a:e].cpu(), oi.cpu()) < 2e-3, i
+            else:
+                oi, ci = layer(x[:, a:e].contiguous(), ci, use_cache=True)
+                if e > a:
+                    assert rel_err(out[:, a:e].cpu(), oi.cpu()) < 2e-3, i
+            assert rel_err(st2[i:i + 1].cpu(), ci.recurrent_state.cpu()) < 2e-3, i
+            if conv:
+                assert rel_err(cv2[i:i + 1].cpu(), ci.conv_state.cpu()) < 1e-5, i
+            di, _ = layer.decode(x_dec[i:i + 1], ci)
+            assert rel_err(dec[i:i + 1].cpu(), di.cpu()) < 2e-3, i
 
 
 @pytest.mark.parametrize("DV,ld_pad", [(32, 0), (128, 0), (512, 0), (96, 8), (36, 0), (520, 0), (128, 3)])
