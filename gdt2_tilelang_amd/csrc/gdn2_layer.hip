@@ -186,9 +186,13 @@ __global__ __launch_bounds__(kProThreads) void prologue_kernel(ProArgs a) {
             float xin = win[t + jj][e];
             if constexpr (VL) {
               const long p = t0 - K1 + t + jj;       // before its sequence: cached tail entry or zero
-              if (p < sstart[t])
-                xin = a.conv_in ? ld<DT>(a.conv_in, (static_cast<long>(sseq[t]) * C + c0 + e) * K1 + (p - sstart[t] + K1))
-                                : 0.f;
+              if (p < sstart[t]) {
+                // tail entry p - start + K1, in [0, K1) for well-formed offsets
+                // (bounded here so that malformed ones cannot read outside conv_in)
+                const long ti = p - sstart[t] + K1;
+                xin = (a.conv_in && ti >= 0) ? ld<DT>(a.conv_in, (static_cast<long>(sseq[t]) * C + c0 + e) * K1 + ti)
+                                             : 0.f;
+              }
             }
             acc += wflat[e * K + jj] * xin;
           }
