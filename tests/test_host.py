@@ -78,6 +78,28 @@ def test_c_abi_rejects_bad_arguments_before_launch():
                                      64, nul) == -1
     assert lib.gdn2_hip_prefill_chunks(*args, 1, nul, fake, fake, 1, nul, 1, 1, 1, 128, 128, 64, 0, 64,
                                        0.1, nul) == -1
+    # packed sequences: offsets required, at least one sequence, the prefill shapes
+    #                                   dt  cu    N  s_in s_out o  odt  ws   H  HK  DK   DV   T
+    assert lib.gdn2_hip_prefill_varlen(*args, 1, nul, 2, nul, fake, fake, 1, fake, 2, 2, 128, 128, 100, 0.1,
+                                       nul) == -1
+    assert lib.gdn2_hip_prefill_varlen(*args, 1, fake, 0, nul, fake, fake, 1, fake, 2, 2, 128, 128, 100, 0.1,
+                                       nul) == -1
+    assert lib.gdn2_hip_prefill_varlen(*args, 1, fake, 2, nul, fake, fake, 1, fake, 2, 2, 32, 128, 100, 0.1,
+                                       nul) == -2
+    assert lib.gdn2_hip_prefill_varlen(*args, 1, fake, 2, nul, fake, fake, 1, fake, 2, 2, 128, 24, 100, 0.1,
+                                       nul) == -2
+    assert lib.gdn2_hip_prefill_varlen(*args, 1, fake, 2, nul, fake, fake, 1, fake, 6, 4, 128, 128, 100, 0.1,
+                                       nul) == -1
+    # ceil(T / 64) + nseq record slots per key head
+    assert (lib.gdn2_hip_prefill_varlen_workspace_bytes(3, 2, 128, 100)
+            == lib.gdn2_hip_prefill_workspace_bytes(1, 2, 128, 64 * (2 + 3)))
+    assert lib.gdn2_hip_prefill_varlen_workspace_bytes(0, 2, 128, 100) == 0
+    lds = [256] * 6
+    #                                               x*6    ld*6  dt conv_w conv_b K cin  cout a_log dtb  es
+    assert lib.gdn2_hip_layer_prologue_varlen(*args, *lds, 1, fake, nul, 4, nul, nul, fake, fake, 1.0,
+                                              *args, nul, 2, 100, 2, 2, 64, 64, nul) == -1   # no offsets
+    assert lib.gdn2_hip_layer_prologue_varlen(*args, *lds, 1, fake, nul, 4, nul, nul, fake, fake, 1.0,
+                                              *args, fake, 0, 100, 2, 2, 64, 64, nul) == -1  # no sequence
 
 
 def test_backend_policy():
