@@ -112,6 +112,31 @@ def bench_prefill(steps, warmup):
     return ms_step, cl, sc
 
 
+def bench_public_prefill(reps=20):
+    """Config 1 through the public ``gdn2_prefill`` (Python checks, the
+    workspace and outputs from torch's caching allocator, both kernels), as a
+    caller of the package sees it; the headline times the C ABI pair on
+    preallocated buffers."""
+    from gdt2_tilelang_amd import gdn2_prefill
+
+    sets = [cfg_inputs(B1, S1, H1, D1, D1, seed=s) for s in (11, 12)]
+    for i in range(3):
+        gdn2_prefill(*sets[i % 2])
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    t0 = time.perf_counter()
+    e0.record()
+    for i in range(reps):
+        gdn2_prefill(*sets[i % 2])
+    e1.record()
+    torch.cuda.synchronize()
+    wall = (time.perf_counter() - t0) / reps * 1e3
+    ms = e0.elapsed_time(e1) / reps
+    return {"entry": "gdn2_prefill(q, k, v, g, b, w) at config 1, bf16 o, fp32 state",
+            "ms_per_call": round(ms, 5), "host_wall_ms_per_call": round(wall, 5),
+            "tokens_per_s": round(B1 * S1 / (ms * 1e-3), 1)}
+
+
 def bench_varlen(reps=20, nseq=16):
     """Config 1's 8192 tokens packed as nseq sequences of seeded random lengths
     (one gdn2_hip_prefill_varlen call: one chunk-local and one scan launch),
@@ -257,35 +282,120 @@ def bench_layer(reps=3):
 
     run()
     pf, dc = min(run() for _ in range(reps))
+
+    # the same 128 step() calls captured once in a HIP graph and replayed: the
+    # GPU time of a step without the per-call host work (Python, ctypes, launches)
+    cache = None
+    for lo, hi in zip(bounds[:-1], bounds[1:]):
+        _, cache = layer.prefill(x[:, lo:hi], cache)
+    xs = x[:, S:S + steps].clone()
+    for t in range(3):                                  # warm the allocator and caches outside the capture
+        layer.step(xs[:, t], cache)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        for t in range(steps):
+            layer.step(xs[:, t], cache)
+    graph.replay()
+    torch.cuda.synchronize()
+    g0, g1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    g0.record()
+    for _ in range(reps):
+        graph.replay()
+    g1.record()
+    torch.cuda.synchronize()
+    dg = g0.elapsed_time(g1) / reps
     return dict(workload="GatedDeltaNet2 layer, BASELINE config 4: hidden 2048, H=16 HK=8 DK=DV=128, "
                          "bf16, B=1, 32700-token prompt in 4 segments then 128 step() calls",
                 prefill_ms=round(pf, 3), prefill_tokens_per_s=round(S / (pf * 1e-3), 1),
                 decode_ms_128_steps=round(dc, 3), decode_steps_per_s=round(steps / (dc * 1e-3), 1),
+                decode_graph_ms_128_steps=round(dg, 3), decode_graph_steps_per_s=round(steps / (dg * 1e-3), 1),
+                decode_graph_timing="the 128 step() calls captured in one HIP graph, replayed %d times" % reps,
                 timing="eager Python calls, HIP events, best of %d" % reps)
 
 
-def cpu_baseline(budget_s=12.0):
-    """The oracle's chunkwise torch path (reference gdn2/reference.py:168-261)
-    on the host cores, over repeated full config-1 prefills."""
+def cpu_model():
+    """The host CPU's model string (``/proc/cpuinfo``), or the platform's."""
+    try:
+        with open("/proc/cpuinfo") as f:
+            for line in f:
+                if line.startswith("model name"):
+                    return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return platform.processor() or "host CPU"
+
+
+def _timed(fn, budget_s, max_reps):
+    """(reps, seconds): run fn until budget_s is spent or max_reps reached."""
+    reps, t0 = 0, time.perf_counter()
+    while True:
+        fn()
+        reps += 1
+        el = time.perf_counter() - t0
+        if el > budget_s or reps >= max_reps:
+            return reps, el
+
+
+def cpu_baseline(budget_s=8.0):
+    """The oracle's restatements of the reference's torch paths on the host
+    cores, one bounded sample per BASELINE config (kind "port": the
+    reference's Python does not travel to the GPU box):
+
+    * config 1: the chunkwise torch form (reference gdn2/reference.py:168-261)
+      on full config-1 prefills -- the headline comparison;
+    * configs 2 and 3: the per-token torch decode loop
+      (reference gdn2/inference.py:337-345) on the full-size batch;
+    * config 4: the torch layer (reference gdn2/attention.py:360-479) on a
+      2048-token prompt segment and 16 single-token decode calls.
+    """
     sys.path.insert(0, os.path.dirname(os.path.abspath(__file__)))
+    import oracle
     from oracle import chunk_gdn2
 
     threads = os.cpu_count() or 1
     torch.set_num_threads(threads)
-    q, k, v, g, b, w = cfg_inputs(B1, S1, H1, D1, D1, seed=11, device="cpu")
-    ins = tuple(t.float() for t in (q, k, v)) + (g,) + tuple(t.float() for t in (b, w))
+    cpu = cpu_model()
+
+    def f32(ins):
+        q, k, v, g, b, w = ins
+        return tuple(t.float() for t in (q, k, v)) + (g,) + tuple(t.float() for t in (b, w))
+
+    ins = f32(cfg_inputs(B1, S1, H1, D1, D1, seed=11, device="cpu"))
     chunk_gdn2(*(t[:, :256] for t in ins))          # warm-up
-    reps, t_start = 0, time.perf_counter()
-    while True:
-        chunk_gdn2(*ins, output_final_state=True)
-        reps += 1
-        el = time.perf_counter() - t_start
-        if el > budget_s or reps >= 20:
-            break
-    tps = reps * B1 * S1 / el
-    return {"value": round(tps, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
-            "sample": f"{reps} full config-1 prefills (B=2 S=4096 H=16 D=128, fp32 torch "
-                      f"chunkwise oracle) in {el:.1f} s on {platform.processor() or 'host CPU'}"}
+    reps, el = _timed(lambda: chunk_gdn2(*ins, output_final_state=True), budget_s, 20)
+    out = {"value": round(reps * B1 * S1 / el, 1), "unit": "tokens/s", "cores": threads, "kind": "port",
+           "cpu_model": cpu,
+           "sample": f"{reps} full config-1 prefills (B=2 S=4096 H=16 D=128, fp32 torch chunkwise "
+                     f"oracle) in {el:.1f} s on {threads} threads of {cpu}"}
+    per = {}
+    for name, B, n in (("config2_decode_step", 64, 1), ("config3_decode_multi_n8", 32, 8)):
+        tok = f32(cfg_inputs(B, n, H1, D1, D1, seed=100, device="cpu"))
+        st = torch.randn(B, H1, D1, D1, generator=torch.Generator().manual_seed(5)) * 0.1
+        oracle.decode_loop(*tok, st, None)
+        reps, el = _timed(lambda: oracle.decode_loop(*tok, st, None), budget_s / 3, 400)
+        us = el / reps * 1e6
+        gbs = 2 * B * H1 * D1 * D1 * 4 / (us * 1e-6) / 1e9
+        per[name] = {"us_per_call": round(us, 1), "state_GBps": round(gbs, 2),
+                     "tokens_per_s": round(B * n / (us * 1e-6), 1),
+                     "sample": f"{reps} calls of the fp32 torch per-token decode loop, B={B} n={n} H=16 D=128"}
+    from gdt2_tilelang_amd import GatedDeltaNet2, GatedDeltaNet2Config
+    torch.manual_seed(0)
+    cfg = GatedDeltaNet2Config(hidden_size=2048, num_heads=16, num_kv_heads=8, head_dim_k=128, head_dim_v=128)
+    ref = oracle.LayerOracle(GatedDeltaNet2(cfg).state_dict(), 2048, 16, 8, 128, 128)
+    x = torch.randn(1, 2048 + 16, 2048, generator=torch.Generator().manual_seed(1))
+    t0 = time.perf_counter()
+    _, cache = ref.prefill(x[:, :2048])
+    t_pf = time.perf_counter() - t0
+    t0 = time.perf_counter()
+    for i in range(16):
+        ref.decode(x[:, 2048 + i:2049 + i], cache)
+    t_dc = time.perf_counter() - t0
+    per["config4_layer"] = {"prefill_tokens_per_s": round(2048 / t_pf, 1), "decode_steps_per_s": round(16 / t_dc, 1),
+                            "sample": "fp32 torch layer (hidden 2048, H=16 HK=8, D=128, B=1): one 2048-token "
+                                      f"prompt segment in {t_pf:.2f} s, 16 one-token decode calls in {t_dc:.2f} s"}
+    out["configs"] = per
+    return out
 
 
 def read_traffic():
@@ -405,6 +515,7 @@ def main():
             "config2_decode_step": bench_decode(64, 1, calls=64, steps_per_buf_min=1),
             "config3_decode_multi_n8": bench_decode(32, 8, calls=64, steps_per_buf_min=1),
         }
+    out["public_prefill"] = bench_public_prefill()
     if not args.no_varlen:
         out["varlen"] = bench_varlen()
     if not args.no_layer:

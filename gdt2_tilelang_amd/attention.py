@@ -320,6 +320,8 @@ class GatedDeltaNet2(nn.Module):
 
     def _finish_gpu(self, x, o, proj):
         B, S, _ = x.shape
+        if B * S == 0:
+            return x.new_empty(B, S, self.cfg.hidden_size)
         H, DV = self.num_heads, self.head_dim_v
         dqk, dv = self.num_kv_heads * self.head_dim_k, H * DV
         ld = proj.shape[1]

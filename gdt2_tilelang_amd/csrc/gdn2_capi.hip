@@ -162,9 +162,12 @@ static int layer_prologue(const void* xq, const void* xk, const void* xv, const 
                           const float* a_log, const float* dt_bias, float erase_scale, void* q,
                           void* k, void* v, void* b, void* w, float* g, int B, long S, int H,
                           int HK, int DK, int DV, const int* cu_seqlens, int nseq, void* stream) {
-  if (!xq || !xk || !xv || !xb || !xw || !xf || !a_log || !dt_bias) return GDN2_ERR_ARG;
-  if (!q || !k || !v || !b || !w || !g) return GDN2_ERR_ARG;
   if (!dtype_ok(act_dtype) || B < 0 || S < 0 || H < 1 || HK < 1 || H % HK || DV < 1) return GDN2_ERR_ARG;
+  // with no tokens nothing is read from the token buffers (they may be null);
+  // only a packed batch's conv tails are written
+  const bool tokens = static_cast<long>(B) * S > 0;
+  if (tokens && (!xq || !xk || !xv || !xb || !xw || !xf || !a_log || !dt_bias)) return GDN2_ERR_ARG;
+  if (tokens && (!q || !k || !v || !b || !w || !g)) return GDN2_ERR_ARG;
   const int dqk = HK * DK, dv = H * DV;
   if (ld_q < dqk || ld_k < dqk || ld_b < dqk || ld_f < dqk || ld_v < dv || ld_w < dv) return GDN2_ERR_ARG;
   // 8-channel lane items: DK / 8 lanes per q, k head, a power of two <= 64
@@ -173,10 +176,10 @@ static int layer_prologue(const void* xq, const void* xk, const void* xv, const 
   const long lds[6] = {ld_q, ld_k, ld_v, ld_b, ld_w, ld_f};
   const void* xs[6] = {xq, xk, xv, xb, xw, xf};
   for (int i = 0; i < 6; ++i)
-    if (lds[i] % 8 || reinterpret_cast<uintptr_t>(xs[i]) % 16) return GDN2_ERR_ARG;
+    if (lds[i] % 8 || (tokens && reinterpret_cast<uintptr_t>(xs[i]) % 16)) return GDN2_ERR_ARG;
   const void* outs[6] = {q, k, v, b, w, g};
   for (int i = 0; i < 6; ++i)
-    if (reinterpret_cast<uintptr_t>(outs[i]) % 16) return GDN2_ERR_ARG;
+    if (tokens && reinterpret_cast<uintptr_t>(outs[i]) % 16) return GDN2_ERR_ARG;
   if (conv_w && (conv_k < 1 || conv_k > 4)) return GDN2_ERR_SHAPE;
   const void* cv[4] = {conv_w, conv_b, conv_in, conv_out};   // read / written as 16-byte vectors
   for (int i = 0; i < 4; ++i)
@@ -279,7 +282,21 @@ int gdn2_hip_layer_decode(const void* x, const void* w_proj, const void* conv_w,
   if (!x || !w_proj || !w_out || !out || !workspace || !state || !norm_w) return GDN2_ERR_ARG;
   if (B < 1 || n < 1 || hidden < 1 || H < 1 || HK < 1 || H % HK || !dtype_ok(dtype)) return GDN2_ERR_ARG;
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return GDN2_ERR_ARG;
-  const int M = B * n;
+  // Every stage's shape and alignment rule is checked before the first launch,
+  // so the call either runs all five stages or changes nothing.
+  const long Ml = static_cast<long>(B) * n;
+  if (Ml > 8) return GDN2_ERR_SHAPE;                                      // GEMV rows
+  if (DK != 32 && DK != 64 && DK != 128 && DK != 256) return GDN2_ERR_SHAPE;   // decode
+  if (DV % 32 || DV > 4096 || hidden % 8) return GDN2_ERR_SHAPE;           // decode, GEMV K
+  const auto mis16 = [](const void* p) { return (reinterpret_cast<uintptr_t>(p) & 15) != 0; };
+  if (mis16(x) || mis16(w_proj) || mis16(w_out) || mis16(norm_w)) return GDN2_ERR_ARG;
+  if (conv_w) {
+    if (conv_k < 1 || conv_k > 4) return GDN2_ERR_SHAPE;
+    if (mis16(conv_w) || mis16(conv_b) || mis16(conv_in) || mis16(conv_out)) return GDN2_ERR_ARG;
+    if (conv_out && conv_out == conv_in) return GDN2_ERR_ARG;
+  }
+  if (!a_log || !dt_bias) return GDN2_ERR_ARG;
+  const int M = static_cast<int>(Ml);
   const long dqk = static_cast<long>(HK) * DK, dv = static_cast<long>(H) * DV;
   const long ldp = 4 * dqk + 3 * dv;
   const DecodeWs s = decode_ws(M, H, HK, DK, DV, dtype);

@@ -383,43 +383,60 @@ __global__ __launch_bounds__(kThreads) void epilogue8_kernel(const void* __restr
 
 }  // namespace lay
 
+namespace {
+// the new per-sequence conv tails of a packed batch (K - 1 inputs per channel)
+template <int DT>
+void launch_conv_tail(const lay::ProArgs& a, int kc, hipStream_t stream) {
+  const long tail_items = static_cast<long>(a.nseq) * ((2L * a.HK * a.DK + a.H * a.DV) / 8);
+  const dim3 grid(static_cast<unsigned>((tail_items + lay::kThreads - 1) / lay::kThreads));
+  switch (kc) {
+    case 2: hipLaunchKernelGGL((lay::conv_tail_varlen_kernel<DT, 1>), grid, dim3(lay::kThreads), 0, stream, a); break;
+    case 3: hipLaunchKernelGGL((lay::conv_tail_varlen_kernel<DT, 2>), grid, dim3(lay::kThreads), 0, stream, a); break;
+    case 4: hipLaunchKernelGGL((lay::conv_tail_varlen_kernel<DT, 3>), grid, dim3(lay::kThreads), 0, stream, a); break;
+    default: break;
+  }
+}
+}  // namespace
+
 hipError_t launch_layer_prologue(const lay::ProArgs& a, int act_dt, hipStream_t stream) {
-  if (a.B == 0 || a.S == 0) return hipSuccess;
-  // conv items (q, k, v channels) plus gate items (b, w, f channels), both 2*HK*DK + H*DV wide
-  const long items = 2 * ((2L * a.HK * a.DK + a.H * a.DV) / 8);
-  const dim3 grid(static_cast<unsigned>((a.S + lay::TT - 1) / lay::TT),
-                  static_cast<unsigned>((items + lay::kProThreads - 1) / lay::kProThreads), static_cast<unsigned>(a.B));
+  if (a.B == 0) return hipSuccess;
+  if (act_dt != DT_BF16 && act_dt != DT_F16 && act_dt != DT_F32) return hipErrorInvalidValue;
   const int kc = a.conv_w ? a.K : 0;
   if (kc < 0 || kc > lay::kMaxConv) return hipErrorInvalidValue;
   const bool vl = a.cu != nullptr && kc > 0;
-  // packed batch with a cache: the new per-sequence conv tails
-  const long tail_items = static_cast<long>(a.nseq) * ((2L * a.HK * a.DK + a.H * a.DV) / 8);
-  const dim3 tail_grid(static_cast<unsigned>((tail_items + lay::kThreads - 1) / lay::kThreads));
-#define GDN2_PRO_K(DTV, KV)                                                                             \
-  if (vl) {                                                                                             \
-    hipLaunchKernelGGL((lay::prologue_kernel<DTV, KV, true>), grid, dim3(lay::kProThreads), 0, stream, a); \
-    if (KV > 1 && a.conv_out)                                                                           \
-      hipLaunchKernelGGL((lay::conv_tail_varlen_kernel<DTV, (KV > 1 ? KV - 1 : 1)>), tail_grid,         \
-                         dim3(lay::kThreads), 0, stream, a);                                             \
-  } else {                                                                                              \
-    hipLaunchKernelGGL((lay::prologue_kernel<DTV, KV, false>), grid, dim3(lay::kProThreads), 0, stream, a); \
-  }                                                                                                     \
-  break;
-#define GDN2_PRO(DTV)                                                                                   \
-  if (act_dt == DTV) {                                                                                  \
-    switch (kc) {                                                                                       \
-      case 0: hipLaunchKernelGGL((lay::prologue_kernel<DTV, 0, false>), grid, dim3(lay::kProThreads), 0, stream, a); break; \
-      case 1: GDN2_PRO_K(DTV, 1)                                                                        \
-      case 2: GDN2_PRO_K(DTV, 2)                                                                        \
-      case 3: GDN2_PRO_K(DTV, 3)                                                                        \
-      default: GDN2_PRO_K(DTV, 4)                                                                       \
-    }                                                                                                   \
-    return hipGetLastError();                                                                           \
-  }
-  GDN2_PRO(DT_BF16) GDN2_PRO(DT_F16) GDN2_PRO(DT_F32)
+  const bool tails = vl && kc > 1 && a.conv_out != nullptr;
+  if (a.S > 0) {
+    // conv items (q, k, v channels) plus gate items (b, w, f channels), both 2*HK*DK + H*DV wide
+    const long items = 2 * ((2L * a.HK * a.DK + a.H * a.DV) / 8);
+    const dim3 grid(static_cast<unsigned>((a.S + lay::TT - 1) / lay::TT),
+                    static_cast<unsigned>((items + lay::kProThreads - 1) / lay::kProThreads),
+                    static_cast<unsigned>(a.B));
+#define GDN2_PRO_K(DTV, KV)                                                                                  \
+    if (vl) hipLaunchKernelGGL((lay::prologue_kernel<DTV, KV, true>), grid, dim3(lay::kProThreads), 0, stream, a); \
+    else hipLaunchKernelGGL((lay::prologue_kernel<DTV, KV, false>), grid, dim3(lay::kProThreads), 0, stream, a);   \
+    break;
+#define GDN2_PRO(DTV)                                                                                        \
+    if (act_dt == DTV) {                                                                                     \
+      switch (kc) {                                                                                          \
+        case 0: hipLaunchKernelGGL((lay::prologue_kernel<DTV, 0, false>), grid, dim3(lay::kProThreads), 0, stream, a); break; \
+        case 1: GDN2_PRO_K(DTV, 1)                                                                           \
+        case 2: GDN2_PRO_K(DTV, 2)                                                                           \
+        case 3: GDN2_PRO_K(DTV, 3)                                                                           \
+        default: GDN2_PRO_K(DTV, 4)                                                                          \
+      }                                                                                                      \
+    }
+    GDN2_PRO(DT_BF16) GDN2_PRO(DT_F16) GDN2_PRO(DT_F32)
 #undef GDN2_PRO
 #undef GDN2_PRO_K
-  return hipErrorInvalidValue;
+  }
+  // a packed batch with a cache writes each sequence's new tail; with no
+  // tokens at all every sequence keeps (copies through) its cached one
+  if (tails) {
+    if (act_dt == DT_BF16) launch_conv_tail<DT_BF16>(a, kc, stream);
+    else if (act_dt == DT_F16) launch_conv_tail<DT_F16>(a, kc, stream);
+    else launch_conv_tail<DT_F32>(a, kc, stream);
+  }
+  return hipGetLastError();
 }
 
 hipError_t launch_layer_epilogue(const void* o, int o_dt, const void* gate, long ld_gate, const float* weight,

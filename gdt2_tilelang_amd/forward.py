@@ -42,7 +42,8 @@ def chunk_gdn2_fwd(q, k, v, g, b, w, scale, initial_state=None, output_final_sta
     (q, k, v, g, b, w), s_alloc = _token_layout((q, k, v, g.float(), b, w))
     if initial_state is not None:
         _require_device(q, initial_state)
-        initial_state = initial_state.to(torch.float32).contiguous()
+        # the reference casts to config.state_dtype first (forward.py:874-877)
+        initial_state = initial_state.to(config.state_dtype).to(torch.float32).contiguous()
     final = torch.empty(B, H, DK, DV, dtype=torch.float32, device=dev)
     o = torch.empty(B, S, H, DV, dtype=config.output_dtype or q.dtype, device=dev)
     if S:
@@ -51,6 +52,8 @@ def chunk_gdn2_fwd(q, k, v, g, b, w, scale, initial_state=None, output_final_sta
         final.copy_(initial_state)
     else:
         final.zero_()
+    if config.state_dtype != torch.float32:
+        final = final.to(config.state_dtype)
     return o, (final if output_final_state else None)
 
 
@@ -85,7 +88,7 @@ def chunk_gdn2_varlen_fwd(q, k, v, g, b, w, scale, cu_seqlens, initial_state=Non
         initial_state: ``[N, H, DK, DV]`` or ``None`` (zeros); never modified.
 
     Returns:
-        ``(o [1, T, H, DV], final_state [N, H, DK, DV] fp32 or None)``. Both
+        ``(o [1, T, H, DV], final_state [N, H, DK, DV] in config.state_dtype or None)``. Both
         kernels run once for the whole batch; sequence i's result equals a
         separate call on its tokens alone.
     """
@@ -105,15 +108,16 @@ def chunk_gdn2_varlen_fwd(q, k, v, g, b, w, scale, cu_seqlens, initial_state=Non
         _require_device(q, initial_state)
         if tuple(initial_state.shape) != (N, H, DK, DV):
             raise ValueError(f"initial_state has shape {tuple(initial_state.shape)}, expected {(N, H, DK, DV)}")
-        initial_state = initial_state.to(torch.float32).contiguous()
+        initial_state = initial_state.to(config.state_dtype).to(torch.float32).contiguous()
     final = torch.empty(N, H, DK, DV, dtype=torch.float32, device=dev)
     o = torch.empty(1, T, H, DV, dtype=config.output_dtype or q.dtype, device=dev)
+    st_dt = config.state_dtype
     if T == 0:                          # every sequence empty: the states pass through
         if initial_state is not None:
             final.copy_(initial_state)
         else:
             final.zero_()
-        return o, (final if output_final_state else None)
+        return o, (final.to(st_dt) if output_final_state else None)
     lib = _hip.lib()
     ws = torch.empty(lib.gdn2_hip_prefill_varlen_workspace_bytes(N, HK, DK, T), dtype=torch.uint8, device=dev)
     _hip.check(lib.gdn2_hip_prefill_varlen(
@@ -121,7 +125,7 @@ def chunk_gdn2_varlen_fwd(q, k, v, g, b, w, scale, cu_seqlens, initial_state=Non
         _hip.dtype_code(q.dtype), _hip.ptr(cu), N, _hip.ptr(initial_state), _hip.ptr(final), _hip.ptr(o),
         _hip.dtype_code(o.dtype), _hip.ptr(ws), H, HK, DK, DV, T, float(scale),
         _hip.stream_of(dev)), "gdn2_hip_prefill_varlen")
-    return o, (final if output_final_state else None)
+    return o, (final.to(st_dt) if output_final_state else None)
 
 
 def chunk_gdn2_bwd(*args, **kwargs):

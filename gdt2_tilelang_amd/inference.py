@@ -32,7 +32,7 @@ import torch
 from . import _hip
 from .config import DEFAULT_KERNEL_CONFIG, GDN2Config
 
-__all__ = ["gdn2_prefill", "gdn2_decode", "gdn2_decode_step"]
+__all__ = ["gdn2_prefill", "gdn2_decode", "gdn2_decode_step", "check_state_dtype"]
 
 _PREFILL_DK = (64, 128)
 _DECODE_DK = (32, 64, 128, 256)
@@ -74,6 +74,16 @@ def _token_layout(ts):
     return [t if t.is_contiguous() else t.contiguous() for t in ts], ts[0].shape[1]
 
 
+_STATE_DTYPES = (torch.float32, torch.bfloat16, torch.float16)
+
+
+def check_state_dtype(dt: torch.dtype) -> None:
+    """The state dtypes the reference's kernels take (``_tl_dtype``,
+    ``gdn2/forward.py:733-745``); anything else is a ``TypeError``."""
+    if dt not in _STATE_DTYPES:
+        raise TypeError(f"unsupported state dtype {dt}; use float32, bfloat16 or float16")
+
+
 def _check_state(state, B, H, DK, DV, dev):
     if state.dtype != torch.float32:
         raise TypeError(f"the hip kernels carry an fp32 state; got {state.dtype}")
@@ -101,7 +111,10 @@ def gdn2_decode(q, k, v, g, b, w, state, scale=None):
         q, k, b: ``[B, n, HK, DK]``; v, w: ``[B, n, H, DV]`` (fp32, bf16 or fp16);
             HK == H as in the reference, or HK dividing H (grouped heads).
         g: ``[B, n, HK, DK]`` log decay (<= 0), used as fp32.
-        state: fp32 contiguous ``[B, H, DK, DV]``, mutated.
+        state: contiguous ``[B, H, DK, DV]`` (fp32, or bf16 / fp16 as the
+            reference's kernels also take), mutated. The kernel carries it in
+            fp32 across the call's tokens; a bf16 / fp16 state is rounded back
+            once at the end, as the reference's kernel stores it.
         scale: query scale; defaults to ``DK ** -0.5``.
 
     Returns:
@@ -111,7 +124,9 @@ def gdn2_decode(q, k, v, g, b, w, state, scale=None):
     _check_shapes(q, k, v, g, b, w)
     B, n, _, DK = q.shape
     H, DV = v.shape[2], v.shape[3]
-    _check_state(state, B, H, DK, DV, dev)
+    check_state_dtype(state.dtype)
+    work = state if state.dtype == torch.float32 else state.float()
+    _check_state(work, B, H, DK, DV, dev)
     if not state.is_contiguous():
         raise ValueError("state must be contiguous (it is updated in place)")
     scale = DK ** -0.5 if scale is None else scale
@@ -119,7 +134,9 @@ def gdn2_decode(q, k, v, g, b, w, state, scale=None):
     (q, k, v, g, b, w), s_alloc = _token_layout((q, k, v, g, b, w))
     o = torch.empty(B, s_alloc, H, DV, dtype=v.dtype, device=dev)
     if n:
-        _decode_into(q, k, v, g, b, w, state, o, s_alloc, 0, n, scale)
+        _decode_into(q, k, v, g, b, w, work, o, s_alloc, 0, n, scale)
+        if work is not state:
+            state.copy_(work)
     return o
 
 
@@ -157,8 +174,7 @@ def check_prefill_config(config: GDN2Config) -> None:
         raise ValueError(f"need at least 2 sub-chunks per chunk, got chunk {BS} / sub-chunk {BC}")
     if BS != 64:
         raise ValueError(f"the hip kernels are built for chunk_size 64, got {BS}")
-    if config.state_dtype != torch.float32:
-        raise TypeError(f"the hip kernels carry an fp32 state; got state_dtype {config.state_dtype}")
+    check_state_dtype(config.state_dtype)
 
 
 @torch.no_grad()
@@ -176,13 +192,15 @@ def gdn2_prefill(q, k, v, g, b, w, state=None, scale=None, config: GDN2Config = 
         q, k, b: ``[B, S, HK, DK]``; v, w: ``[B, S, H, DV]``; g: ``[B, S, HK, DK]``
             (HK == H as in the reference, or HK dividing H: grouped heads).
         state: ``[B, H, DK, DV]`` to continue from, or ``None`` for zeros. As in
-            the reference, a prompt shorter than one chunk updates an fp32
-            contiguous ``state`` in place.
+            the reference it is first cast to ``config.state_dtype``, and a
+            prompt shorter than one chunk updates that (contiguous) state in
+            place, so a state already in ``state_dtype`` is mutated.
         scale: query scale; defaults to ``DK ** -0.5``.
         config: kernel configuration (``output_dtype`` selects the dtype of o).
 
     Returns:
-        ``(o [B, S, H, DV], state [B, H, DK, DV] fp32)``.
+        ``(o [B, S, H, DV], state [B, H, DK, DV])``, the state in
+        ``config.state_dtype`` (the kernels compute in fp32 and round once).
     """
     dev = _require_device(q, k, v, g, b, w)
     _check_shapes(q, k, v, g, b, w)
@@ -194,12 +212,14 @@ def gdn2_prefill(q, k, v, g, b, w, state=None, scale=None, config: GDN2Config = 
     scale = DK ** -0.5 if scale is None else scale
     BS = config.chunk_size
     n_full = (S // BS) * BS
+    st_dt = config.state_dtype
     if state is None:
-        state = torch.zeros(B, H, DK, DV, dtype=torch.float32, device=dev)
+        state = torch.zeros(B, H, DK, DV, dtype=st_dt, device=dev)
     else:
         _require_device(q, state)
-        state = state.to(torch.float32).contiguous()
-        _check_state(state, B, H, DK, DV, dev)
+        state = state.to(st_dt).contiguous()
+    work = state if st_dt == torch.float32 else state.float()
+    _check_state(work, B, H, DK, DV, dev)
     out_dtype = config.output_dtype or v.dtype
     _hip.dtype_code(out_dtype)
     g = g.float()
@@ -208,11 +228,13 @@ def gdn2_prefill(q, k, v, g, b, w, state=None, scale=None, config: GDN2Config = 
     if n_full:
         # the ragged tail rides along as a last, partly filled chunk (its missing
         # rows read as zeros, which the chunkwise form treats as inert)
-        new_state = torch.empty_like(state)
-        _prefill_chunks(q, k, v, g, b, w, state, new_state, o, s_alloc, 0, S, scale)
-        state = new_state
+        new_state = torch.empty_like(work)
+        _prefill_chunks(q, k, v, g, b, w, work, new_state, o, s_alloc, 0, S, scale)
+        state = new_state if st_dt == torch.float32 else new_state.to(st_dt)
     elif S:
         # shorter than one chunk: the recurrence, updating state in place as the
         # reference's decode path does
-        _decode_into(q, k, v, g, b, w, state, o, s_alloc, 0, S, scale)
+        _decode_into(q, k, v, g, b, w, work, o, s_alloc, 0, S, scale)
+        if work is not state:
+            state.copy_(work)
     return o, state

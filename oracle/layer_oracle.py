@@ -50,6 +50,23 @@ class LayerOracle:
         y = F.conv1d(buf, wgt, bias, groups=wgt.shape[0]).transpose(1, 2)
         return F.silu(y), buf[..., buf.shape[-1] - (self.conv_size - 1):]
 
+    def gates(self, x):
+        """``(g, b, w)`` of ``x [B, S, hidden]`` on the key (g, b) and value (w)
+        heads: ``g = -exp(A_log) * softplus(f + dt_bias)`` (``attention.py:290-293``),
+        ``b = sigmoid(.) * erase_scale``, ``w = sigmoid(.)`` (``:401-402``)."""
+        B, S, _ = x.shape
+        f = self._lin("f_proj", x).view(B, S, self.HK, self.DK)
+        g = -self.p["A_log"].exp()[:, None] * F.softplus(f + self.p["dt_bias"])
+        b = torch.sigmoid(self._lin("b_proj", x).view(B, S, self.HK, self.DK)) * self.erase
+        w = torch.sigmoid(self._lin("w_proj", x).view(B, S, self.H, self.DV))
+        return g, b, w
+
+    def gated_norm(self, o, gate):
+        """``o * rsqrt(mean o^2 + eps) * weight * silu(gate)`` per value head
+        (``attention.py:218-229``)."""
+        o = o * torch.rsqrt(o.pow(2).mean(-1, keepdim=True) + self.eps)
+        return o * self.p["o_norm.weight"] * F.silu(gate)
+
     def init_cache(self, B):
         C = 2 * self.HK * self.DK + self.H * self.DV
         state = torch.zeros(B, self.H, self.DK, self.DV)
@@ -71,10 +88,7 @@ class LayerOracle:
         q = F.normalize(q.view(B, S, HK, DK), dim=-1)
         k = F.normalize(k.view(B, S, HK, DK), dim=-1)
         v = v.view(B, S, H, DV)
-        f = self._lin("f_proj", x).view(B, S, HK, DK)
-        g = -self.p["A_log"].exp()[:, None] * F.softplus(f + self.p["dt_bias"])
-        b = torch.sigmoid(self._lin("b_proj", x).view(B, S, HK, DK)) * self.erase
-        w = torch.sigmoid(self._lin("w_proj", x).view(B, S, H, DV))
+        g, b, w = self.gates(x)
         if self.rep > 1:
             q, k, b, g = (t.repeat_interleave(self.rep, dim=2) for t in (q, k, b, g))
         if use_decode:
@@ -82,8 +96,7 @@ class LayerOracle:
         else:
             o, cache[0] = prefill(q, k, v, g, b, w, cache[0], None, chunk_size=self.chunk)
         gate = self._lin("o_gate_proj", x).view(B, S, H, DV)
-        o = o * torch.rsqrt(o.pow(2).mean(-1, keepdim=True) + self.eps)
-        o = o * self.p["o_norm.weight"] * F.silu(gate)
+        o = self.gated_norm(o, gate)
         return self._lin("o_proj", o.reshape(B, S, H * DV))
 
     def prefill(self, x, cache=None):

@@ -74,6 +74,55 @@ def test_config4_segmented_prefill_then_decode():
     assert e_pre < 1e-2 and e_dec < 1e-2
 
 
+def test_config4_geometry_fp32_layer():
+    """Config-4 geometry (hidden 2048, 16 value heads over 8 key heads,
+    DK=DV=128, B=1) with fp32 weights, so the layer output itself is held to
+    the 2e-3 bar: a 32700-token prompt in 4 segments of 8175 tokens (each with
+    a 47-token ragged tail) against one-shot prefill, then 16 decode steps from
+    each cache; and a 700-token prompt in two ragged segments plus decode
+    against the CPU LayerOracle."""
+    print("config-4 geometry fp32 layer: 4 segments vs one-shot, and vs LayerOracle", flush=True)
+    torch.manual_seed(0)
+    cfg = GatedDeltaNet2Config(hidden_size=2048, num_heads=16, num_kv_heads=8,
+                               head_dim_k=128, head_dim_v=128)
+    layer = GatedDeltaNet2(cfg).eval()
+    ref = LayerOracle(layer.state_dict(), 2048, 16, 8, 128, 128)
+    layer = layer.cuda()
+    S, steps = 32700, 16
+    gen = torch.Generator(device="cuda").manual_seed(1)
+    x = torch.randn(1, S + steps, 2048, device="cuda", generator=gen)
+    bounds = [0, 8175, 16350, 24525, S]
+    with torch.no_grad():
+        one, c1 = layer.prefill(x[:, :S])
+        segs, c2 = [], None
+        for lo, hi in zip(bounds[:-1], bounds[1:]):
+            o, c2 = layer.prefill(x[:, lo:hi], c2)
+            segs.append(o)
+        seg = torch.cat(segs, 1)
+        d1 = torch.stack([layer.step(x[:, S + t], c1)[0] for t in range(steps)], 1)
+        d2 = torch.stack([layer.step(x[:, S + t], c2)[0] for t in range(steps)], 1)
+    torch.cuda.synchronize()
+    e_pre, e_dec = rel_err(seg, one), rel_err(d2, d1)
+    e_st = rel_err(c2.recurrent_state, c1.recurrent_state)
+    print(f"  segmented vs one-shot: prefill {e_pre:.2e} decode {e_dec:.2e} state {e_st:.2e}", flush=True)
+    assert e_pre < 2e-3 and e_dec < 2e-3 and e_st < 2e-3
+    xs = x[:, :716].cpu()
+    with torch.no_grad():
+        a, cg = layer.prefill(x[:, :333])
+        b_, cg = layer.prefill(x[:, 333:700], cg)
+        c_, cg = layer.decode(x[:, 700:708], cg)
+        d_ = torch.stack([layer.step(x[:, t], cg)[0] for t in range(708, 716)], 1)
+    torch.cuda.synchronize()
+    r1, rc = ref.prefill(xs[:, :333])
+    r2, rc = ref.prefill(xs[:, 333:700], rc)
+    r3, rc = ref.decode(xs[:, 700:708], rc)
+    r4, rc = ref.decode(xs[:, 708:716], rc)
+    e_o = rel_err(torch.cat([a, b_, c_, d_], 1).cpu(), torch.cat([r1, r2, r3, r4], 1))
+    e_s = rel_err(cg.recurrent_state.cpu(), rc[0])
+    print(f"  vs LayerOracle: o {e_o:.2e} state {e_s:.2e}", flush=True)
+    assert e_o < 2e-3 and e_s < 2e-3
+
+
 @pytest.mark.parametrize("dtype,tol,ptol", [(torch.float32, 2e-3, 1e-5), (torch.bfloat16, 2e-2, 1.6e-2)])
 @pytest.mark.parametrize("DK,H,HK,conv", [(64, 4, 2, 4), (128, 2, 2, 3), (64, 4, 4, 0)])
 def test_layer_forward_packed_sequences(dtype, tol, ptol, DK, H, HK, conv):
@@ -274,3 +323,30 @@ def test_fused_decode_call_matches_stagewise(dtype, tol, B, n, conv):
         assert rel_err(cache.conv_state.float().cpu(), conv_out.float().cpu()) < tol
     else:
         assert cache.conv_state is None and conv_out is None
+
+
+@pytest.mark.parametrize("conv", [4, 0])
+def test_layer_packed_all_empty(conv):
+    """A packed batch whose sequences are all empty (cu = [0, 0, 0]): prefill
+    keeps every cached state and conv tail; forward(use_cache=True) keeps the
+    states and returns fresh (zero) conv tails; both return an empty output."""
+    print(f"layer packed all-empty conv={conv}", flush=True)
+    torch.manual_seed(0)
+    cfg = GatedDeltaNet2Config(hidden_size=256, num_heads=4, num_kv_heads=2, head_dim_k=64, head_dim_v=64,
+                               conv_size=conv)
+    layer = GatedDeltaNet2(cfg).cuda().eval()
+    cu = torch.tensor([0, 0, 0], dtype=torch.int32)
+    with torch.no_grad():
+        c0 = [layer.prefill(torch.randn(1, n, 256, device="cuda"))[1] for n in (70, 5)]
+        cache = type(c0[0])(torch.cat([c.recurrent_state for c in c0]),
+                            None if conv == 0 else torch.cat([c.conv_state for c in c0]))
+        x = torch.randn(1, 0, 256, device="cuda")
+        out, c1 = layer.prefill(x, cache, cu_seqlens=cu)
+        out2, c2 = layer(x, cache, use_cache=True, cu_seqlens=cu)
+    torch.cuda.synchronize()
+    assert out.shape == (1, 0, 256) and out2.shape == (1, 0, 256)
+    assert torch.equal(c1.recurrent_state, cache.recurrent_state)
+    assert torch.equal(c2.recurrent_state, cache.recurrent_state)
+    if conv:
+        assert torch.equal(c1.conv_state, cache.conv_state)
+        assert c2.conv_state.shape == cache.conv_state.shape and not c2.conv_state.any()

@@ -11,17 +11,22 @@ them, so input quantisation is not counted as error.
 
 from __future__ import annotations
 
+import os
+
+import numpy as np
 import pytest
 import torch
 
 import oracle
-from gdt2_tilelang_amd import GDN2Config, chunk_gdn2_fwd, gdn2_attention, gdn2_prefill
+from gdt2_tilelang_amd import GDN2Config, chunk_gdn2_fwd, gdn2_attention, gdn2_decode, gdn2_prefill
+from tests.golden.make_golden import config0_inputs
 from tests.helpers import device_inputs, seeded_state
 
 pytestmark = pytest.mark.gpu
 rel_err = oracle.rel_err
 TOL = 2e-3
 F32 = GDN2Config(output_dtype=torch.float32)
+GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "config0.npz")
 
 
 def _check(B, S, H, DK, DV, dtype=torch.bfloat16, decay_scale=4.0, dist="ref", with_state=True, seed=0):
@@ -221,3 +226,55 @@ def test_prefill_random_shapes():
         eo, es = rel_err(o.cpu(), o_ref), rel_err(st.cpu(), s_ref)
         print(f"  rel_err o={eo:.2e} state={es:.2e}", flush=True)
         assert eo < TOL and es < TOL
+
+
+def test_config0_golden_on_hip():
+    """BASELINE config 0 (B=1 S=256 H=2 D=64, fp32 inputs, logsigmoid decay,
+    seed 0) through the public op and prefill on the GPU, against the float64
+    golden vectors of tests/golden/config0.npz (independent numpy recurrence)."""
+    print("config 0 golden: gdn2_attention + gdn2_prefill, fp32", flush=True)
+    ref = np.load(GOLDEN)
+    o_ref, s_ref = torch.from_numpy(ref["o"]).float(), torch.from_numpy(ref["S"]).float()
+    dev = [t.cuda() for t in config0_inputs()]
+    assert all(t.dtype == torch.float32 for t in dev)
+    o1, s1 = gdn2_attention(*dev, output_final_state=True)
+    o2, s2 = gdn2_prefill(*dev)
+    torch.cuda.synchronize()
+    assert o1.dtype == torch.float32 and o2.dtype == torch.float32
+    errs = [rel_err(o1.cpu(), o_ref), rel_err(s1.cpu(), s_ref), rel_err(o2.cpu(), o_ref), rel_err(s2.cpu(), s_ref)]
+    print("  rel_err attention o/S, prefill o/S: " + " ".join(f"{e:.2e}" for e in errs), flush=True)
+    assert max(errs) < TOL
+
+
+@pytest.mark.parametrize("st_dt", [torch.bfloat16, torch.float16])
+def test_state_dtype_is_honoured(st_dt):
+    """config.state_dtype as in the reference (inference.py:523-526): the
+    incoming state is cast to it, the returned state is in it (the kernels
+    compute in fp32 and round once), and a prompt shorter than one chunk or a
+    decode call updates a state already in that dtype in place."""
+    print(f"state_dtype {st_dt}", flush=True)
+    B, S, H, D = 2, 200, 2, 64
+    cpu, dev = device_inputs(B, S + 5, H, D, D, torch.bfloat16)
+    s0 = seeded_state(B, H, D, D).to(st_dt)
+    cfg = GDN2Config(output_dtype=torch.float32, state_dtype=st_dt)
+    o, st = gdn2_prefill(*(t[:, :S] for t in dev), s0.cuda(), config=cfg)
+    o_ref, s_ref = oracle.prefill(*(t[:, :S] for t in cpu), s0.float().clone())
+    torch.cuda.synchronize()
+    assert st.dtype == st_dt
+    assert rel_err(o.cpu(), o_ref) < TOL
+    assert rel_err(st.float().cpu(), s_ref) < TOL + 2.0 ** -8
+    # short prompt: the state in state_dtype is updated in place
+    st_short = st.clone()
+    o2, st2 = gdn2_prefill(*(t[:, S:S + 5] for t in dev), st_short, config=cfg)
+    o2_ref = oracle.decode_loop(*(t[:, S:S + 5] for t in cpu), st.float().cpu().clone(), None).float()
+    torch.cuda.synchronize()
+    assert st2 is st_short and st2.dtype == st_dt
+    assert rel_err(o2.cpu(), o2_ref) < TOL
+    st3 = st.clone()
+    gdn2_decode(*(t[:, S:S + 5] for t in dev), st3)
+    torch.cuda.synchronize()
+    assert st3.dtype == st_dt and torch.equal(st3, st2)
+    _, fin = gdn2_attention(*(t[:, :S] for t in dev), initial_state=s0.cuda(), output_final_state=True,
+                            config=cfg)
+    torch.cuda.synchronize()
+    assert fin.dtype == st_dt and rel_err(fin.float().cpu(), s_ref) < TOL + 2.0 ** -8

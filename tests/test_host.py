@@ -102,6 +102,27 @@ def test_c_abi_rejects_bad_arguments_before_launch():
                                               *args, fake, 0, 100, 2, 2, 64, 64, nul) == -1  # no sequence
 
 
+def test_layer_decode_validates_every_stage_first():
+    """gdn2_hip_layer_decode rejects what any of its five stages would reject
+    (B*n > 8 GEMV rows, an unsupported DK, DV % 32, hidden % 8, a misaligned
+    buffer) before its first launch, so a rejected call changes nothing. The
+    pointers are never dereferenced: validation fails first."""
+    lib = _hip.lib()
+    nul = None
+    f = ctypes.c_void_p(256)
+    ws = ctypes.c_void_p(512)
+    def call(B=1, n=1, hid=2048, H=16, HK=8, DK=128, DV=128, x=f):  # noqa: E306
+        #                            x  wproj cw cb  K  cin  cout alog dtb  es   st  nw  eps  wo  out ws
+        return lib.gdn2_hip_layer_decode(x, f, f, f, 4, f, ctypes.c_void_p(768), f, f, 1.0, f, f, 1e-5, f, f,
+                                         ws, 1, B, n, hid, H, HK, DK, DV, 0.1, nul)
+    assert call(B=3, n=3) == -2             # 9 rows > 8 (checked in long arithmetic)
+    assert call(B=1 << 16, n=1 << 16) == -2
+    assert call(DK=96) == -2
+    assert call(DV=48) == -2
+    assert call(hid=2044) == -2
+    assert call(x=ctypes.c_void_p(258)) == -1
+
+
 def test_backend_policy():
     assert resolve_backend("auto", on_cuda=False, needs_grad=False) == "torch"
     assert resolve_backend("auto", on_cuda=True, needs_grad=True) == "hip"
@@ -177,8 +198,9 @@ def test_tiling_and_dtype_validation():
         check_prefill_config(GDN2Config(chunk_size=64, sub_chunk_size=64))
     with pytest.raises(ValueError, match="chunk_size 64"):
         check_prefill_config(GDN2Config(chunk_size=128))
-    with pytest.raises(TypeError, match="fp32 state"):
-        check_prefill_config(GDN2Config(state_dtype=torch.bfloat16))
+    with pytest.raises(TypeError, match="state dtype"):
+        check_prefill_config(GDN2Config(state_dtype=torch.int32))
+    check_prefill_config(GDN2Config(state_dtype=torch.bfloat16))
     check_prefill_config(GDN2Config(chunk_size=64, sub_chunk_size=32))
     with pytest.raises(TypeError, match="unsupported dtype"):
         _hip.dtype_code(torch.int32)

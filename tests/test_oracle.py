@@ -214,3 +214,118 @@ def test_log2_space_cumsum():
     g = make_inputs(1, 128, 2, 16, 16)[3]
     G = chunk_local_cumsum(g, 64)
     assert torch.allclose(torch.exp2(G * math.log2(math.e)), G.exp(), rtol=1e-5, atol=1e-30)
+
+
+# ---------------------------------------------------------------------------
+# LayerOracle: each step against what the mathematics fixes (reference
+# gdn2/attention.py:186-229, 290-297, 397-402), on hand-built weights
+# ---------------------------------------------------------------------------
+
+def _layer_params(hid, H, HK, DK, DV, K=4, seed=0):
+    gen = torch.Generator().manual_seed(seed)
+    r = lambda *s: torch.randn(*s, generator=gen) * 0.3  # noqa: E731
+    dqk, dv = HK * DK, H * DV
+    p = {"q_proj.weight": r(dqk, hid), "k_proj.weight": r(dqk, hid), "v_proj.weight": r(dv, hid),
+         "b_proj.weight": r(dqk, hid), "w_proj.weight": r(dv, hid), "f_proj.weight": r(dqk, hid),
+         "o_gate_proj.weight": r(dv, hid), "o_proj.weight": r(hid, dv),
+         "A_log": torch.rand(HK, generator=gen).log(), "dt_bias": r(HK, DK),
+         "o_norm.weight": 1.0 + r(DV)}
+    if K > 0:
+        for name, c in (("q_conv", dqk), ("k_conv", dqk), ("v_conv", dv)):
+            p[f"{name}.conv.weight"] = r(c, 1, K)
+            p[f"{name}.conv.bias"] = r(c)
+    return p
+
+
+@pytest.mark.parametrize("shift", [0, 1, 3])
+def test_layer_oracle_conv_one_hot_taps(shift):
+    """A one-hot tap at position K-1-shift with zero bias is SiLU of the input
+    delayed by `shift` tokens; the first `shift` outputs read the cached tail,
+    and the new tail is the last K-1 inputs."""
+    K, C, S = 4, 6, 9
+    wgt = torch.zeros(C, 1, K)
+    wgt[:, 0, K - 1 - shift] = 1.0
+    lo = oracle.LayerOracle({"c.conv.weight": wgt, "c.conv.bias": torch.zeros(C)}, 8, 1, 1, 4, 4, conv_size=K)
+    gen = torch.Generator().manual_seed(7)
+    x = torch.randn(2, S, C, generator=gen)
+    tail = torch.randn(2, C, K - 1, generator=gen)
+    y, new_tail = lo._conv("c", x, tail)
+    seq = torch.cat([tail.transpose(1, 2), x], 1)            # [B, K-1+S, C]
+    want = F.silu(seq[:, K - 1 - shift:K - 1 - shift + S])
+    torch.testing.assert_close(y, want, rtol=0, atol=1e-6)
+    torch.testing.assert_close(new_tail, x[:, S - (K - 1):].transpose(1, 2), rtol=0, atol=0)
+
+
+def test_layer_oracle_gates_closed_form():
+    """f = 0 (zero f_proj) gives g = -a * softplus(dt_bias) with a = exp(A_log);
+    zero b_proj / w_proj give b = erase_scale / 2 and w = 1/2; b is linear in
+    erase_scale."""
+    hid, H, HK, DK, DV = 8, 4, 2, 3, 2
+    p = _layer_params(hid, H, HK, DK, DV, K=0)
+    p["f_proj.weight"].zero_()
+    p["A_log"] = torch.tensor([math.log(3.0), math.log(0.5)])
+    p["dt_bias"] = torch.tensor([[0.0, 1.0, -2.0], [5.0, -1.0, 0.25]])
+    x = torch.randn(2, 5, hid, generator=torch.Generator().manual_seed(1))
+    g, b, w = oracle.LayerOracle(p, hid, H, HK, DK, DV, conv_size=0, erase_gate_scale=0.7).gates(x)
+    sp = lambda z: math.log1p(math.exp(z))  # noqa: E731
+    want = torch.tensor([[-3.0 * sp(z) for z in (0.0, 1.0, -2.0)], [-0.5 * sp(z) for z in (5.0, -1.0, 0.25)]])
+    assert abs(want[0, 0] + 3.0 * math.log(2.0)) < 1e-12
+    torch.testing.assert_close(g, want.expand_as(g), rtol=1e-6, atol=1e-7)
+    _, b1, _ = oracle.LayerOracle(p, hid, H, HK, DK, DV, conv_size=0, erase_gate_scale=1.0).gates(x)
+    torch.testing.assert_close(b, 0.7 * b1, rtol=1e-6, atol=0)
+    p["b_proj.weight"].zero_()
+    p["w_proj.weight"].zero_()
+    _, b0, w0 = oracle.LayerOracle(p, hid, H, HK, DK, DV, conv_size=0, erase_gate_scale=0.7).gates(x)
+    assert torch.all(b0 == 0.35) and torch.all(w0 == 0.5)
+
+
+def test_layer_oracle_gated_norm_constant_row():
+    """A constant row o = c gives rsqrt(c^2 + eps) * c * weight * silu(gate)."""
+    DV, eps, c = 5, 1e-5, -0.75
+    p = _layer_params(8, 1, 1, 4, DV, K=0)
+    lo = oracle.LayerOracle(p, 8, 1, 1, 4, DV, conv_size=0, norm_eps=eps)
+    gate = torch.tensor([-2.0, -0.5, 0.0, 1.0, 3.0])
+    got = lo.gated_norm(torch.full((1, 1, 1, DV), c), gate.view(1, 1, 1, DV))
+    silu = [z / (1.0 + math.exp(-z)) for z in gate.tolist()]
+    want = [c / math.sqrt(c * c + eps) * wt * s for wt, s in zip(p["o_norm.weight"].tolist(), silu)]
+    torch.testing.assert_close(got.flatten(), torch.tensor(want), rtol=1e-6, atol=1e-7)
+
+
+def test_layer_oracle_end_to_end_float64():
+    """The whole layer (no conv) against a float64 numpy composition of its
+    definition: projections, per-key-head L2 norm, the gates, value head h
+    reading key head h // (H / HK), the recurrence from tests/golden (written
+    independently of oracle/), the gated RMSNorm and o_proj. Prefill in two
+    segments, then a decode call, with the state carried."""
+    from tests.golden.make_golden import numpy_recurrence
+
+    hid, H, HK, DK, DV, S = 12, 4, 2, 8, 6, 150
+    p = _layer_params(hid, H, HK, DK, DV, K=0, seed=3)
+    lo = oracle.LayerOracle(p, hid, H, HK, DK, DV, conv_size=0, erase_gate_scale=0.9)
+    x = torch.randn(1, S, hid, generator=torch.Generator().manual_seed(2))
+    o1, c = lo.prefill(x[:, :70])
+    o2, c = lo.prefill(x[:, 70:140], c)
+    o3, c = lo.decode(x[:, 140:], c)
+    got = torch.cat([o1, o2, o3], 1).double().numpy()
+
+    P = {k: v.double().numpy() for k, v in p.items()}
+    xn = x.double().numpy()[0]
+    def heads(a, n, d):  # noqa: E306
+        return a.reshape(S, n, d)
+    nrm = lambda a: a / np.linalg.norm(a, axis=-1, keepdims=True)  # noqa: E731
+    sig = lambda a: 1.0 / (1.0 + np.exp(-a))  # noqa: E731
+    q = nrm(heads(xn @ P["q_proj.weight"].T, HK, DK))
+    k = nrm(heads(xn @ P["k_proj.weight"].T, HK, DK))
+    v = heads(xn @ P["v_proj.weight"].T, H, DV)
+    f = heads(xn @ P["f_proj.weight"].T, HK, DK) + P["dt_bias"]
+    g = -np.exp(P["A_log"])[:, None] * np.log1p(np.exp(f))
+    b = sig(heads(xn @ P["b_proj.weight"].T, HK, DK)) * 0.9
+    w = sig(heads(xn @ P["w_proj.weight"].T, H, DV))
+    kh = [h * HK // H for h in range(H)]
+    o, _ = numpy_recurrence(*(a[None][:, :, kh] for a in (q, k)), v[None], *(a[None][:, :, kh] for a in (g, b)),
+                            w[None], DK ** -0.5)
+    o = o[0]
+    gate = heads(xn @ P["o_gate_proj.weight"].T, H, DV)
+    o = o / np.sqrt((o ** 2).mean(-1, keepdims=True) + 1e-5) * P["o_norm.weight"] * gate * sig(gate)
+    want = o.reshape(S, H * DV) @ P["o_proj.weight"].T
+    assert np.abs(got[0] - want).max() / np.abs(want).max() < 2e-5
