@@ -29,6 +29,8 @@ SIGNATURES = {
     "gdn2_hip_prefill_scan": (_I, [_P, _P, _I, _P, _P, _P, _P, _I, _I, _I, _I, _I, _I, _L, _L, _L, _P]),
     "gdn2_hip_prefill_chunks": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I, _I,
                                      _L, _L, _L, _F, _P]),
+    "gdn2_hip_prefill_chunks_noalloc": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _P, _P, _I, _I, _I, _I, _I, _I,
+                                             _L, _L, _L, _F, _P]),
     "gdn2_hip_prefill_varlen_workspace_bytes": (_S, [_I, _I, _I, _L]),
     "gdn2_hip_prefill_varlen": (_I, [_P, _P, _P, _P, _P, _P, _I, _P, _I, _P, _P, _P, _I, _P, _I, _I, _I, _I,
                                      _L, _F, _P]),

@@ -53,6 +53,7 @@ const char* gdn2_hip_status_string(int s) {
   if (s == 0) return "success";
   if (s == GDN2_ERR_ARG) return "invalid argument (null pointer, negative size or bad dtype code)";
   if (s == GDN2_ERR_SHAPE) return "unsupported shape for the gfx950 kernels";
+  if (s == GDN2_ERR_SCRATCH) return "the call needs more chunk records than the no-alloc scratch holds";
   if (s > 0) return hipGetErrorString(static_cast<hipError_t>(s));
   return "unknown status";
 }

@@ -36,6 +36,7 @@ extern "C" {
 
 #define GDN2_ERR_ARG (-1)    /* null pointer, negative size, bad dtype code */
 #define GDN2_ERR_SHAPE (-2)  /* head dim / token count the kernels do not support */
+#define GDN2_ERR_SCRATCH (-3) /* call needs more than the no-alloc entry point's fixed scratch */
 
 /* Library ABI version (bumped on any signature or layout change). */
 int gdn2_hip_version(void);
@@ -102,6 +103,27 @@ int gdn2_hip_prefill_chunks(const void* q, const void* k, const void* v, const f
                             float* state_out, void* o, int out_dtype, void* workspace, int B,
                             int H, int HK, int DK, int DV, long s_alloc, long t0, long n_tokens,
                             float scale, void* stream);
+
+/*
+ * gdn2_hip_prefill_chunks without the workspace argument: the chunk records go
+ * to a scratch array the library holds in device memory, one per GPU, of
+ * GDN2_NOALLOC_SCRATCH_BYTES (64 MiB: B * HK * ceil(n_tokens / 64) records of
+ * 66 304 B at DK = 128, 41 472 B at DK = 64; e.g. 4032 tokens of 16 key heads).
+ * A larger call returns GDN2_ERR_SCRATCH and launches nothing (prefill it in
+ * segments, passing state_out back as state_in). The call allocates nothing:
+ * no hipMalloc / hipFree, nothing from a caching allocator, so it can run
+ * where allocation is not allowed. Every call on one GPU shares that GPU's
+ * scratch, so calls that overlap in time on one GPU (different streams, or
+ * different threads) race: serialise them. Results equal
+ * gdn2_hip_prefill_chunks on the same arguments.
+ * No counterpart in the reference: it is for callers that cannot allocate
+ * device memory (HIP graph capture, serving loops, harnesses that forbid it).
+ */
+#define GDN2_NOALLOC_SCRATCH_BYTES (64L * 1024 * 1024)
+int gdn2_hip_prefill_chunks_noalloc(const void* q, const void* k, const void* v, const float* g,
+                                    const void* b, const void* w, int in_dtype, const float* state_in,
+                                    float* state_out, void* o, int out_dtype, int B, int H, int HK, int DK,
+                                    int DV, long s_alloc, long t0, long n_tokens, float scale, void* stream);
 
 /*
  * Both prefill stages over a packed variable-length batch: nseq sequences
