@@ -24,7 +24,7 @@ bool dtype_ok(int dt) { return dt == GDN2_DTYPE_F32 || dt == GDN2_DTYPE_BF16 || 
 
 long record_elems(int DK) {
   if (DK == 64) return gdn2::ChunkLayout<64>::STRIDE;
-  if (DK == 128) return gdn2::ChunkLayout<128>::STRIDE;
+  if (DK == 128) return gdn2::ChunkLayoutM<128>::STRIDE;
   return 0;
 }
 
@@ -103,6 +103,8 @@ int gdn2_hip_prefill_scan(const void* v, const void* w, int in_dtype, const void
   if (int e = check_prefill(B, H, DK, s_alloc, t0, n_tokens)) return e;
   if (DV < 16 || DV % 16 || DV > 4096) return GDN2_ERR_SHAPE;
   if (n_tokens == 0) return GDN2_ERR_SHAPE;
+  // the DK = 128 scan addresses a call's tokens with 32-bit byte offsets
+  if (n_tokens * H * DV * 4 >= (1L << 31)) return GDN2_ERR_SHAPE;
   return status(gdn2::launch_scan(v, w, in_dtype, static_cast<const unsigned short*>(workspace),
                                   state_in, state_out, o, out_dtype, B, H, HK, DK, DV, s_alloc, t0,
                                   static_cast<int>((n_tokens + gdn2::kBS - 1) / gdn2::kBS), n_tokens,
@@ -143,6 +145,7 @@ int gdn2_hip_prefill_varlen(const void* q, const void* k, const void* v, const f
   if (nseq < 1 || T < 0 || H < 1 || HK < 1 || H % HK) return GDN2_ERR_ARG;
   if (DK != 64 && DK != 128) return GDN2_ERR_SHAPE;
   if (DV < 16 || DV % 16 || DV > 4096) return GDN2_ERR_SHAPE;
+  if (T * H * DV * 4 >= (1L << 31)) return GDN2_ERR_SHAPE;   // 32-bit offsets in the DK = 128 scan
   const long slots = varlen_slots(nseq, T);
   if (static_cast<long>(HK) * slots > 0x7fffffffL || static_cast<long>(nseq) * H * (DV / 16) > 0x7fffffffL)
     return GDN2_ERR_SHAPE;

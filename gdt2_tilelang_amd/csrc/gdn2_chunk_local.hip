@@ -440,15 +440,15 @@ static hipError_t launch_chunk_local_t(const void* q, const void* k, const void*
   return hipGetLastError();
 }
 
-hipError_t launch_chunk_local2(const void* q, const void* k, const void* b, const float* g,
-                               int in_dt, int B, int H, long s_alloc, long t0, int NC, long n_tok,
-                               float scale, unsigned short* ws, Varlen vl, hipStream_t stream);
+hipError_t launch_chunk_local_m(const void* q, const void* k, const void* b, const float* g,
+                                int in_dt, int B, int H, long s_alloc, long t0, int NC, long n_tok,
+                                float scale, unsigned short* ws, Varlen vl, hipStream_t stream);
 
 hipError_t launch_chunk_local(const void* q, const void* k, const void* b, const float* g,
                               int in_dt, int B, int H, int DK, long s_alloc, long t0, int NC,
                               long n_tok, float scale, unsigned short* ws, Varlen vl, hipStream_t stream) {
-  // DK = 128 runs the channel-sliced kernel (gdn2_chunk_local2.hip); DK = 64 this one.
-  if (DK == 128) return launch_chunk_local2(q, k, b, g, in_dt, B, H, s_alloc, t0, NC, n_tok, scale, ws, vl, stream);
+  // DK = 128 writes the transition-form record (gdn2_chunk_local_m.hip); DK = 64 this one.
+  if (DK == 128) return launch_chunk_local_m(q, k, b, g, in_dt, B, H, s_alloc, t0, NC, n_tok, scale, ws, vl, stream);
 #define GDN2_CL_CASE(DKV, DTV)                                                             \
   if (DK == DKV && in_dt == DTV)                                                           \
     return launch_chunk_local_t<DKV, DTV>(q, k, b, g, B, H, s_alloc, t0, NC, n_tok, scale, ws, vl, stream);

@@ -54,6 +54,48 @@ struct ChunkLayout {
 static_assert((ChunkLayout<128>::STRIDE * 2) % 256 == 0, "record must keep 256-byte alignment");
 static_assert((ChunkLayout<64>::STRIDE * 2) % 256 == 0, "record must keep 256-byte alignment");
 
+// Transition-form record (DK = 128). With Z = w * v of the chunk, the scan
+// needs only
+//
+//   S <- diag(gamma_last) S - M S + KA Z        o = QP S + MOZ Z
+//
+// where, from the chunk's WY factors (Ai = (I + Akk)^-1, E = b*k*gamma,
+// KG = k*gamma_last/gamma, Qg = scale*q*gamma, Aqk with its diagonal):
+//
+//   MOZ = Aqk Ai  [64 x 64]    KA = KG^T Ai  [DK x 64]
+//   M   = KA E    [DK x DK]    QP = Qg - MOZ E  [64 x DK]
+//
+// so one chunk of the scan is a single state product on its critical path.
+// Fragments are fp16 MFMA A operands as above, each matrix with its own
+// power-of-two scale:
+//
+//   M   [DK/16 m][DK/32 kk]   rows = state row, k = state row      / SC[0]
+//   KA  [DK/16 m][2 kk]       rows = state row, k = token          / SC[1]
+//   QP  [4 m][DK/32 kk]       rows = token,     k = state row      / SC[2]
+//   MOZ [4 m][2 kk]           rows = token,     k = token          / SC[3]
+//   GL  [DK] fp32 gamma_last;  SC [8] fp32
+enum RecordScaleM : int { SCM_M = 0, SCM_KA = 1, SCM_QP = 2, SCM_MOZ = 3 };
+
+template <int DK>
+struct ChunkLayoutM {
+  static constexpr int KT = DK / 32;
+  static constexpr int MT = DK / 16;
+  static constexpr long M_OFF = 0;
+  static constexpr long KA_OFF = M_OFF + static_cast<long>(MT) * KT * kFrag;
+  static constexpr long QP_OFF = KA_OFF + static_cast<long>(MT) * 2 * kFrag;
+  static constexpr long MOZ_OFF = QP_OFF + 4L * KT * kFrag;
+  static constexpr long GL_OFF = MOZ_OFF + 4L * 2 * kFrag;
+  static constexpr long SC_OFF = GL_OFF + 2L * DK;
+  static constexpr long STRIDE = ((SC_OFF + 2L * 8) + 127) / 128 * 128;   // 256-byte records
+
+  __host__ __device__ static constexpr long m_frag(int m, int kk) { return M_OFF + (m * KT + kk) * kFrag; }
+  __host__ __device__ static constexpr long ka_frag(int m, int kk) { return KA_OFF + (m * 2 + kk) * kFrag; }
+  __host__ __device__ static constexpr long qp_frag(int m, int kk) { return QP_OFF + (m * KT + kk) * kFrag; }
+  __host__ __device__ static constexpr long moz_frag(int m, int kk) { return MOZ_OFF + (m * 2 + kk) * kFrag; }
+};
+
+static_assert((ChunkLayoutM<128>::STRIDE * 2) % 256 == 0, "record must keep 256-byte alignment");
+
 // Packed variable-length batches (cu_seqlens). Sequence s holds tokens
 // [cu[s], cu[s+1]) of one [T, H, D] allocation and its chunk c (64 tokens, the
 // last one possibly ragged) has the record slot  s + floor(cu[s] / 64) + c.

@@ -1,0 +1,514 @@
+// GDN-2 prefill, stage 2 for DK = 128: the sequential state scan fused with the
+// output (reference gdn2/inference.py:356-479 prefill_scan_kernel; maths
+// gdn2/reference.py:252-258), on the transition-form chunk records
+// (gdn2_prefill_layout.h: ChunkLayoutM). Per chunk, with Z = w * v:
+//
+//   o = QP S + MOZ Z                       S <- diag(gamma_last) S - M S + KA Z
+//
+// which is the reference's  Un = Ai Z - W S,  o = Qg S + Aqk Un,
+// S <- gamma_last S + KG^T Un  with the products that do not involve S formed
+// once per chunk by the chunk-local stage. The state's critical path is one
+// product (M S) per chunk and one barrier.
+//
+// One 512-thread workgroup per (b, h, 16 NT value columns); the fp32 state tile
+// S[128, DVT] lives in registers. Wave roles:
+//   waves 0-3   state rows 32w .. 32w+31: M S and KA Z, the update, then the
+//               hand-off of those rows to LDS as fp16;
+//   waves 4-7   output row block m = w - 4: QP S + MOZ Z, stored; waves 4 and
+//               5 also stage the Z of the next chunk (token rows 32u ..).
+// S and Z travel through LDS in B-operand order ([column][k], k contiguous)
+// as fp16, each 32-row k block of a column at its own power-of-two scale
+// (largest entry in [2^14, 2^15), so every entry keeps 11 significant bits
+// relative to its block's largest), undone on that k step's fp32 product; the
+// record fragments are fp16 with one power-of-two scale per matrix. A CPU
+// emulation of this arithmetic against a float64 reference stays within
+// 6.5e-4 (o and state) at S = 4096 with no decay, the worst case. Record
+// fragments are double-buffered in registers and refilled right after use.
+//
+// The workgroup -> (head, tile) map puts every tile of the value heads that
+// share a key head on one XCD, so a key head's records come from HBM once into
+// that XCD's L2.
+#include "gdn2_common.h"
+#include "gdn2_prefill_layout.h"
+
+#include <type_traits>
+
+// Optional per-wave timing hook (empty in the library build).
+#ifndef GDN2_SCAN_STAMP
+#define GDN2_SCAN_STAMP(slot, nc)
+#endif
+
+namespace gdn2 {
+
+namespace scm {
+
+constexpr int DK = 128;
+constexpr int KT = DK / 32;          // 32-row k blocks of S = state waves
+constexpr int kBufWord3 = 0x00020000;   // raw (untyped) buffer resource, gfx9 family
+typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+constexpr int kWaves = 8;
+constexpr int kThreads = 64 * kWaves;
+
+typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
+
+__device__ __forceinline__ f32x4 mfma_f16(const uint4& a, const uint4& b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
+                                                0, 0, 0);
+}
+
+// max |x| over the column of a D-layout 16 x 16 tile (lane (lq, lr) holds rows
+// 4lq .. 4lq+3 of column lr); every lane of the column gets it.
+__device__ __forceinline__ float tile_col_max(const f32x4& x) {
+  float m = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
+  uint32_t u = __float_as_uint(m);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  m = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+  u = __float_as_uint(m);
+  const auto r16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+}
+
+// 2^s putting mx in [2^14, 2^15) (s clamped to +-126: a zero column stays
+// zero); *inv = 2^-s exactly.
+__device__ __forceinline__ float col_scale(float mx, float* inv) {
+  const int ex = static_cast<int>((__float_as_uint(mx) >> 23) & 0xffu);
+  int se = 141 - ex;
+  se = se < -126 ? -126 : (se > 126 ? 126 : se);
+  *inv = __uint_as_float(static_cast<uint32_t>(127 - se) << 23);
+  return __uint_as_float(static_cast<uint32_t>(127 + se) << 23);
+}
+
+// A D-layout quad (4 consecutive k of one column) times sc as fp16 (round to nearest even).
+__device__ __forceinline__ void put_quad_f16(unsigned short* dst, const f32x4& x, float sc) {
+  const unsigned short a = f32_to_f16_bits(x[0] * sc), b = f32_to_f16_bits(x[1] * sc);
+  const unsigned short c = f32_to_f16_bits(x[2] * sc), d = f32_to_f16_bits(x[3] * sc);
+  *reinterpret_cast<uint2*>(dst) = make_uint2(static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16),
+                                              static_cast<uint32_t>(c) | (static_cast<uint32_t>(d) << 16));
+}
+
+// Four floats at p with a vector load. The zero offset comes from a VGPR, so
+// the load cannot become a scalar-cache load: a scalar load returning out of
+// order with LDS traffic would make every LDS wait in the chunk loop also
+// wait for it (one memory round trip per chunk).
+__device__ __forceinline__ float4 vload_f4(const float* p) {
+  int z;
+  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
+  return *reinterpret_cast<const float4*>(p + z);
+}
+
+template <int DT>
+__device__ __forceinline__ float load_elem_t(const void* p, size_t i) {
+  if constexpr (DT == DT_F32) return static_cast<const float*>(p)[i];
+  else if constexpr (DT == DT_BF16) return bf16_bits_to_f32(static_cast<const unsigned short*>(p)[i]);
+  else return f16_bits_to_f32(static_cast<const unsigned short*>(p)[i]);
+}
+
+template <int DT>
+__device__ __forceinline__ void store_elem_t(void* p, size_t i, float x) {
+  if constexpr (DT == DT_F32) static_cast<float*>(p)[i] = x;
+  else if constexpr (DT == DT_BF16) static_cast<unsigned short*>(p)[i] = f32_to_bf16_bits(x);
+  else static_cast<unsigned short*>(p)[i] = f32_to_f16_bits(x);
+}
+
+constexpr int kRoleState = 1, kRoleOut = 2, kRoleZ = 4;
+
+}  // namespace scm
+
+template <int NT, int IN_DT, int OUT_DT>
+__global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
+    const void* __restrict__ v, const void* __restrict__ w, const unsigned short* __restrict__ ws,
+    const float* __restrict__ s_in, float* __restrict__ s_out, void* __restrict__ o,
+    int BH, int H, int HK, int DV, long s_alloc, long t0, int NC, long n_tok, Varlen vl) {
+  using namespace scm;
+  using L = ChunkLayoutM<DK>;
+  constexpr int DVT = 16 * NT;
+  constexpr int SP = DK + 8;           // 16-bit pitch of S^T [DVT][DK]
+  constexpr int ZP = kBS + 8;          // 16-bit pitch of Z^T [DVT][64]
+
+  __shared__ __align__(16) unsigned short sS[2][DVT * SP];
+  __shared__ __align__(16) unsigned short sZ[2][DVT * ZP];
+  __shared__ __align__(16) float sSinv[2][DVT][KT];     // inverse k-block scales of S^T
+  __shared__ __align__(16) float sZinv[2][DVT][2];      // of Z^T
+
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
+  const int lr = lane & 15;
+  const int lq = lane >> 4;
+
+  // XCD-aware block -> (head, tile) map (workgroups are dealt round-robin to 8
+  // XCDs): all tiles of the value heads that share a key head land on one XCD.
+  const int ntile = DV / DVT;
+  const int rep = H / HK;
+  const int per = ntile * rep;
+  const int BHK = BH / rep;
+  int bhk, r;
+  const int Lb = blockIdx.x;
+  if (BHK % 8 == 0) {
+    const int xcd = Lb & 7, jj = Lb >> 3;
+    bhk = (jj / per) * 8 + xcd;
+    r = jj % per;
+  } else {
+    bhk = Lb / per;
+    r = Lb % per;
+  }
+  const int bi = bhk / HK;
+  const int h = (bhk % HK) * rep + r / ntile;
+  const int tile = r % ntile;
+  const int bh = bi * H + h;
+  const int d0 = tile * DVT;
+  size_t slot0 = static_cast<size_t>(bhk) * NC;
+  int bt = bi;
+  if (vl.cu) {
+    // a packed batch: batch row bi is sequence bi, tokens [cu[bi], cu[bi+1]),
+    // chunks at slots bi + floor(cu[bi] / 64) + c of its key head
+    const long a = varlen_off(vl.cu, bi, s_alloc);
+    const long e = max(varlen_off(vl.cu, bi + 1, s_alloc), a);
+    slot0 = static_cast<size_t>(bhk % HK) * NC + bi + a / kBS;
+    t0 = a;
+    n_tok = e - a;
+    NC = static_cast<int>((n_tok + kBS - 1) / kBS);
+    bt = 0;
+    if (n_tok == 0) {                    // an empty sequence passes its state through
+      for (int i = threadIdx.x; i < DK * DVT; i += kThreads) {
+        const size_t si = (static_cast<size_t>(bh) * DK + i / DVT) * DV + d0 + i % DVT;
+        s_out[si] = s_in ? s_in[si] : 0.f;
+      }
+      return;
+    }
+  }
+  const unsigned short* rec0 = ws + slot0 * L::STRIDE;
+  const int last = NC - 1;
+  auto recp = [&](int c) { return rec0 + static_cast<size_t>(min(c, last)) * L::STRIDE; };
+  auto frag = [&](const unsigned short* rec, long off) {
+    return *reinterpret_cast<const uint4*>(rec + off + lane * 8);
+  };
+  auto bop = [&](const unsigned short* a, int pitch, int nn, int k0) {
+    return *reinterpret_cast<const uint4*>(&a[(16 * nn + lr) * pitch + k0 + 8 * lq]);
+  };
+
+  auto run = [&](auto role_tag) {
+    constexpr int R = decltype(role_tag)::value;
+    constexpr bool STATE = R & kRoleState, OUT = R & kRoleOut, ZS = R & kRoleZ;
+    const int sw = wave & 3;             // state rows 32 sw .. (STATE)
+    const int m = wave & 3;              // output row block (OUT)
+    const int u = wave & 1;              // Z token half (ZS)
+
+    // ---- record fragments: double-buffered by chunk parity (refilled two
+    //      chunks ahead) at NT = 1, single-buffered (one chunk ahead) at NT = 2,
+    //      which keeps the wider tile out of scratch --------------------------------
+    constexpr int NB = NT == 1 ? 2 : 1;
+    uint4 fm[NB][STATE ? 2 : 1][STATE ? KT : 1];   // M rows 32 sw + 16 t, k steps
+    uint4 fka[NB][STATE ? 2 : 1][STATE ? 2 : 1];   // KA rows 32 sw + 16 t
+    float4 gam[NB][STATE ? 2 : 1];
+    uint4 fqp[NB][OUT ? KT : 1], fmz[NB][OUT ? 2 : 1];
+    float4 sc[NB];                                 // the record's four scales
+    auto load_all = [&](int p, const unsigned short* rec) {
+      if constexpr (STATE) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+#pragma unroll
+          for (int kk = 0; kk < KT; ++kk) fm[p][t][kk] = frag(rec, L::m_frag(2 * sw + t, kk));
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk) fka[p][t][kk] = frag(rec, L::ka_frag(2 * sw + t, kk));
+          gam[p][t] = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(rec + L::GL_OFF) +
+                                                        32 * sw + 16 * t + 4 * lq);
+        }
+      }
+      if constexpr (OUT) {
+#pragma unroll
+        for (int kk = 0; kk < KT; ++kk) fqp[p][kk] = frag(rec, L::qp_frag(m, kk));
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) fmz[p][kk] = frag(rec, L::moz_frag(m, kk));
+      }
+      sc[p] = vload_f4(reinterpret_cast<const float*>(rec + L::SC_OFF));
+    };
+
+    // ---- Z staging (waves 4, 5: token rows 32u .. 32u+31; lane e = (token,
+    //      column quad), vector loads of four v and w values) fetched two chunks
+    //      ahead into the register buffer of that chunk's parity. The loads go
+    //      through buffer resources that end at the call's last token, so rows
+    //      past a ragged end (and chunks past the last) read as zeros with no
+    //      branch in the loop.
+    constexpr int ZQ = NT * 2;                      // quads per lane (32 tokens x DVT / 4 / 64)
+    constexpr int CQ = DVT / 4;                     // column quads per token row
+    constexpr int ES = IN_DT == DT_F32 ? 4 : 2;
+    using RawT = typename std::conditional<IN_DT == DT_F32, u32x4, u32x2v>::type;
+    RawT zv[1][ZS ? ZQ : 1], zw[1][ZS ? ZQ : 1];
+    const size_t tok_base = (static_cast<size_t>(bt) * s_alloc + t0) * H;   // row of the call's first token
+    const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(static_cast<const char*>(v)) + tok_base * DV * ES, 0, static_cast<int>(n_tok * H * DV * ES),
+        kBufWord3);
+    const __amdgpu_buffer_rsrc_t rw = __builtin_amdgcn_make_buffer_rsrc(
+        const_cast<char*>(static_cast<const char*>(w)) + tok_base * DV * ES, 0, static_cast<int>(n_tok * H * DV * ES),
+        kBufWord3);
+    auto fetch_z = [&](int zb, int nc) {
+      if constexpr (ZS) {
+#pragma unroll
+        for (int it = 0; it < ZQ; ++it) {
+          const int e = lane + 64 * it;
+          const int tt = 32 * u + e / CQ, cq = e % CQ;
+          const int off = ((nc * kBS + tt) * H + h) * DV + d0 + 4 * cq;
+          if constexpr (IN_DT == DT_F32) {
+            zv[zb][it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rv, off * 4, 0, 0));
+            zw[zb][it] = __builtin_bit_cast(u32x4, __builtin_amdgcn_raw_buffer_load_b128(rw, off * 4, 0, 0));
+          } else {
+            zv[zb][it] = __builtin_bit_cast(u32x2v, __builtin_amdgcn_raw_buffer_load_b64(rv, off * 2, 0, 0));
+            zw[zb][it] = __builtin_bit_cast(u32x2v, __builtin_amdgcn_raw_buffer_load_b64(rw, off * 2, 0, 0));
+          }
+        }
+      }
+    };
+    auto raw4 = [&](const RawT& r, float* x) {
+      if constexpr (IN_DT == DT_F32) {
+        x[0] = __uint_as_float(r[0]); x[1] = __uint_as_float(r[1]);
+        x[2] = __uint_as_float(r[2]); x[3] = __uint_as_float(r[3]);
+      } else if constexpr (IN_DT == DT_BF16) {
+        x[0] = bf16_lo_f32(r[0]); x[1] = bf16_hi_f32(r[0]); x[2] = bf16_lo_f32(r[1]); x[3] = bf16_hi_f32(r[1]);
+      } else {
+        x[0] = f16_bits_to_f32(r[0] & 0xffff); x[1] = f16_bits_to_f32(r[0] >> 16);
+        x[2] = f16_bits_to_f32(r[1] & 0xffff); x[3] = f16_bits_to_f32(r[1] >> 16);
+      }
+    };
+    // Z = w * v from register buffer rb -> Z^T buffer zb, each column of the
+    // wave's 32-token block at its own scale. The lanes of column quad cq are
+    // those with lane % CQ == cq (over every it): a rotate within rows of 16
+    // (CQ = 4: by 4 and 8; CQ = 8: by 8) and the 16- / 32-lane swaps.
+    auto put_z = [&](int rbf, int zb) {
+      if constexpr (ZS) {
+        float z[ZQ][4];
+#pragma unroll
+        for (int it = 0; it < ZQ; ++it) {
+          float a[4], b[4];
+          raw4(zv[rbf][it], a);
+          raw4(zw[rbf][it], b);
+#pragma unroll
+          for (int q = 0; q < 4; ++q) z[it][q] = a[q] * b[q];
+        }
+#pragma unroll
+        for (int q = 0; q < 4; ++q) {
+          float r = 0.f;
+#pragma unroll
+          for (int it = 0; it < ZQ; ++it) r = fmaxf(r, fabsf(z[it][q]));
+          if constexpr (CQ == 4)
+            r = fmaxf(r, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, r), 0x124,
+                                                                               0xf, 0xf, false)));   // row_ror:4
+          r = fmaxf(r, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, r), 0x128,
+                                                                             0xf, 0xf, false)));     // row_ror:8
+          uint32_t uu = __float_as_uint(r);
+          const auto a16 = __builtin_amdgcn_permlane16_swap(uu, uu, false, false);
+          r = fmaxf(__uint_as_float(a16[0]), __uint_as_float(a16[1]));
+          uu = __float_as_uint(r);
+          const auto a32 = __builtin_amdgcn_permlane32_swap(uu, uu, false, false);
+          r = fmaxf(__uint_as_float(a32[0]), __uint_as_float(a32[1]));
+          float inv;
+          const float scl = col_scale(r, &inv);
+#pragma unroll
+          for (int it = 0; it < ZQ; ++it) {
+            const int e = lane + 64 * it;
+            const int tt = 32 * u + e / CQ, col = 4 * (e % CQ) + q;
+            sZ[zb][col * ZP + tt] = f32_to_f16_bits(z[it][q] * scl);
+            if (e < CQ) sZinv[zb][col][u] = inv;
+          }
+        }
+      }
+    };
+
+    // ---- state (STATE waves: rows 32sw + 16t + 4lq + e, column d0 + 16nn + lr) ---
+    f32x4 S[STATE ? 2 : 1][NT];
+    auto put_state = [&](int b) {
+      if constexpr (STATE) {
+#pragma unroll
+        for (int nn = 0; nn < NT; ++nn) {
+          const float mx = fmaxf(tile_col_max(S[0][nn]), tile_col_max(S[1][nn]));
+          float inv;
+          const float scl = col_scale(mx, &inv);
+          const int col = 16 * nn + lr;
+#pragma unroll
+          for (int t = 0; t < 2; ++t) {
+            const int c = 32 * sw + 16 * t + 4 * lq;
+            put_quad_f16(&sS[b][col * SP + c], S[t][nn], scl);
+          }
+          if (lq == 0) sSinv[b][col][sw] = inv;
+        }
+      }
+    };
+    // A (fp16 fragments over the 4 k blocks of S) times S in buffer b
+    auto times_state = [&](const uint4* fr, int b, f32x4* X) {
+#pragma unroll
+      for (int nn = 0; nn < NT; ++nn) {
+        const float4 iv = *reinterpret_cast<const float4*>(&sSinv[b][16 * nn + lr][0]);
+        const float inv[4] = {iv.x, iv.y, iv.z, iv.w};
+        X[nn] = zero4();
+#pragma unroll
+        for (int kk = 0; kk < KT; ++kk) {
+          X[nn] += mfma_f16(fr[kk], bop(sS[b], SP, nn, 32 * kk), zero4()) * inv[kk];
+        }
+      }
+    };
+    // A (fp16 fragments over the 2 token blocks) times Z in buffer b
+    auto times_z = [&](const uint4* fr, int b, f32x4* Y) {
+#pragma unroll
+      for (int nn = 0; nn < NT; ++nn) {
+        const float2 iv = *reinterpret_cast<const float2*>(&sZinv[b][16 * nn + lr][0]);
+        Y[nn] = mfma_f16(fr[0], bop(sZ[b], ZP, nn, 0), zero4()) * iv.x +
+                mfma_f16(fr[1], bop(sZ[b], ZP, nn, 32), zero4()) * iv.y;
+      }
+    };
+    // o tile of chunk nc straight from the D layout: row 16m + 4lq + e, column
+    // d0 + 16nn + lr (16 lanes cover one row's 16 contiguous columns), through a
+    // buffer resource that ends at the call's last token (rows past a ragged
+    // end are dropped by the hardware, no branch)
+    constexpr int OS = OUT_DT == DT_F32 ? 4 : 2;
+    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+        static_cast<char*>(o) + tok_base * DV * OS, 0, static_cast<int>(n_tok * H * DV * OS), kBufWord3);
+    auto store_o = [&](int nc, const f32x4* Ot) {
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int off = ((nc * kBS + 16 * m + 4 * lq + e) * H + h) * DV + d0 + lr;
+#pragma unroll
+        for (int nn = 0; nn < NT; ++nn) {
+          if constexpr (OUT_DT == DT_F32)
+            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(Ot[nn][e]), ro, (off + 16 * nn) * 4, 0, 0);
+          else if constexpr (OUT_DT == DT_BF16)
+            __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(Ot[nn][e]), ro, (off + 16 * nn) * 2, 0, 0);
+          else
+            __builtin_amdgcn_raw_buffer_store_b16(f32_to_f16_bits(Ot[nn][e]), ro, (off + 16 * nn) * 2, 0, 0);
+        }
+      }
+    };
+
+    // ---- set-up: records of chunks 0 and 1, Z_0, S_0 --------------------------------
+    load_all(0, recp(0));
+    if constexpr (NB == 2) load_all(1, recp(1));
+    if constexpr (ZS) {
+      fetch_z(0, 0);
+      put_z(0, 0);
+    }
+    if constexpr (STATE) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int nn = 0; nn < NT; ++nn)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int c = 32 * sw + 16 * t + 4 * lq + e;
+            S[t][nn][e] = s_in ? s_in[(static_cast<size_t>(bh) * DK + c) * DV + d0 + 16 * nn + lr] : 0.f;
+          }
+      put_state(0);
+    }
+    __syncthreads();
+
+    // ---- the chunk loop: S_n and Z_n in LDS buffer ph = n & 1 ------------------------
+    auto step = [&](auto parity, int nc) {
+      constexpr int ph = decltype(parity)::value;    // LDS buffers
+      constexpr int p = ph % NB;                      // record-fragment buffer
+      GDN2_SCAN_STAMP(0, nc);
+      const unsigned short* rp = recp(nc + NB);       // refills: chunk nc + NB into buffer p
+      if constexpr (STATE) {
+#pragma unroll
+        for (int t = 0; t < 2; ++t) {
+          f32x4 X[NT], Y[NT];
+          times_state(fm[p][t], ph, X);
+          times_z(fka[p][t], ph, Y);
+#pragma unroll
+          for (int kk = 0; kk < KT; ++kk) fm[p][t][kk] = frag(rp, L::m_frag(2 * sw + t, kk));
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk) fka[p][t][kk] = frag(rp, L::ka_frag(2 * sw + t, kk));
+          const float4 g4 = gam[p][t];
+          const float smm = sc[p].x, ska = sc[p].y;   // SCM_M, SCM_KA
+#pragma unroll
+          for (int nn = 0; nn < NT; ++nn) {
+            S[t][nn][0] = S[t][nn][0] * g4.x - X[nn][0] * smm + Y[nn][0] * ska;
+            S[t][nn][1] = S[t][nn][1] * g4.y - X[nn][1] * smm + Y[nn][1] * ska;
+            S[t][nn][2] = S[t][nn][2] * g4.z - X[nn][2] * smm + Y[nn][2] * ska;
+            S[t][nn][3] = S[t][nn][3] * g4.w - X[nn][3] * smm + Y[nn][3] * ska;
+          }
+          gam[p][t] = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(rp + L::GL_OFF) +
+                                                         32 * sw + 16 * t + 4 * lq);
+        }
+        put_state(ph ^ 1);
+      }
+      if constexpr (ZS) fetch_z(0, nc + 1);   // Z of chunk nc + 1, staged at the end of this step
+      if constexpr (OUT) {
+        f32x4 P[NT], Q[NT], Ot[NT];
+        times_state(fqp[p], ph, P);
+        times_z(fmz[p], ph, Q);
+        GDN2_SCAN_STAMP(2, nc);
+#pragma unroll
+        for (int kk = 0; kk < KT; ++kk) fqp[p][kk] = frag(rp, L::qp_frag(m, kk));
+#pragma unroll
+        for (int kk = 0; kk < 2; ++kk) fmz[p][kk] = frag(rp, L::moz_frag(m, kk));
+#pragma unroll
+        for (int nn = 0; nn < NT; ++nn) Ot[nn] = P[nn] * sc[p].z + Q[nn] * sc[p].w;   // SCM_QP, SCM_MOZ
+        if constexpr (ZS) {
+          put_z(0, ph ^ 1);        // Z of chunk nc + 1 (loads issued at the top of this step)
+          GDN2_SCAN_STAMP(3, nc);
+          GDN2_SCAN_STAMP(4, nc);
+        }
+        store_o(nc, Ot);
+      }
+      sc[p] = vload_f4(reinterpret_cast<const float*>(rp + L::SC_OFF));
+      GDN2_SCAN_STAMP(1, nc);
+      __syncthreads();
+    };
+
+    using P0 = std::integral_constant<int, 0>;
+    using P1 = std::integral_constant<int, 1>;
+    int nc = 0;
+    for (; nc + 1 < NC; nc += 2) {
+      step(P0{}, nc);
+      step(P1{}, nc + 1);
+    }
+    if (nc < NC) step(P0{}, nc);
+
+    if constexpr (STATE) {
+#pragma unroll
+      for (int t = 0; t < 2; ++t)
+#pragma unroll
+        for (int nn = 0; nn < NT; ++nn)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            const int c = 32 * sw + 16 * t + 4 * lq + e;
+            s_out[(static_cast<size_t>(bh) * DK + c) * DV + d0 + 16 * nn + lr] = S[t][nn][e];
+          }
+    }
+  };
+
+  if (wave < 4) run(std::integral_constant<int, kRoleState>{});
+  else if (wave < 6) run(std::integral_constant<int, kRoleOut | kRoleZ>{});
+  else run(std::integral_constant<int, kRoleOut>{});
+}
+
+template <int NT, int IN_DT, int OUT_DT>
+static hipError_t launch_scan_m_t(const void* v, const void* w, const unsigned short* ws, const float* s_in,
+                                  float* s_out, void* o, int B, int H, int HK, int DV, long s_alloc, long t0,
+                                  int NC, long n_tok, Varlen vl, hipStream_t stream) {
+  const int BH = B * H;
+  const unsigned grid = static_cast<unsigned>(BH) * (DV / (16 * NT));
+  hipLaunchKernelGGL((scan_m_kernel<NT, IN_DT, OUT_DT>), dim3(grid), dim3(scm::kThreads), 0, stream, v, w, ws,
+                     s_in, s_out, o, BH, H, HK, DV, s_alloc, t0, NC, n_tok, vl);
+  return hipGetLastError();
+}
+
+int scan_nt_for(int B, int H, int DV);
+
+hipError_t launch_scan_m(const void* v, const void* w, int in_dt, const unsigned short* ws, const float* s_in,
+                         float* s_out, void* o, int out_dt, int B, int H, int HK, int DV, long s_alloc, long t0,
+                         int NC, long n_tok, Varlen vl, hipStream_t stream) {
+  const int nt = scan_nt_for(B, H, DV);
+#define GDN2_SCANM_CASE(NTV, DTV, ODV)                                                                     \
+  if (nt == NTV && in_dt == DTV && out_dt == ODV)                                                          \
+    return launch_scan_m_t<NTV, DTV, ODV>(v, w, ws, s_in, s_out, o, B, H, HK, DV, s_alloc, t0, NC, n_tok, vl, \
+                                          stream);
+#define GDN2_SCANM_OUT(NTV, DTV) \
+  GDN2_SCANM_CASE(NTV, DTV, DT_BF16) GDN2_SCANM_CASE(NTV, DTV, DT_F16) GDN2_SCANM_CASE(NTV, DTV, DT_F32)
+#define GDN2_SCANM_DT(NTV) GDN2_SCANM_OUT(NTV, DT_BF16) GDN2_SCANM_OUT(NTV, DT_F16) GDN2_SCANM_OUT(NTV, DT_F32)
+  GDN2_SCANM_DT(1) GDN2_SCANM_DT(2)
+#undef GDN2_SCANM_DT
+#undef GDN2_SCANM_OUT
+#undef GDN2_SCANM_CASE
+  return hipErrorInvalidValue;
+}
+
+}  // namespace gdn2
