@@ -46,8 +46,9 @@ def test_version_and_status_strings():
 
 def test_workspace_size():
     lib = _hip.lib()
-    # one record per (b, key head, 64-token chunk); 66304 bytes at DK=128, 41472 at DK=64
-    assert lib.gdn2_hip_prefill_workspace_bytes(2, 16, 128, 4096) == 2 * 16 * 64 * 66304
+    # one record per (b, key head, 64-token chunk): 74496 bytes at DK=128 (transition form:
+    # M 32 KiB, KA 16, QP 16, MOZ 8, gamma_last, scales), 41472 at DK=64
+    assert lib.gdn2_hip_prefill_workspace_bytes(2, 16, 128, 4096) == 2 * 16 * 64 * 74496
     assert lib.gdn2_hip_prefill_workspace_bytes(1, 2, 64, 100) == 1 * 2 * 2 * 41472
     assert lib.gdn2_hip_prefill_workspace_bytes(1, 2, 96, 64) == 0
 
