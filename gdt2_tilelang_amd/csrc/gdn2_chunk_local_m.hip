@@ -40,6 +40,11 @@
 #include "gdn2_common.h"
 #include "gdn2_prefill_layout.h"
 
+// Optional per-wave timing hook (empty in the library build).
+#ifndef GDN2_CL_STAMP
+#define GDN2_CL_STAMP(slot)
+#endif
+
 namespace gdn2 {
 
 namespace clm {
@@ -133,6 +138,34 @@ __device__ __forceinline__ uint2 pack_f16x4(const f32x4& x, float inv) {
                     static_cast<uint32_t>(c) | (static_cast<uint32_t>(d) << 16));
 }
 
+// max over the 64 lanes of a wave, VALU only (rotations within rows of 16,
+// then the 16- and 32-lane swaps)
+__device__ __forceinline__ float wave_max(float x) {
+  x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x121, 0xf, 0xf, false)));
+  x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x122, 0xf, 0xf, false)));
+  x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x124, 0xf, 0xf, false)));
+  x = fmaxf(x, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), 0x128, 0xf, 0xf, false)));
+  uint32_t u = __float_as_uint(x);
+  const auto r16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
+  x = fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
+  u = __float_as_uint(x);
+  const auto r32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
+  return fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
+}
+
+// B operand of a 32 x 16 selection matrix I[k][n] = (k == 16 cb + n), fp16:
+// A (16 rows x 32 k) times it is the 16 x 16 column block cb of A, and the
+// product's D layout (lane (lr, lq): rows 4lq .. 4lq+3 of column lr) holds
+// that block transposed relative to A's operand layout (row lr, 8 columns).
+__device__ __forceinline__ uint4 select_b(int cb, int lr, int lq) {
+  const int j = 16 * cb + lr - 8 * lq;   // the element of this lane's 8 that is 1
+  uint32_t w[4];
+#pragma unroll
+  for (int i = 0; i < 4; ++i)
+    w[i] = (j == 2 * i ? 0x3c00u : 0u) | (j == 2 * i + 1 ? 0x3c000000u : 0u);
+  return make_uint4(w[0], w[1], w[2], w[3]);
+}
+
 // Where the accumulator quad of C^T block (m, nn) (lane (lr, lq): C[16nn + lr]
 // [16m + 4lq .. +3]) sits in the fragments of C: fragment (nn, m / 2), lane
 // 16 (2 (m % 2) + lq / 2) + lr, elements 4 (lq % 2) .. +3 -> offset in halfs.
@@ -179,6 +212,7 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
   // the chunkwise form treats as inert; their loads re-read the last valid row
   int nvalid = static_cast<int>(min(static_cast<long>(kBS), n_tok - static_cast<long>(n) * kBS));
   if (vl.cu && !varlen_chunk(vl, s_alloc, n, tok0, nvalid)) return;
+  GDN2_CL_STAMP(0);
   const int row = 16 * rb + lr;
   const size_t rbase = ((static_cast<size_t>(bi) * s_alloc + tok0 + min(row, nvalid - 1)) * H + h) * DK + 8 * lq;
 
@@ -212,12 +246,9 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
         mk = fmaxf(mk, fabsf(kr[kk][j]));
         mbk = fmaxf(mbk, fabsf(br[kk][j] * kr[kk][j]));
       }
-#pragma unroll
-    for (int off = 1; off < 64; off <<= 1) {
-      mq = fmaxf(mq, __shfl_xor(mq, off));
-      mk = fmaxf(mk, __shfl_xor(mk, off));
-      mbk = fmaxf(mbk, __shfl_xor(mbk, off));
-    }
+    mq = wave_max(mq);
+    mk = wave_max(mk);
+    mbk = wave_max(mbk);
     if (lane == 0) {
       sMax[4 * wave + 0] = mq;
       sMax[4 * wave + 1] = mk;
@@ -245,6 +276,7 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
       reinterpret_cast<float4*>(d)[1] = make_float4(G[kk][4], G[kk][5], G[kk][6], G[kk][7]);
     }
   }
+  GDN2_CL_STAMP(1);
   __syncthreads();   // #1: block sums and maxima
 
   float maxq, maxk, maxbk;
@@ -369,11 +401,16 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
       dq = mfma3(ah, al, ch, cl, dq);
       dk = mfma3(bh, bl, ch, cl, dk);
     }
+    {   // E^T, KG^T [channel][token]: the selection product transposes each 16 x 16 block
+      const uint4 ea = pack_f16x8(e, ise), ka = pack_f16x8(kg, isk);
 #pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      const int c = 32 * kk + 8 * lq + j;
-      sEt[c * TTP + row] = f32_to_f16_bits(e[j] * ise);
-      sKgt[c * TTP + row] = f32_to_f16_bits(kg[j] * isk);
+      for (int cb = 0; cb < 2; ++cb) {
+        const uint4 sel = select_b(cb, lr, lq);
+        const f32x4 te = mfma16(ea, sel, zero4()), tk = mfma16(ka, sel, zero4());
+        const int c = 32 * kk + 16 * cb + lr;
+        *reinterpret_cast<uint2*>(&sEt[c * TTP + 16 * rb + 4 * lq]) = pack_f16x4(te, 1.f);
+        *reinterpret_cast<uint2*>(&sKgt[c * TTP + 16 * rb + 4 * lq]) = pack_f16x4(tk, 1.f);
+      }
     }
     if (rb == 0 && lr == 0) {   // gamma_last for the lane's channels
       float* gl = reinterpret_cast<float*>(rec + L::GL_OFF) + 32 * kk + 8 * lq;
@@ -383,6 +420,7 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
                                                      fast_exp2(gla[7]));
     }
   }
+  GDN2_CL_STAMP(2);
   __syncthreads();   // #2: column operands, E^T, KG^T
 
   // ---- B: row block rb of Aqk and Akk -------------------------------------------------
@@ -449,8 +487,10 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
       }
     }
   }
+  GDN2_CL_STAMP(3);
   __syncthreads();   // #3: Aqk, Akk; the column operands are dead
 
+  GDN2_CL_STAMP(4);
   // ---- C: Ai = (I + Akk)^-1 (tiles column-major in sXT) ------------------------------
   if (lane < 16) {
     const float* A = sAkk + pair_idx(wave, wave) * TF;
@@ -517,14 +557,14 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
     }
   }
 
+  GDN2_CL_STAMP(5);
   // ---- D: MOZ = Aqk Ai and KA = KG^T Ai (transposed: Ai^T as the A operand) ------------
   float mai = 0.f;                         // max |Ai| (every wave reads all of Ai)
   for (int i = lane; i < NPAIR * 256; i += 64) {
     const int p = i >> 8, e = i & 255;
     mai = fmaxf(mai, fabsf(sXT[p * TF + (e >> 4) * TP + (e & 15)]));
   }
-#pragma unroll
-  for (int off = 1; off < 64; off <<= 1) mai = fmaxf(mai, __shfl_xor(mai, off));
+  mai = wave_max(mai);
   const float sai = fp16_range_scale(mai), isai = 1.f / sai;
   // Ai^T fragments: row block m (columns of Ai), k step kk (rows of Ai)
   uint4 ait[4][2];
@@ -583,6 +623,7 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
       }
     }
   }
+  GDN2_CL_STAMP(6);
   __syncthreads();   // #8: Ai, Aqk and KG^T are read
   // fragments of MOZ and KA, and Qg [t][c], to LDS
 #pragma unroll
@@ -597,6 +638,7 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
           kaq[c2][m];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) *reinterpret_cast<uint4*>(&sQg[row * KHP + 32 * kk + 8 * lq]) = qg16[kk];
+  GDN2_CL_STAMP(7);
   __syncthreads();   // #9
 
   // MOZ and KA fragments to the record (24 KiB, 16 bytes per lane per step)
@@ -662,6 +704,7 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
       }
     }
   }
+  GDN2_CL_STAMP(8);
   if (tid == 0) {
     float* sc = reinterpret_cast<float*>(rec + L::SC_OFF);
     sc[SCM_M] = sc_m;

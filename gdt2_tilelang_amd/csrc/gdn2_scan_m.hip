@@ -14,8 +14,10 @@
 // S[128, DVT] lives in registers. Wave roles:
 //   waves 0-3   state rows 32w .. 32w+31: M S and KA Z, the update, then the
 //               hand-off of those rows to LDS as fp16;
-//   waves 4-7   output row block m = w - 4: QP S + MOZ Z, stored; waves 4 and
-//               5 also stage the Z of the next chunk (token rows 32u ..).
+//   waves 4-5   stage the Z of the chunk after next (token rows 32u ..,
+//               u = w - 4), fetched two chunks ahead: they issue no other
+//               loads, so their waits cover only those;
+//   waves 6-7   output row blocks 2u, 2u + 1 (u = w - 6): QP S + MOZ Z, stored.
 // S and Z travel through LDS in B-operand order ([column][k], k contiguous)
 // as fp16, each 32-row k block of a column at its own power-of-two scale
 // (largest entry in [2^14, 2^15), so every entry keeps 11 significant bits
@@ -191,7 +193,7 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
     constexpr int R = decltype(role_tag)::value;
     constexpr bool STATE = R & kRoleState, OUT = R & kRoleOut, ZS = R & kRoleZ;
     const int sw = wave & 3;             // state rows 32 sw .. (STATE)
-    const int m = wave & 3;              // output row block (OUT)
+    const int m0 = 2 * (wave & 1);       // output row blocks m0, m0 + 1 (OUT)
     const int u = wave & 1;              // Z token half (ZS)
 
     // ---- record fragments: double-buffered by chunk parity (refilled two
@@ -201,7 +203,7 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
     uint4 fm[NB][STATE ? 2 : 1][STATE ? KT : 1];   // M rows 32 sw + 16 t, k steps
     uint4 fka[NB][STATE ? 2 : 1][STATE ? 2 : 1];   // KA rows 32 sw + 16 t
     float4 gam[NB][STATE ? 2 : 1];
-    uint4 fqp[NB][OUT ? KT : 1], fmz[NB][OUT ? 2 : 1];
+    uint4 fqp[NB][OUT ? 2 : 1][OUT ? KT : 1], fmz[NB][OUT ? 2 : 1][OUT ? 2 : 1];
     float4 sc[NB];                                 // the record's four scales
     auto load_all = [&](int p, const unsigned short* rec) {
       if constexpr (STATE) {
@@ -217,9 +219,12 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
       }
       if constexpr (OUT) {
 #pragma unroll
-        for (int kk = 0; kk < KT; ++kk) fqp[p][kk] = frag(rec, L::qp_frag(m, kk));
+        for (int i = 0; i < 2; ++i) {
 #pragma unroll
-        for (int kk = 0; kk < 2; ++kk) fmz[p][kk] = frag(rec, L::moz_frag(m, kk));
+          for (int kk = 0; kk < KT; ++kk) fqp[p][i][kk] = frag(rec, L::qp_frag(m0 + i, kk));
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk) fmz[p][i][kk] = frag(rec, L::moz_frag(m0 + i, kk));
+        }
       }
       sc[p] = vload_f4(reinterpret_cast<const float*>(rec + L::SC_OFF));
     };
@@ -234,7 +239,7 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
     constexpr int CQ = DVT / 4;                     // column quads per token row
     constexpr int ES = IN_DT == DT_F32 ? 4 : 2;
     using RawT = typename std::conditional<IN_DT == DT_F32, u32x4, u32x2v>::type;
-    RawT zv[1][ZS ? ZQ : 1], zw[1][ZS ? ZQ : 1];
+    RawT zv[2][ZS ? ZQ : 1], zw[2][ZS ? ZQ : 1];
     const size_t tok_base = (static_cast<size_t>(bt) * s_alloc + t0) * H;   // row of the call's first token
     const __amdgpu_buffer_rsrc_t rv = __builtin_amdgcn_make_buffer_rsrc(
         const_cast<char*>(static_cast<const char*>(v)) + tok_base * DV * ES, 0, static_cast<int>(n_tok * H * DV * ES),
@@ -362,7 +367,7 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
     constexpr int OS = OUT_DT == DT_F32 ? 4 : 2;
     const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
         static_cast<char*>(o) + tok_base * DV * OS, 0, static_cast<int>(n_tok * H * DV * OS), kBufWord3);
-    auto store_o = [&](int nc, const f32x4* Ot) {
+    auto store_o = [&](int nc, int m, const f32x4* Ot) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
         const int off = ((nc * kBS + 16 * m + 4 * lq + e) * H + h) * DV + d0 + lr;
@@ -379,11 +384,15 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
     };
 
     // ---- set-up: records of chunks 0 and 1, Z_0, S_0 --------------------------------
-    load_all(0, recp(0));
-    if constexpr (NB == 2) load_all(1, recp(1));
+    if constexpr (STATE || OUT) {
+      load_all(0, recp(0));
+      if constexpr (NB == 2) load_all(1, recp(1));
+    }
     if constexpr (ZS) {
       fetch_z(0, 0);
+      fetch_z(1, 1);
       put_z(0, 0);
+      fetch_z(0, 2);
     }
     if constexpr (STATE) {
 #pragma unroll
@@ -429,26 +438,29 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
         }
         put_state(ph ^ 1);
       }
-      if constexpr (ZS) fetch_z(0, nc + 1);   // Z of chunk nc + 1, staged at the end of this step
-      if constexpr (OUT) {
-        f32x4 P[NT], Q[NT], Ot[NT];
-        times_state(fqp[p], ph, P);
-        times_z(fmz[p], ph, Q);
+      if constexpr (ZS) {
+        // Z of chunk nc + 1 (fetched two steps ago), then the fetch for nc + 3;
+        // the staging waves issue no other loads, so the wait is for those alone
+        put_z(ph ^ 1, ph ^ 1);
         GDN2_SCAN_STAMP(2, nc);
-#pragma unroll
-        for (int kk = 0; kk < KT; ++kk) fqp[p][kk] = frag(rp, L::qp_frag(m, kk));
-#pragma unroll
-        for (int kk = 0; kk < 2; ++kk) fmz[p][kk] = frag(rp, L::moz_frag(m, kk));
-#pragma unroll
-        for (int nn = 0; nn < NT; ++nn) Ot[nn] = P[nn] * sc[p].z + Q[nn] * sc[p].w;   // SCM_QP, SCM_MOZ
-        if constexpr (ZS) {
-          put_z(0, ph ^ 1);        // Z of chunk nc + 1 (loads issued at the top of this step)
-          GDN2_SCAN_STAMP(3, nc);
-          GDN2_SCAN_STAMP(4, nc);
-        }
-        store_o(nc, Ot);
+        fetch_z(ph ^ 1, nc + 3);
       }
-      sc[p] = vload_f4(reinterpret_cast<const float*>(rp + L::SC_OFF));
+      if constexpr (OUT) {
+#pragma unroll
+        for (int i = 0; i < 2; ++i) {
+          f32x4 P[NT], Q[NT], Ot[NT];
+          times_state(fqp[p][i], ph, P);
+          times_z(fmz[p][i], ph, Q);
+#pragma unroll
+          for (int kk = 0; kk < KT; ++kk) fqp[p][i][kk] = frag(rp, L::qp_frag(m0 + i, kk));
+#pragma unroll
+          for (int kk = 0; kk < 2; ++kk) fmz[p][i][kk] = frag(rp, L::moz_frag(m0 + i, kk));
+#pragma unroll
+          for (int nn = 0; nn < NT; ++nn) Ot[nn] = P[nn] * sc[p].z + Q[nn] * sc[p].w;   // SCM_QP, SCM_MOZ
+          store_o(nc, m0 + i, Ot);
+        }
+      }
+      if constexpr (STATE || OUT) sc[p] = vload_f4(reinterpret_cast<const float*>(rp + L::SC_OFF));
       GDN2_SCAN_STAMP(1, nc);
       __syncthreads();
     };
@@ -476,7 +488,7 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
   };
 
   if (wave < 4) run(std::integral_constant<int, kRoleState>{});
-  else if (wave < 6) run(std::integral_constant<int, kRoleOut | kRoleZ>{});
+  else if (wave < 6) run(std::integral_constant<int, kRoleZ>{});
   else run(std::integral_constant<int, kRoleOut>{});
 }
 
