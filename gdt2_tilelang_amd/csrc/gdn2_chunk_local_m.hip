@@ -40,11 +40,6 @@
 #include "gdn2_common.h"
 #include "gdn2_prefill_layout.h"
 
-// Optional per-wave timing hook (empty in the library build).
-#ifndef GDN2_CL_STAMP
-#define GDN2_CL_STAMP(slot)
-#endif
-
 namespace gdn2 {
 
 namespace clm {
@@ -212,7 +207,6 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
   // the chunkwise form treats as inert; their loads re-read the last valid row
   int nvalid = static_cast<int>(min(static_cast<long>(kBS), n_tok - static_cast<long>(n) * kBS));
   if (vl.cu && !varlen_chunk(vl, s_alloc, n, tok0, nvalid)) return;
-  GDN2_CL_STAMP(0);
   const int row = 16 * rb + lr;
   const size_t rbase = ((static_cast<size_t>(bi) * s_alloc + tok0 + min(row, nvalid - 1)) * H + h) * DK + 8 * lq;
 
@@ -276,7 +270,6 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
       reinterpret_cast<float4*>(d)[1] = make_float4(G[kk][4], G[kk][5], G[kk][6], G[kk][7]);
     }
   }
-  GDN2_CL_STAMP(1);
   __syncthreads();   // #1: block sums and maxima
 
   float maxq, maxk, maxbk;
@@ -420,7 +413,6 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
                                                      fast_exp2(gla[7]));
     }
   }
-  GDN2_CL_STAMP(2);
   __syncthreads();   // #2: column operands, E^T, KG^T
 
   // ---- B: row block rb of Aqk and Akk -------------------------------------------------
@@ -487,10 +479,8 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
       }
     }
   }
-  GDN2_CL_STAMP(3);
   __syncthreads();   // #3: Aqk, Akk; the column operands are dead
 
-  GDN2_CL_STAMP(4);
   // ---- C: Ai = (I + Akk)^-1 (tiles column-major in sXT) ------------------------------
   if (lane < 16) {
     const float* A = sAkk + pair_idx(wave, wave) * TF;
@@ -557,7 +547,6 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
     }
   }
 
-  GDN2_CL_STAMP(5);
   // ---- D: MOZ = Aqk Ai and KA = KG^T Ai (transposed: Ai^T as the A operand) ------------
   float mai = 0.f;                         // max |Ai| (every wave reads all of Ai)
   for (int i = lane; i < NPAIR * 256; i += 64) {
@@ -623,7 +612,6 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
       }
     }
   }
-  GDN2_CL_STAMP(6);
   __syncthreads();   // #8: Ai, Aqk and KG^T are read
   // fragments of MOZ and KA, and Qg [t][c], to LDS
 #pragma unroll
@@ -638,7 +626,6 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
           kaq[c2][m];
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) *reinterpret_cast<uint4*>(&sQg[row * KHP + 32 * kk + 8 * lq]) = qg16[kk];
-  GDN2_CL_STAMP(7);
   __syncthreads();   // #9
 
   // MOZ and KA fragments to the record (24 KiB, 16 bytes per lane per step)
@@ -704,7 +691,6 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
       }
     }
   }
-  GDN2_CL_STAMP(8);
   if (tid == 0) {
     float* sc = reinterpret_cast<float*>(rec + L::SC_OFF);
     sc[SCM_M] = sc_m;

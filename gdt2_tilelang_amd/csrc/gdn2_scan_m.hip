@@ -35,11 +35,6 @@
 
 #include <type_traits>
 
-// Optional per-wave timing hook (empty in the library build).
-#ifndef GDN2_SCAN_STAMP
-#define GDN2_SCAN_STAMP(slot, nc)
-#endif
-
 namespace gdn2 {
 
 namespace scm {
@@ -113,6 +108,12 @@ __device__ __forceinline__ void store_elem_t(void* p, size_t i, float x) {
 }
 
 constexpr int kRoleState = 1, kRoleOut = 2, kRoleZ = 4;
+// output row blocks per output wave: 2 on two waves (Z staged by two more), or
+// 1 on each of four waves, two of which also stage Z
+#ifndef GDN2_SCAN_OUT_BLOCKS
+#define GDN2_SCAN_OUT_BLOCKS 2
+#endif
+constexpr int kOutBlocks = GDN2_SCAN_OUT_BLOCKS;
 
 }  // namespace scm
 
@@ -193,7 +194,8 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
     constexpr int R = decltype(role_tag)::value;
     constexpr bool STATE = R & kRoleState, OUT = R & kRoleOut, ZS = R & kRoleZ;
     const int sw = wave & 3;             // state rows 32 sw .. (STATE)
-    const int m0 = 2 * (wave & 1);       // output row blocks m0, m0 + 1 (OUT)
+    constexpr int NOB = kOutBlocks;
+    const int m0 = NOB == 2 ? 2 * (wave & 1) : (wave & 3);   // output row blocks m0 .. m0 + NOB - 1 (OUT)
     const int u = wave & 1;              // Z token half (ZS)
 
     // ---- record fragments: double-buffered by chunk parity (refilled two
@@ -203,7 +205,7 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
     uint4 fm[NB][STATE ? 2 : 1][STATE ? KT : 1];   // M rows 32 sw + 16 t, k steps
     uint4 fka[NB][STATE ? 2 : 1][STATE ? 2 : 1];   // KA rows 32 sw + 16 t
     float4 gam[NB][STATE ? 2 : 1];
-    uint4 fqp[NB][OUT ? 2 : 1][OUT ? KT : 1], fmz[NB][OUT ? 2 : 1][OUT ? 2 : 1];
+    uint4 fqp[NB][OUT ? NOB : 1][OUT ? KT : 1], fmz[NB][OUT ? NOB : 1][OUT ? 2 : 1];
     float4 sc[NB];                                 // the record's four scales
     auto load_all = [&](int p, const unsigned short* rec) {
       if constexpr (STATE) {
@@ -219,7 +221,7 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
       }
       if constexpr (OUT) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < NOB; ++i) {
 #pragma unroll
           for (int kk = 0; kk < KT; ++kk) fqp[p][i][kk] = frag(rec, L::qp_frag(m0 + i, kk));
 #pragma unroll
@@ -412,7 +414,6 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
     auto step = [&](auto parity, int nc) {
       constexpr int ph = decltype(parity)::value;    // LDS buffers
       constexpr int p = ph % NB;                      // record-fragment buffer
-      GDN2_SCAN_STAMP(0, nc);
       const unsigned short* rp = recp(nc + NB);       // refills: chunk nc + NB into buffer p
       if constexpr (STATE) {
 #pragma unroll
@@ -442,12 +443,11 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
         // Z of chunk nc + 1 (fetched two steps ago), then the fetch for nc + 3;
         // the staging waves issue no other loads, so the wait is for those alone
         put_z(ph ^ 1, ph ^ 1);
-        GDN2_SCAN_STAMP(2, nc);
         fetch_z(ph ^ 1, nc + 3);
       }
       if constexpr (OUT) {
 #pragma unroll
-        for (int i = 0; i < 2; ++i) {
+        for (int i = 0; i < NOB; ++i) {
           f32x4 P[NT], Q[NT], Ot[NT];
           times_state(fqp[p][i], ph, P);
           times_z(fmz[p][i], ph, Q);
@@ -461,7 +461,6 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
         }
       }
       if constexpr (STATE || OUT) sc[p] = vload_f4(reinterpret_cast<const float*>(rp + L::SC_OFF));
-      GDN2_SCAN_STAMP(1, nc);
       __syncthreads();
     };
 
@@ -488,7 +487,7 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
   };
 
   if (wave < 4) run(std::integral_constant<int, kRoleState>{});
-  else if (wave < 6) run(std::integral_constant<int, kRoleZ>{});
+  else if (wave < 6) run(std::integral_constant<int, kOutBlocks == 2 ? kRoleZ : (kRoleZ | kRoleOut)>{});
   else run(std::integral_constant<int, kRoleOut>{});
 }
 
