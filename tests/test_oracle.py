@@ -239,19 +239,20 @@ def _layer_params(hid, H, HK, DK, DV, K=4, seed=0):
 
 @pytest.mark.parametrize("shift", [0, 1, 3])
 def test_layer_oracle_conv_one_hot_taps(shift):
-    """A one-hot tap at position K-1-shift with zero bias is SiLU of the input
-    delayed by `shift` tokens; the first `shift` outputs read the cached tail,
-    and the new tail is the last K-1 inputs."""
+    """A one-hot tap at position K-1-shift is SiLU of the input delayed by
+    `shift` tokens plus the channel's bias; the first `shift` outputs read the
+    cached tail, and the new tail is the last K-1 inputs."""
     K, C, S = 4, 6, 9
     wgt = torch.zeros(C, 1, K)
     wgt[:, 0, K - 1 - shift] = 1.0
-    lo = oracle.LayerOracle({"c.conv.weight": wgt, "c.conv.bias": torch.zeros(C)}, 8, 1, 1, 4, 4, conv_size=K)
+    bias = torch.linspace(-1.0, 1.5, C)
+    lo = oracle.LayerOracle({"c.conv.weight": wgt, "c.conv.bias": bias}, 8, 1, 1, 4, 4, conv_size=K)
     gen = torch.Generator().manual_seed(7)
     x = torch.randn(2, S, C, generator=gen)
     tail = torch.randn(2, C, K - 1, generator=gen)
     y, new_tail = lo._conv("c", x, tail)
     seq = torch.cat([tail.transpose(1, 2), x], 1)            # [B, K-1+S, C]
-    want = F.silu(seq[:, K - 1 - shift:K - 1 - shift + S])
+    want = F.silu(seq[:, K - 1 - shift:K - 1 - shift + S] + bias)
     torch.testing.assert_close(y, want, rtol=0, atol=1e-6)
     torch.testing.assert_close(new_tail, x[:, S - (K - 1):].transpose(1, 2), rtol=0, atol=0)
 
