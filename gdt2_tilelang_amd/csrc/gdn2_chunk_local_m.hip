@@ -68,6 +68,16 @@ constexpr int KAF_OFF = KGT_OFF + 8 * 1024;          // KA fragments [8][2]
 static_assert(XT_OFF + NPAIR * TF * 4 <= ET_OFF, "Ai tiles overlap E^T");
 static_assert(KAF_OFF + 16 * 1024 <= AKK_OFF, "fragment staging overlaps Akk");
 static_assert(LDS_BYTES <= 81920, "two workgroups per CU");
+// Per-wave channel tables, live from barrier #1 through the end of phase A (in
+// the Akk tiles' space, first written in phase B): the block sum t and the
+// factors 2^(-t/2), scale 2^B_rb / s_qg, 2^B_rb / s_e, 2^(G_last - B_rb+1) / s_k.
+constexpr int NFAC = 5;
+constexpr int FAC_OFF = AKK_OFF;
+static_assert(4 * NFAC * DK * 4 <= NPAIR * TF * 4, "factor tables overlap");
+// Per-wave gap factors 2^(B_rb - B_j+1) for column blocks j < rb - 1, live until
+// the end of phase B: in the wave's own rows of the Aqk array, written at the end of B
+constexpr int GAP_BYTES = 16 * TTP * 2;
+static_assert(2 * DK * 4 <= GAP_BYTES, "gap factors exceed the wave's Aqk rows");
 
 __device__ __forceinline__ int pair_idx(int i, int j) { return i * (i + 1) / 2 + j; }
 
@@ -131,6 +141,14 @@ __device__ __forceinline__ uint2 pack_f16x4(const f32x4& x, float inv) {
   const unsigned short c = f32_to_f16_bits(x[2] * inv), d = f32_to_f16_bits(x[3] * inv);
   return make_uint2(static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16),
                     static_cast<uint32_t>(c) | (static_cast<uint32_t>(d) << 16));
+}
+
+// eight floats times eight per-channel factors -> eight packed fp16
+__device__ __forceinline__ uint4 pack_f16x8v(const float* x, const float* f) {
+  float y[8];
+#pragma unroll
+  for (int j = 0; j < 8; ++j) y[j] = x[j] * f[j];
+  return pack_f16x8(y, 1.f);
 }
 
 // max over the 64 lanes of a wave, VALU only (rotations within rows of 16,
@@ -296,14 +314,52 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
   }
 
   // ---- A.3 operands -------------------------------------------------------------
+  const float sqg = fp16_range_scale(scale * maxq), isqg = 1.f / sqg;
+  const float se = sbk, ise = isbk;    // |E| <= max |b k|
+  float* sFac = reinterpret_cast<float*>(smem + FAC_OFF) + wave * NFAC * DK;
+  float* sGap = reinterpret_cast<float*>(smem + AQ_OFF + rb * GAP_BYTES);
+  // the block boundaries of channel c: B_i = t_0 + .. + t_{i-1} (block sums t_i)
+#pragma unroll
+  for (int h2 = 0; h2 < 2; ++h2) {
+    const int c = lane + 64 * h2;
+    float t[4];
+#pragma unroll
+    for (int i = 0; i < 4; ++i) t[i] = sTot[i * DK + c];
+    float bst = 0.f, tb = 0.f, gla = 0.f;
+#pragma unroll
+    for (int i = 0; i < 4; ++i) {
+      if (i == rb) bst = gla;
+      if (i == rb) tb = t[i];
+      gla += t[i];
+    }
+    const float ben = bst + tb;
+    sFac[0 * DK + c] = tb;
+    sFac[1 * DK + c] = fast_exp2(-0.5f * tb);
+    const float pr = fast_exp2(bst);
+    sFac[2 * DK + c] = scale * pr * isqg;
+    sFac[3 * DK + c] = pr * ise;
+    sFac[4 * DK + c] = fast_exp2(gla - ben) * isk;
+    if (rb == 0) reinterpret_cast<float*>(rec + L::GL_OFF)[c] = fast_exp2(gla);   // gamma_last
+    // 2^(B_rb - B_{j+1}) = 2^(t_{j+1} + .. + t_{rb-1}) for j = rb - 2, rb - 3
+    if (rb >= 2) {
+      float gp = 0.f;
+#pragma unroll
+      for (int i = 3; i >= 1; --i) {
+        if (i < rb) {
+          gp += t[i];
+          if (i == rb - 1) sGap[0 * DK + c] = fast_exp2(gp);  // j = rb - 2
+          if (i == rb - 2) sGap[1 * DK + c] = fast_exp2(gp);  // j = rb - 3
+        }
+      }
+    }
+  }
+  __builtin_amdgcn_wave_barrier();   // the tables are read by other lanes of the wave
   // per 8 channels: the block boundaries B_rb, B_{rb+1} and G_last from the block
   // sums; G becomes the chunk cumsum; off-diagonal fp16 operands; the diagonal
   // block on split bf16 operands; Qg kept (fp16) for QP; E^T and KG^T to LDS
   // ([channel][token]) for the record products
   uint4 qh16[4], bh16[4];              // row operands q 2^(G - B_rb), b k 2^(G - B_rb)
   uint4 qg16[4];                       // Qg / sqg
-  const float sqg = fp16_range_scale(scale * maxq), isqg = 1.f / sqg;
-  const float se = sbk, ise = isbk;    // |E| <= max |b k|
   f32x4 dq = zero4(), dk = zero4();    // diagonal block of Aqk (unscaled) and Akk
   if (exact_diag) {
     // exact diagonal (block-local G: the block's carry cancels in G_t - G_s):
@@ -342,47 +398,29 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
   }
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
-    float bst[8], ben[8], gla[8];
-    {
-      float t[4][8];
-#pragma unroll
-      for (int i = 0; i < 4; ++i) ld8f(sTot + i * DK + 32 * kk + 8 * lq, t[i]);
-#pragma unroll
-      for (int j = 0; j < 8; ++j) {
-        float c = 0.f;
-#pragma unroll
-        for (int i = 0; i < 4; ++i) {
-          if (i == rb) bst[j] = c;
-          c += t[i][j];
-          if (i == rb) ben[j] = c;
-        }
-        gla[j] = c;
-      }
-    }
-    float xq[8], xb[8], xk[8], yq[8], yb[8], yk[8], qg[8], e[8], kg[8];
+    float tb[8], fd[8], fq[8], fe[8], fk[8];
+    ld8f(sFac + 0 * DK + 32 * kk + 8 * lq, tb);
+    ld8f(sFac + 1 * DK + 32 * kk + 8 * lq, fd);
+    ld8f(sFac + 2 * DK + 32 * kk + 8 * lq, fq);
+    ld8f(sFac + 3 * DK + 32 * kk + 8 * lq, fe);
+    ld8f(sFac + 4 * DK + 32 * kk + 8 * lq, fk);
+    // G is the block-local cumsum: G - B_rb of the chunk's
+    float xq[8], xb[8], xk[8], yq[8], yb[8], yk[8];
 #pragma unroll
     for (int j = 0; j < 8; ++j) {
-      const float gg = G[kk][j] + bst[j];
-      G[kk][j] = gg;
-      const float er = fast_exp2(gg - bst[j]);                 // <= 1
-      const float ec = fast_exp2(ben[j] - gg);                 // <= 1
-      const float fd = fast_exp2(0.5f * (bst[j] - ben[j]));    // 2^(spread / 2)
-      const float pr = fast_exp2(bst[j]);                      // 2^G = er * pr
-      const float pk = fast_exp2(gla[j] - ben[j]);             // KG = k ec pk
+      const float er = fast_exp2(G[kk][j]);                    // 2^(G - B_rb) <= 1
+      const float ec = fast_exp2(tb[j] - G[kk][j]);            // 2^(B_rb+1 - G) <= 1
       const float q = qr[kk][j], k = kr[kk][j], bk = br[kk][j] * k;
       xq[j] = q * er;
       xb[j] = bk * er;
       xk[j] = k * ec;
-      yq[j] = xq[j] * fd;
-      yb[j] = xb[j] * fd;
-      yk[j] = xk[j] * fd;
-      qg[j] = scale * xq[j] * pr;
-      e[j] = xb[j] * pr;
-      kg[j] = xk[j] * pk;
+      yq[j] = xq[j] * fd[j];
+      yb[j] = xb[j] * fd[j];
+      yk[j] = xk[j] * fd[j];
     }
     qh16[kk] = pack_f16x8(xq, isq);
     bh16[kk] = pack_f16x8(xb, isbk);
-    qg16[kk] = pack_f16x8(qg, isqg);
+    qg16[kk] = pack_f16x8v(xq, fq);   // Qg = scale q 2^G
     *reinterpret_cast<uint4*>(&sKh[row * KHP + 32 * kk + 8 * lq]) = pack_f16x8(xk, isk);
     if (!exact_diag) {
       // the diagonal block: rows and columns both this block (the B operand of
@@ -395,7 +433,7 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
       dk = mfma3(bh, bl, ch, cl, dk);
     }
     {   // E^T, KG^T [channel][token]: the selection product transposes each 16 x 16 block
-      const uint4 ea = pack_f16x8(e, ise), ka = pack_f16x8(kg, isk);
+      const uint4 ea = pack_f16x8v(xb, fe), ka = pack_f16x8v(xk, fk);   // E = b k 2^G, KG = k 2^(G_last - G)
 #pragma unroll
       for (int cb = 0; cb < 2; ++cb) {
         const uint4 sel = select_b(cb, lr, lq);
@@ -404,13 +442,6 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
         *reinterpret_cast<uint2*>(&sEt[c * TTP + 16 * rb + 4 * lq]) = pack_f16x4(te, 1.f);
         *reinterpret_cast<uint2*>(&sKgt[c * TTP + 16 * rb + 4 * lq]) = pack_f16x4(tk, 1.f);
       }
-    }
-    if (rb == 0 && lr == 0) {   // gamma_last for the lane's channels
-      float* gl = reinterpret_cast<float*>(rec + L::GL_OFF) + 32 * kk + 8 * lq;
-      reinterpret_cast<float4*>(gl)[0] = make_float4(fast_exp2(gla[0]), fast_exp2(gla[1]), fast_exp2(gla[2]),
-                                                     fast_exp2(gla[3]));
-      reinterpret_cast<float4*>(gl)[1] = make_float4(fast_exp2(gla[4]), fast_exp2(gla[5]), fast_exp2(gla[6]),
-                                                     fast_exp2(gla[7]));
     }
   }
   __syncthreads();   // #2: column operands, E^T, KG^T
@@ -431,17 +462,10 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
           uint4 col = *reinterpret_cast<const uint4*>(&sKh[(16 * j + lr) * KHP + 32 * kk + 8 * lq]);
           if (j < rb - 1) {
             // the blocks between: 2^(B_rb - B_{j+1}) = 2^(sum of their block sums) <= 1
-            float x[8], gap[8], t[8];
+            float x[8], gap[8];
             unpack_f16x8(col, x);
-            ld8f(sTot + (j + 1) * DK + 32 * kk + 8 * lq, gap);
-            for (int i = j + 2; i < rb; ++i) {
-              ld8f(sTot + i * DK + 32 * kk + 8 * lq, t);
-#pragma unroll
-              for (int e2 = 0; e2 < 8; ++e2) gap[e2] += t[e2];
-            }
-#pragma unroll
-            for (int e2 = 0; e2 < 8; ++e2) x[e2] *= fast_exp2(gap[e2]);
-            col = pack_f16x8(x, 1.f);
+            ld8f(sGap + (rb - 2 - j) * DK + 32 * kk + 8 * lq, gap);
+            col = pack_f16x8v(x, gap);
           }
           aq[j] = mfma16(qh16[kk], col, aq[j]);
           ak[j] = mfma16(bh16[kk], col, ak[j]);
