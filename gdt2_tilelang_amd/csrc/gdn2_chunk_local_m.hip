@@ -52,7 +52,7 @@ constexpr float kDiagSpread = 120.0f;   // split-bf16 diagonal while every block
 
 // LDS (bytes)
 constexpr int TOT_OFF = 0;              // fp32 [4 blocks][128]: block sums of the log2 cumsum
-constexpr int MAX_OFF = 2048;           // fp32 [4 waves][4]: max |q|, |k|, |b k|
+constexpr int MAX_OFF = 2048;           // fp32 [4 waves][4]: max |q|, |k|, |b k|, |Ai|
 constexpr int KH_OFF = 2304;            // fp16 [64 t][KHP]: column operands k 2^(B_{j+1} - G)
 constexpr int KHP = 136;
 constexpr int XT_OFF = KH_OFF;          // fp32 Ai tiles (column-major), over the dead column operands
@@ -228,21 +228,47 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
   const int row = 16 * rb + lr;
   const size_t rbase = ((static_cast<size_t>(bi) * s_alloc + tok0 + min(row, nvalid - 1)) * H + h) * DK + 8 * lq;
 
-  // ---- A.1 loads ----------------------------------------------------------------
+  // ---- A.1 loads: g first, so that the cumsum runs while q, k, b are in flight --------
   float G[4][8];
   Raw8<IN_DT> qr[4], kr[4], br[4];
 #pragma unroll
+  for (int kk = 0; kk < 4; ++kk) ld8f(g + rbase + 32 * kk, G[kk]);
+  __builtin_amdgcn_sched_barrier(0);
+#pragma unroll
   for (int kk = 0; kk < 4; ++kk) {
-    ld8f(g + rbase + 32 * kk, G[kk]);
     qr[kk].load(qp, rbase + 32 * kk);
     kr[kk].load(kp, rbase + 32 * kk);
     br[kk].load(bp, rbase + 32 * kk);
   }
-  if (row >= nvalid) {
+  __builtin_amdgcn_sched_barrier(0);
+  const bool pad_row = row >= nvalid;
+  // a padded row's g (a copy of the last valid row's, finite) times zero: a select
+  // on the loaded value instead would move the load under a branch
+  const float g_log2e = pad_row ? 0.f : kLog2e;
+
+  // ---- A.2 log2 cumsum: DPP prefix over the block's 16 rows, block sums out ----------
+#pragma unroll
+  for (int kk = 0; kk < 4; ++kk)
+#pragma unroll
+    for (int j = 0; j < 8; ++j) {
+      float x = G[kk][j] * g_log2e;
+      x += row_shr<1>(x);
+      x += row_shr<2>(x);
+      x += row_shr<4>(x);
+      x += row_shr<8>(x);
+      G[kk][j] = x;
+    }
+  if (lr == 15) {
 #pragma unroll
     for (int kk = 0; kk < 4; ++kk) {
+      float* d = sTot + rb * DK + 32 * kk + 8 * lq;
+      reinterpret_cast<float4*>(d)[0] = make_float4(G[kk][0], G[kk][1], G[kk][2], G[kk][3]);
+      reinterpret_cast<float4*>(d)[1] = make_float4(G[kk][4], G[kk][5], G[kk][6], G[kk][7]);
+    }
+  }
+  if (pad_row) {
 #pragma unroll
-      for (int j = 0; j < 8; ++j) G[kk][j] = 0.f;
+    for (int kk = 0; kk < 4; ++kk) {
       qr[kk].zero();
       kr[kk].zero();
       br[kk].zero();
@@ -265,27 +291,6 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
       sMax[4 * wave + 0] = mq;
       sMax[4 * wave + 1] = mk;
       sMax[4 * wave + 2] = mbk;
-    }
-  }
-
-  // ---- A.2 log2 cumsum: DPP prefix over the block's 16 rows, block sums out ----------
-#pragma unroll
-  for (int kk = 0; kk < 4; ++kk)
-#pragma unroll
-    for (int j = 0; j < 8; ++j) {
-      float x = G[kk][j] * kLog2e;
-      x += row_shr<1>(x);
-      x += row_shr<2>(x);
-      x += row_shr<4>(x);
-      x += row_shr<8>(x);
-      G[kk][j] = x;
-    }
-  if (lr == 15) {
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      float* d = sTot + rb * DK + 32 * kk + 8 * lq;
-      reinterpret_cast<float4*>(d)[0] = make_float4(G[kk][0], G[kk][1], G[kk][2], G[kk][3]);
-      reinterpret_cast<float4*>(d)[1] = make_float4(G[kk][4], G[kk][5], G[kk][6], G[kk][7]);
     }
   }
   __syncthreads();   // #1: block sums and maxima
@@ -506,6 +511,7 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
   __syncthreads();   // #3: Aqk, Akk; the column operands are dead
 
   // ---- C: Ai = (I + Akk)^-1 (tiles column-major in sXT) ------------------------------
+  float mai = 0.f;   // max |Ai| over what this wave computes
   if (lane < 16) {
     const float* A = sAkk + pair_idx(wave, wave) * TF;
     float x[16];
@@ -515,6 +521,7 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
 #pragma unroll
       for (int s = 0; s < rr; ++s) val -= A[rr * TP + s] * x[s];
       x[rr] = val;
+      mai = fmaxf(mai, fabsf(val));
     }
     float* xt = sXT + pair_idx(wave, wave) * TF + lane * TP;   // column `lane`
 #pragma unroll
@@ -566,18 +573,18 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
         const f32x4 R = mfma3(ah, al, bh, bl, zero4());
         *reinterpret_cast<float4*>(&sXT[pair_idx(i, j) * TF + lr * TP + 4 * lq]) =
             make_float4(-R[0], -R[1], -R[2], -R[3]);
+        mai = fmaxf(mai, fmaxf(fmaxf(fabsf(R[0]), fabsf(R[1])), fmaxf(fabsf(R[2]), fabsf(R[3]))));
+      }
+      if (d == 3) {
+        mai = wave_max(mai);
+        if (lane == 0) sMax[4 * wave + 3] = mai;
       }
       __syncthreads();
     }
   }
 
   // ---- D: MOZ = Aqk Ai and KA = KG^T Ai (transposed: Ai^T as the A operand) ------------
-  float mai = 0.f;                         // max |Ai| (every wave reads all of Ai)
-  for (int i = lane; i < NPAIR * 256; i += 64) {
-    const int p = i >> 8, e = i & 255;
-    mai = fmaxf(mai, fabsf(sXT[p * TF + (e >> 4) * TP + (e & 15)]));
-  }
-  mai = wave_max(mai);
+  mai = fmaxf(fmaxf(sMax[3], sMax[7]), fmaxf(sMax[11], sMax[15]));   // max |Ai|
   const float sai = fp16_range_scale(mai), isai = 1.f / sai;
   // Ai^T fragments: row block m (columns of Ai), k step kk (rows of Ai)
   uint4 ait[4][2];
