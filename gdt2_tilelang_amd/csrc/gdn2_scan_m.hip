@@ -15,9 +15,10 @@
 //   waves 0-3   state rows 32w .. 32w+31: M S and KA Z, the update, then the
 //               hand-off of those rows to LDS as fp16;
 //   waves 4-5   stage the Z of the chunk after next (token rows 32u ..,
-//               u = w - 4), fetched two chunks ahead: they issue no other
-//               loads, so their waits cover only those;
-//   waves 6-7   output row blocks 2u, 2u + 1 (u = w - 6): QP S + MOZ Z, stored.
+//               u = w - 4), fetched two chunks ahead, and store the previous
+//               chunk's o rows 32u .. from LDS: they issue no other loads, so
+//               their waits cover only those;
+//   waves 6-7   output row blocks 2u, 2u + 1 (u = w - 6): QP S + MOZ Z, to LDS.
 // S and Z travel through LDS in B-operand order ([column][k], k contiguous)
 // as fp16, each 32-row k block of a column at its own power-of-two scale
 // (largest entry in [2^14, 2^15), so every entry keeps 11 significant bits
@@ -108,12 +109,7 @@ __device__ __forceinline__ void store_elem_t(void* p, size_t i, float x) {
 }
 
 constexpr int kRoleState = 1, kRoleOut = 2, kRoleZ = 4;
-// output row blocks per output wave: 2 on two waves (Z staged by two more), or
-// 1 on each of four waves, two of which also stage Z
-#ifndef GDN2_SCAN_OUT_BLOCKS
-#define GDN2_SCAN_OUT_BLOCKS 2
-#endif
-constexpr int kOutBlocks = GDN2_SCAN_OUT_BLOCKS;
+constexpr int kOutBlocks = 2;        // output row blocks per output wave
 
 }  // namespace scm
 
@@ -132,6 +128,8 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
   __shared__ __align__(16) unsigned short sZ[2][DVT * ZP];
   __shared__ __align__(16) float sSinv[2][DVT][KT];     // inverse k-block scales of S^T
   __shared__ __align__(16) float sZinv[2][DVT][2];      // of Z^T
+  constexpr int OS = OUT_DT == DT_F32 ? 4 : 2;          // bytes per o element
+  __shared__ __align__(16) unsigned char sO[2][kBS * DVT * OS];   // o tile [token][column], out format
 
   const int tid = threadIdx.x;
   const int lane = tid & 63;
@@ -195,7 +193,7 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
     constexpr bool STATE = R & kRoleState, OUT = R & kRoleOut, ZS = R & kRoleZ;
     const int sw = wave & 3;             // state rows 32 sw .. (STATE)
     constexpr int NOB = kOutBlocks;
-    const int m0 = NOB == 2 ? 2 * (wave & 1) : (wave & 3);   // output row blocks m0 .. m0 + NOB - 1 (OUT)
+    const int m0 = 2 * (wave & 1);       // output row blocks m0 .. m0 + NOB - 1 (OUT)
     const int u = wave & 1;              // Z token half (ZS)
 
     // ---- record fragments: double-buffered by chunk parity (refilled two
@@ -362,26 +360,40 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
                 mfma_f16(fr[1], bop(sZ[b], ZP, nn, 32), zero4()) * iv.y;
       }
     };
-    // o tile of chunk nc straight from the D layout: row 16m + 4lq + e, column
-    // d0 + 16nn + lr (16 lanes cover one row's 16 contiguous columns), through a
-    // buffer resource that ends at the call's last token (rows past a ragged
-    // end are dropped by the hardware, no branch)
-    constexpr int OS = OUT_DT == DT_F32 ? 4 : 2;
-    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
-        static_cast<char*>(o) + tok_base * DV * OS, 0, static_cast<int>(n_tok * H * DV * OS), kBufWord3);
-    auto store_o = [&](int nc, int m, const f32x4* Ot) {
+    // The o tile of a chunk goes to LDS (output waves, from the D layout: row
+    // 16m + 4lq + e, column 16nn + lr) and from there to HBM one chunk later,
+    // from the Z staging waves, as 16-byte row pieces. Stores and loads retire
+    // in order, so stores issued by the output waves would hold up their record
+    // refills behind the writes; the staging waves have two chunks of slack.
+    auto put_o = [&](int b, int m, const f32x4* Ot) {
 #pragma unroll
       for (int e = 0; e < 4; ++e) {
-        const int off = ((nc * kBS + 16 * m + 4 * lq + e) * H + h) * DV + d0 + lr;
+        const int row = 16 * m + 4 * lq + e;
 #pragma unroll
         for (int nn = 0; nn < NT; ++nn) {
+          const int el = row * DVT + 16 * nn + lr;
           if constexpr (OUT_DT == DT_F32)
-            __builtin_amdgcn_raw_buffer_store_b32(__float_as_uint(Ot[nn][e]), ro, (off + 16 * nn) * 4, 0, 0);
+            reinterpret_cast<float*>(sO[b])[el] = Ot[nn][e];
           else if constexpr (OUT_DT == DT_BF16)
-            __builtin_amdgcn_raw_buffer_store_b16(f32_to_bf16_bits(Ot[nn][e]), ro, (off + 16 * nn) * 2, 0, 0);
+            reinterpret_cast<unsigned short*>(sO[b])[el] = f32_to_bf16_bits(Ot[nn][e]);
           else
-            __builtin_amdgcn_raw_buffer_store_b16(f32_to_f16_bits(Ot[nn][e]), ro, (off + 16 * nn) * 2, 0, 0);
+            reinterpret_cast<unsigned short*>(sO[b])[el] = f32_to_f16_bits(Ot[nn][e]);
         }
+      }
+    };
+    // through a buffer resource that ends at the call's last token: rows past a
+    // ragged end are dropped by the hardware, no branch
+    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+        static_cast<char*>(o) + tok_base * DV * OS, 0, static_cast<int>(n_tok * H * DV * OS), kBufWord3);
+    constexpr int RU = DVT * OS / 16;               // 16-byte units per token row
+    auto flush_o = [&](int b, int nc) {              // token rows 32u .. 32u+31 of chunk nc
+#pragma unroll
+      for (int it = 0; it < 32 * RU / 64; ++it) {
+        const int e = lane + 64 * it;
+        const int tt = 32 * u + e / RU, pc = e % RU;
+        const u32x4 x = *reinterpret_cast<const u32x4*>(&sO[b][(tt * RU + pc) * 16]);
+        const int off = (((nc * kBS + tt) * H + h) * DV + d0) * OS + 16 * pc;
+        __builtin_amdgcn_raw_buffer_store_b128(x, ro, off, 0, 0);
       }
     };
 
@@ -444,6 +456,7 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
         // the staging waves issue no other loads, so the wait is for those alone
         put_z(ph ^ 1, ph ^ 1);
         fetch_z(ph ^ 1, nc + 3);
+        if (nc > 0) flush_o(ph ^ 1, nc - 1);
       }
       if constexpr (OUT) {
 #pragma unroll
@@ -457,7 +470,7 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
           for (int kk = 0; kk < 2; ++kk) fmz[p][i][kk] = frag(rp, L::moz_frag(m0 + i, kk));
 #pragma unroll
           for (int nn = 0; nn < NT; ++nn) Ot[nn] = P[nn] * sc[p].z + Q[nn] * sc[p].w;   // SCM_QP, SCM_MOZ
-          store_o(nc, m0 + i, Ot);
+          put_o(ph, m0 + i, Ot);
         }
       }
       if constexpr (STATE || OUT) sc[p] = vload_f4(reinterpret_cast<const float*>(rp + L::SC_OFF));
@@ -472,6 +485,7 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
       step(P1{}, nc + 1);
     }
     if (nc < NC) step(P0{}, nc);
+    if constexpr (ZS) flush_o((NC - 1) & 1, NC - 1);
 
     if constexpr (STATE) {
 #pragma unroll
@@ -487,7 +501,7 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
   };
 
   if (wave < 4) run(std::integral_constant<int, kRoleState>{});
-  else if (wave < 6) run(std::integral_constant<int, kOutBlocks == 2 ? kRoleZ : (kRoleZ | kRoleOut)>{});
+  else if (wave < 6) run(std::integral_constant<int, kRoleZ>{});
   else run(std::integral_constant<int, kRoleOut>{});
 }
 
