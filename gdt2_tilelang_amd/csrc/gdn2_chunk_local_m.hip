@@ -137,18 +137,16 @@ __device__ __forceinline__ void unpack_f16x8(const uint4& r, float* x) {
 
 // four floats times `inv` -> four packed fp16 (round to nearest even)
 __device__ __forceinline__ uint2 pack_f16x4(const f32x4& x, float inv) {
-  const unsigned short a = f32_to_f16_bits(x[0] * inv), b = f32_to_f16_bits(x[1] * inv);
-  const unsigned short c = f32_to_f16_bits(x[2] * inv), d = f32_to_f16_bits(x[3] * inv);
-  return make_uint2(static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16),
-                    static_cast<uint32_t>(c) | (static_cast<uint32_t>(d) << 16));
+  return make_uint2(pack2_f16(x[0], x[1], inv), pack2_f16(x[2], x[3], inv));
 }
 
 // eight floats times eight per-channel factors -> eight packed fp16
+__device__ __forceinline__ uint32_t pack2v_f16(float a, float fa, float b, float fb) {
+  return pack2_f16(a * fa, b * fb, 1.f);
+}
 __device__ __forceinline__ uint4 pack_f16x8v(const float* x, const float* f) {
-  float y[8];
-#pragma unroll
-  for (int j = 0; j < 8; ++j) y[j] = x[j] * f[j];
-  return pack_f16x8(y, 1.f);
+  return make_uint4(pack2v_f16(x[0], f[0], x[1], f[1]), pack2v_f16(x[2], f[2], x[3], f[3]),
+                    pack2v_f16(x[4], f[4], x[5], f[5]), pack2v_f16(x[6], f[6], x[7], f[7]));
 }
 
 // max over the 64 lanes of a wave, VALU only (rotations within rows of 16,

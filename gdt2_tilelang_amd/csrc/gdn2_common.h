@@ -125,16 +125,20 @@ __device__ __forceinline__ float fp16_range_scale(float bound) {
   return __uint_as_float(static_cast<uint32_t>(127 + e) << 23);
 }
 
+// a * s (low half) and b * s (high half) as packed fp16, rounded to nearest
+// even: a vector conversion, which gfx950 does in one v_cvt_pk_f16_f32 where
+// two scalar conversions take four instructions
+typedef _Float16 f16x2v __attribute__((ext_vector_type(2)));
+typedef float f32x2c __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t pack2_f16(float a, float b, float s) {
+  const f32x2c x = {a * s, b * s};
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector(x, f16x2v));
+}
+
 // Eight floats times `inv` -> eight fp16 (round to nearest even), packed.
 __device__ __forceinline__ uint4 pack_f16x8(const float* x, float inv) {
-  uint32_t r[4];
-#pragma unroll
-  for (int j = 0; j < 4; ++j) {
-    const unsigned short a = __builtin_bit_cast(unsigned short, static_cast<_Float16>(x[2 * j] * inv));
-    const unsigned short b = __builtin_bit_cast(unsigned short, static_cast<_Float16>(x[2 * j + 1] * inv));
-    r[j] = static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16);
-  }
-  return make_uint4(r[0], r[1], r[2], r[3]);
+  return make_uint4(pack2_f16(x[0], x[1], inv), pack2_f16(x[2], x[3], inv), pack2_f16(x[4], x[5], inv),
+                    pack2_f16(x[6], x[7], inv));
 }
 
 // Eight packed fp16 -> exact bf16 hi + lo (hi keeps the top 8 significant bits,
