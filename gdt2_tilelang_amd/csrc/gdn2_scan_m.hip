@@ -78,10 +78,7 @@ __device__ __forceinline__ float col_scale(float mx, float* inv) {
 
 // A D-layout quad (4 consecutive k of one column) times sc as fp16 (round to nearest even).
 __device__ __forceinline__ void put_quad_f16(unsigned short* dst, const f32x4& x, float sc) {
-  const unsigned short a = f32_to_f16_bits(x[0] * sc), b = f32_to_f16_bits(x[1] * sc);
-  const unsigned short c = f32_to_f16_bits(x[2] * sc), d = f32_to_f16_bits(x[3] * sc);
-  *reinterpret_cast<uint2*>(dst) = make_uint2(static_cast<uint32_t>(a) | (static_cast<uint32_t>(b) << 16),
-                                              static_cast<uint32_t>(c) | (static_cast<uint32_t>(d) << 16));
+  *reinterpret_cast<uint2*>(dst) = make_uint2(pack2_f16(x[0], x[1], sc), pack2_f16(x[2], x[3], sc));
 }
 
 // Four floats at p with a vector load. The zero offset comes from a VGPR, so
