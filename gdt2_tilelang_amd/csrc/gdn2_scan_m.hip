@@ -178,8 +178,19 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
   const unsigned short* rec0 = ws + slot0 * L::STRIDE;
   const int last = NC - 1;
   auto recp = [&](int c) { return rec0 + static_cast<size_t>(min(c, last)) * L::STRIDE; };
+  // record accesses through a resource per chunk record: the per-lane part of
+  // the address is one VGPR and the field offset a scalar, so no vector address
+  // arithmetic per load
+  auto rrs = [&](const unsigned short* rec) {
+    return __builtin_amdgcn_make_buffer_rsrc(const_cast<unsigned short*>(rec), 0, static_cast<int>(L::STRIDE * 2),
+                                             kBufWord3);
+  };
+  const int lane16 = lane * 16;
   auto frag = [&](const unsigned short* rec, long off) {
-    return *reinterpret_cast<const uint4*>(rec + off + lane * 8);
+    return __builtin_bit_cast(uint4, __builtin_amdgcn_raw_buffer_load_b128(rrs(rec), lane16, static_cast<int>(off * 2), 0));
+  };
+  auto rec_f4 = [&](const unsigned short* rec, long off, int voff) {   // four floats at element off, lane byte offset voff
+    return __builtin_bit_cast(float4, __builtin_amdgcn_raw_buffer_load_b128(rrs(rec), voff, static_cast<int>(off * 2), 0));
   };
   auto bop = [&](const unsigned short* a, int pitch, int nn, int k0) {
     return *reinterpret_cast<const uint4*>(&a[(16 * nn + lr) * pitch + k0 + 8 * lq]);
@@ -210,8 +221,7 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
           for (int kk = 0; kk < KT; ++kk) fm[p][t][kk] = frag(rec, L::m_frag(2 * sw + t, kk));
 #pragma unroll
           for (int kk = 0; kk < 2; ++kk) fka[p][t][kk] = frag(rec, L::ka_frag(2 * sw + t, kk));
-          gam[p][t] = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(rec + L::GL_OFF) +
-                                                        32 * sw + 16 * t + 4 * lq);
+          gam[p][t] = rec_f4(rec, L::GL_OFF, (32 * sw + 16 * t + 4 * lq) * 4);
         }
       }
       if constexpr (OUT) {
@@ -223,7 +233,7 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
           for (int kk = 0; kk < 2; ++kk) fmz[p][i][kk] = frag(rec, L::moz_frag(m0 + i, kk));
         }
       }
-      sc[p] = vload_f4(reinterpret_cast<const float*>(rec + L::SC_OFF));
+      sc[p] = rec_f4(rec, L::SC_OFF, 0);
     };
 
     // ---- Z staging (waves 4, 5: token rows 32u .. 32u+31; lane e = (token,
@@ -443,8 +453,7 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
             S[t][nn][2] = S[t][nn][2] * g4.z - X[nn][2] * smm + Y[nn][2] * ska;
             S[t][nn][3] = S[t][nn][3] * g4.w - X[nn][3] * smm + Y[nn][3] * ska;
           }
-          gam[p][t] = *reinterpret_cast<const float4*>(reinterpret_cast<const float*>(rp + L::GL_OFF) +
-                                                         32 * sw + 16 * t + 4 * lq);
+          gam[p][t] = rec_f4(rp, L::GL_OFF, (32 * sw + 16 * t + 4 * lq) * 4);
         }
         put_state(ph ^ 1);
       }
@@ -470,7 +479,7 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
           put_o(ph, m0 + i, Ot);
         }
       }
-      if constexpr (STATE || OUT) sc[p] = vload_f4(reinterpret_cast<const float*>(rp + L::SC_OFF));
+      if constexpr (STATE || OUT) sc[p] = rec_f4(rp, L::SC_OFF, 0);
       __syncthreads();
     };
 
