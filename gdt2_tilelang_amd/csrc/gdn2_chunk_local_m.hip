@@ -88,16 +88,17 @@ __device__ __forceinline__ float row_shr(float x) {
 }
 
 // Eight consecutive input elements in their storage format, expanded on use.
+// Nontemporal loads: each input is read once, and should not displace records.
 template <int IN_DT>
 struct Raw8 {
   u32x4 a, b;   // b only used for fp32
   __device__ __forceinline__ void load(const void* base, size_t idx) {
     if constexpr (IN_DT == DT_F32) {
       const u32x4* p = reinterpret_cast<const u32x4*>(static_cast<const float*>(base) + idx);
-      a = p[0];
-      b = p[1];
+      a = __builtin_nontemporal_load(p);
+      b = __builtin_nontemporal_load(p + 1);
     } else {
-      a = *reinterpret_cast<const u32x4*>(static_cast<const unsigned short*>(base) + idx);
+      a = __builtin_nontemporal_load(reinterpret_cast<const u32x4*>(static_cast<const unsigned short*>(base) + idx));
     }
   }
   __device__ __forceinline__ void zero() {
@@ -212,7 +213,11 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
   unsigned short* sMozF = reinterpret_cast<unsigned short*>(smem + MOZF_OFF);
   unsigned short* sKaF = reinterpret_cast<unsigned short*>(smem + KAF_OFF);
 
-  const int ch = blockIdx.x;
+  // workgroups run chunk-major from the last chunk back, so the records the scan
+  // reads first (chunk 0 of every head) are written last and are still in the
+  // last-level cache when it starts
+  const int nbh = static_cast<int>(gridDim.x) / NC;
+  const int ch = static_cast<int>(blockIdx.x % nbh) * NC + (NC - 1 - static_cast<int>(blockIdx.x / nbh));
   const int bh = ch / NC;
   const int n = ch % NC;
   const int bi = bh / H;
