@@ -33,6 +33,7 @@
 // that XCD's L2.
 #include "gdn2_common.h"
 #include "gdn2_prefill_layout.h"
+#include "gdn2_scan_tile.h"
 
 #include <type_traits>
 
@@ -42,68 +43,9 @@ namespace scm {
 
 constexpr int DK = 128;
 constexpr int KT = DK / 32;          // 32-row k blocks of S = state waves
-constexpr int kBufWord3 = 0x00020000;   // raw (untyped) buffer resource, gfx9 family
-typedef uint32_t u32x2v __attribute__((ext_vector_type(2)));
+using namespace sct;
 constexpr int kWaves = 8;
 constexpr int kThreads = 64 * kWaves;
-
-typedef _Float16 f16x8 __attribute__((ext_vector_type(8)));
-
-__device__ __forceinline__ f32x4 mfma_f16(const uint4& a, const uint4& b, f32x4 c) {
-  return __builtin_amdgcn_mfma_f32_16x16x32_f16(__builtin_bit_cast(f16x8, a), __builtin_bit_cast(f16x8, b), c,
-                                                0, 0, 0);
-}
-
-// max |x| over the column of a D-layout 16 x 16 tile (lane (lq, lr) holds rows
-// 4lq .. 4lq+3 of column lr); every lane of the column gets it.
-__device__ __forceinline__ float tile_col_max(const f32x4& x) {
-  float m = fmaxf(fmaxf(fabsf(x[0]), fabsf(x[1])), fmaxf(fabsf(x[2]), fabsf(x[3])));
-  uint32_t u = __float_as_uint(m);
-  const auto r32 = __builtin_amdgcn_permlane32_swap(u, u, false, false);
-  m = fmaxf(__uint_as_float(r32[0]), __uint_as_float(r32[1]));
-  u = __float_as_uint(m);
-  const auto r16 = __builtin_amdgcn_permlane16_swap(u, u, false, false);
-  return fmaxf(__uint_as_float(r16[0]), __uint_as_float(r16[1]));
-}
-
-// 2^s putting mx in [2^14, 2^15) (s clamped to +-126: a zero column stays
-// zero); *inv = 2^-s exactly.
-__device__ __forceinline__ float col_scale(float mx, float* inv) {
-  const int ex = static_cast<int>((__float_as_uint(mx) >> 23) & 0xffu);
-  int se = 141 - ex;
-  se = se < -126 ? -126 : (se > 126 ? 126 : se);
-  *inv = __uint_as_float(static_cast<uint32_t>(127 - se) << 23);
-  return __uint_as_float(static_cast<uint32_t>(127 + se) << 23);
-}
-
-// A D-layout quad (4 consecutive k of one column) times sc as fp16 (round to nearest even).
-__device__ __forceinline__ void put_quad_f16(unsigned short* dst, const f32x4& x, float sc) {
-  *reinterpret_cast<uint2*>(dst) = make_uint2(pack2_f16(x[0], x[1], sc), pack2_f16(x[2], x[3], sc));
-}
-
-// Four floats at p with a vector load. The zero offset comes from a VGPR, so
-// the load cannot become a scalar-cache load: a scalar load returning out of
-// order with LDS traffic would make every LDS wait in the chunk loop also
-// wait for it (one memory round trip per chunk).
-__device__ __forceinline__ float4 vload_f4(const float* p) {
-  int z;
-  asm volatile("v_mov_b32 %0, 0" : "=v"(z));
-  return *reinterpret_cast<const float4*>(p + z);
-}
-
-template <int DT>
-__device__ __forceinline__ float load_elem_t(const void* p, size_t i) {
-  if constexpr (DT == DT_F32) return static_cast<const float*>(p)[i];
-  else if constexpr (DT == DT_BF16) return bf16_bits_to_f32(static_cast<const unsigned short*>(p)[i]);
-  else return f16_bits_to_f32(static_cast<const unsigned short*>(p)[i]);
-}
-
-template <int DT>
-__device__ __forceinline__ void store_elem_t(void* p, size_t i, float x) {
-  if constexpr (DT == DT_F32) static_cast<float*>(p)[i] = x;
-  else if constexpr (DT == DT_BF16) static_cast<unsigned short*>(p)[i] = f32_to_bf16_bits(x);
-  else static_cast<unsigned short*>(p)[i] = f32_to_f16_bits(x);
-}
 
 constexpr int kRoleState = 1, kRoleOut = 2, kRoleZ = 4;
 constexpr int kOutBlocks = 2;        // output row blocks per output wave
@@ -285,7 +227,8 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
     // Z = w * v from register buffer rb -> Z^T buffer zb, each column of the
     // wave's 32-token block at its own scale. The lanes of column quad cq are
     // those with lane % CQ == cq (over every it): a rotate within rows of 16
-    // (CQ = 4: by 4 and 8; CQ = 8: by 8) and the 16- / 32-lane swaps.
+    // (CQ = 4: by 4 and 8; CQ = 8: by 8), then the 16-lane (CQ <= 16) and
+    // 32-lane swaps.
     auto put_z = [&](int rbf, int zb) {
       if constexpr (ZS) {
         float z[ZQ][4];
@@ -302,17 +245,7 @@ __global__ __launch_bounds__(scm::kThreads) void scan_m_kernel(
           float r = 0.f;
 #pragma unroll
           for (int it = 0; it < ZQ; ++it) r = fmaxf(r, fabsf(z[it][q]));
-          if constexpr (CQ == 4)
-            r = fmaxf(r, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, r), 0x124,
-                                                                               0xf, 0xf, false)));   // row_ror:4
-          r = fmaxf(r, __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, r), 0x128,
-                                                                             0xf, 0xf, false)));     // row_ror:8
-          uint32_t uu = __float_as_uint(r);
-          const auto a16 = __builtin_amdgcn_permlane16_swap(uu, uu, false, false);
-          r = fmaxf(__uint_as_float(a16[0]), __uint_as_float(a16[1]));
-          uu = __float_as_uint(r);
-          const auto a32 = __builtin_amdgcn_permlane32_swap(uu, uu, false, false);
-          r = fmaxf(__uint_as_float(a32[0]), __uint_as_float(a32[1]));
+          r = quad_group_max<CQ>(r);
           float inv;
           const float scl = col_scale(r, &inv);
 #pragma unroll
@@ -524,9 +457,18 @@ static hipError_t launch_scan_m_t(const void* v, const void* w, const unsigned s
 
 int scan_nt_for(int B, int H, int DV);
 
+hipError_t launch_scan_q(const void* v, const void* w, int in_dt, const unsigned short* ws, const float* s_in,
+                         float* s_out, void* o, int out_dt, int B, int H, int HK, int DV, long s_alloc, long t0,
+                         int NC, long n_tok, hipStream_t stream);
+
 hipError_t launch_scan_m(const void* v, const void* w, int in_dt, const unsigned short* ws, const float* s_in,
                          float* s_out, void* o, int out_dt, int B, int H, int HK, int DV, long s_alloc, long t0,
                          int NC, long n_tok, Varlen vl, hipStream_t stream) {
+  // Past 512 16-column tiles a one-tile workgroup per CU takes several rounds;
+  // four tiles per workgroup (gdn2_scan_q.hip) then fetch each record fragment
+  // once for four tiles (B=8 H=16 DV=128: 244 against 310 us)
+  if (!vl.cu && DV % 64 == 0 && static_cast<long>(B) * H * (DV / 16) > 512)
+    return launch_scan_q(v, w, in_dt, ws, s_in, s_out, o, out_dt, B, H, HK, DV, s_alloc, t0, NC, n_tok, stream);
   const int nt = scan_nt_for(B, H, DV);
 #define GDN2_SCANM_CASE(NTV, DTV, ODV)                                                                     \
   if (nt == NTV && in_dt == DTV && out_dt == ODV)                                                          \

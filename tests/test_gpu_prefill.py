@@ -51,12 +51,21 @@ def test_prefill_matches_oracle(B, S, H, DK, DV):
     _check(B, S, H, DK, DV)
 
 
-@pytest.mark.parametrize("B,H,DK,DV", [(1, 66, 128, 128), (2, 34, 64, 128), (1, 130, 64, 64)])
-def test_prefill_two_value_tiles_per_workgroup(B, H, DK, DV):
-    """Enough heads (B*H*DV/16 > 512) that the scan gives each workgroup two
-    16-column value tiles, where every thread stages Z."""
+@pytest.mark.parametrize("B,H,DK,DV,dtype", [
+    (1, 66, 128, 128, torch.bfloat16), (1, 66, 128, 128, torch.float32), (1, 88, 128, 96, torch.bfloat16),
+    (2, 34, 64, 128, torch.bfloat16), (1, 130, 64, 64, torch.bfloat16)])
+def test_prefill_several_value_tiles_per_workgroup(B, H, DK, DV, dtype):
+    """Enough heads (B*H*DV/16 > 512) that the scan gives each workgroup
+    several 16-column value tiles: four at DK = 128 with DV % 64 == 0
+    (gdn2_scan_q.hip, eight waves), two otherwise. The bf16 output of the
+    four-tile scan is the fp32 one rounded."""
     assert B * H * DV // 16 > 512
-    _check(B, 192, H, DK, DV)
+    dev, o, st = _check(B, 192, H, DK, DV, dtype=dtype, seed=3)
+    if DK == 128 and DV % 64 == 0:
+        ob, sb = gdn2_prefill(*dev, seeded_state(B, H, DK, DV).cuda(), config=GDN2Config(output_dtype=torch.bfloat16))
+        torch.cuda.synchronize()
+        assert ob.dtype == torch.bfloat16
+        assert torch.equal(ob, o.to(torch.bfloat16)) and torch.equal(sb, st)
 
 
 @pytest.mark.parametrize("decay_scale", [0.0, 1.0, 8.0, 30.0])
@@ -135,7 +144,7 @@ def test_gdn2_attention_and_chunk_fwd():
     assert o16.dtype == torch.bfloat16 and o16.shape == (B, S, H, D)
 
 
-@pytest.mark.parametrize("DK,H,HK", [(128, 8, 4), (64, 6, 2), (128, 4, 1)])
+@pytest.mark.parametrize("DK,H,HK", [(128, 8, 4), (64, 6, 2), (128, 4, 1), (128, 72, 8)])
 def test_grouped_heads_equal_repeated(DK, H, HK):
     """q, k, b, g on HK key heads with v, w on H value heads must give exactly
     what the reference's repeat_interleave expansion gives (attention.py:
