@@ -513,7 +513,8 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
   }
   __syncthreads();   // #3: Aqk, Akk; the column operands are dead
 
-  // ---- C: Ai = (I + Akk)^-1 (tiles column-major in sXT) ------------------------------
+  // ---- C: Ai = (I + Akk)^-1 (tiles column-major in sXT): the diagonal inverses,
+  //      then wave j walks down column block j, X_ij = -X_ii sum_k A_ik X_kj ------
   float mai = 0.f;   // max |Ai| over what this wave computes
   if (lane < 16) {
     const float* A = sAkk + pair_idx(wave, wave) * TF;
@@ -578,13 +579,15 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
             make_float4(-R[0], -R[1], -R[2], -R[3]);
         mai = fmaxf(mai, fmaxf(fmaxf(fabsf(R[0]), fabsf(R[1])), fmaxf(fabsf(R[2]), fabsf(R[3]))));
       }
-      if (d == 3) {
-        mai = wave_max(mai);
-        if (lane == 0) sMax[4 * wave + 3] = mai;
-      }
-      __syncthreads();
+      // the next sub-diagonal of column block j reads only this wave's results
+      // above it and the diagonal inverses: no workgroup barrier, but the
+      // compiler must keep this step's LDS stores ahead of the next step's loads
+      asm volatile("" ::: "memory");
     }
+    mai = wave_max(mai);
+    if (lane == 0) sMax[4 * wave + 3] = mai;
   }
+  __syncthreads();
 
   // ---- D: MOZ = Aqk Ai and KA = KG^T Ai (transposed: Ai^T as the A operand) ------------
   mai = fmaxf(fmaxf(sMax[3], sMax[7]), fmaxf(sMax[11], sMax[15]));   // max |Ai|
