@@ -77,6 +77,8 @@ size_t gdn2_hip_prefill_workspace_bytes(int B, int HK, int DK, long n_tokens) {
   const long rec = record_elems(DK);
   if (rec == 0 || B < 1 || HK < 1 || n_tokens < 0) return 0;
   const long nc = (n_tokens + gdn2::kBS - 1) / gdn2::kBS;
+  if (gdn2::use_pair_records(B, HK, DK, n_tokens, false))
+    return static_cast<size_t>(B) * HK * ((nc + 1) / 2) * gdn2::ChunkLayoutP::STRIDE * 2;
   return static_cast<size_t>(B) * HK * nc * rec * 2;
 }
 
@@ -130,8 +132,9 @@ int gdn2_hip_prefill_chunks(const void* q, const void* k, const void* v, const f
 }
 
 size_t gdn2_hip_prefill_varlen_workspace_bytes(int nseq, int HK, int DK, long T) {
-  if (nseq < 1 || T < 0) return 0;
-  return gdn2_hip_prefill_workspace_bytes(1, HK, DK, varlen_slots(nseq, T) * gdn2::kBS);
+  const long rec = record_elems(DK);
+  if (nseq < 1 || T < 0 || rec == 0 || HK < 1) return 0;
+  return static_cast<size_t>(HK) * varlen_slots(nseq, T) * rec * 2;   // chunk records
 }
 
 int gdn2_hip_prefill_varlen(const void* q, const void* k, const void* v, const float* g,

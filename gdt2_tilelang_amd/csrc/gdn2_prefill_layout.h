@@ -96,6 +96,69 @@ struct ChunkLayoutM {
 
 static_assert((ChunkLayoutM<128>::STRIDE * 2) % 256 == 0, "record must keep 256-byte alignment");
 
+// Pair record (DK = 128): the transition of two consecutive 64-token chunks a, b
+// as one 128-token step of the scan, in the same form
+//
+//   S <- diag(gamma) S - M S + KA Z        o = QP S + MOZ Z       (Z: 128 tokens)
+//
+// With A_c = diag(gamma_c) - M_c the transition of chunk c, composing
+// S_b = A_b (A_a S + KA_a Z_a) + KA_b Z_b and o_b = QP_b (A_a S + KA_a Z_a) + MOZ_b Z_b:
+//
+//   gamma = gamma_a gamma_b       M = gamma_b M_a + M_b gamma_a - M_b M_a
+//   KA  = [ gamma_b KA_a - M_b KA_a | KA_b ]
+//   QP  = [ QP_a ; QP_b gamma_a - QP_b M_a ]
+//   MOZ = [ MOZ_a  0 ; QP_b KA_a  MOZ_b ]
+//
+// (gamma_b M_a scales rows, M_b gamma_a columns). Fragments as above, each
+// block with its own power-of-two scale:
+//
+//   M   [8 m][4 kk]   / SC[0]
+//   KA  [8 m][4 kk]   kk 0-1: tokens of a / SC[1], kk 2-3: tokens of b / SC[2]
+//   QP  [8 m][4 kk]   m 0-3: tokens of a / SC[3],  m 4-7: tokens of b / SC[4]
+//   MOZ m 0-3: [kk 0-1] / SC[5];  m 4-7: [kk 0-1] / SC[6], [kk 2-3] / SC[7]
+//       (the zero block above the diagonal is not stored)
+//   GL  [DK] fp32 gamma;  SC [8] fp32
+enum RecordScaleP : int {
+  SCP_M = 0, SCP_KAL = 1, SCP_KAR = 2, SCP_QPT = 3, SCP_QPB = 4, SCP_MOZTL = 5, SCP_MOZLL = 6, SCP_MOZBR = 7
+};
+
+struct ChunkLayoutP {
+  static constexpr int DK = 128;
+  static constexpr int TOK = 2 * kBS;   // tokens per record
+  static constexpr long M_OFF = 0;
+  static constexpr long KA_OFF = M_OFF + 32L * kFrag;
+  static constexpr long QP_OFF = KA_OFF + 32L * kFrag;
+  static constexpr long MOZ_OFF = QP_OFF + 32L * kFrag;
+  static constexpr long GL_OFF = MOZ_OFF + 24L * kFrag;
+  static constexpr long SC_OFF = GL_OFF + 2L * DK;
+  static constexpr long STRIDE = ((SC_OFF + 2L * 8) + 127) / 128 * 128;
+
+  __host__ __device__ static constexpr long m_frag(int m, int kk) { return M_OFF + (m * 4 + kk) * kFrag; }
+  __host__ __device__ static constexpr long ka_frag(int m, int kk) { return KA_OFF + (m * 4 + kk) * kFrag; }
+  __host__ __device__ static constexpr long qp_frag(int m, int kk) { return QP_OFF + (m * 4 + kk) * kFrag; }
+  __host__ __device__ static constexpr long moz_frag(int m, int kk) {
+    return MOZ_OFF + (m < 4 ? m * 2 + kk : 8 + (m - 4) * 4 + kk) * kFrag;
+  }
+};
+
+static_assert((ChunkLayoutP::STRIDE * 2) % 256 == 0, "record must keep 256-byte alignment");
+
+// Which record form a DK = 128 call uses; the chunk-local and scan entry points
+// decide it from the arguments both receive. Pair records halve the scan's
+// serial steps but cost the chunk-local stage more (two chunks and their
+// composition in one workgroup, one per CU); they pay off where the scan has
+// fewer workgroups than the GPU has CUs, so they are used for dense calls of
+// up to 16 key heads (at most 128 16-column value tiles per key head group of
+// DV = 128) and at least 32 chunks: a short call's chunk-local stage runs as
+// few workgroups whose latency the pair form lengthens, while its scan has few
+// steps to save. Chunk records for packed batches and the other calls.
+constexpr long kPairMaxKeyHeads = 16;
+constexpr long kPairMinChunks = 32;
+inline bool use_pair_records(int B, int HK, int DK, long n_tokens, bool varlen) {
+  return !varlen && DK == 128 && static_cast<long>(B) * HK <= kPairMaxKeyHeads &&
+         (n_tokens + kBS - 1) / kBS >= kPairMinChunks;
+}
+
 // Packed variable-length batches (cu_seqlens). Sequence s holds tokens
 // [cu[s], cu[s+1]) of one [T, H, D] allocation and its chunk c (64 tokens, the
 // last one possibly ragged) has the record slot  s + floor(cu[s] / 64) + c.

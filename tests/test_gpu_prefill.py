@@ -24,6 +24,13 @@ from tests.helpers import device_inputs, seeded_state
 
 pytestmark = pytest.mark.gpu
 rel_err = oracle.rel_err
+
+
+def pair_form(B, HK, n):
+    """Dense DK = 128 calls of up to 16 key heads and at least 32 chunks run on
+    pair records (two chunks per scan step)."""
+    return B * HK <= 16 and (n + 63) // 64 >= 32
+
 TOL = 2e-3
 F32 = GDN2Config(output_dtype=torch.float32)
 GOLDEN = os.path.join(os.path.dirname(__file__), "golden", "config0.npz")
@@ -66,6 +73,17 @@ def test_prefill_several_value_tiles_per_workgroup(B, H, DK, DV, dtype):
         torch.cuda.synchronize()
         assert ob.dtype == torch.bfloat16
         assert torch.equal(ob, o.to(torch.bfloat16)) and torch.equal(sb, st)
+
+
+@pytest.mark.parametrize("decay_scale,DV,dtype", [
+    (0.3, 128, torch.bfloat16), (4.0, 128, torch.bfloat16), (30.0, 128, torch.bfloat16),
+    (4.0, 64, torch.float32), (1.0, 32, torch.float16)])
+def test_prefill_pair_records(decay_scale, DV, dtype):
+    """Long calls of few key heads run the scan on pair records: 33 chunks (an
+    odd count, so the last pair's second chunk is all padding) with a ragged
+    last chunk of 52 rows, across the decay regimes of the chunk bodies."""
+    assert pair_form(1, 2, 2100)
+    _check(1, 2100, 2, 128, DV, dtype=dtype, decay_scale=decay_scale, seed=7)
 
 
 @pytest.mark.parametrize("decay_scale", [0.0, 1.0, 8.0, 30.0])
@@ -166,7 +184,14 @@ def test_grouped_heads_equal_repeated(DK, H, HK):
     d1 = gdn2_decode(q[:, S:], k[:, S:], v[:, S:], g[:, S:], b[:, S:], w[:, S:], s1)
     d2 = gdn2_decode(qe[:, S:], ke[:, S:], v[:, S:], ge[:, S:], be[:, S:], w[:, S:], s2)
     torch.cuda.synchronize()
-    assert torch.equal(o1, o2) and torch.equal(s1, s2) and torch.equal(d1, d2)
+    if pair_form(B, HK, S) == pair_form(B, H, S) or DK != 128:
+        assert torch.equal(o1, o2) and torch.equal(s1, s2) and torch.equal(d1, d2)
+    else:
+        # long dense DK = 128 calls of up to 16 key heads run on pair records (two chunks per
+        # scan step), wider ones on chunk records: the same algebra, rounded differently
+        for x, y in ((o1, o2), (s1, s2), (d1, d2)):
+            # fp32 prefill results; the decode output is bf16 (one rounding step apart)
+            assert rel_err(x.float().cpu(), y.float().cpu()) < (2e-4 if x.dtype == torch.float32 else 4e-3)
 
 
 @pytest.mark.parametrize("DK,DV", [(64, 64), (128, 64), (128, 16), (64, 48)])

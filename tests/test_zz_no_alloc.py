@@ -45,7 +45,8 @@ def _inputs(B, S, H, HK, DK, DV, seed):
     return (q, k, v, g, b, w)
 
 
-@pytest.mark.parametrize("B,S,H,HK,DK,DV,seed", [(2, 1000, 4, 2, 128, 128, 0), (1, 300, 3, 3, 64, 96, 1)])
+@pytest.mark.parametrize("B,S,H,HK,DK,DV,seed", [(2, 1000, 4, 2, 128, 128, 0), (1, 300, 3, 3, 64, 96, 1),
+                                                (1, 2100, 4, 2, 128, 128, 2)])   # the last on pair records
 def test_noalloc_prefill_equals_workspace_prefill(B, S, H, HK, DK, DV, seed):
     print(f"noalloc prefill B={B} S={S} H={H} HK={HK} DK={DK} DV={DV}", flush=True)
     dev = _inputs(B, S, H, HK, DK, DV, seed)
@@ -73,9 +74,9 @@ def test_noalloc_two_calls_second_smaller():
 
 def test_noalloc_rejects_calls_beyond_the_scratch():
     lib = _hip.lib()
-    per_chunk = lib.gdn2_hip_prefill_workspace_bytes(1, 1, 128, 64)
+    HK = 32                                  # past 16 key heads: one 64-token chunk record each
+    per_chunk = lib.gdn2_hip_prefill_workspace_bytes(1, HK, 128, 64) // HK
     max_chunks = SCRATCH // per_chunk
-    HK = 16
     S_ok = (max_chunks // HK) * 64
     assert lib.gdn2_hip_prefill_workspace_bytes(1, HK, 128, S_ok) <= SCRATCH
     assert lib.gdn2_hip_prefill_workspace_bytes(1, HK, 128, S_ok + 64) > SCRATCH
