@@ -20,10 +20,11 @@
 // Layout. A wave owns 32 value columns and all DK key rows. Lane l = 16k + m
 // holds, for each step s < DK/4, the float pair S[(DK/4) k + s][2m .. 2m+1]:
 // every state access is a dwordx2 whose 16-lane groups cover a 128-byte row
-// segment. Register e of step s is, as it stands, the A operand
-// A[m][k] = S[(DK/4)k + s][2m + e] of the 16x16x4 fp32 MFMA, so the projections
+// segment. The projections
 //   P_e[m][n] = sum_rows S[row][2m + e] V[row][n]      (16 stacked vectors V)
-// run straight off the state registers. The rank-L update is then a VALU pass
+// run straight off the state registers on split-bf16 MFMAs: k step t8 takes
+// the lane's rows (DK/4) k + 8 t8 .. +7 (its own registers) as the K index, so
+// no state value moves between lanes. The rank-L update is then a VALU pass
 // over the same registers (9 FMAs per element per block, against 32 for the
 // per-token form), and in the last block each step is stored as soon as it is
 // final.
@@ -64,7 +65,9 @@ __device__ __forceinline__ f32x4 mfma4(float a, float b, f32x4 c) {
 template <int DK>
 struct Lds {
   static constexpr int RP = DK + 4;          // pitch of [.][row] arrays
-  float vec[16][RP];                         // [n][row]: n<8 e^{c_n} b_n k_n; n>=8 scale e^{c} q
+  static constexpr int BP = DK + 8;          // pitch of the bf16 [.][row] arrays
+  unsigned short vh[16][BP];                 // [n][row] as bf16 hi + lo: n<8 e^{c_n} b_n k_n;
+  unsigned short vl[16][BP];                 //   n>=8 scale e^{c} q
   float kt[TB][RP];                          // e^{c_last - c_t} k_t
   float dl[RP];                              // e^{c_last}
   float cl[TB][RP];                          // c_t in log2 units
@@ -196,8 +199,12 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(
       sm.bk[t][i] = bk;
       sm.qs[t][i] = qs;
       const float ec = fast_exp2(c);
-      sm.vec[t][i] = ec * bk;
-      sm.vec[TB + t][i] = ec * qs;
+      uint32_t h, l;
+      split_pk(ec * bk, ec * qs, h, l);
+      sm.vh[t][i] = static_cast<unsigned short>(h & 0xffffu);
+      sm.vl[t][i] = static_cast<unsigned short>(l & 0xffffu);
+      sm.vh[TB + t][i] = static_cast<unsigned short>(h >> 16);
+      sm.vl[TB + t][i] = static_cast<unsigned short>(l >> 16);
     }
 #pragma unroll
     for (int t = 0; t < TB; ++t) sm.kt[t][i] = fast_exp2(c - cs[t]) * kz[t];
@@ -298,16 +305,24 @@ __global__ __launch_bounds__(256, 2) void decode_mfma_kernel(
     // ---- P_e = (state columns 2m+e)^T V: 16 projections per column (fp32 MFMA),
     // consuming the state rows as they arrive (a wave past DV works on zeros).
     // In the first block the Gram work above runs while the state is in flight.
+    // K index 8kq + j of k step t8 is state row NS*kq + 8t8 + j: eight rows of the
+    // lane's own registers (steps 2t8, 2t8 + 1) against the staged vectors' same
+    // rows, on split-bf16 operands (x = hi + lo, three bf16 MFMAs, ~16 mantissa bits)
     f32x4 P[2][2];
 #pragma unroll
     for (int e = 0; e < 2; ++e) P[e][0] = P[e][1] = zero4();
 #pragma unroll
-    for (int s = 0; s < NS; s += 4) {
-      const f32x4 bv = *reinterpret_cast<const f32x4*>(&sm.vec[m][NS * kq + s]);
+    for (int t8 = 0; t8 < NS / 8; ++t8) {
+      const bf16x8 bh = *reinterpret_cast<const bf16x8*>(&sm.vh[m][NS * kq + 8 * t8]);
+      const bf16x8 bl = *reinterpret_cast<const bf16x8*>(&sm.vl[m][NS * kq + 8 * t8]);
 #pragma unroll
-      for (int ss = 0; ss < 4; ++ss)
-#pragma unroll
-        for (int e = 0; e < 2; ++e) P[e][ss & 1] = mfma4(T[e][s / 4][ss], bv[ss], P[e][ss & 1]);
+      for (int e = 0; e < 2; ++e) {
+        const float x[8] = {T[e][2 * t8][0], T[e][2 * t8][1], T[e][2 * t8][2], T[e][2 * t8][3],
+                            T[e][2 * t8 + 1][0], T[e][2 * t8 + 1][1], T[e][2 * t8 + 1][2], T[e][2 * t8 + 1][3]};
+        bf16x8 ah, al;
+        split_bf16x8(x, ah, al);
+        P[e][t8 & 1] = mfma3(ah, al, bh, bl, P[e][t8 & 1]);
+      }
     }
     if (active) {
       // D layout: lane (kq, m) holds P[col 2(4kq + r) + e][vector m]
