@@ -1,6 +1,7 @@
 // GDN-2 multi-token decode: blocks of up to 8 tokens applied to the
-// register-resident fp32 state, with the state projections on the fp32 matrix
-// cores (v_mfma_f32_16x16x4_f32).
+// register-resident fp32 state, with the state projections on split-bf16
+// matrix cores (v_mfma_f32_16x16x32_bf16, three per product) and the rank-L
+// update on fp32 ones (v_mfma_f32_16x16x4_f32).
 //
 // Same recurrence as gdn2_decode.hip (reference gdn2/inference.py:199-303
 // decode_multi_kernel; torch restatement gdn2/inference.py:337-345), evaluated
