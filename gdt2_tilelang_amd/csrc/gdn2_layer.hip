@@ -39,15 +39,37 @@ __device__ __forceinline__ void st(void* p, long i, float x) {
   else static_cast<unsigned short*>(p)[i] = f32_to_f16_bits(x);
 }
 
-__device__ __forceinline__ float sigmoid(float x) { return 1.f / (1.f + __expf(-x)); }
+// The activations run on the hardware exp2 / log2 / reciprocal (about 1 ulp
+// each) rather than IEEE division and libm calls: the prologue is bound by its
+// per-element VALU work, not by its 34 KiB per token of HBM traffic.
+__device__ __forceinline__ float sigmoid(float x) { return __builtin_amdgcn_rcpf(1.f + __expf(-x)); }
 __device__ __forceinline__ float silu(float x) { return x * sigmoid(x); }
-// torch.nn.functional.softplus with beta = 1, threshold = 20
-__device__ __forceinline__ float softplus(float x) { return x > 20.f ? x : log1pf(__expf(x)); }
+// torch.nn.functional.softplus with beta = 1, threshold = 20; log1p(y) as
+// log(u) * y / (u - 1) with u = 1 + y rounded (exact to rounding of log, and y
+// itself when u rounds to 1)
+__device__ __forceinline__ float softplus(float x) {
+  if (x > 20.f) return x;
+  const float y = __expf(x);
+  const float u = 1.f + y;
+  return u == 1.f ? y : __logf(u) * (y * __builtin_amdgcn_rcpf(u - 1.f));
+}
+
+template <int CTRL>
+__device__ __forceinline__ float dpp(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
+}
 
 // Sum over the `group` consecutive lanes that hold one head (group a power of
-// two <= 64, groups aligned).
+// two <= 64, groups aligned, wave-uniform). Within a row of 16 lanes by DPP:
+// quad_perm swaps of 1 and 2 give every lane its quad's sum, row_half_mirror
+// adds the other quad of its 8, row_mirror the other 8 of its 16; wider groups
+// by lane shuffles.
 __device__ __forceinline__ float group_sum(float x, int group) {
-  for (int off = 1; off < group; off <<= 1) x += __shfl_xor(x, off);
+  if (group > 1) x += dpp<0xb1>(x);    // quad_perm [1, 0, 3, 2]
+  if (group > 2) x += dpp<0x4e>(x);    // quad_perm [2, 3, 0, 1]
+  if (group > 4) x += dpp<0x141>(x);   // row_half_mirror
+  if (group > 8) x += dpp<0x140>(x);   // row_mirror
+  for (int off = 16; off < group; off <<= 1) x += __shfl_xor(x, off);
   return x;
 }
 
@@ -230,7 +252,7 @@ __global__ __launch_bounds__(kProThreads) void prologue_kernel(ProArgs a) {
 #pragma unroll
         for (int e = 0; e < 8; ++e) ss += y[t][e] * y[t][e];
         ss = group_sum(ss, group);
-        const float inv = 1.f / fmaxf(sqrtf(ss), 1e-12f);
+        const float inv = rsqrtf(fmaxf(ss, 1e-24f));   // 1 / max(||y||, 1e-12)
 #pragma unroll
         for (int e = 0; e < 8; ++e) y[t][e] *= inv;
       }
