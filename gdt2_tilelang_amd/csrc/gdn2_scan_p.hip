@@ -438,6 +438,12 @@ __global__ __launch_bounds__(scp::kThreads) void scan_p_kernel(
     }
   };
 
+  // Issue priority: the state waves carry the serial chain (M S, the update, the
+  // hand-off), then the Z staging for the next step; the output waves, whose
+  // products are off the chain, take what issue slots are left. (Measured at
+  // B = 1, H = 16, HK = 8, 8175 tokens: 143 -> 117 us.)
+  if (wave < 4) __builtin_amdgcn_s_setprio(3);
+  else if (wave < 6) __builtin_amdgcn_s_setprio(1);
   if (wave < 4) run(std::integral_constant<int, scp::kRoleState>{});
   else if (wave < 6) run(std::integral_constant<int, scp::kRoleZ>{});
   else run(std::integral_constant<int, scp::kRoleOut>{});
