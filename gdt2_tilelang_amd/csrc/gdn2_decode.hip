@@ -112,7 +112,7 @@ __global__ __launch_bounds__(kDecMaxThreads) void decode_kernel(
   const int rg = lane >> 3;
   const int cg = lane & 7;
   const int c0 = rg * RPT;                                                     // first key row
-  const int col = blockIdx.x * kDecMaxCols + (tid >> 6) * kDecCols + 4 * cg;   // first column
+  const int col = blockIdx.x * (nthr >> 6) * kDecCols + (tid >> 6) * kDecCols + 4 * cg;   // first column
 
   // a wave past the last column (DV not a multiple of 128) only helps staging
   const bool active = col < DV;   // wave-uniform: a wave covers 32 columns, DV % 32 == 0
@@ -234,9 +234,16 @@ static hipError_t launch_decode_t(const void* q, const void* k, const void* v, c
                                   const void* b, const void* w, float* state, void* o, int B,
                                   int H, int HK, int DV, long s_alloc, long t0, int n, float scale,
                                   hipStream_t stream) {
-  // one workgroup per (b, h, up to kDecMaxCols columns); one wave per 32 columns
-  const int tiles = (DV + kDecMaxCols - 1) / kDecMaxCols;
-  const int threads = 64 * (DV < kDecMaxCols ? DV : kDecMaxCols) / kDecCols;
+  // one workgroup per (b, h, up to kDecMaxCols columns); one wave per 32 columns.
+  // A call with fewer such workgroups than the GPU has CUs (a small batch:
+  // B = 1, H = 16 is 16 of them) takes one-wave workgroups of 32 columns
+  // instead, so more CUs stream the state (B = 1, H = 16, D = 128: 64).
+  int tiles = (DV + kDecMaxCols - 1) / kDecMaxCols;
+  int threads = 64 * (DV < kDecMaxCols ? DV : kDecMaxCols) / kDecCols;
+  if (static_cast<long>(B) * H * tiles < 256) {
+    tiles = DV / kDecCols;
+    threads = 64;
+  }
   if (n == 1)
     hipLaunchKernelGGL((decode_kernel<DK, IN_DT, OUT_DT, 1>), dim3(tiles, B * H), dim3(threads), 0,
                        stream, q, k, v, g, b, w, state, o, H, HK, DV, s_alloc, t0, n, scale);
