@@ -60,7 +60,11 @@ int gdn2_hip_decode(const void* q, const void* k, const void* v, const float* g,
 
 /* Bytes of workspace gdn2_hip_chunk_local / gdn2_hip_prefill_chunks need for
  * n_tokens tokens (rounded up to whole 64-token chunks) of B x HK key heads; 0 for an unsupported
- * DK. The records depend on q, k, b, g only, so grouped value heads share them. */
+ * DK. One record per key head and chunk (74 496 B at DK = 128, 41 472 B at DK = 64), except that
+ * dense DK = 128 calls of at most 16 key heads (B * HK <= 16) and at least 32 chunks use one
+ * record per two consecutive chunks (123 648 B), which halves the scan's serial steps. Both stages
+ * derive the form from (B, HK, DK, n_tokens), so they must be called with the same values. The
+ * records depend on q, k, b, g only, so grouped value heads share them. */
 size_t gdn2_hip_prefill_workspace_bytes(int B, int HK, int DK, long n_tokens);
 
 /*
@@ -107,8 +111,8 @@ int gdn2_hip_prefill_chunks(const void* q, const void* k, const void* v, const f
 /*
  * gdn2_hip_prefill_chunks without the workspace argument: the chunk records go
  * to a scratch array the library holds in device memory, one per GPU, of
- * GDN2_NOALLOC_SCRATCH_BYTES (64 MiB: B * HK * ceil(n_tokens / 64) records of
- * 66 304 B at DK = 128, 41 472 B at DK = 64; e.g. 4032 tokens of 16 key heads).
+ * GDN2_NOALLOC_SCRATCH_BYTES (64 MiB of gdn2_hip_prefill_workspace_bytes: e.g.
+ * 1792 tokens of 32 key heads on chunk records, 8576 tokens of 8 key heads on pair records).
  * A larger call returns GDN2_ERR_SCRATCH and launches nothing (prefill it in
  * segments, passing state_out back as state_in). The call allocates nothing:
  * no hipMalloc / hipFree, nothing from a caching allocator, so it can run
