@@ -28,6 +28,8 @@ decay, new conv tail) and ``gdn2_hip_layer_epilogue`` (gated RMSNorm); then
 
 from __future__ import annotations
 
+import ctypes
+
 from dataclasses import dataclass
 
 import torch
@@ -335,6 +337,73 @@ class GatedDeltaNet2(nn.Module):
             "gdn2_hip_layer_epilogue")
         return self._linear(out.reshape(B * S, dv), self.o_proj.weight).view(B, S, -1)
 
+    def _decode_params(self):
+        """The parameters the fused decode reads, looked up through the module
+        dicts (not nn.Module attribute access, which costs ~0.3 us a lookup)."""
+        m = self._modules
+        ps = [m[n]._parameters["weight"] for n in ("q_proj", "k_proj", "v_proj", "b_proj", "w_proj", "f_proj",
+                                                    "o_gate_proj", "o_proj")]
+        if m.get("q_conv") is not None:
+            for n in ("q_conv", "k_conv", "v_conv"):
+                cp = m[n]._modules["conv"]._parameters
+                ps.append(cp["weight"])
+                ps.append(cp["bias"])
+        ps.append(self._parameters["A_log"])
+        ps.append(self._parameters["dt_bias"])
+        ps.append(m["o_norm"]._parameters["weight"])
+        return ps
+
+    def _decode_plan(self, B, n, dt, device):
+        """The static part of a fused decode call for (B, n, dtype, device): the
+        cached weight buffers and the C-ABI arguments that do not change between
+        calls, rebuilt when any parameter is replaced or changed in place.
+        None when the shapes do not qualify."""
+        ps = self._decode_params()
+        key = (B, n, dt, device, tuple(map(id, ps)), tuple(t._version for t in ps))
+        hit = self.__dict__.get("_dec_plan")
+        if hit is not None and hit[0] == key:
+            return hit[1]
+        HK, H, DK, DV = self.num_kv_heads, self.num_heads, self.head_dim_k, self.head_dim_v
+        hid = self.cfg.hidden_size
+        plan = None
+        if not (B * n > 8 or hid % 8 or (H * DV) % 8 or DK % 8 or (DK // 8) & (DK // 8 - 1) or DK > 512
+                or DV % 32 or DK not in (32, 64, 128, 256) or self.o_proj.weight.dtype != dt):
+            w_out = self.o_proj.weight.detach()
+            if w_out.is_contiguous():
+                lib = _hip.lib()
+                code = _hip.dtype_code(dt)
+                ws = torch.empty(lib.gdn2_hip_layer_decode_workspace_bytes(B, n, H, HK, DK, DV, code) + 256,
+                                 dtype=torch.uint8, device=device)
+                w_proj = self._proj_weights()
+                conv_w = conv_b = None
+                K = 0
+                if self.q_conv is not None:
+                    K = self.cfg.conv_size
+                    convs = (self.q_conv.conv, self.k_conv.conv, self.v_conv.conv)
+                    conv_w = self._cat_cached("_convw", [c.weight for c in convs])
+                    if conv_w.dtype != dt:
+                        conv_w = conv_w.to(dt)
+                    if all(c.bias is not None for c in convs):
+                        conv_b = self._cat_cached("_convb", [c.bias for c in convs])
+                        conv_b = conv_b.to(dt).reshape(-1) if conv_b.dtype != dt else conv_b.reshape(-1)
+                alog = self._f32_cached("_alog32", self.A_log)
+                dtb = self._f32_cached("_dtb32", self.dt_bias)
+                onw = self._f32_cached("_onw32", self.o_norm.weight)
+                P = _hip.ptr
+                ws_ptr = (ws.data_ptr() + 255) // 256 * 256
+                plan = dict(
+                    # the parameters are held too, so the ids in the key stay theirs
+                    keep=(ws, w_proj, conv_w, conv_b, alog, dtb, onw, w_out, ps), K=K,
+                    C=2 * HK * DK + H * DV, fn=lib.gdn2_hip_layer_decode,
+                    # arguments between x and conv_in, conv_out and the state, the state and
+                    # out, and after out (gdn2_hip_layer_decode's order)
+                    a1=(P(w_proj), P(conv_w), P(conv_b), K),
+                    a2=(P(alog), P(dtb), float(self.erase_scale)),
+                    a3=(P(onw), float(self.o_norm.eps), P(w_out)),
+                    a4=(ctypes.c_void_p(ws_ptr), code, B, n, hid, H, HK, DK, DV, float(self.scale)))
+        self.__dict__["_dec_plan"] = (key, plan)
+        return plan
+
     def _decode_fused(self, x, cache):
         """A decode call of B*n <= 8 tokens as one library call
         (gdn2_hip_layer_decode: projections, prologue, recurrence, gated norm,
@@ -342,54 +411,34 @@ class GatedDeltaNet2(nn.Module):
         qualify (the caller then takes the per-stage path)."""
         B, n, hid = x.shape
         st = cache.recurrent_state
-        HK, H, DK, DV = self.num_kv_heads, self.num_heads, self.head_dim_k, self.head_dim_v
         dt = x.dtype
-        if (B * n > 8 or hid % 8 or (H * DV) % 8 or DK % 8 or (DK // 8) & (DK // 8 - 1) or DK > 512
-                or DV % 32 or DK not in (32, 64, 128, 256) or st is None or st.dtype != torch.float32
-                or not st.is_contiguous() or tuple(st.shape) != (B, H, DK, DV) or st.device != x.device
-                or self.o_proj.weight.dtype != dt):
+        if (st is None or st.dtype != torch.float32 or not st.is_contiguous() or st.device != x.device
+                or tuple(st.shape) != (B, self.num_heads, self.head_dim_k, self.head_dim_v)):
             return None
-        lib = _hip.lib()
-        code = _hip.dtype_code(dt)
-        key = (B, n, dt, x.device)
-        hit = self.__dict__.get("_dec_ws")
-        if hit is None or hit[0] != key:
-            nbytes = lib.gdn2_hip_layer_decode_workspace_bytes(B, n, H, HK, DK, DV, code)
-            hit = (key, torch.empty(nbytes + 256, dtype=torch.uint8, device=x.device))
-            self.__dict__["_dec_ws"] = hit
-        ws_ptr = (hit[1].data_ptr() + 255) // 256 * 256
-        x2 = x.reshape(B * n, hid).contiguous()
+        plan = self._decode_plan(B, n, dt, x.device)
+        if plan is None:
+            return None
+        x2 = x.reshape(B * n, hid)
+        if not x2.is_contiguous():
+            x2 = x2.contiguous()
         if x2.data_ptr() % 16:
             x2 = x2.clone()
-        w_proj = self._proj_weights()
-        w_out = self.o_proj.weight.detach()
-        if not w_out.is_contiguous():
-            return None
-        conv_w = conv_b = conv_in = conv_out = None
-        K = 0
-        if self.q_conv is not None:
-            K = self.cfg.conv_size
-            convs = (self.q_conv.conv, self.k_conv.conv, self.v_conv.conv)
-            conv_w = self._cat_cached("_convw", [c.weight for c in convs])
-            if conv_w.dtype != dt:
-                conv_w = conv_w.to(dt)
-            if all(c.bias is not None for c in convs):
-                conv_b = self._cat_cached("_convb", [c.bias for c in convs])
-                conv_b = conv_b.to(dt).reshape(-1) if conv_b.dtype != dt else conv_b.reshape(-1)
-            if cache.conv_state is not None:
-                conv_in = cache.conv_state.to(dt).contiguous()
+        conv_in = conv_out = None
+        K = plan["K"]
+        if K:
+            conv_in = cache.conv_state
+            if conv_in is not None and (conv_in.dtype != dt or not conv_in.is_contiguous()
+                                        or conv_in.data_ptr() % 16):
+                conv_in = conv_in.to(dt).contiguous()
                 if conv_in.data_ptr() % 16:
                     conv_in = conv_in.clone()
-            conv_out = torch.empty(B, 2 * HK * DK + H * DV, K - 1, device=x.device, dtype=dt)
+            conv_out = torch.empty(B, plan["C"], K - 1, device=x.device, dtype=dt)
         out = torch.empty(B, n, hid, device=x.device, dtype=dt)
         P = _hip.ptr
-        _hip.check(lib.gdn2_hip_layer_decode(
-            P(x2), P(w_proj), P(conv_w), P(conv_b), K, P(conv_in), P(conv_out),
-            P(self._f32_cached("_alog32", self.A_log)), P(self._f32_cached("_dtb32", self.dt_bias)),
-            float(self.erase_scale), P(st), P(self._f32_cached("_onw32", self.o_norm.weight)),
-            float(self.o_norm.eps), P(w_out), P(out), ws_ptr, code, B, n, hid, H, HK, DK, DV,
-            float(self.scale), _hip.stream_of(x.device)), "gdn2_hip_layer_decode")
-        if self.q_conv is not None:
+        _hip.check(plan["fn"](P(x2), *plan["a1"], P(conv_in), P(conv_out), *plan["a2"], st.data_ptr(),
+                              *plan["a3"], out.data_ptr(), *plan["a4"], _hip.stream_of(x.device)),
+                   "gdn2_hip_layer_decode")
+        if K:
             cache.conv_state = conv_out
         return out
 
@@ -554,6 +603,9 @@ class GatedDeltaNet2(nn.Module):
     @torch.no_grad()
     def decode(self, hidden_states, cache):
         """Decode ``n`` tokens ``[B, n, hidden]``, updating ``cache`` in place."""
+        return self._decode(hidden_states, cache)
+
+    def _decode(self, hidden_states, cache):
         if hidden_states.is_cuda:
             out = self._decode_fused(hidden_states, cache)
             if out is not None:
@@ -569,7 +621,7 @@ class GatedDeltaNet2(nn.Module):
     @torch.no_grad()
     def step(self, hidden_states, cache):
         """Decode one token ``[B, hidden]``."""
-        out, cache = self.decode(hidden_states.unsqueeze(1), cache)
+        out, cache = self._decode(hidden_states.unsqueeze(1), cache)
         return out[:, 0], cache
 
     def init_cache(self, batch_size, device=None, dtype=torch.float32):
