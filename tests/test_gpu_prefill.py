@@ -194,8 +194,10 @@ def test_grouped_heads_equal_repeated(DK, H, HK):
             assert rel_err(x.float().cpu(), y.float().cpu()) < (2e-4 if x.dtype == torch.float32 else 4e-3)
 
 
-@pytest.mark.parametrize("DK,DV", [(64, 64), (128, 64), (128, 16), (64, 48)])
-def test_c_abi_ragged_window(DK, DV):
+@pytest.mark.parametrize("DK,DV,B,S_alloc,t0,n", [
+    (64, 64, 2, 230, 10, 150), (128, 64, 2, 230, 10, 150), (128, 16, 2, 230, 10, 150), (64, 48, 2, 230, 10, 150),
+    (128, 128, 1, 2200, 37, 2100)])   # the last on pair records (33 chunks of 2 key heads)
+def test_c_abi_ragged_window(DK, DV, B, S_alloc, t0, n):
     """The C ABI on a window [t0, t0 + n) of a larger allocation with n not a
     chunk multiple: the last chunk's missing rows are read as zeros, o rows
     outside the window are left alone, and the result equals the recurrence on
@@ -203,7 +205,7 @@ def test_c_abi_ragged_window(DK, DV):
     16) below the Python API's multiples of 32."""
     from gdt2_tilelang_amd import _hip
 
-    B, S_alloc, H, t0, n = 2, 230, 2, 10, 150
+    H = 2
     print(f"ragged window DK={DK} DV={DV} t0={t0} n={n} s_alloc={S_alloc}", flush=True)
     cpu, dev = device_inputs(B, S_alloc, H, DK, DV, torch.bfloat16)
     s0 = seeded_state(B, H, DK, DV)
