@@ -306,24 +306,35 @@ int gdn2_hip_layer_decode(const void* x, const void* w_proj, const void* conv_w,
   const int M = static_cast<int>(Ml);
   const long dqk = static_cast<long>(HK) * DK, dv = static_cast<long>(H) * DV;
   const long ldp = 4 * dqk + 3 * dv;
+  if (ldp > 0x7fffffffL) return GDN2_ERR_SHAPE;
   const DecodeWs s = decode_ws(M, H, HK, DK, DV, dtype);
   char* ws = static_cast<char*>(workspace);
   const size_t es = dtype == gdn2::DT_F32 ? 4 : 2;
-  char* proj = ws + s.proj;
-  // projections: one [M, 4 dqk + 3 dv] product (q | k | v | b | w | f | o_gate)
-  if (int e = gdn2_hip_gemv(x, hidden, w_proj, proj, ldp, dtype, M, static_cast<int>(ldp), hidden, stream)) return e;
-  const long offs[6] = {0, dqk, 2 * dqk, 2 * dqk + dv, 3 * dqk + dv, 3 * dqk + 2 * dv};   // q k v b w f
-  if (int e = gdn2_hip_layer_prologue(proj + offs[0] * es, proj + offs[1] * es, proj + offs[2] * es,
-                                      proj + offs[3] * es, proj + offs[4] * es, proj + offs[5] * es, ldp, ldp,
-                                      ldp, ldp, ldp, ldp, dtype, conv_w, conv_b, conv_k, conv_in, conv_out,
-                                      a_log, dt_bias, erase_scale, ws + s.q, ws + s.k, ws + s.v, ws + s.b,
-                                      ws + s.w, reinterpret_cast<float*>(ws + s.g), B, n, H, HK, DK, DV, stream))
-    return e;
-  if (int e = gdn2_hip_decode(ws + s.q, ws + s.k, ws + s.v, reinterpret_cast<const float*>(ws + s.g), ws + s.b,
-                              ws + s.w, dtype, state, ws + s.o, dtype, B, H, HK, DK, DV, n, 0, n, scale, stream))
-    return e;
-  if (int e = gdn2_hip_layer_epilogue(ws + s.o, dtype, proj + (4 * dqk + 2 * dv) * es, ldp, norm_w, norm_eps,
-                                      ws + s.normed, dtype, dv, B, n, H, DV, stream))
+  char* gate = ws + s.proj + (4 * dqk + 2 * dv) * es;   // o_gate rows, stride ldp
+  const hipStream_t st = static_cast<hipStream_t>(stream);
+  // 1. projections (one fused weight, rows q | k | v | b | w | f | o_gate)
+  //    with conv + SiLU, gates and decay applied to the sums
+  gdn2::gv::StepArgs a;
+  a.x = x; a.W = w_proj; a.N = static_cast<int>(ldp); a.K = hidden; a.ldx = hidden;
+  a.B = B; a.n = n; a.dqk = static_cast<int>(dqk); a.dv = static_cast<int>(dv); a.DK = DK;
+  a.KC = conv_w ? conv_k : 0;
+  a.conv_w = conv_w; a.conv_b = conv_w ? conv_b : nullptr;
+  a.conv_in = conv_w ? conv_in : nullptr; a.conv_out = conv_w ? conv_out : nullptr;
+  a.a_log = a_log; a.dt_bias = dt_bias; a.erase_scale = erase_scale;
+  a.q = ws + s.q; a.k = ws + s.k; a.v = ws + s.v; a.b = ws + s.b; a.w = ws + s.w;
+  a.g = reinterpret_cast<float*>(ws + s.g); a.gate = gate; a.ldg = ldp;
+  if (hipError_t e = gdn2::launch_gemv_step(a, dtype, st)) return status(e);
+  // 2. the recurrence, with the L2 norm of q and k in its staging pass
+  if (hipError_t e = gdn2::launch_decode_layer(ws + s.q, ws + s.k, ws + s.v, reinterpret_cast<const float*>(ws + s.g),
+                                               ws + s.b, ws + s.w, state, ws + s.o, B, H, HK, DK, DV, n, scale,
+                                               dtype, st))
+    return status(e);
+  // 3. o_proj with the gated RMSNorm applied to its input on the fly
+  if (gdn2::gemv_norm_supported(DV))
+    return status(gdn2::launch_gemv_norm(ws + s.o, gate, ldp, norm_w, norm_eps, DV, w_out, out, dtype, M, hidden,
+                                         static_cast<int>(dv), hidden, st));
+  if (int e = gdn2_hip_layer_epilogue(ws + s.o, dtype, gate, ldp, norm_w, norm_eps, ws + s.normed, dtype, dv, B,
+                                      n, H, DV, stream))
     return e;
   return gdn2_hip_gemv(ws + s.normed, dv, w_out, out, hidden, dtype, M, hidden, static_cast<int>(dv), stream);
 }

@@ -62,6 +62,33 @@ __device__ __forceinline__ void store_elem(void* p, size_t i, int dt, float x) {
   else static_cast<float*>(p)[i] = x;
 }
 
+template <int CTRL>
+__device__ __forceinline__ float dpp_f32(float x) {
+  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
+}
+
+// Sum over the `group` consecutive lanes that hold one head or row (group a
+// power of two <= 64, groups aligned, wave-uniform). Within a row of 16 lanes
+// by DPP: quad_perm swaps of 1 and 2 give every lane its quad's sum,
+// row_half_mirror adds the other quad of its 8, row_mirror the other 8 of its
+// 16; wider groups by lane shuffles.
+__device__ __forceinline__ float lane_group_sum(float x, int group) {
+  if (group > 1) x += dpp_f32<0xb1>(x);    // quad_perm [1, 0, 3, 2]
+  if (group > 2) x += dpp_f32<0x4e>(x);    // quad_perm [2, 3, 0, 1]
+  if (group > 4) x += dpp_f32<0x141>(x);   // row_half_mirror
+  if (group > 8) x += dpp_f32<0x140>(x);   // row_mirror
+  for (int off = 16; off < group; off <<= 1) x += __shfl_xor(x, off);
+  return x;
+}
+
+// x rounded to the storage precision of DT (round to nearest even), as a float.
+template <int DT>
+__device__ __forceinline__ float round_to(float x) {
+  if constexpr (DT == DT_BF16) return bf16_bits_to_f32(f32_to_bf16_bits(x));
+  else if constexpr (DT == DT_F16) return f16_bits_to_f32(f32_to_f16_bits(x));
+  else return x;
+}
+
 typedef uint32_t u32x4 __attribute__((ext_vector_type(4)));
 
 // Eight bf16 values from eight floats (round to nearest even).

@@ -21,6 +21,7 @@
 //     loads, and each lane holds its v, w columns of those tokens in registers,
 //     so a multi-token call pays the memory latency once per 8 tokens.
 #include "gdn2_common.h"
+#include "gdn2_layer.h"
 
 #include <type_traits>
 
@@ -97,7 +98,7 @@ __global__ __launch_bounds__(kDecMaxThreads) void decode_kernel(
     const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ v,
     const float* __restrict__ g, const void* __restrict__ b, const void* __restrict__ w,
     float* __restrict__ state, void* __restrict__ o, int H, int HK, int DV, long s_alloc, long t0,
-    int n, float scale) {
+    int n, float scale, int qk_norm) {
   constexpr int RPT = DK / kDecRowGroups;
   constexpr int GPT = DK / 8;             // 8-channel groups per token
   __shared__ __align__(16) DecLds<DK, TB> sm;
@@ -154,9 +155,33 @@ __global__ __launch_bounds__(kDecMaxThreads) void decode_kernel(
 #pragma unroll
       for (int j = 0; j < 8; ++j) {
         kv[j] = kr.get(j);
+        qv[j] = qr.get(j);
+      }
+      if (qk_norm) {
+        // q and k of the layer's decode step arrive before their per-head L2
+        // normalisation (x / max(||x||, 1e-12), rounded to the input dtype):
+        // the GPT items of a token are GPT consecutive lanes of one wave, and
+        // every pass of this loop covers whole tokens (GPT divides 64)
+        float sq = 0.f, sk = 0.f;
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          sq += qv[j] * qv[j];
+          sk += kv[j] * kv[j];
+        }
+        sq = lane_group_sum(sq, GPT);
+        sk = lane_group_sum(sk, GPT);
+        const float iq = rsqrtf(fmaxf(sq, 1e-24f)), ik = rsqrtf(fmaxf(sk, 1e-24f));
+#pragma unroll
+        for (int j = 0; j < 8; ++j) {
+          qv[j] = round_to<IN_DT>(qv[j] * iq);
+          kv[j] = round_to<IN_DT>(kv[j] * ik);
+        }
+      }
+#pragma unroll
+      for (int j = 0; j < 8; ++j) {
         ea[j] = fast_exp2(gr.get(j) * kLog2e);
         bk[j] = br.get(j) * kv[j];
-        qv[j] = qr.get(j) * scale;
+        qv[j] *= scale;
       }
 #pragma unroll
       for (int j = 0; j < 8; j += 4) {
@@ -233,7 +258,7 @@ template <int DK, int IN_DT, int OUT_DT>
 static hipError_t launch_decode_t(const void* q, const void* k, const void* v, const float* g,
                                   const void* b, const void* w, float* state, void* o, int B,
                                   int H, int HK, int DV, long s_alloc, long t0, int n, float scale,
-                                  hipStream_t stream) {
+                                  hipStream_t stream, int qk_norm = 0) {
   // one workgroup per (b, h, up to kDecMaxCols columns); one wave per 32 columns.
   // A call with fewer such workgroups than the GPU has CUs (a small batch:
   // B = 1, H = 16 is 16 of them) takes one-wave workgroups of 32 columns
@@ -246,11 +271,11 @@ static hipError_t launch_decode_t(const void* q, const void* k, const void* v, c
   }
   if (n == 1)
     hipLaunchKernelGGL((decode_kernel<DK, IN_DT, OUT_DT, 1>), dim3(tiles, B * H), dim3(threads), 0,
-                       stream, q, k, v, g, b, w, state, o, H, HK, DV, s_alloc, t0, n, scale);
+                       stream, q, k, v, g, b, w, state, o, H, HK, DV, s_alloc, t0, n, scale, qk_norm);
   else
     hipLaunchKernelGGL((decode_kernel<DK, IN_DT, OUT_DT, kDecTokBlock>), dim3(tiles, B * H),
                        dim3(threads), 0, stream, q, k, v, g, b, w, state, o, H, HK, DV, s_alloc, t0, n,
-                       scale);
+                       scale, qk_norm);
   return hipGetLastError();
 }
 
@@ -280,6 +305,28 @@ hipError_t launch_decode(const void* q, const void* k, const void* v, const floa
 #undef GDN2_DEC_IN
 #undef GDN2_DEC_OUT
 #undef GDN2_DEC_CASE
+  return hipErrorInvalidValue;
+}
+
+}  // namespace gdn2
+
+namespace gdn2 {
+
+// The recurrence of a layer decode call (gdn2_hip_layer_decode): q and k not
+// yet L2-normalised (the normalisation runs in the staging pass), inputs and
+// output in one dtype, always the per-token kernel (a layer call holds at most
+// 8 tokens in all, where the state stream is short and latency-bound).
+hipError_t launch_decode_layer(const void* q, const void* k, const void* v, const float* g, const void* b,
+                               const void* w, float* state, void* o, int B, int H, int HK, int DK, int DV, int n,
+                               float scale, int dt, hipStream_t stream) {
+  if (DV % kDecCols != 0) return hipErrorInvalidValue;
+#define GDN2_DECL_CASE(DKV, DTV)                                                                            \
+  if (DK == DKV && dt == DTV)                                                                               \
+    return launch_decode_t<DKV, DTV, DTV>(q, k, v, g, b, w, state, o, B, H, HK, DV, n, 0, n, scale, stream, 1);
+#define GDN2_DECL_DT(DKV) GDN2_DECL_CASE(DKV, DT_BF16) GDN2_DECL_CASE(DKV, DT_F16) GDN2_DECL_CASE(DKV, DT_F32)
+  GDN2_DECL_DT(32) GDN2_DECL_DT(64) GDN2_DECL_DT(128) GDN2_DECL_DT(256)
+#undef GDN2_DECL_DT
+#undef GDN2_DECL_CASE
   return hipErrorInvalidValue;
 }
 

@@ -54,26 +54,6 @@ __device__ __forceinline__ float softplus(float x) {
   return u == 1.f ? y : __logf(u) * (y * __builtin_amdgcn_rcpf(u - 1.f));
 }
 
-template <int CTRL>
-__device__ __forceinline__ float dpp(float x) {
-  return __builtin_bit_cast(float, __builtin_amdgcn_update_dpp(0, __builtin_bit_cast(int, x), CTRL, 0xf, 0xf, true));
-}
-
-// Sum over the `group` consecutive lanes that hold one head (group a power of
-// two <= 64, groups aligned, wave-uniform). Within a row of 16 lanes by DPP:
-// quad_perm swaps of 1 and 2 give every lane its quad's sum, row_half_mirror
-// adds the other quad of its 8, row_mirror the other 8 of its 16; wider groups
-// by lane shuffles.
-__device__ __forceinline__ float group_sum(float x, int group) {
-  if (group > 1) x += dpp<0xb1>(x);    // quad_perm [1, 0, 3, 2]
-  if (group > 2) x += dpp<0x4e>(x);    // quad_perm [2, 3, 0, 1]
-  if (group > 4) x += dpp<0x141>(x);   // row_half_mirror
-  if (group > 8) x += dpp<0x140>(x);   // row_mirror
-  for (int off = 16; off < group; off <<= 1) x += __shfl_xor(x, off);
-  return x;
-}
-
-
 constexpr int TT = 4;            // tokens per prologue workgroup (8 measured slower: fewer waves per SIMD)
 constexpr int kProThreads = 128;
 
@@ -251,7 +231,7 @@ __global__ __launch_bounds__(kProThreads) void prologue_kernel(ProArgs a) {
         float ss = 0.f;
 #pragma unroll
         for (int e = 0; e < 8; ++e) ss += y[t][e] * y[t][e];
-        ss = group_sum(ss, group);
+        ss = lane_group_sum(ss, group);
         const float inv = rsqrtf(fmaxf(ss, 1e-24f));   // 1 / max(||y||, 1e-12)
 #pragma unroll
         for (int e = 0; e < 8; ++e) y[t][e] *= inv;
@@ -392,7 +372,7 @@ __global__ __launch_bounds__(kThreads) void epilogue8_kernel(const void* __restr
   float ss = 0.f;
 #pragma unroll
   for (int e = 0; e < 8; ++e) ss += x[e] * x[e];
-  ss = group_sum(ss, G);                       // every lane takes part in the shuffles
+  ss = lane_group_sum(ss, G);                       // every lane takes part in the shuffles
   if (!act) return;
   const float r = rsqrtf(ss / DV + eps);
   const float4 w0 = *reinterpret_cast<const float4*>(weight + c);

@@ -290,22 +290,29 @@ def test_gemv_matches_linear(dtype, tol, M, N, K):
     assert err < tol
 
 
-@pytest.mark.parametrize("dtype,tol,B,n,conv", [
-    (torch.float32, 1e-4, 2, 3, 4), (torch.bfloat16, 2e-2, 2, 3, 4), (torch.float16, 1e-2, 1, 8, 4),
-    (torch.bfloat16, 2e-2, 1, 1, 2), (torch.float32, 1e-4, 4, 2, 0), (torch.bfloat16, 2e-2, 3, 3, 4),
+@pytest.mark.parametrize("dtype,tol,B,n,conv,H,HK,DV", [
+    (torch.float32, 1e-4, 2, 3, 4, 4, 2, 64), (torch.bfloat16, 2e-2, 2, 3, 4, 4, 2, 64),
+    (torch.float16, 1e-2, 1, 8, 4, 4, 2, 64), (torch.bfloat16, 2e-2, 1, 1, 2, 4, 2, 64),
+    (torch.float32, 1e-4, 4, 2, 0, 4, 2, 64), (torch.bfloat16, 2e-2, 3, 3, 4, 4, 2, 64),
+    (torch.float32, 1e-4, 2, 2, 3, 8, 4, 512), (torch.bfloat16, 2e-2, 1, 3, 4, 4, 4, 96),
+    (torch.float32, 1e-4, 1, 1, 4, 16, 8, 128),
 ])
-def test_fused_decode_call_matches_stagewise(dtype, tol, B, n, conv):
+def test_fused_decode_call_matches_stagewise(dtype, tol, B, n, conv, H, HK, DV):
     """GatedDeltaNet2.decode for B*n <= 8 runs as one library call
-    (gdn2_hip_layer_decode); it must agree with the per-stage GPU path
-    (hipBLASLt projections, the same prologue / decode / epilogue kernels).
-    B*n = 9 takes the per-stage path itself; conv 0 is a layer without the
-    short convolution."""
+    (gdn2_hip_layer_decode: projections with the prologue folded in, the
+    recurrence with the q / k norm, o_proj with the gated norm folded in); it
+    must agree with the per-stage GPU path (hipBLASLt projections, the
+    separate prologue / decode / epilogue kernels). B*n = 9 takes the
+    per-stage path itself; conv 0 is a layer without the short convolution.
+    H*DV = 4096 takes the per-wave gated-norm GEMV (above 2048 the LDS form is
+    not used), DV = 96 the separate epilogue (not a power of two), H*DV = 2048
+    the LDS form at config 4's head geometry."""
     from gdt2_tilelang_amd.inference import gdn2_decode
     torch.manual_seed(0)
-    cfg = GatedDeltaNet2Config(hidden_size=256, num_heads=4, num_kv_heads=2, head_dim_k=64, head_dim_v=64,
+    cfg = GatedDeltaNet2Config(hidden_size=256, num_heads=H, num_kv_heads=HK, head_dim_k=64, head_dim_v=DV,
                                conv_size=conv)
     layer = GatedDeltaNet2(cfg).cuda().to(dtype).eval()
-    print(f"fused decode {dtype} B={B} n={n} conv={conv}", flush=True)
+    print(f"fused decode {dtype} B={B} n={n} conv={conv} H={H} HK={HK} DV={DV}", flush=True)
     x0 = torch.randn(B, 70, 256, device="cuda").to(dtype)
     xs = torch.randn(B, n, 256, device="cuda").to(dtype)
     _, cache = layer.prefill(x0, None)
