@@ -290,7 +290,7 @@ int gdn2_hip_layer_decode(const void* x, const void* w_proj, const void* conv_w,
   if (B < 1 || n < 1 || hidden < 1 || H < 1 || HK < 1 || H % HK || !dtype_ok(dtype)) return GDN2_ERR_ARG;
   if (reinterpret_cast<uintptr_t>(workspace) % 256) return GDN2_ERR_ARG;
   // Every stage's shape and alignment rule is checked before the first launch,
-  // so the call either runs all five stages or changes nothing.
+  // so the call either runs all of its launches or changes nothing.
   const long Ml = static_cast<long>(B) * n;
   if (Ml > 8) return GDN2_ERR_SHAPE;                                      // GEMV rows
   if (DK != 32 && DK != 64 && DK != 128 && DK != 256) return GDN2_ERR_SHAPE;   // decode

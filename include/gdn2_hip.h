@@ -217,11 +217,15 @@ int gdn2_hip_gemv(const void* x, long ldx, const void* W, void* y, long ldy, int
 
 /*
  * One GatedDeltaNet2 decode call of n tokens for B sequences (B*n <= 8), as
- * the five launches above on one stream: projections (gdn2_hip_gemv with the
- * fused weight w_proj [4*HK*DK + 3*H*DV, hidden], rows q | k | v | b | w | f |
- * o_gate), the layer prologue (conv with conv_in -> conv_out, L2 norm, gates,
- * decay), the recurrence on `state` (fp32 [B, H, DK, DV], updated in place),
- * the gated RMSNorm (norm_w fp32 [DV]) and o_proj (w_out [hidden, H*DV]).
+ * three launches on one stream: the projections (the fused weight w_proj
+ * [4*HK*DK + 3*H*DV, hidden], rows q | k | v | b | w | f | o_gate) with the
+ * layer prologue applied to their sums (conv with conv_in -> conv_out, SiLU,
+ * gates, decay), the recurrence on `state` (fp32 [B, H, DK, DV], updated in
+ * place) with the q / k L2 norm, and o_proj (w_out [hidden, H*DV]) with the
+ * gated RMSNorm (norm_w fp32 [DV]) applied to its input. The result agrees,
+ * to the rounding of the activation dtype, with
+ * gdn2_hip_gemv + gdn2_hip_layer_prologue + gdn2_hip_decode +
+ * gdn2_hip_layer_epilogue + gdn2_hip_gemv run stage by stage.
  * x [B*n, hidden] and out [B*n, hidden] in dtype. Intermediates live in
  * `workspace` (256-byte aligned, gdn2_hip_layer_decode_workspace_bytes).
  * Replaces: GatedDeltaNet2.decode / step (gdn2/attention.py:417-478).
