@@ -10,13 +10,13 @@ Module layout::
     config.py      GDN2Config / GatedDeltaNet2Config
     attention.py   gdn2_attention, resolve_backend, GDN2Cache, GatedDeltaNet2
     inference.py   gdn2_prefill, gdn2_decode, gdn2_decode_step
-    forward.py     chunk_gdn2_fwd (fused scan; no per-chunk states)
+    forward.py     chunk_gdn2_fwd (fused scan; no per-chunk states), chunk_gdn2_bwd
     _hip.py        ctypes binding of _lib/libgdn2_hip.so (include/gdn2_hip.h)
     build.py       hipcc build of csrc/*.hip for gfx950
     csrc/          the HIP kernels and the C ABI
 
 The reference's torch oracles (``recurrent_gdn2``, ``chunk_gdn2_torch``) are
-not part of this package; the backward is not provided.
+not part of this package.
 """
 
 from .attention import GDN2Cache, GatedDeltaNet2, gdn2_attention, resolve_backend

@@ -8,7 +8,8 @@ reference ``state_dict`` loads unchanged.
 Backends: ``"auto"`` resolves to ``"hip"`` on a GPU and to ``"torch"``
 elsewhere, like the reference's ``"tilelang"`` policy. The ``"torch"`` backend
 is the reference package's own CPU path and is not part of this package, so it
-raises ``NotImplementedError`` here; so does the backward.
+raises ``NotImplementedError`` here. Autograd through ``gdn2_attention`` runs
+the hip backward (``chunk_gdn2_bwd``).
 
 Two layer details differ on purpose:
 
@@ -38,7 +39,7 @@ from torch import nn
 
 from . import _hip
 from .config import DEFAULT_KERNEL_CONFIG, GDN2Config, GatedDeltaNet2Config
-from .forward import check_cu_seqlens, chunk_gdn2_fwd, chunk_gdn2_varlen_fwd
+from .forward import check_cu_seqlens, chunk_gdn2_bwd, chunk_gdn2_fwd, chunk_gdn2_varlen_fwd
 from .inference import gdn2_decode, gdn2_prefill
 
 __all__ = ["gdn2_attention", "GatedDeltaNet2", "GDN2Cache", "resolve_backend"]
@@ -62,16 +63,23 @@ def resolve_backend(backend: str, on_cuda: bool, needs_grad: bool) -> str:
 
 
 class _GDN2Function(torch.autograd.Function):
-    """hip forward; the backward is not provided by this backend."""
+    """hip forward and backward (reference: ``gdn2/attention.py:60-99``)."""
 
     @staticmethod
     def forward(ctx, q, k, v, g, b, w, scale, initial_state, output_final_state, config):
+        ctx.save_for_backward(q, k, v, g, b, w, initial_state)
+        ctx.scale, ctx.config = scale, config
         return chunk_gdn2_fwd(q, k, v, g, b, w, scale, initial_state, output_final_state, config)
 
     @staticmethod
     @torch.autograd.function.once_differentiable
     def backward(ctx, do, dfinal_state):
-        raise NotImplementedError("the hip backend is forward-only; the GDN-2 backward is not implemented")
+        q, k, v, g, b, w, initial_state = ctx.saved_tensors
+        if do is None:
+            do = torch.zeros(*v.shape, dtype=q.dtype, device=q.device)
+        dq, dk, dv, dg, db, dw, ds0 = chunk_gdn2_bwd(q, k, v, g, b, w, ctx.scale, initial_state, do, dfinal_state,
+                                                     ctx.config)
+        return dq, dk, dv, dg, db, dw, None, ds0, None, None
 
 
 def gdn2_attention(q, k, v, g, b, w, scale=None, initial_state=None, output_final_state=False,
@@ -514,7 +522,11 @@ class GatedDeltaNet2(nn.Module):
                                       "run on the GPU only")
         if hidden_states.is_cuda and S == 0:             # nothing to run: the state carries over
             return self._empty_call(hidden_states, cache, use_cache, fresh_conv=True)
-        if hidden_states.is_cuda:
+        # training: the projections, conv, gates and norm as torch ops (autograd),
+        # the attention op through gdn2_attention's hip forward and backward
+        trains = torch.is_grad_enabled() and (hidden_states.requires_grad or
+                                              any(p.requires_grad for p in self.parameters()))
+        if hidden_states.is_cuda and not trains:
             (q, k, v, g, b, w), proj, conv_state = self._project_gpu(hidden_states, None, conv_tail=use_cache)
             o, final_state = gdn2_attention(
                 q, k, v, g, b, w, scale=self.scale,

@@ -29,7 +29,7 @@ class GDN2Config:
             with the reference's TileLang tiling; unused by the hip kernels.
         state_dtype: dtype of the carried state; the hip kernels keep fp32.
         backend: ``"auto"``, ``"hip"`` or ``"torch"``.
-        backward: accepted for compatibility; the hip backend is forward-only.
+        backward: accepted for compatibility; autograd runs the hip backward.
         output_dtype: dtype of ``o``; ``None`` means ``v.dtype``.
     """
 

@@ -14,6 +14,10 @@ hipError_t launch_chunk_local(const void*, const void*, const void*, const float
 hipError_t launch_scan(const void*, const void*, int, const unsigned short*, const float*, float*,
                        void*, int, int, int, int, int, int, long, long, int, long, Varlen, hipStream_t);
 hipError_t launch_gemv(const void*, const void*, void*, int, int, int, int, long, long, hipStream_t);
+size_t backward_workspace_bytes(int, int, int, int, int, long);
+hipError_t launch_backward(const void*, const void*, const void*, const float*, const void*, const void*, int, float,
+                           const float*, const void*, int, const float*, void*, void*, void*, float*, void*, void*,
+                           float*, void*, int, int, int, int, int, long, hipStream_t);
 }  // namespace gdn2
 
 namespace {
@@ -337,6 +341,37 @@ int gdn2_hip_layer_decode(const void* x, const void* w_proj, const void* conv_w,
                                       n, H, DV, stream))
     return e;
   return gdn2_hip_gemv(ws + s.normed, dv, w_out, out, hidden, dtype, M, hidden, static_cast<int>(dv), stream);
+}
+
+static int backward_shape(int B, long S, int H, int HK, int DK, int DV) {
+  if (B < 1 || S < 0 || H < 1 || HK < 1 || H % HK) return GDN2_ERR_ARG;
+  if (DK != 32 && DK != 64 && DK != 128) return GDN2_ERR_SHAPE;
+  if (DV < 16 || DV % 16 || DV > 4096) return GDN2_ERR_SHAPE;
+  const long NC = (S + gdn2::kBS - 1) / gdn2::kBS;
+  // grid dimensions and 32-bit element counts of the fp32 intermediates
+  if (NC > 65535 || static_cast<long>(B) * H > 65535) return GDN2_ERR_SHAPE;
+  if (static_cast<long>(B) * S * HK * DK > 0x7fffffffL) return GDN2_ERR_SHAPE;
+  return 0;
+}
+
+size_t gdn2_hip_backward_workspace_bytes(int B, int H, int HK, int DK, int DV, long S) {
+  if (backward_shape(B, S, H, HK, DK, DV)) return 0;
+  return gdn2::backward_workspace_bytes(B, H, HK, DK, DV, S);
+}
+
+int gdn2_hip_backward(const void* q, const void* k, const void* v, const float* g, const void* b, const void* w,
+                      int in_dtype, float scale, const float* initial_state, const void* d_out, int do_dtype,
+                      const float* d_final_state, void* dq, void* dk, void* dv, float* dg, void* db, void* dw,
+                      float* d_initial_state, void* workspace, int B, long S, int H, int HK, int DK, int DV,
+                      void* stream) {
+  if (!dtype_ok(in_dtype) || !dtype_ok(do_dtype)) return GDN2_ERR_ARG;
+  if (int e = backward_shape(B, S, H, HK, DK, DV)) return e;
+  if (S > 0 && (!q || !k || !v || !g || !b || !w || !d_out || !dq || !dk || !dv || !dg || !db || !dw || !workspace))
+    return GDN2_ERR_ARG;
+  if (reinterpret_cast<uintptr_t>(workspace) % 256) return GDN2_ERR_ARG;
+  return status(gdn2::launch_backward(q, k, v, g, b, w, in_dtype, scale, initial_state, d_out, do_dtype,
+                                      d_final_state, dq, dk, dv, dg, db, dw, d_initial_state, workspace, B, H, HK,
+                                      DK, DV, S, static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

@@ -4,7 +4,7 @@
 but runs the serving pipeline: the chunk-local kernel then the fused
 scan + output kernel, so the per-chunk states ``h`` are never materialised
 (the reference's ``state_kernel`` / ``output_kernel`` pair stores them only
-for its backward, which this backend does not provide). A sequence that is
+for its backward; ``chunk_gdn2_bwd`` here recomputes what it needs). A sequence that is
 not a chunk multiple needs no padded copy (the reference zero-pads,
 ``gdn2/forward.py:748-753``): the kernels read the missing rows of the last
 chunk as zeros, which are inert because g = 0 keeps the decay at 1 and
@@ -128,6 +128,45 @@ def chunk_gdn2_varlen_fwd(q, k, v, g, b, w, scale, cu_seqlens, initial_state=Non
     return o, (final.to(st_dt) if output_final_state else None)
 
 
-def chunk_gdn2_bwd(*args, **kwargs):
-    """Not provided: the hip backend is a forward / serving backend."""
-    raise NotImplementedError("the hip backend is forward-only; the GDN-2 backward is not implemented")
+def chunk_gdn2_bwd(q, k, v, g, b, w, scale, initial_state, do, dht, config: GDN2Config = DEFAULT_KERNEL_CONFIG):
+    """Chunkwise training backward on the gfx950 kernels.
+
+    Same contract as the reference (``gdn2/backward.py:912-994``): the
+    gradients of ``(o * do).sum() + (final_state * dht).sum()`` with respect
+    to the forward inputs. Returns ``(dq, dk, dv, dg, db, dw, dinitial_state)``;
+    the last is ``None`` when ``initial_state`` is ``None``. Each gradient has
+    its input's dtype. The arithmetic is fp32 throughout (chunk 64):
+    ``gdn2_hip_backward`` recomputes the per-chunk factors, scans the
+    chunk-entry states forward and the state gradients backward, then forms
+    every chunk's gradients in parallel.
+    """
+    dev = _require_device(q, k, v, g, b, w, do)
+    _check_shapes(q, k, v, g, b, w)
+    B, S, HK, DK = q.shape
+    H, DV = v.shape[2], v.shape[3]
+    if DK not in (32, 64, 128) or DV % 16:
+        raise ValueError(f"hip backward supports DK in (32, 64, 128) and DV % 16 == 0; got DK={DK}, DV={DV}")
+    if tuple(do.shape) != (B, S, H, DV):
+        raise ValueError(f"do has shape {tuple(do.shape)}, expected {(B, S, H, DV)}")
+    scale = DK ** -0.5 if scale is None else scale
+    q, k, v, b, w, do = (t.contiguous() for t in (q, k, v, b, w, do))
+    g32 = g.float().contiguous()
+    s0 = None
+    if initial_state is not None:
+        _require_device(q, initial_state)
+        s0 = initial_state.to(config.state_dtype).to(torch.float32).contiguous()
+    dht32 = None if dht is None else dht.to(torch.float32).contiguous()
+    dq, dk, db = (torch.empty(B, S, HK, DK, dtype=q.dtype, device=dev) for _ in range(3))
+    dv, dw = (torch.empty(B, S, H, DV, dtype=q.dtype, device=dev) for _ in range(2))
+    dg = torch.empty(B, S, HK, DK, dtype=torch.float32, device=dev)
+    ds0 = None if s0 is None else torch.empty(B, H, DK, DV, dtype=torch.float32, device=dev)
+    lib = _hip.lib()
+    ws = torch.empty(max(lib.gdn2_hip_backward_workspace_bytes(B, H, HK, DK, DV, S), 1), dtype=torch.uint8,
+                     device=dev)
+    _hip.check(lib.gdn2_hip_backward(
+        _hip.ptr(q), _hip.ptr(k), _hip.ptr(v), _hip.ptr(g32), _hip.ptr(b), _hip.ptr(w), _hip.dtype_code(q.dtype),
+        float(scale), _hip.ptr(s0), _hip.ptr(do), _hip.dtype_code(do.dtype), _hip.ptr(dht32),
+        _hip.ptr(dq), _hip.ptr(dk), _hip.ptr(dv), _hip.ptr(dg), _hip.ptr(db), _hip.ptr(dw), _hip.ptr(ds0),
+        _hip.ptr(ws), B, S, H, HK, DK, DV, _hip.stream_of(dev)), "gdn2_hip_backward")
+    return (dq, dk, dv, dg.to(g.dtype), db, dw,
+            None if ds0 is None else ds0.to(initial_state.dtype))

@@ -216,6 +216,29 @@ int gdn2_hip_gemv(const void* x, long ldx, const void* W, void* y, long ldy, int
                   int K, void* stream);
 
 /*
+ * Training backward of the attention op: given the forward inputs and the
+ * gradient d_out [B, S, H, DV] (do_dtype) of o, and optionally the gradient
+ * d_final_state [B, H, DK, DV] fp32 of the final state, writes
+ *   dq, dk, db [B, S, HK, DK] and dv, dw [B, S, H, DV] in in_dtype,
+ *   dg [B, S, HK, DK] fp32, and, if d_initial_state is not null, the
+ *   gradient of initial_state (fp32 [B, H, DK, DV]; null initial_state means
+ *   zeros) into d_initial_state.
+ * Chunkwise form in fp32 (chunk 64): per-chunk local factors, a forward scan
+ * of the chunk-entry states, a reverse scan of the state gradients, per-chunk
+ * gradients, and the sum over the value heads of each key head. DK in {32,
+ * 64, 128}, DV a multiple of 16 (<= 4096). `workspace` (256-byte aligned)
+ * holds gdn2_hip_backward_workspace_bytes(B, H, HK, DK, DV, S) bytes.
+ * Replaces: chunk_gdn2_bwd (gdn2/backward.py:912-994), called from
+ * _GDN2Function.backward (gdn2/attention.py:79-99).
+ */
+size_t gdn2_hip_backward_workspace_bytes(int B, int H, int HK, int DK, int DV, long S);
+int gdn2_hip_backward(const void* q, const void* k, const void* v, const float* g, const void* b, const void* w,
+                      int in_dtype, float scale, const float* initial_state, const void* d_out, int do_dtype,
+                      const float* d_final_state, void* dq, void* dk, void* dv, float* dg, void* db, void* dw,
+                      float* d_initial_state, void* workspace, int B, long S, int H, int HK, int DK, int DV,
+                      void* stream);
+
+/*
  * One GatedDeltaNet2 decode call of n tokens for B sequences (B*n <= 8), as
  * three launches on one stream: the projections (the fused weight w_proj
  * [4*HK*DK + 3*H*DV, hidden], rows q | k | v | b | w | f | o_gate) with the

@@ -213,6 +213,33 @@ def test_tiling_and_dtype_validation():
         _hip.dtype_code(torch.int32)
 
 
-def test_backward_is_not_provided():
-    with pytest.raises(NotImplementedError, match="forward-only"):
-        chunk_gdn2_bwd()
+def test_backward_host_validation():
+    """chunk_gdn2_bwd checks its device on the host; the C ABI rejects unsupported
+    head dims, bad dtypes, null pointers and misaligned workspaces before any
+    launch, and sizes no workspace for an unsupported shape."""
+    lib = _hip.lib()
+    with pytest.raises(ValueError, match="CUDA"):
+        x = torch.zeros(1, 4, 2, 64)
+        chunk_gdn2_bwd(x, x, x, x, x, x, None, None, x, None)
+    assert lib.gdn2_hip_prefill_workspace_bytes(1, 2, 96, 64) == 0
+    wsb = lib.gdn2_hip_backward_workspace_bytes
+    assert wsb(1, 2, 2, 48, 64, 128) == 0          # DK not in (32, 64, 128)
+    assert wsb(1, 2, 2, 64, 24, 128) == 0          # DV % 16
+    assert wsb(1, 3, 2, 64, 64, 128) == 0          # HK must divide H
+    # B=2 H=4 HK=2 DK=64 DV=32 S=100 (2 chunks): records 2*2*2 of 18496 floats,
+    # two state checkpoints 2*4*2*64*32 floats each, four gradient shares B*S*H*DK
+    rec = 2 * 2 * 2 * (64 * 64 + 64 * 64 + 64 * 64 + 4096 + 4096 + 64) * 4
+    ck = 2 * 4 * 2 * 64 * 32 * 4
+    part = 4 * 2 * 100 * 4 * 64 * 4
+    up = lambda x: (x + 255) // 256 * 256
+    assert wsb(2, 4, 2, 64, 32, 100) == up(rec) + 2 * up(ck) + up(part)
+    fake = ctypes.c_void_p(256)   # never dereferenced: validation fails first
+    args = [fake] * 6
+    tail = [fake] * 8
+    call = lambda dt, dk, dv, ws=fake, ptrs=args: lib.gdn2_hip_backward(
+        *ptrs, dt, 0.1, None, fake, 1, None, *tail[:3], fake, fake, fake, None, ws, 1, 64, 2, 2, dk, dv, None)
+    assert call(7, 64, 64) == -1
+    assert call(1, 48, 64) == -2
+    assert call(1, 64, 24) == -2
+    assert call(1, 64, 64, ws=ctypes.c_void_p(264)) == -1
+    assert call(1, 64, 64, ptrs=[None] + args[1:]) == -1
