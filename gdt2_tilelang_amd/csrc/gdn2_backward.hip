@@ -62,7 +62,7 @@ __device__ __forceinline__ size_t key_index(int bi, long S, long t, int HK, int 
 
 // ---------------------------------------------------------------- kernel 1
 template <int DK>
-constexpr int local_lds_floats() { return 4 * L * (DK + 4) + L * L + DK; }
+constexpr int local_lds_floats() { return 3 * L * (DK + 4) + L * (DK + 4 > L ? DK + 4 : L) + L * L + DK + 9 * 256; }
 
 template <int DK>
 __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const void* __restrict__ q, const void* __restrict__ k,
@@ -74,10 +74,12 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const void* __restr
   extern __shared__ __align__(16) float sm[];
   float* sq = sm;                 // q, then Qg
   float* sk = sq + L * P;         // k, then KG
-  float* sbk = sk + L * P;        // b k, then E
-  float* sG = sbk + L * P;        // G, then W = Ai E
+  float* sbk = sk + L * P;        // b k, then E, then Aqk (L x L: the slot is at least that large)
+  float* sG = sbk + L * (P > L ? P : L);   // G, then W = Ai E
   float* sA = sG + L * P;         // Akk, then Ai   [L][L]
   float* sgam = sA + L * L;       // gamma          [DK]
+  float* sXo = sgam + DK;         // off-diagonal 16 x 16 blocks of Ai [6][16][16]
+  float* sT = sXo + 6 * 256;      // block products [3][16][16]
   const int tid = threadIdx.x;
   const int c = blockIdx.x, bhk = blockIdx.y;
   const int bi = bhk / HK, hk = bhk % HK;
@@ -145,21 +147,71 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const void* __restr
   }
   __syncthreads();
 
-  // Ai = (I + Akk)^-1 in place, one column per lane of wave 0: row t of X is
-  // formed from rows < t (already X) and row t of Akk (still Akk: every lane
-  // of the wave finishes its sum before any lane stores row t)
+  // Ai = (I + Akk)^-1 by 16 x 16 blocks. Diagonal blocks in place, one
+  // column per lane of wave 0 (row r of a block is formed from its rows < r,
+  // already inverted, and row r of Akk, still Akk: every lane of the wave
+  // finishes its sum before any lane stores row r); then the off-diagonal
+  // blocks by distance from the diagonal, X_ij = -X_ii sum_{k=j}^{i-1} Akk_ik X_kj,
+  // into sXo (Akk_ij is still needed by blocks further out), copied over
+  // Akk at the end.
   if (tid < L) {
-    const int j = tid;
-    for (int t = 0; t < L; ++t) {
+    const int bb = tid >> 4, j = tid & 15, o = 16 * bb;
+    for (int r = 0; r < 16; ++r) {
       float s = 0.f;
-      for (int u = j; u < t; ++u) s += sA[t * L + u] * sA[u * L + j];
-      sA[t * L + j] = j < t ? -s : (j == t ? 1.f : 0.f);
+      for (int u = j; u < r; ++u) s += sA[(o + r) * L + o + u] * sA[(o + u) * L + o + j];
+      sA[(o + r) * L + o + j] = j < r ? -s : (j == r ? 1.f : 0.f);
+    }
+  }
+  __syncthreads();
+  {
+    // X block (k, j), k >= j: diagonal in sA, off-diagonal in sXo[k (k-1) / 2 + j]
+    auto xb = [&](int kb, int jb, int r, int c) -> float {
+      return kb == jb ? sA[(16 * kb + r) * L + 16 * jb + c] : sXo[((kb * (kb - 1) / 2 + jb) * 16 + r) * 16 + c];
+    };
+    for (int d = 1; d < 4; ++d) {
+      // T = sum_{k=j}^{i-1} Akk_ik X_kj for the 4 - d blocks (i = j + d); 256 entries each
+      float tv[3];
+#pragma unroll
+      for (int n = 0; n < 3; ++n) {
+        tv[n] = 0.f;
+        const int e = tid + n * kThreads;
+        if (e < (4 - d) * 256) {
+          const int jb = e >> 8, ib = jb + d, r = (e >> 4) & 15, c = e & 15;
+          float s = 0.f;
+          for (int kb = jb; kb < ib; ++kb)
+            for (int u = 0; u < 16; ++u) s += sA[(16 * ib + r) * L + 16 * kb + u] * xb(kb, jb, u, c);
+          tv[n] = s;
+        }
+      }
+      __syncthreads();
+#pragma unroll
+      for (int n = 0; n < 3; ++n) {
+        const int e = tid + n * kThreads;
+        if (e < (4 - d) * 256) sT[e] = tv[n];
+      }
+      __syncthreads();
+#pragma unroll
+      for (int n = 0; n < 3; ++n) {
+        const int e = tid + n * kThreads;
+        if (e < (4 - d) * 256) {
+          const int jb = e >> 8, ib = jb + d, r = (e >> 4) & 15, c = e & 15;
+          float s = 0.f;
+          for (int u = 0; u <= r; ++u) s += sA[(16 * ib + r) * L + 16 * ib + u] * sT[(jb * 16 + u) * 16 + c];
+          sXo[((ib * (ib - 1) / 2 + jb) * 16 + r) * 16 + c] = -s;
+        }
+      }
+      __syncthreads();
+    }
+    for (int e = tid; e < 6 * 256; e += kThreads) {
+      const int blk = e >> 8, r = (e >> 4) & 15, c = e & 15;
+      const int ib = blk < 1 ? 1 : (blk < 3 ? 2 : 3), jb = blk - ib * (ib - 1) / 2;
+      sA[(16 * ib + r) * L + 16 * jb + c] = sXo[e];
     }
   }
   __syncthreads();
   for (int e = tid; e < L * L; e += kThreads) rc[R::AI + e] = sA[e];
   if (tid < DK) rc[R::GM + tid] = sgam[tid];
-  // q -> Qg, b k -> E, k -> KG (G_L from gamma's exponent: row L-1 of G)
+  // q -> Qg, b k -> E, k -> KG (G_L: row L-1 of G)
   for (int e = tid; e < L * DK; e += kThreads) {
     const int t = e / DK, i = e % DK;
     const float gt = sG[t * P + i], gl = sG[(L - 1) * P + i];
@@ -169,72 +221,206 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const void* __restr
     sk[t * P + i] *= __expf(gl - gt);
   }
   __syncthreads();
-  // W = Ai E over G (dead)
-  float wv[L * DK / kThreads];
+  // Register tiles: an L x DK product gives thread (rg, cg) rows 4 rg .. and
+  // columns CW cg ..; a DK x DK product rows and columns CW rg .., CW cg ..
+  constexpr int CW = DK / 16;
+  const int rg = tid >> 4, cg = tid & 15;
+  {
+    // W = Ai E over G (dead)
+    float acc[4][CW];
 #pragma unroll
-  for (int r = 0; r < L * DK / kThreads; ++r) {
-    const int e = tid + r * kThreads, t = e / DK, i = e % DK;
-    float s = 0.f;
-    for (int u = 0; u <= t; ++u) s += sA[t * L + u] * sbk[u * P + i];
-    wv[r] = s;
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int u = 0; u < CW; ++u) acc[r][u] = 0.f;
+#pragma unroll 4
+    for (int s2 = 0; s2 < L; ++s2) {
+      float ev[CW];
+#pragma unroll
+      for (int u = 0; u < CW; ++u) ev[u] = sbk[s2 * P + CW * cg + u];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float x = sA[(4 * rg + r) * L + s2];
+#pragma unroll
+        for (int u = 0; u < CW; ++u) acc[r][u] += x * ev[u];
+      }
+    }
+    __syncthreads();
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int u = 0; u < CW; ++u) sG[(4 * rg + r) * P + CW * cg + u] = acc[r][u];
   }
   __syncthreads();
+  // Aqk back from the record into the E slot (E is dead once W is formed)
+  float* sAq = sbk;
+  for (int e = tid; e < L * L; e += kThreads) sAq[e] = rc[R::AQ + e];
+  {
+    // A = diag(gamma) - KG^T W
+    float acc[CW][CW];
 #pragma unroll
-  for (int r = 0; r < L * DK / kThreads; ++r) {
-    const int e = tid + r * kThreads, t = e / DK, i = e % DK;
-    sG[t * P + i] = wv[r];
+    for (int r = 0; r < CW; ++r)
+#pragma unroll
+      for (int u = 0; u < CW; ++u) acc[r][u] = 0.f;
+#pragma unroll 4
+    for (int t = 0; t < L; ++t) {
+      float kv[CW], wv[CW];
+#pragma unroll
+      for (int u = 0; u < CW; ++u) {
+        kv[u] = sk[t * P + CW * rg + u];
+        wv[u] = sG[t * P + CW * cg + u];
+      }
+#pragma unroll
+      for (int r = 0; r < CW; ++r)
+#pragma unroll
+        for (int u = 0; u < CW; ++u) acc[r][u] += kv[r] * wv[u];
+    }
+#pragma unroll
+    for (int r = 0; r < CW; ++r)
+#pragma unroll
+      for (int u = 0; u < CW; ++u) {
+        const int i = CW * rg + r, j = CW * cg + u;
+        rc[R::A + static_cast<long>(i) * DK + j] = (i == j ? sgam[i] : 0.f) - acc[r][u];
+      }
   }
-  __syncthreads();
-  // A = diag(gamma) - KG^T W
-  for (int e = tid; e < DK * DK; e += kThreads) {
-    const int i = e / DK, j = e % DK;
-    float s = 0.f;
-    for (int t = 0; t < L; ++t) s += sk[t * P + i] * sG[t * P + j];
-    rc[R::A + e] = (i == j ? sgam[i] : 0.f) - s;
+  {
+    // KA = KG^T Ai: rows CW rg .., columns 4 cg ..
+    float acc[CW][4];
+#pragma unroll
+    for (int r = 0; r < CW; ++r)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) acc[r][u] = 0.f;
+#pragma unroll 4
+    for (int t = 0; t < L; ++t) {
+      float kv[CW], av[4];
+#pragma unroll
+      for (int r = 0; r < CW; ++r) kv[r] = sk[t * P + CW * rg + r];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) av[u] = sA[t * L + 4 * cg + u];
+#pragma unroll
+      for (int r = 0; r < CW; ++r)
+#pragma unroll
+        for (int u = 0; u < 4; ++u) acc[r][u] += kv[r] * av[u];
+    }
+#pragma unroll
+    for (int r = 0; r < CW; ++r)
+#pragma unroll
+      for (int u = 0; u < 4; ++u) rc[R::KA + static_cast<long>(CW * rg + r) * L + 4 * cg + u] = acc[r][u];
   }
-  // KA = KG^T Ai
-  for (int e = tid; e < DK * L; e += kThreads) {
-    const int i = e / L, u = e % L;
-    float s = 0.f;
-    for (int t = u; t < L; ++t) s += sk[t * P + i] * sA[t * L + u];
-    rc[R::KA + e] = s;
-  }
-  // QP = Qg - Aqk W (Aqk read back from the record: written before the
-  // barriers above by this workgroup)
-  for (int e = tid; e < L * DK; e += kThreads) {
-    const int t = e / DK, i = e % DK;
-    float s = 0.f;
-    for (int u = 0; u <= t; ++u) s += rc[R::AQ + t * L + u] * sG[u * P + i];
-    rc[R::QP + e] = sq[t * P + i] - s;
+  __syncthreads();   // Aqk staged
+  {
+    // QP = Qg - Aqk W
+    float acc[4][CW];
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int u = 0; u < CW; ++u) acc[r][u] = 0.f;
+#pragma unroll 4
+    for (int s2 = 0; s2 < L; ++s2) {
+      float wv[CW];
+#pragma unroll
+      for (int u = 0; u < CW; ++u) wv[u] = sG[s2 * P + CW * cg + u];
+#pragma unroll
+      for (int r = 0; r < 4; ++r) {
+        const float x = sAq[(4 * rg + r) * L + s2];
+#pragma unroll
+        for (int u = 0; u < CW; ++u) acc[r][u] += x * wv[u];
+      }
+    }
+#pragma unroll
+    for (int r = 0; r < 4; ++r)
+#pragma unroll
+      for (int u = 0; u < CW; ++u) {
+        const int t = 4 * rg + r, i = CW * cg + u;
+        rc[R::QP + static_cast<long>(t) * DK + i] = sq[t * P + i] - acc[r][u];
+      }
   }
 }
 
 // ---------------------------------------------------------------- kernels 2, 3
-// Thread (row i, CPT consecutive columns of the 16-column tile).
+// The chunk's matrices (A and KA, or A and QP: (DK + L) rows of DK or L
+// floats) are staged in LDS; the next chunk's are requested into registers
+// while the current one is applied. Thread (row i, CPT consecutive columns of
+// the 16-column tile).
 template <int DK>
-__global__ __launch_bounds__(kThreads) void bwd_fscan_kernel(const void* __restrict__ v, const void* __restrict__ w,
+struct ScanLds {
+  static constexpr int AP = DK + 4;                  // pitch of A rows
+  static constexpr int XP = (DK > L ? DK : L) + 4;   // pitch of KA / QP rows
+  static constexpr int NF4 = (DK * DK + DK * L) / 4; // float4s staged per chunk (A and KA, or A and QP)
+  static constexpr int PER = (NF4 + kThreads - 1) / kThreads;
+};
+
+// Both matrices are whole multiples of kThreads float4s (DK in {32, 64, 128}),
+// so each register slot n belongs to one of them at compile time.
+template <int DK>
+__device__ __forceinline__ void scan_fetch(const float* rc, long off2, f32x4 (&buf)[ScanLds<DK>::PER]) {
+  constexpr int NA = DK * DK / 4 / kThreads;
+  static_assert(DK * DK / 4 % kThreads == 0 && ScanLds<DK>::NF4 % kThreads == 0, "whole slots");
+  const f32x4* a = reinterpret_cast<const f32x4*>(rc);
+  const f32x4* x = reinterpret_cast<const f32x4*>(rc + off2);
+#pragma unroll
+  for (int n = 0; n < ScanLds<DK>::PER; ++n) {
+    const int f = threadIdx.x + n * kThreads;
+    if (n < NA) buf[n] = a[f];
+    else buf[n] = x[f - NA * kThreads];
+  }
+}
+
+// A [DK][DK] -> sA (pitch AP); the second matrix (DK x L for KA, L x DK for QP,
+// row length RL) -> sX (pitch XP)
+template <int DK, int RL>
+__device__ __forceinline__ void scan_stage(const f32x4 (&buf)[ScanLds<DK>::PER], float* sA, float* sX) {
+  constexpr int NA = DK * DK / 4 / kThreads;
+  using SL = ScanLds<DK>;
+#pragma unroll
+  for (int n = 0; n < SL::PER; ++n) {
+    const int f = threadIdx.x + n * kThreads;
+    if (n < NA) {
+      const int e = 4 * f, r = e / DK, c = e % DK;
+      *reinterpret_cast<f32x4*>(&sA[r * SL::AP + c]) = buf[n];
+    } else {
+      const int e = 4 * (f - NA * kThreads), r = e / RL, c = e % RL;
+      *reinterpret_cast<f32x4*>(&sX[r * SL::XP + c]) = buf[n];
+    }
+  }
+}
+
+template <int DK>
+constexpr int scan_lds_floats() {
+  return DK * ScanLds<DK>::AP + (DK > L ? DK : L) * ScanLds<DK>::XP + DK * CT + L * CT;
+}
+
+template <int DK>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void bwd_fscan_kernel(const void* __restrict__ v, const void* __restrict__ w,
                                                              int dt, const float* __restrict__ rec,
                                                              const float* __restrict__ s0, float* __restrict__ sck,
                                                              int H, int HK, int DV, long S, int NC) {
   constexpr int CPT = DK * CT / kThreads, TPR = CT / CPT;
   using R = Rec<DK>;
-  __shared__ __align__(16) float sS[DK][CT];
-  __shared__ __align__(16) float sZ[L][CT];
+  using SL = ScanLds<DK>;
+  extern __shared__ __align__(16) float sm[];
+  float* sA = sm;                               // [DK][AP]
+  float* sX = sA + DK * SL::AP;                 // KA [DK][XP]
+  float* sS = sX + (DK > L ? DK : L) * SL::XP;  // [DK][CT]
+  float* sZ = sS + DK * CT;                     // [L][CT]
   const int tid = threadIdx.x;
   const int bh = blockIdx.y, bi = bh / H, h = bh % H, hk = h / (H / HK);
   const int c0 = blockIdx.x * CT;
   const int i = tid / TPR, cc = (tid % TPR) * CPT;
+  const float* rbase = rec + static_cast<size_t>(bi * HK + hk) * NC * R::STRIDE;
   for (int e = tid; e < DK * CT; e += kThreads) {
     const int r = e / CT, cl = e % CT;
-    sS[r][cl] = s0 ? s0[(static_cast<size_t>(bh) * DK + r) * DV + c0 + cl] : 0.f;
+    sS[r * CT + cl] = s0 ? s0[(static_cast<size_t>(bh) * DK + r) * DV + c0 + cl] : 0.f;
   }
-  __syncthreads();
+  f32x4 buf[SL::PER];
+  scan_fetch<DK>(rbase, R::KA, buf);
   for (int c = 0; c < NC; ++c) {
-    const float* rc = rec + (static_cast<size_t>(bi * HK + hk) * NC + c) * R::STRIDE;
     float* out = sck + (static_cast<size_t>(bh) * NC + c) * DK * DV;
+    __syncthreads();                            // the previous step's readers are done
+    scan_stage<DK, L>(buf, sA, sX);
+    if (c + 1 < NC) scan_fetch<DK>(rbase + static_cast<size_t>(c + 1) * R::STRIDE, R::KA, buf);
     for (int e = tid; e < DK * CT; e += kThreads) {
       const int r = e / CT, cl = e % CT;
-      out[static_cast<size_t>(r) * DV + c0 + cl] = sS[r][cl];
+      out[static_cast<size_t>(r) * DV + c0 + cl] = sS[r * CT + cl];
     }
     for (int e = tid; e < L * CT; e += kThreads) {
       const int t = e / CT, cl = e % CT;
@@ -244,90 +430,102 @@ __global__ __launch_bounds__(kThreads) void bwd_fscan_kernel(const void* __restr
         const size_t ix = ((static_cast<size_t>(bi) * S + tok) * H + h) * DV + c0 + cl;
         z = load_elem(w, ix, dt) * load_elem(v, ix, dt);
       }
-      sZ[t][cl] = z;
+      sZ[t * CT + cl] = z;
     }
     __syncthreads();
     float acc[CPT];
 #pragma unroll
     for (int u = 0; u < CPT; ++u) acc[u] = 0.f;
+#pragma unroll 4
     for (int j = 0; j < DK; j += 4) {
-      const float4 a = *reinterpret_cast<const float4*>(&rc[R::A + static_cast<long>(i) * DK + j]);
+      const float4 a = *reinterpret_cast<const float4*>(&sA[i * SL::AP + j]);
       const float av[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
       for (int jj = 0; jj < 4; ++jj)
 #pragma unroll
-        for (int u = 0; u < CPT; ++u) acc[u] += av[jj] * sS[j + jj][cc + u];
+        for (int u = 0; u < CPT; ++u) acc[u] += av[jj] * sS[(j + jj) * CT + cc + u];
     }
+#pragma unroll 4
     for (int t = 0; t < L; t += 4) {
-      const float4 a = *reinterpret_cast<const float4*>(&rc[R::KA + static_cast<long>(i) * L + t]);
+      const float4 a = *reinterpret_cast<const float4*>(&sX[i * SL::XP + t]);
       const float av[4] = {a.x, a.y, a.z, a.w};
 #pragma unroll
       for (int tt = 0; tt < 4; ++tt)
 #pragma unroll
-        for (int u = 0; u < CPT; ++u) acc[u] += av[tt] * sZ[t + tt][cc + u];
+        for (int u = 0; u < CPT; ++u) acc[u] += av[tt] * sZ[(t + tt) * CT + cc + u];
     }
     __syncthreads();
 #pragma unroll
-    for (int u = 0; u < CPT; ++u) sS[i][cc + u] = acc[u];
-    __syncthreads();
+    for (int u = 0; u < CPT; ++u) sS[i * CT + cc + u] = acc[u];
   }
 }
 
 template <int DK>
-__global__ __launch_bounds__(kThreads) void bwd_bscan_kernel(const void* __restrict__ dout, int do_dt,
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void bwd_bscan_kernel(const void* __restrict__ dout, int do_dt,
                                                              const float* __restrict__ rec,
                                                              const float* __restrict__ dht, float* __restrict__ dsck,
                                                              float* __restrict__ ds0, int H, int HK, int DV, long S,
                                                              int NC) {
   constexpr int CPT = DK * CT / kThreads, TPR = CT / CPT;
   using R = Rec<DK>;
-  __shared__ __align__(16) float sD[DK][CT];
-  __shared__ __align__(16) float sO[L][CT];
+  using SL = ScanLds<DK>;
+  extern __shared__ __align__(16) float sm[];
+  float* sA = sm;                               // [DK][AP]
+  float* sX = sA + DK * SL::AP;                 // QP [L][XP]
+  float* sD = sX + (DK > L ? DK : L) * SL::XP;  // [DK][CT]
+  float* sO = sD + DK * CT;                     // [L][CT]
   const int tid = threadIdx.x;
   const int bh = blockIdx.y, bi = bh / H, h = bh % H, hk = h / (H / HK);
   const int c0 = blockIdx.x * CT;
   const int i = tid / TPR, cc = (tid % TPR) * CPT;
+  const float* rbase = rec + static_cast<size_t>(bi * HK + hk) * NC * R::STRIDE;
   for (int e = tid; e < DK * CT; e += kThreads) {
     const int r = e / CT, cl = e % CT;
-    sD[r][cl] = dht ? dht[(static_cast<size_t>(bh) * DK + r) * DV + c0 + cl] : 0.f;
+    sD[r * CT + cl] = dht ? dht[(static_cast<size_t>(bh) * DK + r) * DV + c0 + cl] : 0.f;
   }
-  __syncthreads();
+  f32x4 buf[SL::PER];
+  if (NC > 0) scan_fetch<DK>(rbase + static_cast<size_t>(NC - 1) * R::STRIDE, R::QP, buf);
   for (int c = NC - 1; c >= 0; --c) {
-    const float* rc = rec + (static_cast<size_t>(bi * HK + hk) * NC + c) * R::STRIDE;
     float* out = dsck + (static_cast<size_t>(bh) * NC + c) * DK * DV;
+    __syncthreads();
+    scan_stage<DK, DK>(buf, sA, sX);
+    if (c > 0) scan_fetch<DK>(rbase + static_cast<size_t>(c - 1) * R::STRIDE, R::QP, buf);
     for (int e = tid; e < DK * CT; e += kThreads) {
       const int r = e / CT, cl = e % CT;
-      out[static_cast<size_t>(r) * DV + c0 + cl] = sD[r][cl];
+      out[static_cast<size_t>(r) * DV + c0 + cl] = sD[r * CT + cl];
     }
     for (int e = tid; e < L * CT; e += kThreads) {
       const int t = e / CT, cl = e % CT;
       const long tok = static_cast<long>(c) * L + t;
-      sO[t][cl] = tok < S ? load_elem(dout, ((static_cast<size_t>(bi) * S + tok) * H + h) * DV + c0 + cl, do_dt)
-                          : 0.f;
+      sO[t * CT + cl] = tok < S
+                            ? load_elem(dout, ((static_cast<size_t>(bi) * S + tok) * H + h) * DV + c0 + cl, do_dt)
+                            : 0.f;
     }
     __syncthreads();
     float acc[CPT];
 #pragma unroll
     for (int u = 0; u < CPT; ++u) acc[u] = 0.f;
+#pragma unroll 8
     for (int j = 0; j < DK; ++j) {
-      const float a = rc[R::A + static_cast<long>(j) * DK + i];   // A^T
+      const float a = sA[j * SL::AP + i];      // A^T
 #pragma unroll
-      for (int u = 0; u < CPT; ++u) acc[u] += a * sD[j][cc + u];
+      for (int u = 0; u < CPT; ++u) acc[u] += a * sD[j * CT + cc + u];
     }
+#pragma unroll 8
     for (int t = 0; t < L; ++t) {
-      const float a = rc[R::QP + static_cast<long>(t) * DK + i];  // QP^T
+      const float a = sX[t * SL::XP + i];      // QP^T
 #pragma unroll
-      for (int u = 0; u < CPT; ++u) acc[u] += a * sO[t][cc + u];
+      for (int u = 0; u < CPT; ++u) acc[u] += a * sO[t * CT + cc + u];
     }
     __syncthreads();
 #pragma unroll
-    for (int u = 0; u < CPT; ++u) sD[i][cc + u] = acc[u];
-    __syncthreads();
+    for (int u = 0; u < CPT; ++u) sD[i * CT + cc + u] = acc[u];
   }
+  __syncthreads();
   if (ds0) {
     for (int e = tid; e < DK * CT; e += kThreads) {
       const int r = e / CT, cl = e % CT;
-      ds0[(static_cast<size_t>(bh) * DK + r) * DV + c0 + cl] = sD[r][cl];
+      ds0[(static_cast<size_t>(bh) * DK + r) * DV + c0 + cl] = sD[r * CT + cl];
     }
   }
 }
@@ -448,6 +646,7 @@ __global__ __launch_bounds__(kThreads) void bwd_grad_kernel(
     // Y = Z - E S (in place: each thread rewrites only its own four entries)
     {
       float4 a = *reinterpret_cast<const float4*>(&sY[pt * CP + pc]);
+#pragma unroll 8
       for (int i = 0; i < DK; ++i) {
         const float e = sE[pt * P + i];
         const float4 s4 = *reinterpret_cast<const float4*>(&sS[i * CP + pc]);
@@ -459,6 +658,7 @@ __global__ __launch_bounds__(kThreads) void bwd_grad_kernel(
     // U = Ai Y
     {
       float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
       for (int u = 0; u <= pt; ++u) {
         const float x = sAi[pt * L + u];
         const float4 y4 = *reinterpret_cast<const float4*>(&sY[u * CP + pc]);
@@ -470,11 +670,13 @@ __global__ __launch_bounds__(kThreads) void bwd_grad_kernel(
     // dU = Aqk^T dO + KG dS' (over Y)
     {
       float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
       for (int u = pt; u < L; ++u) {
         const float x = sAq[u * L + pt];
         const float4 o4 = *reinterpret_cast<const float4*>(&sdO[u * CP + pc]);
         a.x += x * o4.x; a.y += x * o4.y; a.z += x * o4.z; a.w += x * o4.w;
       }
+#pragma unroll 8
       for (int i = 0; i < DK; ++i) {
         const float x = sKG[pt * P + i];
         const float4 d4 = *reinterpret_cast<const float4*>(&sdS[i * CP + pc]);
@@ -486,6 +688,7 @@ __global__ __launch_bounds__(kThreads) void bwd_grad_kernel(
     // dY = Ai^T dU; dv = w dY, dw = v dY
     {
       float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
+#pragma unroll 8
       for (int u = pt; u < L; ++u) {
         const float x = sAi[u * L + pt];
         const float4 y4 = *reinterpret_cast<const float4*>(&sY[u * CP + pc]);
@@ -506,6 +709,7 @@ __global__ __launch_bounds__(kThreads) void bwd_grad_kernel(
     __syncthreads();
     // accumulate dQg = dO S^T, dE = -dY S^T, dKG = U dS'^T, dAqk = dO U^T,
     // dAkk = -dY U^T, dgamma = rowsum(dS' S)
+#pragma unroll 4
     for (int cl = 0; cl < CT; ++cl) {
       float o[4], y[4], uu[4], ut[4], sv[CPB], dsv[CPB];
 #pragma unroll
@@ -585,6 +789,7 @@ __global__ __launch_bounds__(kThreads) void bwd_grad_kernel(
       rq[u] = rk[u] = cq[u] = ck[u] = 0.f;
       gt[u] = pG[t * DK + ib * CPB + u];
     }
+#pragma unroll 4
     for (int s = 0; s <= t; ++s) {            // row sums: partners s <= t
       const float xq = pAq[t * L + s], xk = pAk[t * L + s];
 #pragma unroll
@@ -595,6 +800,7 @@ __global__ __launch_bounds__(kThreads) void bwd_grad_kernel(
         rk[u] += xk * e;
       }
     }
+#pragma unroll 4
     for (int s = t; s < L; ++s) {             // column sums: partners s >= t
       const float xq = pAq[s * L + t], xk = pAk[s * L + t];
 #pragma unroll
@@ -697,10 +903,29 @@ hipError_t launch_backward_t(const void* q, const void* k, const void* v, const 
                              const float* dht, void* dq, void* dk, void* dv, float* dg, void* db, void* dw,
                              float* ds0, void* workspace, int B, int H, int HK, int DV, long S, hipStream_t stream) {
   const int NC = static_cast<int>((S + bw::L - 1) / bw::L);
+  constexpr int lds1 = bw::local_lds_floats<DK>() * 4;
+  constexpr int lds4 = bw::grad_lds_floats<DK>() * 4;
+  constexpr int lds2 = bw::scan_lds_floats<DK>() * 4;
+  static bool configured = false;   // attributes set once per process (same values always)
+  if (!configured) {
+    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&bw::bwd_local_kernel<DK>),
+                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds1);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&bw::bwd_grad_kernel<DK>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds4);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&bw::bwd_fscan_kernel<DK>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds2);
+    if (e == hipSuccess)
+      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&bw::bwd_bscan_kernel<DK>),
+                              hipFuncAttributeMaxDynamicSharedMemorySize, lds2);
+    if (e != hipSuccess) return e;
+    configured = true;
+  }
   if (NC == 0) {   // no tokens: the initial-state gradient is the final-state one (or zero)
     if (ds0)
-      hipLaunchKernelGGL(bw::bwd_bscan_kernel<DK>, dim3(DV / bw::CT, B * H), dim3(bw::kThreads), 0, stream, dout,
-                         do_dt, nullptr, dht, nullptr, ds0, H, HK, DV, S, 0);
+      hipLaunchKernelGGL(bw::bwd_bscan_kernel<DK>, dim3(DV / bw::CT, B * H), dim3(bw::kThreads),
+                         lds2, stream, dout, do_dt, nullptr, dht, nullptr, ds0, H, HK, DV, S, 0);
     return hipGetLastError();
   }
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
@@ -713,24 +938,12 @@ hipError_t launch_backward_t(const void* q, const void* k, const void* v, const 
   ws += up(static_cast<size_t>(B) * H * NC * DK * DV * 4);
   float* part = reinterpret_cast<float*>(ws);
 
-  constexpr int lds1 = bw::local_lds_floats<DK>() * 4;
-  constexpr int lds4 = bw::grad_lds_floats<DK>() * 4;
-  static bool configured = false;   // attributes set once per process (same values always)
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&bw::bwd_local_kernel<DK>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds1);
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&bw::bwd_grad_kernel<DK>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, lds4);
-    if (e != hipSuccess) return e;
-    configured = true;
-  }
   hipLaunchKernelGGL(bw::bwd_local_kernel<DK>, dim3(NC, B * HK), dim3(bw::kThreads), lds1, stream, q, k, b, g, dt,
                      HK, S, NC, scale, rec);
-  hipLaunchKernelGGL(bw::bwd_fscan_kernel<DK>, dim3(DV / bw::CT, B * H), dim3(bw::kThreads), 0, stream, v, w, dt,
-                     rec, s0, sck, H, HK, DV, S, NC);
-  hipLaunchKernelGGL(bw::bwd_bscan_kernel<DK>, dim3(DV / bw::CT, B * H), dim3(bw::kThreads), 0, stream, dout, do_dt,
-                     rec, dht, dsck, ds0, H, HK, DV, S, NC);
+  hipLaunchKernelGGL(bw::bwd_fscan_kernel<DK>, dim3(DV / bw::CT, B * H), dim3(bw::kThreads), lds2, stream, v, w,
+                     dt, rec, s0, sck, H, HK, DV, S, NC);
+  hipLaunchKernelGGL(bw::bwd_bscan_kernel<DK>, dim3(DV / bw::CT, B * H), dim3(bw::kThreads), lds2, stream, dout,
+                     do_dt, rec, dht, dsck, ds0, H, HK, DV, S, NC);
   hipLaunchKernelGGL(bw::bwd_grad_kernel<DK>, dim3(NC, B * H), dim3(bw::kThreads), lds4, stream, q, k, v, g, b, w,
                      dt, dout, do_dt, rec, sck, dsck, dv, dw, part, H, HK, DV, S, NC, scale);
   const long n_key = static_cast<long>(B) * S * HK * DK;
