@@ -23,12 +23,14 @@
 //
 // Kernels, in order on one stream:
 //   1. bwd_local_kernel  per (b, key head, chunk): A, KA, QP, Ai, Aqk, gamma
-//   2. bwd_fscan_kernel  per (b, value head, 16 columns): the chunk-entry
-//      states S_c, forward over the chunks
-//   3. bwd_bscan_kernel  per (b, value head, 16 columns): dS' of every chunk,
-//      backward over the chunks; dS_0 is the initial-state gradient
-//   4. bwd_grad_kernel   per (b, value head, chunk): dv, dw and the value
-//      head's share of dq, dk, db, dg (fp32)
+//   2. bwd_scan_kernel<forward>  per (b, value head, 16 columns): the
+//      chunk-entry states S_c, forward over the chunks
+//   3. bwd_scan_kernel<backward> per (b, value head, 16 columns): dS' of every
+//      chunk, backward over the chunks; dS_0 is the initial-state gradient
+//   4. bwd_gradmm_kernel per (b, value head, chunk): dv, dw and the
+//      DV-contracted sums (fp32 matrix cores); bwd_gradpw_kernel per (b,
+//      value head, chunk, 32 channels): the value head's share of dq, dk, db,
+//      dg
 //   5. bwd_sum_kernel    sums the shares of the value heads of each key head
 //      and rounds to the output dtypes
 // Every exponent taken is G_t - G_s for s <= t (or G_L - G_t, or G_t), <= 0
@@ -53,14 +55,49 @@ struct Rec {                     // fp32 per-(b, key head, chunk) record of kern
   static constexpr long AI = QP + L * DK;    // [L][L]
   static constexpr long AQ = AI + L * L;     // [L][L]
   static constexpr long GM = AQ + L * L;     // [DK]
-  static constexpr long STRIDE = (GM + DK + 63) / 64 * 64;
+  static constexpr long AT = GM + 64;        // [DK][DK]  A^T   (for the reverse scan)
+  static constexpr long QPT = AT + DK * DK;  // [DK][L]   QP^T
+  static constexpr long STRIDE = QPT + DK * L;
 };
+
+// Workgroup barrier for LDS hand-offs only: __syncthreads() also waits for
+// every outstanding global load, which would stall the loads requested for
+// the next step. Used where no thread reads global memory another thread of
+// the workgroup wrote.
+__device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
+
+// Raw element (16-bit types zero-extended by the load itself) and its value:
+// the conversion is left to the consumer, so a prefetch does not wait here.
+__device__ __forceinline__ uint32_t load_raw(const void* p, size_t i, int dt) {
+  if (dt == DT_F32) return __float_as_uint(static_cast<const float*>(p)[i]);
+  return static_cast<const unsigned short*>(p)[i];
+}
+__device__ __forceinline__ float raw_f32(uint32_t u, int dt) {
+  if (dt == DT_BF16) return __uint_as_float(u << 16);
+  if (dt == DT_F16) return f16_bits_to_f32(static_cast<unsigned short>(u));
+  return __uint_as_float(u);
+}
 
 __device__ __forceinline__ size_t key_index(int bi, long S, long t, int HK, int hk, int DK, int i) {
   return ((static_cast<size_t>(bi) * S + t) * HK + hk) * DK + i;
 }
 
 // ---------------------------------------------------------------- kernel 1
+// N consecutive floats (N a multiple of 4, or 2 or 1) to 16-byte (or 8-byte)
+// aligned global memory
+template <int N>
+__device__ __forceinline__ void store_run(float* dst, const float* x) {
+  if constexpr (N % 4 == 0) {
+#pragma unroll
+    for (int q = 0; q < N / 4; ++q) reinterpret_cast<f32x4*>(dst)[q] = f32x4{x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]};
+  } else if constexpr (N == 2) {
+    *reinterpret_cast<f32x2*>(dst) = f32x2{x[0], x[1]};
+  } else {
+#pragma unroll
+    for (int q = 0; q < N; ++q) dst[q] = x[q];
+  }
+}
+
 template <int DK>
 constexpr int local_lds_floats() { return 3 * L * (DK + 4) + L * (DK + 4 > L ? DK + 4 : L) + L * L + DK + 9 * 256; }
 
@@ -279,8 +316,17 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const void* __restr
 #pragma unroll
       for (int u = 0; u < CW; ++u) {
         const int i = CW * rg + r, j = CW * cg + u;
-        rc[R::A + static_cast<long>(i) * DK + j] = (i == j ? sgam[i] : 0.f) - acc[r][u];
+        acc[r][u] = (i == j ? sgam[i] : 0.f) - acc[r][u];
       }
+#pragma unroll
+    for (int r = 0; r < CW; ++r) store_run<CW>(rc + R::A + static_cast<long>(CW * rg + r) * DK + CW * cg, acc[r]);
+#pragma unroll
+    for (int u = 0; u < CW; ++u) {
+      float col[CW];
+#pragma unroll
+      for (int r = 0; r < CW; ++r) col[r] = acc[r][u];
+      store_run<CW>(rc + R::AT + static_cast<long>(CW * cg + u) * DK + CW * rg, col);
+    }
   }
   {
     // KA = KG^T Ai: rows CW rg .., columns 4 cg ..
@@ -302,9 +348,7 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const void* __restr
         for (int u = 0; u < 4; ++u) acc[r][u] += kv[r] * av[u];
     }
 #pragma unroll
-    for (int r = 0; r < CW; ++r)
-#pragma unroll
-      for (int u = 0; u < 4; ++u) rc[R::KA + static_cast<long>(CW * rg + r) * L + 4 * cg + u] = acc[r][u];
+    for (int r = 0; r < CW; ++r) store_run<4>(rc + R::KA + static_cast<long>(CW * rg + r) * L + 4 * cg, acc[r]);
   }
   __syncthreads();   // Aqk staged
   {
@@ -331,275 +375,224 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const void* __restr
 #pragma unroll
       for (int u = 0; u < CW; ++u) {
         const int t = 4 * rg + r, i = CW * cg + u;
-        rc[R::QP + static_cast<long>(t) * DK + i] = sq[t * P + i] - acc[r][u];
+        acc[r][u] = sq[t * P + i] - acc[r][u];
       }
+#pragma unroll
+    for (int r = 0; r < 4; ++r) store_run<CW>(rc + R::QP + static_cast<long>(4 * rg + r) * DK + CW * cg, acc[r]);
+#pragma unroll
+    for (int u = 0; u < CW; ++u) {
+      const float col[4] = {acc[0][u], acc[1][u], acc[2][u], acc[3][u]};
+      store_run<4>(rc + R::QPT + static_cast<long>(CW * cg + u) * L + 4 * rg, col);
+    }
   }
 }
 
 // ---------------------------------------------------------------- kernels 2, 3
-// The chunk's matrices (A and KA, or A and QP: (DK + L) rows of DK or L
-// floats) are staged in LDS; the next chunk's are requested into registers
-// while the current one is applied. Thread (row i, CPT consecutive columns of
-// the 16-column tile).
+// One scan kernel, both directions, on fp32 matrix cores
+// (v_mfma_f32_16x16x4_f32: lane l supplies A[l % 16][k] and B[k][l % 16] and
+// holds D[4 (l / 16) + e][l % 16]). Per chunk step, for the workgroup's 16
+// value columns:
+//   forward:  X <- A X + KA Z,    X = S,   Z = w v,  A, KA from the record
+//   backward: X <- A^T X + QP^T Z, X = dS', Z = dO,  A^T, QP^T from the record
+// X (DK x 16) and Z (L x 16) live in LDS; wave w owns the 16-row output tiles
+// TPW w .., its A-operand rows come straight from the record into registers
+// (the next chunk's requested while the current one is applied). The k index
+// of lane group g = l / 16 runs over its own contiguous quarter of each
+// matrix's columns, so those rows load as 16-byte vectors; the B operand
+// follows the same order.
 template <int DK>
-struct ScanLds {
-  static constexpr int AP = DK + 4;                  // pitch of A rows
-  static constexpr int XP = (DK > L ? DK : L) + 4;   // pitch of KA / QP rows
-  static constexpr int NF4 = (DK * DK + DK * L) / 4; // float4s staged per chunk (A and KA, or A and QP)
-  static constexpr int PER = (NF4 + kThreads - 1) / kThreads;
+struct ScanCfg {
+  static constexpr int TILES = DK / 16;                     // output row tiles
+  static constexpr int TPW = TILES >= 4 ? TILES / 4 : 1;    // tiles per wave
+  static constexpr int KA_ = DK / 4, KZ = L / 4;            // k steps per lane group
+  static constexpr int XP = CT + 1;                         // LDS pitch of X and Z rows
 };
 
-// Both matrices are whole multiples of kThreads float4s (DK in {32, 64, 128}),
-// so each register slot n belongs to one of them at compile time.
-template <int DK>
-__device__ __forceinline__ void scan_fetch(const float* rc, long off2, f32x4 (&buf)[ScanLds<DK>::PER]) {
-  constexpr int NA = DK * DK / 4 / kThreads;
-  static_assert(DK * DK / 4 % kThreads == 0 && ScanLds<DK>::NF4 % kThreads == 0, "whole slots");
-  const f32x4* a = reinterpret_cast<const f32x4*>(rc);
-  const f32x4* x = reinterpret_cast<const f32x4*>(rc + off2);
-#pragma unroll
-  for (int n = 0; n < ScanLds<DK>::PER; ++n) {
-    const int f = threadIdx.x + n * kThreads;
-    if (n < NA) buf[n] = a[f];
-    else buf[n] = x[f - NA * kThreads];
-  }
-}
-
-// A [DK][DK] -> sA (pitch AP); the second matrix (DK x L for KA, L x DK for QP,
-// row length RL) -> sX (pitch XP)
-template <int DK, int RL>
-__device__ __forceinline__ void scan_stage(const f32x4 (&buf)[ScanLds<DK>::PER], float* sA, float* sX) {
-  constexpr int NA = DK * DK / 4 / kThreads;
-  using SL = ScanLds<DK>;
-#pragma unroll
-  for (int n = 0; n < SL::PER; ++n) {
-    const int f = threadIdx.x + n * kThreads;
-    if (n < NA) {
-      const int e = 4 * f, r = e / DK, c = e % DK;
-      *reinterpret_cast<f32x4*>(&sA[r * SL::AP + c]) = buf[n];
-    } else {
-      const int e = 4 * (f - NA * kThreads), r = e / RL, c = e % RL;
-      *reinterpret_cast<f32x4*>(&sX[r * SL::XP + c]) = buf[n];
-    }
-  }
-}
-
-template <int DK>
-constexpr int scan_lds_floats() {
-  return DK * ScanLds<DK>::AP + (DK > L ? DK : L) * ScanLds<DK>::XP + DK * CT + L * CT;
-}
-
-template <int DK>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void bwd_fscan_kernel(const void* __restrict__ v, const void* __restrict__ w,
-                                                             int dt, const float* __restrict__ rec,
-                                                             const float* __restrict__ s0, float* __restrict__ sck,
-                                                             int H, int HK, int DV, long S, int NC) {
-  constexpr int CPT = DK * CT / kThreads, TPR = CT / CPT;
+template <int DK, bool BACK>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void bwd_scan_kernel(
+    const void* __restrict__ x1, const void* __restrict__ x2, int dt, const float* __restrict__ rec,
+    const float* __restrict__ init, float* __restrict__ ck, float* __restrict__ fin, int H, int HK, int DV, long S,
+    int NC) {
   using R = Rec<DK>;
-  using SL = ScanLds<DK>;
-  extern __shared__ __align__(16) float sm[];
-  float* sA = sm;                               // [DK][AP]
-  float* sX = sA + DK * SL::AP;                 // KA [DK][XP]
-  float* sS = sX + (DK > L ? DK : L) * SL::XP;  // [DK][CT]
-  float* sZ = sS + DK * CT;                     // [L][CT]
-  const int tid = threadIdx.x;
+  using C = ScanCfg<DK>;
+  constexpr long M1 = BACK ? R::AT : R::A;
+  constexpr long M2 = BACK ? R::QPT : R::KA;
+  __shared__ float sX[DK * C::XP];
+  __shared__ float sZ[L * C::XP];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int g = lane >> 4, m = lane & 15;
   const int bh = blockIdx.y, bi = bh / H, h = bh % H, hk = h / (H / HK);
   const int c0 = blockIdx.x * CT;
-  const int i = tid / TPR, cc = (tid % TPR) * CPT;
+  const bool computes = wave * C::TPW < C::TILES;   // DK = 32: two waves hold the tiles
   const float* rbase = rec + static_cast<size_t>(bi * HK + hk) * NC * R::STRIDE;
   for (int e = tid; e < DK * CT; e += kThreads) {
     const int r = e / CT, cl = e % CT;
-    sS[r * CT + cl] = s0 ? s0[(static_cast<size_t>(bh) * DK + r) * DV + c0 + cl] : 0.f;
+    sX[r * C::XP + cl] = init ? init[(static_cast<size_t>(bh) * DK + r) * DV + c0 + cl] : 0.f;
   }
-  f32x4 buf[SL::PER];
-  scan_fetch<DK>(rbase, R::KA, buf);
-  for (int c = 0; c < NC; ++c) {
-    float* out = sck + (static_cast<size_t>(bh) * NC + c) * DK * DV;
-    __syncthreads();                            // the previous step's readers are done
-    scan_stage<DK, L>(buf, sA, sX);
-    if (c + 1 < NC) scan_fetch<DK>(rbase + static_cast<size_t>(c + 1) * R::STRIDE, R::KA, buf);
-    for (int e = tid; e < DK * CT; e += kThreads) {
-      const int r = e / CT, cl = e % CT;
-      out[static_cast<size_t>(r) * DV + c0 + cl] = sS[r * CT + cl];
+  // two register sets of A-operand rows: the next chunk's are requested
+  // before the current chunk's products are issued
+  f32x4 aA0[C::TPW][C::KA_ / 4], aZ0[C::TPW][C::KZ / 4], aA1[C::TPW][C::KA_ / 4], aZ1[C::TPW][C::KZ / 4];
+  auto fetch_m = [&](int c, f32x4 (&aA)[C::TPW][C::KA_ / 4], f32x4 (&aZ)[C::TPW][C::KZ / 4]) {
+    if (!computes) return;
+    const float* rc = rbase + static_cast<size_t>(c) * R::STRIDE;
+#pragma unroll
+    for (int r = 0; r < C::TPW; ++r) {
+      const int row = 16 * (wave * C::TPW + r) + m;
+      const f32x4* pa = reinterpret_cast<const f32x4*>(rc + M1 + static_cast<long>(row) * DK + g * C::KA_);
+      const f32x4* pz = reinterpret_cast<const f32x4*>(rc + M2 + static_cast<long>(row) * L + g * C::KZ);
+#pragma unroll
+      for (int q = 0; q < C::KA_ / 4; ++q) aA[r][q] = pa[q];
+#pragma unroll
+      for (int q = 0; q < C::KZ / 4; ++q) aZ[r][q] = pz[q];
     }
-    for (int e = tid; e < L * CT; e += kThreads) {
-      const int t = e / CT, cl = e % CT;
+  };
+  constexpr int NT = L * CT / kThreads;
+  uint32_t p1[NT], p2[NT];
+  auto fetch_z = [&](int c) {
+#pragma unroll
+    for (int n = 0; n < NT; ++n) {
+      const int e = tid + n * kThreads, t = e / CT, cl = e % CT;
       const long tok = static_cast<long>(c) * L + t;
-      float z = 0.f;
+      p1[n] = p2[n] = 0u;
       if (tok < S) {
         const size_t ix = ((static_cast<size_t>(bi) * S + tok) * H + h) * DV + c0 + cl;
-        z = load_elem(w, ix, dt) * load_elem(v, ix, dt);
+        p1[n] = load_raw(x1, ix, dt);
+        if (!BACK) p2[n] = load_raw(x2, ix, dt);
       }
-      sZ[t * CT + cl] = z;
     }
-    __syncthreads();
-    float acc[CPT];
+  };
+  auto chunk_of = [&](int step) { return BACK ? NC - 1 - step : step; };
+  auto run = [&](int step, f32x4 (&aA)[C::TPW][C::KA_ / 4], f32x4 (&aZ)[C::TPW][C::KZ / 4],
+                 f32x4 (&nA)[C::TPW][C::KA_ / 4], f32x4 (&nZ)[C::TPW][C::KZ / 4]) {
+    const int c = chunk_of(step);
+    lds_barrier();                              // X is final; Z's previous readers are done
 #pragma unroll
-    for (int u = 0; u < CPT; ++u) acc[u] = 0.f;
-#pragma unroll 4
-    for (int j = 0; j < DK; j += 4) {
-      const float4 a = *reinterpret_cast<const float4*>(&sA[i * SL::AP + j]);
-      const float av[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-      for (int jj = 0; jj < 4; ++jj)
-#pragma unroll
-        for (int u = 0; u < CPT; ++u) acc[u] += av[jj] * sS[(j + jj) * CT + cc + u];
+    for (int n = 0; n < NT; ++n) {
+      const int e = tid + n * kThreads;
+      sZ[(e / CT) * C::XP + e % CT] = BACK ? raw_f32(p1[n], dt) : raw_f32(p1[n], dt) * raw_f32(p2[n], dt);
     }
-#pragma unroll 4
-    for (int t = 0; t < L; t += 4) {
-      const float4 a = *reinterpret_cast<const float4*>(&sX[i * SL::XP + t]);
-      const float av[4] = {a.x, a.y, a.z, a.w};
-#pragma unroll
-      for (int tt = 0; tt < 4; ++tt)
-#pragma unroll
-        for (int u = 0; u < CPT; ++u) acc[u] += av[tt] * sZ[(t + tt) * CT + cc + u];
+    if (step + 1 < NC) {
+      fetch_m(chunk_of(step + 1), nA, nZ);
+      fetch_z(chunk_of(step + 1));
     }
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < CPT; ++u) sS[i * CT + cc + u] = acc[u];
-  }
-}
-
-template <int DK>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 2))) void bwd_bscan_kernel(const void* __restrict__ dout, int do_dt,
-                                                             const float* __restrict__ rec,
-                                                             const float* __restrict__ dht, float* __restrict__ dsck,
-                                                             float* __restrict__ ds0, int H, int HK, int DV, long S,
-                                                             int NC) {
-  constexpr int CPT = DK * CT / kThreads, TPR = CT / CPT;
-  using R = Rec<DK>;
-  using SL = ScanLds<DK>;
-  extern __shared__ __align__(16) float sm[];
-  float* sA = sm;                               // [DK][AP]
-  float* sX = sA + DK * SL::AP;                 // QP [L][XP]
-  float* sD = sX + (DK > L ? DK : L) * SL::XP;  // [DK][CT]
-  float* sO = sD + DK * CT;                     // [L][CT]
-  const int tid = threadIdx.x;
-  const int bh = blockIdx.y, bi = bh / H, h = bh % H, hk = h / (H / HK);
-  const int c0 = blockIdx.x * CT;
-  const int i = tid / TPR, cc = (tid % TPR) * CPT;
-  const float* rbase = rec + static_cast<size_t>(bi * HK + hk) * NC * R::STRIDE;
-  for (int e = tid; e < DK * CT; e += kThreads) {
-    const int r = e / CT, cl = e % CT;
-    sD[r * CT + cl] = dht ? dht[(static_cast<size_t>(bh) * DK + r) * DV + c0 + cl] : 0.f;
-  }
-  f32x4 buf[SL::PER];
-  if (NC > 0) scan_fetch<DK>(rbase + static_cast<size_t>(NC - 1) * R::STRIDE, R::QP, buf);
-  for (int c = NC - 1; c >= 0; --c) {
-    float* out = dsck + (static_cast<size_t>(bh) * NC + c) * DK * DV;
-    __syncthreads();
-    scan_stage<DK, DK>(buf, sA, sX);
-    if (c > 0) scan_fetch<DK>(rbase + static_cast<size_t>(c - 1) * R::STRIDE, R::QP, buf);
+    float* out = ck + (static_cast<size_t>(bh) * NC + c) * DK * DV;
     for (int e = tid; e < DK * CT; e += kThreads) {
       const int r = e / CT, cl = e % CT;
-      out[static_cast<size_t>(r) * DV + c0 + cl] = sD[r * CT + cl];
+      out[static_cast<size_t>(r) * DV + c0 + cl] = sX[r * C::XP + cl];
     }
-    for (int e = tid; e < L * CT; e += kThreads) {
-      const int t = e / CT, cl = e % CT;
-      const long tok = static_cast<long>(c) * L + t;
-      sO[t * CT + cl] = tok < S
-                            ? load_elem(dout, ((static_cast<size_t>(bi) * S + tok) * H + h) * DV + c0 + cl, do_dt)
-                            : 0.f;
+    lds_barrier();
+    f32x4 acc[C::TPW];
+    if (computes) {
+#pragma unroll
+      for (int r = 0; r < C::TPW; ++r) {
+        acc[r] = zero4();
+#pragma unroll
+        for (int q = 0; q < C::KA_ / 4; ++q)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(aA[r][q][e], sX[(g * C::KA_ + 4 * q + e) * C::XP + m],
+                                                          acc[r], 0, 0, 0);
+#pragma unroll
+        for (int q = 0; q < C::KZ / 4; ++q)
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(aZ[r][q][e], sZ[(g * C::KZ + 4 * q + e) * C::XP + m],
+                                                          acc[r], 0, 0, 0);
+      }
     }
-    __syncthreads();
-    float acc[CPT];
+    lds_barrier();                              // every wave has read X
+    if (computes) {
 #pragma unroll
-    for (int u = 0; u < CPT; ++u) acc[u] = 0.f;
-#pragma unroll 8
-    for (int j = 0; j < DK; ++j) {
-      const float a = sA[j * SL::AP + i];      // A^T
+      for (int r = 0; r < C::TPW; ++r)
 #pragma unroll
-      for (int u = 0; u < CPT; ++u) acc[u] += a * sD[j * CT + cc + u];
+        for (int e = 0; e < 4; ++e) sX[(16 * (wave * C::TPW + r) + 4 * g + e) * C::XP + m] = acc[r][e];
     }
-#pragma unroll 8
-    for (int t = 0; t < L; ++t) {
-      const float a = sX[t * SL::XP + i];      // QP^T
-#pragma unroll
-      for (int u = 0; u < CPT; ++u) acc[u] += a * sO[t * CT + cc + u];
-    }
-    __syncthreads();
-#pragma unroll
-    for (int u = 0; u < CPT; ++u) sD[i * CT + cc + u] = acc[u];
+  };
+  if (NC > 0) {
+    fetch_m(chunk_of(0), aA0, aZ0);
+    fetch_z(chunk_of(0));
+  }
+  for (int step = 0; step < NC; step += 2) {
+    run(step, aA0, aZ0, aA1, aZ1);
+    if (step + 1 < NC) run(step + 1, aA1, aZ1, aA0, aZ0);
   }
   __syncthreads();
-  if (ds0) {
+  if (fin) {
     for (int e = tid; e < DK * CT; e += kThreads) {
       const int r = e / CT, cl = e % CT;
-      ds0[(static_cast<size_t>(bh) * DK + r) * DV + c0 + cl] = sD[r * CT + cl];
+      fin[(static_cast<size_t>(bh) * DK + r) * DV + c0 + cl] = sX[r * C::XP + cl];
     }
   }
 }
 
 // ---------------------------------------------------------------- kernel 4
+// Per (b, value head, chunk), in two launches.
+//
+// 4a, bwd_gradmm_kernel: the DV-contracted products on fp32 matrix cores.
+// Wave w owns chunk rows 16 w .. 16 w + 15. Its A-operand rows stay in
+// registers for the whole call: -E and KG (k over DK), Ai, Ai^T and Aqk^T (k
+// over the 64 rows); lane group g = l / 16 takes its own contiguous quarter
+// of each k range. Per 16-column block of DV:
+//   Y = Z - E S        (Z enters as the accumulator, in the output layout)
+//   U = Ai Y,  dU = Aqk^T dO + KG dS',  dY = Ai^T dU,  dv = w dY, dw = v dY
+//   dQg += dO S^T, dE -= dY S^T, dKG += U dS'^T, dAqk += dO U^T, dAkk -= dY U^T
+// (Y, U and dU pass between the waves through LDS). The sums go to an fp32
+// scratch record with dgamma = rowsum(dS' S).
+// 4b, bwd_gradpw_kernel: per 32-channel block, the pairwise terms that carry
+// dAqk and dAkk to q, k, b and G, the first-order terms, and dg as the reverse
+// cumsum of dG; each value head writes its share of dq, dk, db, dg.
 template <int DK>
-constexpr int grad_lds_floats() {
-  constexpr int p1 = 2 * L * (DK + 4) + 2 * L * L + 2 * DK * CP + 4 * L * CP + DK;
-  constexpr int p2 = 4 * L * DK + 2 * L * L;
-  return p1 > p2 ? p1 : p2;
+struct GS {                      // fp32 scratch record of kernel 4a
+  static constexpr long QG = 0, E = L * DK, KG = 2 * L * DK, AQ = 3 * L * DK, AK = AQ + L * L, GAM = AK + L * L;
+  static constexpr long STRIDE = GAM + DK;
+};
+
+__device__ __forceinline__ f32x4 mma(float a, float b, f32x4 c) {
+  return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-// Thread tiles: the per-column-block products give each thread one row t and
-// four columns; the accumulated gradients give it 4 rows (4 tb ..) by CPB
-// channels (ib CPB ..) of dQg, dE, dKG and 4 x 4 entries (rows 4 tb .., columns
-// 4 ib ..) of dAqk, dAkk. The pairwise phase works on the same (t, i)
-// elements, so their first-order terms come from the thread's own registers.
 template <int DK>
-__global__ __launch_bounds__(kThreads) void bwd_grad_kernel(
-    const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ v, const float* __restrict__ g,
-    const void* __restrict__ b, const void* __restrict__ w, int dt, const void* __restrict__ dout, int do_dt,
-    const float* __restrict__ rec, const float* __restrict__ sck, const float* __restrict__ dsck, void* __restrict__ dv,
-    void* __restrict__ dw, float* __restrict__ part, int H, int HK, int DV, long S, int NC, float scale) {
-  constexpr int P = DK + 4;
-  constexpr int CPB = DK / 16;
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void bwd_gradmm_kernel(
+    const void* __restrict__ k, const void* __restrict__ v, const float* __restrict__ g, const void* __restrict__ b,
+    const void* __restrict__ w, int dt, const void* __restrict__ dout, int do_dt, const float* __restrict__ rec,
+    const float* __restrict__ sck, const float* __restrict__ dsck, void* __restrict__ dv, void* __restrict__ dw,
+    float* __restrict__ gs, int H, int HK, int DV, long S, int NC) {
+  constexpr int XP = CT + 1;          // LDS pitch of the 16-column arrays
+  constexpr int KD = DK / 4;          // k steps per lane group over DK
+  constexpr int KL = L / 4;           // over the 64 rows
+  constexpr int NI = DK / 16;         // 16-channel tiles
   using R = Rec<DK>;
-  extern __shared__ __align__(16) float sm[];
-  // phase 1
-  float* sE = sm;                   // [L][P]
-  float* sKG = sE + L * P;          // [L][P]  (G first)
-  float* sAi = sKG + L * P;         // [L][L]
-  float* sAq = sAi + L * L;         // [L][L]
-  float* sS = sAq + L * L;          // [DK][CP]
-  float* sdS = sS + DK * CP;        // [DK][CP]
-  float* sdO = sdS + DK * CP;       // [L][CP]
-  float* sU = sdO + L * CP;         // [L][CP]
-  float* sY = sU + L * CP;          // [L][CP]  Z, Y, then dU
-  float* sdY = sY + L * CP;         // [L][CP]
-  float* sGL = sdY + L * CP;        // [DK]
-  // phase 2 (over phase 1)
-  float* pq = sm;                   // [L][DK]  q, then dG
-  float* pk = pq + L * DK;          // [L][DK]  k, then KG dKG
-  float* pbk = pk + L * DK;         // [L][DK]
-  float* pG = pbk + L * DK;         // [L][DK]
-  float* pAq = pG + L * DK;         // [L][L]   dAqk
-  float* pAk = pAq + L * L;         // [L][L]   dAkk
-
-  const int tid = threadIdx.x;
+  using G = GS<DK>;
+  constexpr int EP = 4 * (KD + 1);    // LDS row pitch of -E and KG (lane groups 33 floats apart)
+  __shared__ float sG[L * DK];        // G (log decay cumsum)
+  __shared__ float sEn[L * EP], sKG[L * EP];   // -E, KG: row t, lane group gq at gq (KD + 1)
+  __shared__ float sS[DK * XP], sdS[DK * XP];
+  __shared__ float sdO[L * XP], sY[L * XP], sU[L * XP], sdU[L * XP], sdY[L * XP];
+  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
+  const int gq = lane >> 4, m = lane & 15;
   const int c = blockIdx.x, bh = blockIdx.y;
   const int bi = bh / H, h = bh % H, hk = h / (H / HK);
   const long t0 = static_cast<long>(c) * L;
   const float* rc = rec + (static_cast<size_t>(bi * HK + hk) * NC + c) * R::STRIDE;
   const float* Sc = sck + (static_cast<size_t>(bh) * NC + c) * DK * DV;
   const float* dSc = dsck + (static_cast<size_t>(bh) * NC + c) * DK * DV;
+  const int row = 16 * wave + m;      // this lane's A-operand row
 
-  // E and KG from q, k, b, g; Ai and Aqk from the record
+  // G = within-chunk cumsum of g
   for (int e = tid; e < L * DK; e += kThreads) {
     const int t = e / DK, i = e % DK;
-    sKG[t * P + i] = t0 + t < S ? g[key_index(bi, S, t0 + t, HK, hk, DK, i)] : 0.f;
-  }
-  for (int e = tid; e < L * L; e += kThreads) {
-    sAi[e] = rc[R::AI + e];
-    sAq[e] = rc[R::AQ + e];
+    sG[e] = t0 + t < S ? g[key_index(bi, S, t0 + t, HK, hk, DK, i)] : 0.f;
   }
   __syncthreads();
   if (tid < DK) {
     float run = 0.f;
     for (int t = 0; t < L; ++t) {
-      run += sKG[t * P + tid];
-      sKG[t * P + tid] = run;
+      run += sG[t * DK + tid];
+      sG[t * DK + tid] = run;
     }
-    sGL[tid] = run;
   }
   __syncthreads();
+  // A operands: -E, KG (LDS); Ai, Ai^T, Aqk^T rows in registers
   for (int e = tid; e < L * DK; e += kThreads) {
     const int t = e / DK, i = e % DK;
     float kv = 0.f, bv = 0.f;
@@ -608,249 +601,282 @@ __global__ __launch_bounds__(kThreads) void bwd_grad_kernel(
       kv = load_elem(k, ix, dt);
       bv = load_elem(b, ix, dt);
     }
-    const float gt = sKG[t * P + i];
-    sE[t * P + i] = bv * kv * __expf(gt);
-    sKG[t * P + i] = kv * __expf(sGL[i] - gt);
+    const float gt = sG[t * DK + i];
+    const int o = t * EP + (i / KD) * (KD + 1) + i % KD;
+    sEn[o] = -bv * kv * __expf(gt);
+    sKG[o] = kv * __expf(sG[(L - 1) * DK + i] - gt);
   }
-
-  const int tb = tid >> 4, ib = tid & 15;      // accumulator tile
-  const int pt = tid >> 2, pc = (tid & 3) * 4; // column-block products: row pt, columns pc ..
-  float aQg[4][CPB], aE[4][CPB], aKG[4][CPB], aAq[4][4], aAk[4][4], agam = 0.f;
+  float rAi[KL], rAiT[KL], rAqT[KL];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-#pragma unroll
-    for (int u = 0; u < CPB; ++u) aQg[r][u] = aE[r][u] = aKG[r][u] = 0.f;
-#pragma unroll
-    for (int u = 0; u < 4; ++u) aAq[r][u] = aAk[r][u] = 0.f;
+  for (int s2 = 0; s2 < KL; ++s2) {
+    const int u = gq * KL + s2;
+    rAi[s2] = rc[R::AI + row * L + u];
+    rAiT[s2] = rc[R::AI + u * L + row];
+    rAqT[s2] = rc[R::AQ + u * L + row];
   }
+  const float* aEn = sEn + row * EP + gq * (KD + 1);
+  const float* aKGr = sKG + row * EP + gq * (KD + 1);
 
-  for (int cb = 0; cb < DV; cb += CT) {
-    __syncthreads();   // the previous block's arrays are free (and, first time, E / KG are complete)
-    for (int e = tid; e < DK * CT; e += kThreads) {
-      const int r = e / CT, cl = e % CT;
-      sS[r * CP + cl] = Sc[static_cast<size_t>(r) * DV + cb + cl];
-      sdS[r * CP + cl] = dSc[static_cast<size_t>(r) * DV + cb + cl];
+  f32x4 aQg[NI], aE[NI], aKG[NI], aAq[4], aAk[4];
+#pragma unroll
+  for (int n = 0; n < NI; ++n) aQg[n] = aE[n] = aKG[n] = zero4();
+#pragma unroll
+  for (int n = 0; n < 4; ++n) aAq[n] = aAk[n] = zero4();
+  float agam = 0.f;
+
+  // per column block: S, dS' (NSE per thread) and dO into LDS; Z, v, w in the
+  // output layout (rows 16 wave + 4 gq + e, column m) for Y's accumulator and
+  // dv, dw. The next block's are requested while the current one is worked on.
+  constexpr int NSE = DK * CT / kThreads, NTE = L * CT / kThreads;
+  float pS[NSE], pdS[NSE];
+  uint32_t pO[NTE], pV[4], pW[4];
+  auto fetch = [&](int cb) {
+#pragma unroll
+    for (int n = 0; n < NSE; ++n) {
+      const int e = tid + n * kThreads, r = e / CT, cl = e % CT;
+      pS[n] = Sc[static_cast<size_t>(r) * DV + cb + cl];
+      pdS[n] = dSc[static_cast<size_t>(r) * DV + cb + cl];
     }
-    for (int e = tid; e < L * CT; e += kThreads) {
-      const int t = e / CT, cl = e % CT;
-      float o = 0.f, z = 0.f;
+#pragma unroll
+    for (int n = 0; n < NTE; ++n) {
+      const int e = tid + n * kThreads, t = e / CT, cl = e % CT;
+      pO[n] = t0 + t < S ? load_raw(dout, ((static_cast<size_t>(bi) * S + t0 + t) * H + h) * DV + cb + cl, do_dt)
+                         : 0u;
+    }
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      const int t = 16 * wave + 4 * gq + e;
+      pV[e] = pW[e] = 0u;
       if (t0 + t < S) {
-        const size_t ix = ((static_cast<size_t>(bi) * S + t0 + t) * H + h) * DV + cb + cl;
-        o = load_elem(dout, ix, do_dt);
-        z = load_elem(w, ix, dt) * load_elem(v, ix, dt);
+        const size_t ix = ((static_cast<size_t>(bi) * S + t0 + t) * H + h) * DV + cb + m;
+        pV[e] = load_raw(v, ix, dt);
+        pW[e] = load_raw(w, ix, dt);
       }
-      sdO[t * CP + cl] = o;
-      sY[t * CP + cl] = z;
     }
-    __syncthreads();
-    // Y = Z - E S (in place: each thread rewrites only its own four entries)
-    {
-      float4 a = *reinterpret_cast<const float4*>(&sY[pt * CP + pc]);
-#pragma unroll 8
-      for (int i = 0; i < DK; ++i) {
-        const float e = sE[pt * P + i];
-        const float4 s4 = *reinterpret_cast<const float4*>(&sS[i * CP + pc]);
-        a.x -= e * s4.x; a.y -= e * s4.y; a.z -= e * s4.z; a.w -= e * s4.w;
-      }
-      *reinterpret_cast<float4*>(&sY[pt * CP + pc]) = a;
-    }
-    __syncthreads();
-    // U = Ai Y
-    {
-      float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 8
-      for (int u = 0; u <= pt; ++u) {
-        const float x = sAi[pt * L + u];
-        const float4 y4 = *reinterpret_cast<const float4*>(&sY[u * CP + pc]);
-        a.x += x * y4.x; a.y += x * y4.y; a.z += x * y4.z; a.w += x * y4.w;
-      }
-      *reinterpret_cast<float4*>(&sU[pt * CP + pc]) = a;
-    }
-    __syncthreads();
-    // dU = Aqk^T dO + KG dS' (over Y)
-    {
-      float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 8
-      for (int u = pt; u < L; ++u) {
-        const float x = sAq[u * L + pt];
-        const float4 o4 = *reinterpret_cast<const float4*>(&sdO[u * CP + pc]);
-        a.x += x * o4.x; a.y += x * o4.y; a.z += x * o4.z; a.w += x * o4.w;
-      }
-#pragma unroll 8
-      for (int i = 0; i < DK; ++i) {
-        const float x = sKG[pt * P + i];
-        const float4 d4 = *reinterpret_cast<const float4*>(&sdS[i * CP + pc]);
-        a.x += x * d4.x; a.y += x * d4.y; a.z += x * d4.z; a.w += x * d4.w;
-      }
-      *reinterpret_cast<float4*>(&sY[pt * CP + pc]) = a;
-    }
-    __syncthreads();
-    // dY = Ai^T dU; dv = w dY, dw = v dY
-    {
-      float4 a = make_float4(0.f, 0.f, 0.f, 0.f);
-#pragma unroll 8
-      for (int u = pt; u < L; ++u) {
-        const float x = sAi[u * L + pt];
-        const float4 y4 = *reinterpret_cast<const float4*>(&sY[u * CP + pc]);
-        a.x += x * y4.x; a.y += x * y4.y; a.z += x * y4.z; a.w += x * y4.w;
-      }
-      *reinterpret_cast<float4*>(&sdY[pt * CP + pc]) = a;
-      if (t0 + pt < S) {
-        const size_t ix = ((static_cast<size_t>(bi) * S + t0 + pt) * H + h) * DV + cb + pc;
-        const float av[4] = {a.x, a.y, a.z, a.w};
+  };
+  fetch(0);
+  for (int cb = 0; cb < DV; cb += CT) {
+    lds_barrier();                    // the previous block's readers are done
 #pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          const float vv = load_elem(v, ix + u, dt), ww = load_elem(w, ix + u, dt);
-          store_elem(dv, ix + u, dt, ww * av[u]);
-          store_elem(dw, ix + u, dt, vv * av[u]);
+    for (int n = 0; n < NSE; ++n) {
+      const int e = tid + n * kThreads, r = e / CT, cl = e % CT;
+      sS[r * XP + cl] = pS[n];
+      sdS[r * XP + cl] = pdS[n];
+    }
+#pragma unroll
+    for (int n = 0; n < NTE; ++n) {
+      const int e = tid + n * kThreads, t = e / CT, cl = e % CT;
+      sdO[t * XP + cl] = raw_f32(pO[n], do_dt);
+    }
+    f32x4 zc;
+    float vv[4], ww[4];
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      vv[e] = raw_f32(pV[e], dt);
+      ww[e] = raw_f32(pW[e], dt);
+      zc[e] = ww[e] * vv[e];
+    }
+    if (cb + CT < DV) fetch(cb + CT);
+    lds_barrier();
+    // Y = Z - E S (this wave's rows) -> LDS
+    {
+      f32x4 acc = zc;
+#pragma unroll
+      for (int s2 = 0; s2 < KD; ++s2) acc = mma(aEn[s2], sS[(gq * KD + s2) * XP + m], acc);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) sY[(16 * wave + 4 * gq + e) * XP + m] = acc[e];
+    }
+    lds_barrier();
+    // U = Ai Y, dU = Aqk^T dO + KG dS'
+    f32x4 uo = zero4(), du = zero4();
+#pragma unroll
+    for (int s2 = 0; s2 < KL; ++s2) {
+      uo = mma(rAi[s2], sY[(gq * KL + s2) * XP + m], uo);
+      du = mma(rAqT[s2], sdO[(gq * KL + s2) * XP + m], du);
+    }
+#pragma unroll
+    for (int s2 = 0; s2 < KD; ++s2) du = mma(aKGr[s2], sdS[(gq * KD + s2) * XP + m], du);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      sU[(16 * wave + 4 * gq + e) * XP + m] = uo[e];
+      sdU[(16 * wave + 4 * gq + e) * XP + m] = du[e];
+    }
+    lds_barrier();
+    // dY = Ai^T dU; dv = w dY, dw = v dY; -dY to LDS (this wave's rows)
+    {
+      f32x4 dy = zero4();
+#pragma unroll
+      for (int s2 = 0; s2 < KL; ++s2) dy = mma(rAiT[s2], sdU[(gq * KL + s2) * XP + m], dy);
+#pragma unroll
+      for (int e = 0; e < 4; ++e) {
+        const int t = 16 * wave + 4 * gq + e;
+        sdY[t * XP + m] = -dy[e];
+        if (t0 + t < S) {
+          const size_t ix = ((static_cast<size_t>(bi) * S + t0 + t) * H + h) * DV + cb + m;
+          store_elem(dv, ix, dt, ww[e] * dy[e]);
+          store_elem(dw, ix, dt, vv[e] * dy[e]);
         }
       }
     }
-    __syncthreads();
-    // accumulate dQg = dO S^T, dE = -dY S^T, dKG = U dS'^T, dAqk = dO U^T,
-    // dAkk = -dY U^T, dgamma = rowsum(dS' S)
-#pragma unroll 4
-    for (int cl = 0; cl < CT; ++cl) {
-      float o[4], y[4], uu[4], ut[4], sv[CPB], dsv[CPB];
+    // within the wave: its own -dY rows are read below (LDS is in order per wave)
+    // accumulate: A operands are this wave's rows of dO, -dY, U (k = column)
 #pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        o[r] = sdO[(4 * tb + r) * CP + cl];
-        y[r] = sdY[(4 * tb + r) * CP + cl];
-        uu[r] = sU[(4 * tb + r) * CP + cl];
-        ut[r] = sU[(4 * ib + r) * CP + cl];
+    for (int s2 = 0; s2 < 4; ++s2) {
+      const int cl = 4 * gq + s2;
+      const float ao = sdO[row * XP + cl], ay = sdY[row * XP + cl], au = sU[row * XP + cl];
+#pragma unroll
+      for (int n = 0; n < NI; ++n) {
+        const float bs = sS[(16 * n + m) * XP + cl], bd = sdS[(16 * n + m) * XP + cl];
+        aQg[n] = mma(ao, bs, aQg[n]);
+        aE[n] = mma(ay, bs, aE[n]);
+        aKG[n] = mma(au, bd, aKG[n]);
       }
 #pragma unroll
-      for (int u = 0; u < CPB; ++u) {
-        sv[u] = sS[(ib * CPB + u) * CP + cl];
-        dsv[u] = sdS[(ib * CPB + u) * CP + cl];
-      }
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-#pragma unroll
-        for (int u = 0; u < CPB; ++u) {
-          aQg[r][u] += o[r] * sv[u];
-          aE[r][u] -= y[r] * sv[u];
-          aKG[r][u] += uu[r] * dsv[u];
-        }
-#pragma unroll
-        for (int u = 0; u < 4; ++u) {
-          aAq[r][u] += o[r] * ut[u];
-          aAk[r][u] -= y[r] * ut[u];
-        }
+      for (int n = 0; n < 4; ++n) {
+        const float bu = sU[(16 * n + m) * XP + cl];
+        aAq[n] = mma(ao, bu, aAq[n]);
+        aAk[n] = mma(ay, bu, aAk[n]);
       }
     }
     if (tid < DK) {
-      for (int cl = 0; cl < CT; ++cl) agam += sdS[tid * CP + cl] * sS[tid * CP + cl];
+#pragma unroll
+      for (int cl = 0; cl < CT; ++cl) agam += sdS[tid * XP + cl] * sS[tid * XP + cl];
     }
   }
-  __syncthreads();   // phase 1 arrays are dead
+  // the sums (output layout: rows 16 wave + 4 gq + e, column 16 n + m)
+  float* out = gs + (static_cast<size_t>(bh) * NC + c) * G::STRIDE;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    const int t = 16 * wave + 4 * gq + e;
+#pragma unroll
+    for (int n = 0; n < NI; ++n) {
+      out[G::QG + t * DK + 16 * n + m] = aQg[n][e];
+      out[G::E + t * DK + 16 * n + m] = aE[n][e];
+      out[G::KG + t * DK + 16 * n + m] = aKG[n][e];
+    }
+#pragma unroll
+    for (int n = 0; n < 4; ++n) {
+      out[G::AQ + t * L + 16 * n + m] = aAq[n][e];
+      out[G::AK + t * L + 16 * n + m] = aAk[n][e];
+    }
+  }
+  if (tid < DK) out[G::GAM + tid] = agam;
+}
 
-  // phase 2: q, k, b k, G and the masked dAqk, dAkk
-  for (int e = tid; e < L * DK; e += kThreads) {
-    const int t = e / DK, i = e % DK;
+constexpr int PWC = 32;               // channels per pairwise workgroup
+constexpr int PWP = PWC + 1;          // LDS pitch
+
+template <int DK>
+__global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
+    const void* __restrict__ q, const void* __restrict__ k, const float* __restrict__ g, const void* __restrict__ b,
+    int dt, const float* __restrict__ gs, float* __restrict__ part, int H, int HK, long S, int NC, float scale) {
+  constexpr int NB = DK / PWC > 0 ? DK / PWC : 1;   // channel blocks
+  constexpr int CW = DK < PWC ? DK : PWC;            // channels in a block
+  constexpr int EPT = L * CW / kThreads;             // elements per thread
+  using G = GS<DK>;
+  __shared__ float pq[L * PWP], pk[L * PWP], pbk[L * PWP], pG[L * PWP];
+  __shared__ float pAq[L * (L + 1)], pAk[L * (L + 1)];
+  const int tid = threadIdx.x;
+  const int c = blockIdx.x / NB, cb = blockIdx.x % NB;
+  const int bh = blockIdx.y, bi = bh / H, h = bh % H, hk = h / (H / HK);
+  const long t0 = static_cast<long>(c) * L;
+  const float* src = gs + (static_cast<size_t>(bh) * NC + c) * G::STRIDE;
+  const int i0 = cb * CW;
+  for (int e = tid; e < L * CW; e += kThreads) {
+    const int t = e / CW, ii = e % CW;
     float qv = 0.f, kv = 0.f, bv = 0.f, gv = 0.f;
     if (t0 + t < S) {
-      const size_t ix = key_index(bi, S, t0 + t, HK, hk, DK, i);
+      const size_t ix = key_index(bi, S, t0 + t, HK, hk, DK, i0 + ii);
       qv = load_elem(q, ix, dt);
       kv = load_elem(k, ix, dt);
       bv = load_elem(b, ix, dt);
       gv = g[ix];
     }
-    pq[e] = qv;
-    pk[e] = kv;
-    pbk[e] = bv * kv;
-    pG[e] = gv;
+    pq[t * PWP + ii] = qv;
+    pk[t * PWP + ii] = kv;
+    pbk[t * PWP + ii] = bv * kv;
+    pG[t * PWP + ii] = gv;
   }
-#pragma unroll
-  for (int r = 0; r < 4; ++r)
-#pragma unroll
-    for (int u = 0; u < 4; ++u) {
-      const int t = 4 * tb + r, s = 4 * ib + u;
-      pAq[t * L + s] = s <= t ? aAq[r][u] : 0.f;
-      pAk[t * L + s] = s < t ? aAk[r][u] : 0.f;
-    }
+  for (int e = tid; e < L * L; e += kThreads) {   // masked: dAqk on s <= t, dAkk on s < t
+    const int t = e / L, s2 = e % L;
+    pAq[t * (L + 1) + s2] = s2 <= t ? src[G::AQ + e] : 0.f;
+    pAk[t * (L + 1) + s2] = s2 < t ? src[G::AK + e] : 0.f;
+  }
   __syncthreads();
-  if (tid < DK) {
+  if (tid < CW) {
     float run = 0.f;
     for (int t = 0; t < L; ++t) {
-      run += pG[t * DK + tid];
-      pG[t * DK + tid] = run;
+      run += pG[t * PWP + tid];
+      pG[t * PWP + tid] = run;
     }
   }
   __syncthreads();
-
-  float dG[4][CPB], kgd[4][CPB];
+  // thread: one channel, EPT rows t_r = tp + (kThreads / CW) r. One pass
+  // over the partners s serves every row: s <= t_r feeds the row sums, s >= t_r
+  // the column sums; an exponent outside its range is taken of -inf (0).
+  const int ii = tid % CW, tp = tid / CW;
+  const int i = i0 + ii;
+  constexpr int TS = kThreads / CW;
+  const float gl = pG[(L - 1) * PWP + ii];
+  float gt[EPT], rq[EPT], rk[EPT], cq[EPT], ck[EPT];
 #pragma unroll
-  for (int r = 0; r < 4; ++r) {
-    const int t = 4 * tb + r;
-    float rq[CPB], rk[CPB], cq[CPB], ck[CPB], gt[CPB];
+  for (int r = 0; r < EPT; ++r) {
+    gt[r] = pG[(tp + TS * r) * PWP + ii];
+    rq[r] = rk[r] = cq[r] = ck[r] = 0.f;
+  }
+  const float ninf = -__builtin_huge_valf();
+#pragma unroll 2
+  for (int s2 = 0; s2 < L; ++s2) {
+    const float gs2 = pG[s2 * PWP + ii], ks = pk[s2 * PWP + ii], qs = pq[s2 * PWP + ii], bks = pbk[s2 * PWP + ii];
 #pragma unroll
-    for (int u = 0; u < CPB; ++u) {
-      rq[u] = rk[u] = cq[u] = ck[u] = 0.f;
-      gt[u] = pG[t * DK + ib * CPB + u];
+    for (int r = 0; r < EPT; ++r) {
+      const int t = tp + TS * r;
+      const float er = __expf(s2 <= t ? gt[r] - gs2 : ninf) * ks;   // row: P[t][s] k_s
+      const float ec = __expf(s2 >= t ? gs2 - gt[r] : ninf);        // column: P[s][t]
+      rq[r] += pAq[t * (L + 1) + s2] * er;
+      rk[r] += pAk[t * (L + 1) + s2] * er;
+      cq[r] += pAq[s2 * (L + 1) + t] * qs * ec;
+      ck[r] += pAk[s2 * (L + 1) + t] * bks * ec;
     }
-#pragma unroll 4
-    for (int s = 0; s <= t; ++s) {            // row sums: partners s <= t
-      const float xq = pAq[t * L + s], xk = pAk[t * L + s];
+  }
+  float dG[EPT], kgd[EPT];
 #pragma unroll
-      for (int u = 0; u < CPB; ++u) {
-        const int i = ib * CPB + u;
-        const float e = __expf(gt[u] - pG[s * DK + i]) * pk[s * DK + i];
-        rq[u] += xq * e;
-        rk[u] += xk * e;
-      }
-    }
-#pragma unroll 4
-    for (int s = t; s < L; ++s) {             // column sums: partners s >= t
-      const float xq = pAq[s * L + t], xk = pAk[s * L + t];
-#pragma unroll
-      for (int u = 0; u < CPB; ++u) {
-        const int i = ib * CPB + u;
-        const float e = __expf(pG[s * DK + i] - gt[u]);
-        cq[u] += xq * pq[s * DK + i] * e;
-        ck[u] += xk * pbk[s * DK + i] * e;
-      }
-    }
+  for (int r = 0; r < EPT; ++r) {
+    const int t = tp + TS * r;
+    const float qv = pq[t * PWP + ii], kv = pk[t * PWP + ii], bkv = pbk[t * PWP + ii];
     const bool valid = t0 + t < S;
-#pragma unroll
-    for (int u = 0; u < CPB; ++u) {
-      const int i = ib * CPB + u;
-      const float qv = pq[t * DK + i], kv = pk[t * DK + i], bkv = pbk[t * DK + i];
-      const float bv = valid ? load_elem(b, key_index(bi, S, t0 + t, HK, hk, DK, i), dt) : 0.f;
-      const float ga = __expf(gt[u]), gl = __expf(pG[(L - 1) * DK + i] - gt[u]);
-      const float dq = scale * (ga * aQg[r][u] + rq[u]);
-      const float dk = bv * ga * aE[r][u] + scale * cq[u] + bv * rk[u] + ck[u] + gl * aKG[r][u];
-      const float db = kv * (ga * aE[r][u] + rk[u]);
-      kgd[r][u] = kv * gl * aKG[r][u];
-      dG[r][u] = scale * qv * (ga * aQg[r][u] + rq[u]) + bkv * (ga * aE[r][u] + rk[u]) - kgd[r][u] -
-                 kv * (scale * cq[u] + ck[u]);
-      if (valid) {
-        const size_t ix = ((static_cast<size_t>(bi) * S + t0 + t) * H + h) * DK + i;
-        const size_t plane = static_cast<size_t>(gridDim.y) / H * S * H * DK;   // B S H DK
-        part[ix] = dq;
-        part[plane + ix] = dk;
-        part[2 * plane + ix] = db;
-      }
+    const float bv = valid ? load_elem(b, key_index(bi, S, t0 + t, HK, hk, DK, i), dt) : 0.f;
+    const float ga = __expf(gt[r]), gd = __expf(gl - gt[r]);
+    const float fQg = src[G::QG + t * DK + i], fE = src[G::E + t * DK + i], fKG = src[G::KG + t * DK + i];
+    const float dq = scale * (ga * fQg + rq[r]);
+    const float dk = bv * ga * fE + scale * cq[r] + bv * rk[r] + ck[r] + gd * fKG;
+    const float db = kv * (ga * fE + rk[r]);
+    kgd[r] = kv * gd * fKG;
+    dG[r] = scale * qv * (ga * fQg + rq[r]) + bkv * (ga * fE + rk[r]) - kgd[r] - kv * (scale * cq[r] + ck[r]);
+    if (valid) {
+      const size_t ix = ((static_cast<size_t>(bi) * S + t0 + t) * H + h) * DK + i;
+      const size_t plane = static_cast<size_t>(gridDim.y) / H * S * H * DK;   // B S H DK
+      part[ix] = dq;
+      part[plane + ix] = dk;
+      part[2 * plane + ix] = db;
     }
   }
   __syncthreads();   // q, k are read no more
 #pragma unroll
-  for (int r = 0; r < 4; ++r)
-#pragma unroll
-    for (int u = 0; u < CPB; ++u) {
-      const int t = 4 * tb + r, i = ib * CPB + u;
-      pq[t * DK + i] = dG[r][u];
-      pk[t * DK + i] = kgd[r][u];
-    }
+  for (int r = 0; r < EPT; ++r) {
+    const int t = tp + TS * r;
+    pq[t * PWP + ii] = dG[r];
+    pk[t * PWP + ii] = kgd[r];
+  }
   __syncthreads();
-  if (tid < DK) {
+  if (tid < CW) {
     // d G_L: sum_t KG dKG + gamma dgamma; dg = reverse cumsum of dG
-    float run = __expf(pG[(L - 1) * DK + tid]) * agam;
-    for (int t = 0; t < L; ++t) run += pk[t * DK + tid];
+    float run = __expf(pG[(L - 1) * PWP + tid]) * src[G::GAM + i0 + tid];
+    for (int t = 0; t < L; ++t) run += pk[t * PWP + tid];
     const size_t plane = static_cast<size_t>(gridDim.y) / H * S * H * DK;
     for (int t = L - 1; t >= 0; --t) {
-      run += pq[t * DK + tid];
-      if (t0 + t < S) part[3 * plane + ((static_cast<size_t>(bi) * S + t0 + t) * H + h) * DK + tid] = run;
+      run += pq[t * PWP + tid];
+      if (t0 + t < S) part[3 * plane + ((static_cast<size_t>(bi) * S + t0 + t) * H + h) * DK + i0 + tid] = run;
     }
   }
 }
@@ -893,7 +919,9 @@ size_t backward_workspace_bytes(int B, int H, int HK, int DK, int DV, long S) {
   const size_t rec = up(static_cast<size_t>(B) * HK * NC * stride * 4);
   const size_t ck = up(static_cast<size_t>(B) * H * NC * DK * DV * 4);
   const size_t part = up(4 * static_cast<size_t>(B) * S * H * DK * 4);
-  return rec + 2 * ck + part;
+  long gstride = DK == 32 ? bw::GS<32>::STRIDE : DK == 64 ? bw::GS<64>::STRIDE : bw::GS<128>::STRIDE;
+  const size_t gsb = up(static_cast<size_t>(B) * H * NC * gstride * 4);
+  return rec + 2 * ck + part + gsb;
 }
 
 namespace {
@@ -904,28 +932,17 @@ hipError_t launch_backward_t(const void* q, const void* k, const void* v, const 
                              float* ds0, void* workspace, int B, int H, int HK, int DV, long S, hipStream_t stream) {
   const int NC = static_cast<int>((S + bw::L - 1) / bw::L);
   constexpr int lds1 = bw::local_lds_floats<DK>() * 4;
-  constexpr int lds4 = bw::grad_lds_floats<DK>() * 4;
-  constexpr int lds2 = bw::scan_lds_floats<DK>() * 4;
   static bool configured = false;   // attributes set once per process (same values always)
   if (!configured) {
     hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&bw::bwd_local_kernel<DK>),
                                        hipFuncAttributeMaxDynamicSharedMemorySize, lds1);
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&bw::bwd_grad_kernel<DK>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, lds4);
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&bw::bwd_fscan_kernel<DK>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, lds2);
-    if (e == hipSuccess)
-      e = hipFuncSetAttribute(reinterpret_cast<const void*>(&bw::bwd_bscan_kernel<DK>),
-                              hipFuncAttributeMaxDynamicSharedMemorySize, lds2);
     if (e != hipSuccess) return e;
     configured = true;
   }
   if (NC == 0) {   // no tokens: the initial-state gradient is the final-state one (or zero)
     if (ds0)
-      hipLaunchKernelGGL(bw::bwd_bscan_kernel<DK>, dim3(DV / bw::CT, B * H), dim3(bw::kThreads),
-                         lds2, stream, dout, do_dt, nullptr, dht, nullptr, ds0, H, HK, DV, S, 0);
+      hipLaunchKernelGGL((bw::bwd_scan_kernel<DK, true>), dim3(DV / bw::CT, B * H), dim3(bw::kThreads), 0, stream,
+                         dout, nullptr, do_dt, nullptr, dht, nullptr, ds0, H, HK, DV, S, 0);
     return hipGetLastError();
   }
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
@@ -937,15 +954,20 @@ hipError_t launch_backward_t(const void* q, const void* k, const void* v, const 
   float* dsck = reinterpret_cast<float*>(ws);
   ws += up(static_cast<size_t>(B) * H * NC * DK * DV * 4);
   float* part = reinterpret_cast<float*>(ws);
+  ws += up(4 * static_cast<size_t>(B) * S * H * DK * 4);
+  float* gsc = reinterpret_cast<float*>(ws);
 
   hipLaunchKernelGGL(bw::bwd_local_kernel<DK>, dim3(NC, B * HK), dim3(bw::kThreads), lds1, stream, q, k, b, g, dt,
                      HK, S, NC, scale, rec);
-  hipLaunchKernelGGL(bw::bwd_fscan_kernel<DK>, dim3(DV / bw::CT, B * H), dim3(bw::kThreads), lds2, stream, v, w,
-                     dt, rec, s0, sck, H, HK, DV, S, NC);
-  hipLaunchKernelGGL(bw::bwd_bscan_kernel<DK>, dim3(DV / bw::CT, B * H), dim3(bw::kThreads), lds2, stream, dout,
-                     do_dt, rec, dht, dsck, ds0, H, HK, DV, S, NC);
-  hipLaunchKernelGGL(bw::bwd_grad_kernel<DK>, dim3(NC, B * H), dim3(bw::kThreads), lds4, stream, q, k, v, g, b, w,
-                     dt, dout, do_dt, rec, sck, dsck, dv, dw, part, H, HK, DV, S, NC, scale);
+  hipLaunchKernelGGL((bw::bwd_scan_kernel<DK, false>), dim3(DV / bw::CT, B * H), dim3(bw::kThreads), 0, stream, v, w,
+                     dt, rec, s0, sck, nullptr, H, HK, DV, S, NC);
+  hipLaunchKernelGGL((bw::bwd_scan_kernel<DK, true>), dim3(DV / bw::CT, B * H), dim3(bw::kThreads), 0, stream, dout,
+                     nullptr, do_dt, rec, dht, dsck, ds0, H, HK, DV, S, NC);
+  hipLaunchKernelGGL(bw::bwd_gradmm_kernel<DK>, dim3(NC, B * H), dim3(bw::kThreads), 0, stream, k, v, g, b, w, dt,
+                     dout, do_dt, rec, sck, dsck, dv, dw, gsc, H, HK, DV, S, NC);
+  constexpr int NB = DK / bw::PWC > 0 ? DK / bw::PWC : 1;
+  hipLaunchKernelGGL(bw::bwd_gradpw_kernel<DK>, dim3(NC * NB, B * H), dim3(bw::kThreads), 0, stream, q, k, g, b, dt,
+                     gsc, part, H, HK, S, NC, scale);
   const long n_key = static_cast<long>(B) * S * HK * DK;
   hipLaunchKernelGGL(bw::bwd_sum_kernel, dim3(static_cast<unsigned>((n_key + bw::kThreads - 1) / bw::kThreads)),
                      dim3(bw::kThreads), 0, stream, part, dq, dk, db, dg, dt, n_key, H, HK, DK);

@@ -226,13 +226,15 @@ def test_backward_host_validation():
     assert wsb(1, 2, 2, 48, 64, 128) == 0          # DK not in (32, 64, 128)
     assert wsb(1, 2, 2, 64, 24, 128) == 0          # DV % 16
     assert wsb(1, 3, 2, 64, 64, 128) == 0          # HK must divide H
-    # B=2 H=4 HK=2 DK=64 DV=32 S=100 (2 chunks): records 2*2*2 of 18496 floats,
-    # two state checkpoints 2*4*2*64*32 floats each, four gradient shares B*S*H*DK
-    rec = 2 * 2 * 2 * (64 * 64 + 64 * 64 + 64 * 64 + 4096 + 4096 + 64) * 4
+    # B=2 H=4 HK=2 DK=64 DV=32 S=100 (2 chunks): records of B*HK*NC chunks (A,
+    # KA, QP, Ai, Aqk, gamma padded to 64, A^T, QP^T), two state checkpoints
+    # B*H*NC*DK*DV floats each, four gradient shares B*S*H*DK
+    rec = 2 * 2 * 2 * (64 * 64 + 64 * 64 + 64 * 64 + 4096 + 4096 + 64 + 64 * 64 + 64 * 64) * 4
+    gs = 2 * 4 * 2 * (3 * 64 * 64 + 2 * 4096 + 64) * 4   # per (b, value head, chunk) sums of the gradient kernel
     ck = 2 * 4 * 2 * 64 * 32 * 4
     part = 4 * 2 * 100 * 4 * 64 * 4
     up = lambda x: (x + 255) // 256 * 256
-    assert wsb(2, 4, 2, 64, 32, 100) == up(rec) + 2 * up(ck) + up(part)
+    assert wsb(2, 4, 2, 64, 32, 100) == up(rec) + 2 * up(ck) + up(part) + up(gs)
     fake = ctypes.c_void_p(256)   # never dereferenced: validation fails first
     args = [fake] * 6
     tail = [fake] * 8
