@@ -188,6 +188,30 @@ def bench_varlen(reps=20, nseq=16):
             "separate_calls_us": round(res["separate_calls"], 1)}
 
 
+def bench_backward(reps=5):
+    """Training backward at config 1's shape (bf16 inputs, fp32 arithmetic):
+    chunk_gdn2_bwd with no initial state and no final-state gradient, the
+    common training case; timed with HIP events on the current stream."""
+    from gdt2_tilelang_amd import chunk_gdn2_bwd
+
+    q, k, v, g, b, w = cfg_inputs(B1, S1, H1, D1, D1, seed=17)
+    do = torch.randn(B1, S1, H1, D1, device="cuda", generator=torch.Generator("cuda").manual_seed(18)).bfloat16()
+    for _ in range(2):
+        chunk_gdn2_bwd(q, k, v, g, b, w, None, None, do, None)
+    torch.cuda.synchronize()
+    stream = torch.cuda.current_stream()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(stream)
+    for _ in range(reps):
+        chunk_gdn2_bwd(q, k, v, g, b, w, None, None, do, None)
+    e1.record(stream)
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    return {"workload": "chunk_gdn2_bwd, BASELINE config 1 shape (B=2 S=4096 H=16 DK=DV=128, bf16 in, fp32 "
+                        "arithmetic, dq dk dv dg db dw)", "ms": round(ms, 3),
+            "tokens_per_s": round(B1 * S1 / (ms * 1e-3), 1), "reps": reps}
+
+
 def bench_decode(B, n, calls, steps_per_buf_min, H=16, D=128):
     """Average µs per decode call with rotating states (> MALL) for config 2/3.
 
@@ -439,6 +463,8 @@ def main():
     ap.add_argument("--no-varlen", action="store_true", help="skip the packed-sequence prefill run")
     ap.add_argument("--varlen-only", action="store_true", help="packed-sequence prefill run only (for profilers)")
     ap.add_argument("--layer-only", action="store_true", help="config-4 layer run only (for profilers)")
+    ap.add_argument("--no-backward", action="store_true", help="skip the training-backward run")
+    ap.add_argument("--backward-only", action="store_true", help="training backward only (for profilers)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="three plain 1 GiB device copies (scales rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -468,6 +494,9 @@ def main():
         return
     if args.varlen_only:
         log(json.dumps(bench_varlen()))
+        return
+    if args.backward_only:
+        log(json.dumps(bench_backward()))
         return
     ms_step, cl_ms, sc_ms = bench_prefill(args.steps, args.warmup)
     if args.prefill_only:
@@ -520,6 +549,8 @@ def main():
         out["varlen"] = bench_varlen()
     if not args.no_layer:
         out["layer"] = bench_layer()
+    if not args.no_backward:
+        out["backward"] = bench_backward()
     if not args.no_cpu:
         out["cpu_baseline"] = cpu_baseline()
     print(json.dumps(out), flush=True)
