@@ -39,7 +39,7 @@ from torch import nn
 
 from . import _hip
 from .config import DEFAULT_KERNEL_CONFIG, GDN2Config, GatedDeltaNet2Config
-from .forward import check_cu_seqlens, chunk_gdn2_bwd, chunk_gdn2_fwd, chunk_gdn2_varlen_fwd
+from .forward import check_cu_seqlens, chunk_gdn2_bwd, chunk_gdn2_fwd, chunk_gdn2_varlen_bwd, chunk_gdn2_varlen_fwd
 from .inference import gdn2_decode, gdn2_prefill
 
 __all__ = ["gdn2_attention", "GatedDeltaNet2", "GDN2Cache", "resolve_backend"]
@@ -82,6 +82,26 @@ class _GDN2Function(torch.autograd.Function):
         return dq, dk, dv, dg, db, dw, None, ds0, None, None
 
 
+class _GDN2VarlenFunction(torch.autograd.Function):
+    """Packed sequences: hip forward in one pass, hip backward per sequence."""
+
+    @staticmethod
+    def forward(ctx, q, k, v, g, b, w, scale, cu_seqlens, initial_state, output_final_state, config):
+        ctx.save_for_backward(q, k, v, g, b, w, initial_state)
+        ctx.scale, ctx.config, ctx.cu = scale, config, cu_seqlens
+        return chunk_gdn2_varlen_fwd(q, k, v, g, b, w, scale, cu_seqlens, initial_state, output_final_state, config)
+
+    @staticmethod
+    @torch.autograd.function.once_differentiable
+    def backward(ctx, do, dfinal_state):
+        q, k, v, g, b, w, initial_state = ctx.saved_tensors
+        if do is None:
+            do = torch.zeros(*v.shape, dtype=q.dtype, device=q.device)
+        dq, dk, dv, dg, db, dw, ds0 = chunk_gdn2_varlen_bwd(q, k, v, g, b, w, ctx.scale, ctx.cu, initial_state, do,
+                                                            dfinal_state, ctx.config)
+        return dq, dk, dv, dg, db, dw, None, None, ds0, None, None
+
+
 def gdn2_attention(q, k, v, g, b, w, scale=None, initial_state=None, output_final_state=False,
                    config: GDN2Config = DEFAULT_KERNEL_CONFIG, cu_seqlens=None):
     """Gated DeltaNet-2 attention over a full sequence.
@@ -98,7 +118,7 @@ def gdn2_attention(q, k, v, g, b, w, scale=None, initial_state=None, output_fina
             row (B = 1); each runs its own recurrence, ``initial_state`` and
             the final state are then ``[N, H, DK, DV]``. The reference rejects
             packed batches (``gdn2/attention.py:142-145``); this backend runs
-            them in one pass (forward only).
+            them in one pass (the backward runs per sequence).
 
     Returns:
         ``(o [B, S, H, DV], final_state or None)``.
@@ -113,7 +133,8 @@ def gdn2_attention(q, k, v, g, b, w, scale=None, initial_state=None, output_fina
             "this package provides the 'hip' backend only")
     if cu_seqlens is not None:
         if needs_grad:
-            raise NotImplementedError("packed sequences (cu_seqlens) are forward-only on the hip backend")
+            return _GDN2VarlenFunction.apply(q, k, v, g, b, w, scale, cu_seqlens, initial_state,
+                                             output_final_state, config)
         return chunk_gdn2_varlen_fwd(q, k, v, g, b, w, scale, cu_seqlens, initial_state, output_final_state,
                                      config)
     if needs_grad:
@@ -499,6 +520,10 @@ class GatedDeltaNet2(nn.Module):
         """Full-sequence mixer (training form). Returns ``(output, cache or None)``."""
         B, S, _ = hidden_states.shape
         if cu_seqlens is not None and hidden_states.is_cuda:
+            if torch.is_grad_enabled() and (hidden_states.requires_grad or
+                                            any(p.requires_grad for p in self.parameters())):
+                raise NotImplementedError("training GatedDeltaNet2 on packed sequences (cu_seqlens) is not "
+                                          "provided; gdn2_attention(cu_seqlens=...) itself is differentiable")
             # packed sequences: per-sequence conv windows in the prologue and the
             # packed op; as for a dense batch, the conv starts fresh (the
             # cache's conv tails are not read) and the recurrent state carries on

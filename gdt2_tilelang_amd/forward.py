@@ -19,7 +19,7 @@ from . import _hip
 from .config import DEFAULT_KERNEL_CONFIG, GDN2Config
 from .inference import _check_shapes, _prefill_chunks, _require_device, _token_layout, check_prefill_config
 
-__all__ = ["chunk_gdn2_fwd", "chunk_gdn2_varlen_fwd", "chunk_gdn2_bwd"]
+__all__ = ["chunk_gdn2_fwd", "chunk_gdn2_varlen_fwd", "chunk_gdn2_bwd", "chunk_gdn2_varlen_bwd"]
 
 
 @torch.no_grad()
@@ -31,7 +31,7 @@ def chunk_gdn2_fwd(q, k, v, g, b, w, scale, initial_state=None, output_final_sta
     ``initial_state`` is read, never modified.
     """
     if return_intermediates:
-        raise NotImplementedError("the hip backend is forward-only; it keeps no backward intermediates")
+        raise NotImplementedError("return_intermediates is not provided: chunk_gdn2_bwd recomputes what it needs")
     dev = _require_device(q, k, v, g, b, w)
     _check_shapes(q, k, v, g, b, w)
     check_prefill_config(config)
@@ -170,3 +170,34 @@ def chunk_gdn2_bwd(q, k, v, g, b, w, scale, initial_state, do, dht, config: GDN2
         _hip.ptr(ws), B, S, H, HK, DK, DV, _hip.stream_of(dev)), "gdn2_hip_backward")
     return (dq, dk, dv, dg.to(g.dtype), db, dw,
             None if ds0 is None else ds0.to(initial_state.dtype))
+
+
+def chunk_gdn2_varlen_bwd(q, k, v, g, b, w, scale, cu_seqlens, initial_state, do, dht,
+                          config: GDN2Config = DEFAULT_KERNEL_CONFIG):
+    """Backward of ``chunk_gdn2_varlen_fwd``: each packed sequence is an
+    independent recurrence, so its gradients are ``chunk_gdn2_bwd`` of its own
+    tokens (one gdn2_hip_backward call per sequence; an empty sequence passes
+    its final-state gradient through to its initial state).
+
+    Returns ``(dq, dk, dv, dg, db, dw, dinitial_state [N, H, DK, DV] or None)``.
+    """
+    dev = _require_device(q, k, v, g, b, w, do)
+    _check_shapes(q, k, v, g, b, w)
+    T = q.shape[1]
+    cu = check_cu_seqlens(cu_seqlens, T).tolist()
+    N = len(cu) - 1
+    grads = [torch.zeros_like(t) for t in (q, k, v)] + [torch.zeros_like(g)] + [torch.zeros_like(t) for t in (b, w)]
+    ds0 = None if initial_state is None else torch.empty_like(initial_state)
+    for i in range(N):
+        a, e = cu[i], cu[i + 1]
+        piece = lambda t: t[:, a:e]
+        s0 = None if initial_state is None else initial_state[i:i + 1]
+        dh = None if dht is None else dht[i:i + 1]
+        if e == a and s0 is None:
+            continue
+        res = chunk_gdn2_bwd(*(piece(t) for t in (q, k, v, g, b, w)), scale, s0, piece(do), dh, config)
+        for full, part in zip(grads, res[:6]):
+            full[:, a:e] = part
+        if ds0 is not None:
+            ds0[i:i + 1] = res[6]
+    return (*grads, ds0)
