@@ -813,7 +813,7 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
   __syncthreads();
   // thread: one channel, EPT rows t_r = tp + (kThreads / CW) r. One pass
   // over the partners s serves every row: s <= t_r feeds the row sums, s >= t_r
-  // the column sums; an exponent outside its range is taken of -inf (0).
+  // the column sums, each pair's exponent taken in the direction that is <= 0.
   const int ii = tid % CW, tp = tid / CW;
   const int i = i0 + ii;
   constexpr int TS = kThreads / CW;
@@ -824,15 +824,16 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
     gt[r] = pG[(tp + TS * r) * PWP + ii];
     rq[r] = rk[r] = cq[r] = ck[r] = 0.f;
   }
-  const float ninf = -__builtin_huge_valf();
 #pragma unroll 2
   for (int s2 = 0; s2 < L; ++s2) {
     const float gs2 = pG[s2 * PWP + ii], ks = pk[s2 * PWP + ii], qs = pq[s2 * PWP + ii], bks = pbk[s2 * PWP + ii];
 #pragma unroll
     for (int r = 0; r < EPT; ++r) {
       const int t = tp + TS * r;
-      const float er = __expf(s2 <= t ? gt[r] - gs2 : ninf) * ks;   // row: P[t][s] k_s
-      const float ec = __expf(s2 >= t ? gs2 - gt[r] : ninf);        // column: P[s][t]
+      // one exponential per pair: P[t][s] (s <= t, row sums) or P[s][t] (s >= t, column sums)
+      const float e = __expf(s2 <= t ? gt[r] - gs2 : gs2 - gt[r]);
+      const float er = s2 <= t ? e * ks : 0.f;
+      const float ec = s2 >= t ? e : 0.f;
       rq[r] += pAq[t * (L + 1) + s2] * er;
       rk[r] += pAk[t * (L + 1) + s2] * er;
       cq[r] += pAq[s2 * (L + 1) + t] * qs * ec;

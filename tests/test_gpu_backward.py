@@ -165,3 +165,22 @@ def test_packed_sequences_backward():
             if n:
                 assert rel_err(sl(leaf.grad), r) < 1e-4, (i, name)
         assert rel_err(leaves[6].grad[i:i + 1], ref[6]) < 1e-4, (i, "dS0")
+
+
+def test_backward_sixteen_chunks_full_head_dims():
+    """DK = DV = 128 over 16 chunks (1000 tokens, a ragged last chunk) with an
+    initial state and a final-state gradient: the scans' chains across many
+    chunk steps, against float64 autograd."""
+    print("backward S=1000 DK=DV=128", flush=True)
+    B, S, H, HK, DK, DV = 1, 1000, 2, 2, 128, 128
+    q, k, v, g, b, w = _inputs(B, S, H, HK, DK, DV, 1.0, 9)
+    s0 = torch.randn(B, H, DK, DV) * 0.3
+    do = torch.randn(B, S, H, DV)
+    dh = torch.randn(B, H, DK, DV) * 0.5
+    ref = _autograd(q, k, v, g, b, w, s0, do, dh, DK ** -0.5, 1)
+    got = chunk_gdn2_bwd(*(t.cuda() for t in (q, k, v, g, b, w)), None, s0.cuda(), do.cuda(), dh.cuda())
+    torch.cuda.synchronize()
+    for name, a, r in zip(NAMES, got, ref):
+        e = rel_err(a, r)
+        print(f"  {name} rel err {e:.2e}", flush=True)
+        assert e < 1e-4, name
