@@ -66,45 +66,38 @@ struct Rec {                     // fp32 per-(b, key head, chunk) record of kern
 // the workgroup wrote.
 __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(0)\n\ts_barrier" ::: "memory"); }
 
-// Raw element (16-bit types zero-extended by the load itself) and its value:
-// the conversion is left to the consumer, so a prefetch does not wait here.
-__device__ __forceinline__ uint32_t load_raw(const void* p, size_t i, int dt) {
-  if (dt == DT_F32) return __float_as_uint(static_cast<const float*>(p)[i]);
-  return static_cast<const unsigned short*>(p)[i];
-}
-__device__ __forceinline__ float raw_f32(uint32_t u, int dt) {
-  if (dt == DT_BF16) return __uint_as_float(u << 16);
-  if (dt == DT_F16) return f16_bits_to_f32(static_cast<unsigned short>(u));
-  return __uint_as_float(u);
-}
+// Loads of a chunk's rows run unconditionally on a row clamped into the
+// sequence (a load under a per-lane branch makes the compiler wait for it
+// inside the branch); rows past the end are then zeroed by the caller.
+__device__ __forceinline__ long clamp_row(long t, long S) { return t < S ? t : S - 1; }
 
 __device__ __forceinline__ size_t key_index(int bi, long S, long t, int HK, int hk, int DK, int i) {
   return ((static_cast<size_t>(bi) * S + t) * HK + hk) * DK + i;
 }
 
 // ---------------------------------------------------------------- kernel 1
-// N consecutive floats (N a multiple of 4, or 2 or 1) to 16-byte (or 8-byte)
-// aligned global memory
-template <int N>
-__device__ __forceinline__ void store_run(float* dst, const float* x) {
-  if constexpr (N % 4 == 0) {
-#pragma unroll
-    for (int q = 0; q < N / 4; ++q) reinterpret_cast<f32x4*>(dst)[q] = f32x4{x[4 * q], x[4 * q + 1], x[4 * q + 2], x[4 * q + 3]};
-  } else if constexpr (N == 2) {
-    *reinterpret_cast<f32x2*>(dst) = f32x2{x[0], x[1]};
-  } else {
-#pragma unroll
-    for (int q = 0; q < N; ++q) dst[q] = x[q];
+// One 16 x 16 tile of C = A B on v_mfma_f32_16x16x4_f32 with both operands in
+// LDS: A[r][k] at a[r as + k ak], B[k][c] at b[k bk + c bc], K a multiple of
+// 4. Lane (gq, m) supplies A[m][4 s + gq] and B[4 s + gq][m] at step s and
+// holds C[4 gq + e][m].
+__device__ __forceinline__ f32x4 mm_tile(const float* a, int as, int ak, const float* b, int bk, int bc, int K, int gq,
+                                         int m) {
+  f32x4 acc = zero4();
+#pragma unroll 4
+  for (int s = 0; s < K / 4; ++s) {
+    const int kk = 4 * s + gq;
+    acc = __builtin_amdgcn_mfma_f32_16x16x4f32(a[m * as + kk * ak], b[kk * bk + m * bc], acc, 0, 0, 0);
   }
+  return acc;
 }
 
 template <int DK>
 constexpr int local_lds_floats() { return 3 * L * (DK + 4) + L * (DK + 4 > L ? DK + 4 : L) + L * L + DK + 9 * 256; }
 
 template <int DK>
-__global__ __launch_bounds__(kThreads) void bwd_local_kernel(const void* __restrict__ q, const void* __restrict__ k,
-                                                             const void* __restrict__ b, const float* __restrict__ g,
-                                                             int dt, int HK, long S, int NC, float scale,
+__global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __restrict__ q, const float* __restrict__ k,
+                                                             const float* __restrict__ b, const float* __restrict__ g,
+                                                             int HK, long S, int NC, float scale,
                                                              float* __restrict__ rec) {
   constexpr int P = DK + 4;
   using R = Rec<DK>;
@@ -123,16 +116,13 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const void* __restr
   const long t0 = static_cast<long>(c) * L;
   float* rc = rec + (static_cast<size_t>(bhk) * NC + c) * R::STRIDE;
 
-  for (int e = tid; e < L * DK; e += kThreads) {       // rows past the sequence are zeros (inert)
+#pragma unroll
+  for (int e0 = 0; e0 < L * DK; e0 += kThreads) {
+    const int e = e0 + tid;       // rows past the sequence are zeros (inert)
     const int t = e / DK, i = e % DK;
-    float qv = 0.f, kv = 0.f, bv = 0.f, gv = 0.f;
-    if (t0 + t < S) {
-      const size_t ix = key_index(bi, S, t0 + t, HK, hk, DK, i);
-      qv = load_elem(q, ix, dt);
-      kv = load_elem(k, ix, dt);
-      bv = load_elem(b, ix, dt);
-      gv = g[ix];
-    }
+    const size_t ix = key_index(bi, S, clamp_row(t0 + t, S), HK, hk, DK, i);
+    const float keep = t0 + t < S ? 1.f : 0.f;
+    const float qv = keep * q[ix], kv = keep * k[ix], bv = keep * b[ix], gv = keep * g[ix];
     sq[t * P + i] = qv;
     sk[t * P + i] = kv;
     sbk[t * P + i] = bv * kv;
@@ -239,17 +229,22 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const void* __restr
       }
       __syncthreads();
     }
-    for (int e = tid; e < 6 * 256; e += kThreads) {
+    #pragma unroll
+    for (int e0 = 0; e0 < 6 * 256; e0 += kThreads) {
+      const int e = e0 + tid;
       const int blk = e >> 8, r = (e >> 4) & 15, c = e & 15;
       const int ib = blk < 1 ? 1 : (blk < 3 ? 2 : 3), jb = blk - ib * (ib - 1) / 2;
       sA[(16 * ib + r) * L + 16 * jb + c] = sXo[e];
     }
   }
   __syncthreads();
-  for (int e = tid; e < L * L; e += kThreads) rc[R::AI + e] = sA[e];
+#pragma unroll
+  for (int e0 = 0; e0 < L * L; e0 += kThreads) rc[R::AI + e0 + tid] = sA[e0 + tid];
   if (tid < DK) rc[R::GM + tid] = sgam[tid];
   // q -> Qg, b k -> E, k -> KG (G_L: row L-1 of G)
-  for (int e = tid; e < L * DK; e += kThreads) {
+#pragma unroll
+  for (int e0 = 0; e0 < L * DK; e0 += kThreads) {
+    const int e = e0 + tid;
     const int t = e / DK, i = e % DK;
     const float gt = sG[t * P + i], gl = sG[(L - 1) * P + i];
     const float ga = __expf(gt);
@@ -258,132 +253,55 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const void* __restr
     sk[t * P + i] *= __expf(gl - gt);
   }
   __syncthreads();
-  // Register tiles: an L x DK product gives thread (rg, cg) rows 4 rg .. and
-  // columns CW cg ..; a DK x DK product rows and columns CW rg .., CW cg ..
-  constexpr int CW = DK / 16;
-  const int rg = tid >> 4, cg = tid & 15;
-  {
-    // W = Ai E over G (dead)
-    float acc[4][CW];
+  // The products on fp32 matrix cores: 16 x 16 output tiles dealt round the
+  // four waves, operands read from LDS (mm_tile).
+  const int lane = tid & 63, wave = tid >> 6, gq = lane >> 4, m = lane & 15;
+  constexpr int NT = DK / 16;
+  // W = Ai E over G (dead)
+  for (int tile = wave; tile < 4 * NT; tile += 4) {
+    const int tt = tile / NT, it = tile % NT;
+    const f32x4 acc = mm_tile(sA + 16 * tt * L, L, 1, sbk + 16 * it, P, 1, L, gq, m);
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int u = 0; u < CW; ++u) acc[r][u] = 0.f;
-#pragma unroll 4
-    for (int s2 = 0; s2 < L; ++s2) {
-      float ev[CW];
-#pragma unroll
-      for (int u = 0; u < CW; ++u) ev[u] = sbk[s2 * P + CW * cg + u];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float x = sA[(4 * rg + r) * L + s2];
-#pragma unroll
-        for (int u = 0; u < CW; ++u) acc[r][u] += x * ev[u];
-      }
-    }
-    __syncthreads();
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int u = 0; u < CW; ++u) sG[(4 * rg + r) * P + CW * cg + u] = acc[r][u];
+    for (int e = 0; e < 4; ++e) sG[(16 * tt + 4 * gq + e) * P + 16 * it + m] = acc[e];
   }
   __syncthreads();
   // Aqk back from the record into the E slot (E is dead once W is formed)
   float* sAq = sbk;
-  for (int e = tid; e < L * L; e += kThreads) sAq[e] = rc[R::AQ + e];
-  {
-    // A = diag(gamma) - KG^T W
-    float acc[CW][CW];
 #pragma unroll
-    for (int r = 0; r < CW; ++r)
+  for (int e0 = 0; e0 < L * L; e0 += kThreads) sAq[e0 + tid] = rc[R::AQ + e0 + tid];
+  // A = diag(gamma) - KG^T W, also stored transposed; KG^T[i][t] is sk[t P + i]
+  for (int tile = wave; tile < NT * NT; tile += 4) {
+    const int ia = tile / NT, ja = tile % NT;
+    f32x4 acc = mm_tile(sk + 16 * ia, 1, P, sG + 16 * ja, P, 1, L, gq, m);
+    const int j = 16 * ja + m;
 #pragma unroll
-      for (int u = 0; u < CW; ++u) acc[r][u] = 0.f;
-#pragma unroll 4
-    for (int t = 0; t < L; ++t) {
-      float kv[CW], wv[CW];
-#pragma unroll
-      for (int u = 0; u < CW; ++u) {
-        kv[u] = sk[t * P + CW * rg + u];
-        wv[u] = sG[t * P + CW * cg + u];
-      }
-#pragma unroll
-      for (int r = 0; r < CW; ++r)
-#pragma unroll
-        for (int u = 0; u < CW; ++u) acc[r][u] += kv[r] * wv[u];
+    for (int e = 0; e < 4; ++e) {
+      const int i = 16 * ia + 4 * gq + e;
+      acc[e] = (i == j ? sgam[i] : 0.f) - acc[e];
+      rc[R::A + static_cast<long>(i) * DK + j] = acc[e];
     }
-#pragma unroll
-    for (int r = 0; r < CW; ++r)
-#pragma unroll
-      for (int u = 0; u < CW; ++u) {
-        const int i = CW * rg + r, j = CW * cg + u;
-        acc[r][u] = (i == j ? sgam[i] : 0.f) - acc[r][u];
-      }
-#pragma unroll
-    for (int r = 0; r < CW; ++r) store_run<CW>(rc + R::A + static_cast<long>(CW * rg + r) * DK + CW * cg, acc[r]);
-#pragma unroll
-    for (int u = 0; u < CW; ++u) {
-      float col[CW];
-#pragma unroll
-      for (int r = 0; r < CW; ++r) col[r] = acc[r][u];
-      store_run<CW>(rc + R::AT + static_cast<long>(CW * cg + u) * DK + CW * rg, col);
-    }
+    *reinterpret_cast<f32x4*>(rc + R::AT + static_cast<long>(j) * DK + 16 * ia + 4 * gq) = acc;
   }
-  {
-    // KA = KG^T Ai: rows CW rg .., columns 4 cg ..
-    float acc[CW][4];
+  // KA = KG^T Ai
+  for (int tile = wave; tile < NT * 4; tile += 4) {
+    const int ia = tile / 4, ua = tile % 4;
+    const f32x4 acc = mm_tile(sk + 16 * ia, 1, P, sA + 16 * ua, L, 1, L, gq, m);
 #pragma unroll
-    for (int r = 0; r < CW; ++r)
-#pragma unroll
-      for (int u = 0; u < 4; ++u) acc[r][u] = 0.f;
-#pragma unroll 4
-    for (int t = 0; t < L; ++t) {
-      float kv[CW], av[4];
-#pragma unroll
-      for (int r = 0; r < CW; ++r) kv[r] = sk[t * P + CW * rg + r];
-#pragma unroll
-      for (int u = 0; u < 4; ++u) av[u] = sA[t * L + 4 * cg + u];
-#pragma unroll
-      for (int r = 0; r < CW; ++r)
-#pragma unroll
-        for (int u = 0; u < 4; ++u) acc[r][u] += kv[r] * av[u];
-    }
-#pragma unroll
-    for (int r = 0; r < CW; ++r) store_run<4>(rc + R::KA + static_cast<long>(CW * rg + r) * L + 4 * cg, acc[r]);
+    for (int e = 0; e < 4; ++e) rc[R::KA + static_cast<long>(16 * ia + 4 * gq + e) * L + 16 * ua + m] = acc[e];
   }
   __syncthreads();   // Aqk staged
-  {
-    // QP = Qg - Aqk W
-    float acc[4][CW];
+  // QP = Qg - Aqk W, also stored transposed
+  for (int tile = wave; tile < 4 * NT; tile += 4) {
+    const int tt = tile / NT, it = tile % NT;
+    f32x4 acc = mm_tile(sAq + 16 * tt * L, L, 1, sG + 16 * it, P, 1, L, gq, m);
+    const int i = 16 * it + m;
 #pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int u = 0; u < CW; ++u) acc[r][u] = 0.f;
-#pragma unroll 4
-    for (int s2 = 0; s2 < L; ++s2) {
-      float wv[CW];
-#pragma unroll
-      for (int u = 0; u < CW; ++u) wv[u] = sG[s2 * P + CW * cg + u];
-#pragma unroll
-      for (int r = 0; r < 4; ++r) {
-        const float x = sAq[(4 * rg + r) * L + s2];
-#pragma unroll
-        for (int u = 0; u < CW; ++u) acc[r][u] += x * wv[u];
-      }
+    for (int e = 0; e < 4; ++e) {
+      const int t = 16 * tt + 4 * gq + e;
+      acc[e] = sq[t * P + i] - acc[e];
+      rc[R::QP + static_cast<long>(t) * DK + i] = acc[e];
     }
-#pragma unroll
-    for (int r = 0; r < 4; ++r)
-#pragma unroll
-      for (int u = 0; u < CW; ++u) {
-        const int t = 4 * rg + r, i = CW * cg + u;
-        acc[r][u] = sq[t * P + i] - acc[r][u];
-      }
-#pragma unroll
-    for (int r = 0; r < 4; ++r) store_run<CW>(rc + R::QP + static_cast<long>(4 * rg + r) * DK + CW * cg, acc[r]);
-#pragma unroll
-    for (int u = 0; u < CW; ++u) {
-      const float col[4] = {acc[0][u], acc[1][u], acc[2][u], acc[3][u]};
-      store_run<4>(rc + R::QPT + static_cast<long>(CW * cg + u) * L + 4 * rg, col);
-    }
+    *reinterpret_cast<f32x4*>(rc + R::QPT + static_cast<long>(i) * L + 16 * tt + 4 * gq) = acc;
   }
 }
 
@@ -410,7 +328,7 @@ struct ScanCfg {
 
 template <int DK, bool BACK>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void bwd_scan_kernel(
-    const void* __restrict__ x1, const void* __restrict__ x2, int dt, const float* __restrict__ rec,
+    const float* __restrict__ x1, const float* __restrict__ x2, const float* __restrict__ rec,
     const float* __restrict__ init, float* __restrict__ ck, float* __restrict__ fin, int H, int HK, int DV, long S,
     int NC) {
   using R = Rec<DK>;
@@ -425,7 +343,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const int c0 = blockIdx.x * CT;
   const bool computes = wave * C::TPW < C::TILES;   // DK = 32: two waves hold the tiles
   const float* rbase = rec + static_cast<size_t>(bi * HK + hk) * NC * R::STRIDE;
-  for (int e = tid; e < DK * CT; e += kThreads) {
+#pragma unroll
+  for (int e0 = 0; e0 < DK * CT; e0 += kThreads) {
+    const int e = e0 + tid;
     const int r = e / CT, cl = e % CT;
     sX[r * C::XP + cl] = init ? init[(static_cast<size_t>(bh) * DK + r) * DV + c0 + cl] : 0.f;
   }
@@ -447,18 +367,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     }
   };
   constexpr int NT = L * CT / kThreads;
-  uint32_t p1[NT], p2[NT];
+  float p1[NT], p2[NT], pk1[NT];   // raw values and their keep factors (applied when staged)
   auto fetch_z = [&](int c) {
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
       const int e = tid + n * kThreads, t = e / CT, cl = e % CT;
       const long tok = static_cast<long>(c) * L + t;
-      p1[n] = p2[n] = 0u;
-      if (tok < S) {
-        const size_t ix = ((static_cast<size_t>(bi) * S + tok) * H + h) * DV + c0 + cl;
-        p1[n] = load_raw(x1, ix, dt);
-        if (!BACK) p2[n] = load_raw(x2, ix, dt);
-      }
+      const size_t ix = ((static_cast<size_t>(bi) * S + clamp_row(tok, S)) * H + h) * DV + c0 + cl;
+      pk1[n] = tok < S ? 1.f : 0.f;
+      p1[n] = x1[ix];
+      p2[n] = BACK ? 0.f : x2[ix];
     }
   };
   auto chunk_of = [&](int step) { return BACK ? NC - 1 - step : step; };
@@ -469,14 +387,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
       const int e = tid + n * kThreads;
-      sZ[(e / CT) * C::XP + e % CT] = BACK ? raw_f32(p1[n], dt) : raw_f32(p1[n], dt) * raw_f32(p2[n], dt);
+      sZ[(e / CT) * C::XP + e % CT] = pk1[n] * (BACK ? p1[n] : p1[n] * p2[n]);
     }
     if (step + 1 < NC) {
       fetch_m(chunk_of(step + 1), nA, nZ);
       fetch_z(chunk_of(step + 1));
     }
     float* out = ck + (static_cast<size_t>(bh) * NC + c) * DK * DV;
-    for (int e = tid; e < DK * CT; e += kThreads) {
+    #pragma unroll
+    for (int e0 = 0; e0 < DK * CT; e0 += kThreads) {
+      const int e = e0 + tid;
       const int r = e / CT, cl = e % CT;
       out[static_cast<size_t>(r) * DV + c0 + cl] = sX[r * C::XP + cl];
     }
@@ -518,7 +438,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   }
   __syncthreads();
   if (fin) {
-    for (int e = tid; e < DK * CT; e += kThreads) {
+    #pragma unroll
+    for (int e0 = 0; e0 < DK * CT; e0 += kThreads) {
+      const int e = e0 + tid;
       const int r = e / CT, cl = e % CT;
       fin[(static_cast<size_t>(bh) * DK + r) * DV + c0 + cl] = sX[r * C::XP + cl];
     }
@@ -553,8 +475,8 @@ __device__ __forceinline__ f32x4 mma(float a, float b, f32x4 c) {
 
 template <int DK>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void bwd_gradmm_kernel(
-    const void* __restrict__ k, const void* __restrict__ v, const float* __restrict__ g, const void* __restrict__ b,
-    const void* __restrict__ w, int dt, const void* __restrict__ dout, int do_dt, const float* __restrict__ rec,
+    const float* __restrict__ k, const float* __restrict__ v, const float* __restrict__ g, const float* __restrict__ b,
+    const float* __restrict__ w, int dt, const float* __restrict__ dout, const float* __restrict__ rec,
     const float* __restrict__ sck, const float* __restrict__ dsck, void* __restrict__ dv, void* __restrict__ dw,
     float* __restrict__ gs, int H, int HK, int DV, long S, int NC) {
   constexpr int XP = CT + 1;          // LDS pitch of the 16-column arrays
@@ -579,9 +501,11 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const int row = 16 * wave + m;      // this lane's A-operand row
 
   // G = within-chunk cumsum of g
-  for (int e = tid; e < L * DK; e += kThreads) {
+#pragma unroll
+  for (int e0 = 0; e0 < L * DK; e0 += kThreads) {
+    const int e = e0 + tid;
     const int t = e / DK, i = e % DK;
-    sG[e] = t0 + t < S ? g[key_index(bi, S, t0 + t, HK, hk, DK, i)] : 0.f;
+    sG[e] = (t0 + t < S ? 1.f : 0.f) * g[key_index(bi, S, clamp_row(t0 + t, S), HK, hk, DK, i)];
   }
   __syncthreads();
   if (tid < DK) {
@@ -593,14 +517,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   }
   __syncthreads();
   // A operands: -E, KG (LDS); Ai, Ai^T, Aqk^T rows in registers
-  for (int e = tid; e < L * DK; e += kThreads) {
+#pragma unroll
+  for (int e0 = 0; e0 < L * DK; e0 += kThreads) {
+    const int e = e0 + tid;
     const int t = e / DK, i = e % DK;
-    float kv = 0.f, bv = 0.f;
-    if (t0 + t < S) {
-      const size_t ix = key_index(bi, S, t0 + t, HK, hk, DK, i);
-      kv = load_elem(k, ix, dt);
-      bv = load_elem(b, ix, dt);
-    }
+    const size_t ix = key_index(bi, S, clamp_row(t0 + t, S), HK, hk, DK, i);
+    const float keep = t0 + t < S ? 1.f : 0.f;
+    const float kv = keep * k[ix], bv = keep * b[ix];
     const float gt = sG[t * DK + i];
     const int o = t * EP + (i / KD) * (KD + 1) + i % KD;
     sEn[o] = -bv * kv * __expf(gt);
@@ -629,7 +552,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   // dv, dw. The next block's are requested while the current one is worked on.
   constexpr int NSE = DK * CT / kThreads, NTE = L * CT / kThreads;
   float pS[NSE], pdS[NSE];
-  uint32_t pO[NTE], pV[4], pW[4];
+  float pO[NTE], pV[4], pW[4], kO[NTE], kVW[4];   // raw values and their keep factors
   auto fetch = [&](int cb) {
 #pragma unroll
     for (int n = 0; n < NSE; ++n) {
@@ -640,18 +563,16 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
     for (int n = 0; n < NTE; ++n) {
       const int e = tid + n * kThreads, t = e / CT, cl = e % CT;
-      pO[n] = t0 + t < S ? load_raw(dout, ((static_cast<size_t>(bi) * S + t0 + t) * H + h) * DV + cb + cl, do_dt)
-                         : 0u;
+      kO[n] = t0 + t < S ? 1.f : 0.f;
+      pO[n] = dout[((static_cast<size_t>(bi) * S + clamp_row(t0 + t, S)) * H + h) * DV + cb + cl];
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int t = 16 * wave + 4 * gq + e;
-      pV[e] = pW[e] = 0u;
-      if (t0 + t < S) {
-        const size_t ix = ((static_cast<size_t>(bi) * S + t0 + t) * H + h) * DV + cb + m;
-        pV[e] = load_raw(v, ix, dt);
-        pW[e] = load_raw(w, ix, dt);
-      }
+      const size_t ix = ((static_cast<size_t>(bi) * S + clamp_row(t0 + t, S)) * H + h) * DV + cb + m;
+      kVW[e] = t0 + t < S ? 1.f : 0.f;
+      pV[e] = v[ix];
+      pW[e] = w[ix];
     }
   };
   fetch(0);
@@ -666,14 +587,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
     for (int n = 0; n < NTE; ++n) {
       const int e = tid + n * kThreads, t = e / CT, cl = e % CT;
-      sdO[t * XP + cl] = raw_f32(pO[n], do_dt);
+      sdO[t * XP + cl] = kO[n] * pO[n];
     }
     f32x4 zc;
     float vv[4], ww[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      vv[e] = raw_f32(pV[e], dt);
-      ww[e] = raw_f32(pW[e], dt);
+      vv[e] = kVW[e] * pV[e];
+      ww[e] = kVW[e] * pW[e];
       zc[e] = ww[e] * vv[e];
     }
     if (cb + CT < DV) fetch(cb + CT);
@@ -768,8 +689,8 @@ constexpr int PWP = PWC + 1;          // LDS pitch
 
 template <int DK>
 __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
-    const void* __restrict__ q, const void* __restrict__ k, const float* __restrict__ g, const void* __restrict__ b,
-    int dt, const float* __restrict__ gs, float* __restrict__ part, int H, int HK, long S, int NC, float scale) {
+    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ g, const float* __restrict__ b,
+    const float* __restrict__ gs, float* __restrict__ part, int H, int HK, long S, int NC, float scale) {
   constexpr int NB = DK / PWC > 0 ? DK / PWC : 1;   // channel blocks
   constexpr int CW = DK < PWC ? DK : PWC;            // channels in a block
   constexpr int EPT = L * CW / kThreads;             // elements per thread
@@ -782,22 +703,21 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
   const long t0 = static_cast<long>(c) * L;
   const float* src = gs + (static_cast<size_t>(bh) * NC + c) * G::STRIDE;
   const int i0 = cb * CW;
-  for (int e = tid; e < L * CW; e += kThreads) {
+#pragma unroll
+  for (int e0 = 0; e0 < L * CW; e0 += kThreads) {
+    const int e = e0 + tid;
     const int t = e / CW, ii = e % CW;
-    float qv = 0.f, kv = 0.f, bv = 0.f, gv = 0.f;
-    if (t0 + t < S) {
-      const size_t ix = key_index(bi, S, t0 + t, HK, hk, DK, i0 + ii);
-      qv = load_elem(q, ix, dt);
-      kv = load_elem(k, ix, dt);
-      bv = load_elem(b, ix, dt);
-      gv = g[ix];
-    }
+    const size_t ix = key_index(bi, S, clamp_row(t0 + t, S), HK, hk, DK, i0 + ii);
+    const float keep = t0 + t < S ? 1.f : 0.f;
+    const float qv = keep * q[ix], kv = keep * k[ix], bv = keep * b[ix], gv = keep * g[ix];
     pq[t * PWP + ii] = qv;
     pk[t * PWP + ii] = kv;
     pbk[t * PWP + ii] = bv * kv;
     pG[t * PWP + ii] = gv;
   }
-  for (int e = tid; e < L * L; e += kThreads) {   // masked: dAqk on s <= t, dAkk on s < t
+#pragma unroll
+  for (int e0 = 0; e0 < L * L; e0 += kThreads) {
+    const int e = e0 + tid;   // masked: dAqk on s <= t, dAkk on s < t
     const int t = e / L, s2 = e % L;
     pAq[t * (L + 1) + s2] = s2 <= t ? src[G::AQ + e] : 0.f;
     pAk[t * (L + 1) + s2] = s2 < t ? src[G::AK + e] : 0.f;
@@ -846,7 +766,7 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
     const int t = tp + TS * r;
     const float qv = pq[t * PWP + ii], kv = pk[t * PWP + ii], bkv = pbk[t * PWP + ii];
     const bool valid = t0 + t < S;
-    const float bv = valid ? load_elem(b, key_index(bi, S, t0 + t, HK, hk, DK, i), dt) : 0.f;
+    const float bv = valid ? b[key_index(bi, S, t0 + t, HK, hk, DK, i)] : 0.f;
     const float ga = __expf(gt[r]), gd = __expf(gl - gt[r]);
     const float fQg = src[G::QG + t * DK + i], fE = src[G::E + t * DK + i], fKG = src[G::KG + t * DK + i];
     const float dq = scale * (ga * fQg + rq[r]);
@@ -880,6 +800,31 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
       if (t0 + t < S) part[3 * plane + ((static_cast<size_t>(bi) * S + t0 + t) * H + h) * DK + i0 + tid] = run;
     }
   }
+}
+
+// ---------------------------------------------------------------- input copies
+// The kernels above read fp32 operands: a 16-bit input is widened into the
+// workspace first (one pass), so their loads carry no dtype dispatch (a
+// run-time dtype switch around a load makes the compiler wait for each load
+// inside its branch).
+__global__ __launch_bounds__(kThreads) void bwd_widen_kernel(const void* __restrict__ src, int dt,
+                                                             float* __restrict__ dst, long n) {
+  const long i0 = (static_cast<long>(blockIdx.x) * kThreads + threadIdx.x) * 4;
+  if (i0 + 4 <= n && (reinterpret_cast<uintptr_t>(src) & 7) == 0) {
+    if (dt == DT_BF16) {
+      const uint2 r = *reinterpret_cast<const uint2*>(static_cast<const unsigned short*>(src) + i0);
+      *reinterpret_cast<f32x4*>(dst + i0) = f32x4{bf16_lo_f32(r.x), bf16_hi_f32(r.x), bf16_lo_f32(r.y), bf16_hi_f32(r.y)};
+      return;
+    }
+    if (dt == DT_F16) {
+      const uint2 r = *reinterpret_cast<const uint2*>(static_cast<const unsigned short*>(src) + i0);
+      *reinterpret_cast<f32x4*>(dst + i0) =
+          f32x4{f16_bits_to_f32(r.x & 0xffff), f16_bits_to_f32(r.x >> 16), f16_bits_to_f32(r.y & 0xffff),
+                f16_bits_to_f32(r.y >> 16)};
+      return;
+    }
+  }
+  for (long i = i0; i < i0 + 4 && i < n; ++i) dst[i] = load_elem(src, i, dt);
 }
 
 // ---------------------------------------------------------------- kernel 5
@@ -922,7 +867,9 @@ size_t backward_workspace_bytes(int B, int H, int HK, int DK, int DV, long S) {
   const size_t part = up(4 * static_cast<size_t>(B) * S * H * DK * 4);
   long gstride = DK == 32 ? bw::GS<32>::STRIDE : DK == 64 ? bw::GS<64>::STRIDE : bw::GS<128>::STRIDE;
   const size_t gsb = up(static_cast<size_t>(B) * H * NC * gstride * 4);
-  return rec + 2 * ck + part + gsb;
+  const size_t nk = static_cast<size_t>(B) * S * HK * DK, nv = static_cast<size_t>(B) * S * H * DV;
+  const size_t wide = 3 * up(nk * 4) + 3 * up(nv * 4);   // fp32 q, k, b, v, w, do
+  return rec + 2 * ck + part + gsb + wide;
 }
 
 namespace {
@@ -943,7 +890,7 @@ hipError_t launch_backward_t(const void* q, const void* k, const void* v, const 
   if (NC == 0) {   // no tokens: the initial-state gradient is the final-state one (or zero)
     if (ds0)
       hipLaunchKernelGGL((bw::bwd_scan_kernel<DK, true>), dim3(DV / bw::CT, B * H), dim3(bw::kThreads), 0, stream,
-                         dout, nullptr, do_dt, nullptr, dht, nullptr, ds0, H, HK, DV, S, 0);
+                         nullptr, nullptr, nullptr, dht, nullptr, ds0, H, HK, DV, S, 0);
     return hipGetLastError();
   }
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
@@ -957,17 +904,34 @@ hipError_t launch_backward_t(const void* q, const void* k, const void* v, const 
   float* part = reinterpret_cast<float*>(ws);
   ws += up(4 * static_cast<size_t>(B) * S * H * DK * 4);
   float* gsc = reinterpret_cast<float*>(ws);
+  ws += up(static_cast<size_t>(B) * H * NC * bw::GS<DK>::STRIDE * 4);
+  const long nk = static_cast<long>(B) * S * HK * DK, nv = static_cast<long>(B) * S * H * DV;
+  // fp32 operands: the inputs themselves when they are fp32, else widened copies
+  auto widen = [&](const void* src, int sdt, long n) -> const float* {
+    float* dst = reinterpret_cast<float*>(ws);
+    ws += up(static_cast<size_t>(n) * 4);
+    if (sdt == DT_F32) return static_cast<const float*>(src);
+    hipLaunchKernelGGL(bw::bwd_widen_kernel, dim3(static_cast<unsigned>((n + 4L * bw::kThreads - 1) / (4L * bw::kThreads))),
+                       dim3(bw::kThreads), 0, stream, src, sdt, dst, n);
+    return dst;
+  };
+  const float* qf = widen(q, dt, nk);
+  const float* kf = widen(k, dt, nk);
+  const float* bf = widen(b, dt, nk);
+  const float* vf = widen(v, dt, nv);
+  const float* wf = widen(w, dt, nv);
+  const float* of = widen(dout, do_dt, nv);
 
-  hipLaunchKernelGGL(bw::bwd_local_kernel<DK>, dim3(NC, B * HK), dim3(bw::kThreads), lds1, stream, q, k, b, g, dt,
+  hipLaunchKernelGGL(bw::bwd_local_kernel<DK>, dim3(NC, B * HK), dim3(bw::kThreads), lds1, stream, qf, kf, bf, g,
                      HK, S, NC, scale, rec);
-  hipLaunchKernelGGL((bw::bwd_scan_kernel<DK, false>), dim3(DV / bw::CT, B * H), dim3(bw::kThreads), 0, stream, v, w,
-                     dt, rec, s0, sck, nullptr, H, HK, DV, S, NC);
-  hipLaunchKernelGGL((bw::bwd_scan_kernel<DK, true>), dim3(DV / bw::CT, B * H), dim3(bw::kThreads), 0, stream, dout,
-                     nullptr, do_dt, rec, dht, dsck, ds0, H, HK, DV, S, NC);
-  hipLaunchKernelGGL(bw::bwd_gradmm_kernel<DK>, dim3(NC, B * H), dim3(bw::kThreads), 0, stream, k, v, g, b, w, dt,
-                     dout, do_dt, rec, sck, dsck, dv, dw, gsc, H, HK, DV, S, NC);
+  hipLaunchKernelGGL((bw::bwd_scan_kernel<DK, false>), dim3(DV / bw::CT, B * H), dim3(bw::kThreads), 0, stream, vf,
+                     wf, rec, s0, sck, nullptr, H, HK, DV, S, NC);
+  hipLaunchKernelGGL((bw::bwd_scan_kernel<DK, true>), dim3(DV / bw::CT, B * H), dim3(bw::kThreads), 0, stream, of,
+                     nullptr, rec, dht, dsck, ds0, H, HK, DV, S, NC);
+  hipLaunchKernelGGL(bw::bwd_gradmm_kernel<DK>, dim3(NC, B * H), dim3(bw::kThreads), 0, stream, kf, vf, g, bf, wf, dt,
+                     of, rec, sck, dsck, dv, dw, gsc, H, HK, DV, S, NC);
   constexpr int NB = DK / bw::PWC > 0 ? DK / bw::PWC : 1;
-  hipLaunchKernelGGL(bw::bwd_gradpw_kernel<DK>, dim3(NC * NB, B * H), dim3(bw::kThreads), 0, stream, q, k, g, b, dt,
+  hipLaunchKernelGGL(bw::bwd_gradpw_kernel<DK>, dim3(NC * NB, B * H), dim3(bw::kThreads), 0, stream, qf, kf, g, bf,
                      gsc, part, H, HK, S, NC, scale);
   const long n_key = static_cast<long>(B) * S * HK * DK;
   hipLaunchKernelGGL(bw::bwd_sum_kernel, dim3(static_cast<unsigned>((n_key + bw::kThreads - 1) / bw::kThreads)),
