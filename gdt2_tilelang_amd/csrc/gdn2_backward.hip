@@ -139,37 +139,69 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
   }
   __syncthreads();
 
-  // Aqk (to the record) and Akk (to LDS): thread (t, 16-column block) -- a
-  // block past the diagonal is skipped, an exponent is only formed for s <= t
+  // Aqk (to the record) and Akk (to LDS) by 16 x 16 blocks.
+  // Below the diagonal blocks (t in block tb, s in an earlier block sb), on
+  // matrix cores: exp(G_t - G_s) = exp(G_t - G_R) exp(G_R - G_s) with
+  // R = 16 tb - 1 (s <= R < t), both factors <= 1, so each block is a plain
+  // product over the channels of (q or b k) exp(G_t - G_R) and k exp(G_R - G_s).
   {
-    const int t = tid >> 2, sb = (tid & 3) * 16;
-    float aq[16], ak[16];
+    const int lane = tid & 63, wave = tid >> 6, gq = lane >> 4, m = lane & 15;
+    for (int tile = wave; tile < 6; tile += 4) {
+      const int tb = tile < 1 ? 1 : (tile < 3 ? 2 : 3), sb = tile - tb * (tb - 1) / 2;
+      const int R = 16 * tb - 1, t = 16 * tb + m, sr = 16 * sb + m;
+      f32x4 aq = zero4(), ak = zero4();
+#pragma unroll 4
+      for (int ks = 0; ks < DK / 4; ++ks) {
+        const int i = 4 * ks + gq;
+        const float gR = sG[R * P + i];
+        const float ea = __expf(sG[t * P + i] - gR);
+        const float eb = __expf(gR - sG[sr * P + i]) * sk[sr * P + i];
+        aq = __builtin_amdgcn_mfma_f32_16x16x4f32(sq[t * P + i] * ea, eb, aq, 0, 0, 0);
+        ak = __builtin_amdgcn_mfma_f32_16x16x4f32(sbk[t * P + i] * ea, eb, ak, 0, 0, 0);
+      }
 #pragma unroll
-    for (int j = 0; j < 16; ++j) aq[j] = ak[j] = 0.f;
-    if (sb <= t) {
-      for (int i = 0; i < DK; i += 4) {
-        const float4 qt = *reinterpret_cast<const float4*>(&sq[t * P + i]);
-        const float4 bt = *reinterpret_cast<const float4*>(&sbk[t * P + i]);
-        const float4 gt = *reinterpret_cast<const float4*>(&sG[t * P + i]);
+      for (int e = 0; e < 4; ++e) {
+        const int row = 16 * tb + 4 * gq + e, col = 16 * sb + m;
+        rc[R::AQ + row * L + col] = scale * aq[e];
+        sA[row * L + col] = ak[e];
+      }
+    }
+    // diagonal blocks exactly: thread (block db, row tl, columns 4 sq4 ..), every
+    // exponent taken for s <= t only (exp(-inf) = 0 elsewhere)
+    const int db = tid >> 6, tl = (tid & 63) >> 2, sq4 = tid & 3;
+    const int t = 16 * db + tl;
+    float aq[4] = {0.f, 0.f, 0.f, 0.f}, ak[4] = {0.f, 0.f, 0.f, 0.f};
+    const float ninf = -__builtin_huge_valf();
+    for (int i = 0; i < DK; i += 4) {
+      const float4 qt = *reinterpret_cast<const float4*>(&sq[t * P + i]);
+      const float4 bt = *reinterpret_cast<const float4*>(&sbk[t * P + i]);
+      const float4 gt = *reinterpret_cast<const float4*>(&sG[t * P + i]);
 #pragma unroll
-        for (int j = 0; j < 16; ++j) {
-          const int s = sb + j;
-          if (s <= t) {
-            const float4 ks = *reinterpret_cast<const float4*>(&sk[s * P + i]);
-            const float4 gs = *reinterpret_cast<const float4*>(&sG[s * P + i]);
-            const float e0 = __expf(gt.x - gs.x) * ks.x, e1 = __expf(gt.y - gs.y) * ks.y;
-            const float e2 = __expf(gt.z - gs.z) * ks.z, e3 = __expf(gt.w - gs.w) * ks.w;
-            aq[j] += qt.x * e0 + qt.y * e1 + qt.z * e2 + qt.w * e3;
-            ak[j] += bt.x * e0 + bt.y * e1 + bt.z * e2 + bt.w * e3;
-          }
-        }
+      for (int j = 0; j < 4; ++j) {
+        const int s2 = 16 * db + 4 * sq4 + j;
+        const bool in = s2 <= t;
+        const float4 ks = *reinterpret_cast<const float4*>(&sk[s2 * P + i]);
+        const float4 gs = *reinterpret_cast<const float4*>(&sG[s2 * P + i]);
+        const float e0 = __expf(in ? gt.x - gs.x : ninf) * ks.x, e1 = __expf(in ? gt.y - gs.y : ninf) * ks.y;
+        const float e2 = __expf(in ? gt.z - gs.z : ninf) * ks.z, e3 = __expf(in ? gt.w - gs.w : ninf) * ks.w;
+        aq[j] += qt.x * e0 + qt.y * e1 + qt.z * e2 + qt.w * e3;
+        ak[j] += bt.x * e0 + bt.y * e1 + bt.z * e2 + bt.w * e3;
       }
     }
 #pragma unroll
-    for (int j = 0; j < 16; ++j) {
-      const int s = sb + j;
-      rc[R::AQ + t * L + s] = s <= t ? scale * aq[j] : 0.f;
-      sA[t * L + s] = s < t ? ak[j] : 0.f;
+    for (int j = 0; j < 4; ++j) {
+      const int s2 = 16 * db + 4 * sq4 + j;
+      rc[R::AQ + t * L + s2] = s2 <= t ? scale * aq[j] : 0.f;
+      sA[t * L + s2] = s2 < t ? ak[j] : 0.f;
+    }
+    // above the diagonal blocks: zeros
+#pragma unroll
+    for (int e0 = 0; e0 < L * L; e0 += kThreads) {
+      const int e = e0 + tid, r = e / L, c2 = e % L;
+      if ((c2 >> 4) > (r >> 4)) {
+        rc[R::AQ + e] = 0.f;
+        sA[e] = 0.f;
+      }
     }
   }
   __syncthreads();
