@@ -165,17 +165,22 @@ __global__ __launch_bounds__(kProThreads) void prologue_kernel(ProArgs a) {
       }
       // window row r is the input at position t0 - K1 + r, r < nt + K1; a
       // position before the segment (then t0 = 0, so row r < K1) is tail entry r
+      // every row is loaded unconditionally from a position clamped into the
+      // segment (a load under a per-lane branch would be waited for inside
+      // it), then the rows outside are replaced
       float win[TT + K1][8];
 #pragma unroll
       for (int r = 0; r < TT + K1; ++r) {
         const long p = t0 - K1 + r;
-        if (r < nt + K1 && p >= 0) ld8<DT>(x, (row0 + p) * ldx + cx, win[r]);
-        else if (r < K1 && p < 0) {
+        const long pc = p < 0 ? 0 : (p < a.S ? p : a.S - 1);
+        ld8<DT>(x, (row0 + pc) * ldx + cx, win[r]);
+      }
 #pragma unroll
-          for (int e = 0; e < 8; ++e) win[r][e] = cin[e * K1 + r];
-        } else {
+      for (int r = 0; r < TT + K1; ++r) {
+        const long p = t0 - K1 + r;
+        if (!(r < nt + K1 && p >= 0)) {
 #pragma unroll
-          for (int e = 0; e < 8; ++e) win[r][e] = 0.f;
+          for (int e = 0; e < 8; ++e) win[r][e] = (r < K1 && p < 0) ? cin[e * K1 + r] : 0.f;
         }
       }
 #pragma unroll
@@ -361,13 +366,19 @@ __global__ __launch_bounds__(kThreads) void epilogue8_kernel(const void* __restr
   const bool act = row < rows && c < DV;
   const long tok = row / H;
   const int h = static_cast<int>(row % H);
+  // loads from a clamped (row, column), unconditionally; inactive lanes zeroed after
   float x[8], gt[8];
-  if (act) {
-    ld8<ODT>(o, row * DV + c, x);
-    ld8<GDT>(gate, tok * ld_gate + static_cast<long>(h) * DV + c, gt);
-  } else {
+  {
+    const long rr = row < rows ? row : rows - 1;
+    const int cc = c < DV ? c : DV - 8;
+    const long tk = rr / H;
+    const int hh = static_cast<int>(rr % H);
+    ld8<ODT>(o, rr * DV + cc, x);
+    ld8<GDT>(gate, tk * ld_gate + static_cast<long>(hh) * DV + cc, gt);
+    if (!act) {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) x[e] = gt[e] = 0.f;
+      for (int e = 0; e < 8; ++e) x[e] = gt[e] = 0.f;
+    }
   }
   float ss = 0.f;
 #pragma unroll
