@@ -49,6 +49,8 @@ def _autograd(q, k, v, g, b, w, s0, do, dht, scale, rep):
     (1, 128, 2, 1, 64, 64, torch.float32, False, False, 25.0),
     (1, 70, 2, 2, 128, 64, torch.float32, True, False, 1.0),
     (2, 100, 2, 2, 64, 64, torch.bfloat16, True, True, 4.0),
+    (1, 300, 4, 2, 128, 128, torch.float32, True, True, 2.0),
+    (1, 64, 2, 2, 128, 32, torch.float16, False, True, 4.0),
 ])
 def test_backward_matches_autograd(B, S, H, HK, DK, DV, dtype, state, dht, decay):
     print(f"backward B={B} S={S} H={H} HK={HK} DK={DK} DV={DV} {dtype} state={state} dht={dht} "
