@@ -93,12 +93,13 @@ struct DecLds {
 };
 
 // TB: tokens staged per block (1 for single-token calls, else kDecTokBlock)
-template <int DK, int IN_DT, int OUT_DT, int TB>
+// QKN: q and k arrive before their per-head L2 normalisation (layer decode)
+template <int DK, int IN_DT, int OUT_DT, int TB, bool QKN = false>
 __global__ __launch_bounds__(kDecMaxThreads) void decode_kernel(
     const void* __restrict__ q, const void* __restrict__ k, const void* __restrict__ v,
     const float* __restrict__ g, const void* __restrict__ b, const void* __restrict__ w,
     float* __restrict__ state, void* __restrict__ o, int H, int HK, int DV, long s_alloc, long t0,
-    int n, float scale, int qk_norm) {
+    int n, float scale) {
   constexpr int RPT = DK / kDecRowGroups;
   constexpr int GPT = DK / 8;             // 8-channel groups per token
   __shared__ __align__(16) DecLds<DK, TB> sm;
@@ -157,7 +158,7 @@ __global__ __launch_bounds__(kDecMaxThreads) void decode_kernel(
         kv[j] = kr.get(j);
         qv[j] = qr.get(j);
       }
-      if (qk_norm) {
+      if constexpr (QKN) {
         // q and k of the layer's decode step arrive before their per-head L2
         // normalisation (x / max(||x||, 1e-12), rounded to the input dtype):
         // the GPT items of a token are GPT consecutive lanes of one wave, and
@@ -269,13 +270,17 @@ static hipError_t launch_decode_t(const void* q, const void* k, const void* v, c
     tiles = DV / kDecCols;
     threads = 64;
   }
-  if (n == 1)
-    hipLaunchKernelGGL((decode_kernel<DK, IN_DT, OUT_DT, 1>), dim3(tiles, B * H), dim3(threads), 0,
-                       stream, q, k, v, g, b, w, state, o, H, HK, DV, s_alloc, t0, n, scale, qk_norm);
-  else
-    hipLaunchKernelGGL((decode_kernel<DK, IN_DT, OUT_DT, kDecTokBlock>), dim3(tiles, B * H),
-                       dim3(threads), 0, stream, q, k, v, g, b, w, state, o, H, HK, DV, s_alloc, t0, n,
-                       scale, qk_norm);
+#define GDN2_DEC_LAUNCH(TBV, QV)                                                                            \
+  hipLaunchKernelGGL((decode_kernel<DK, IN_DT, OUT_DT, TBV, QV>), dim3(tiles, B * H), dim3(threads), 0, stream, q, k, \
+                     v, g, b, w, state, o, H, HK, DV, s_alloc, t0, n, scale)
+  if (qk_norm) {
+    if (n == 1) GDN2_DEC_LAUNCH(1, true);
+    else GDN2_DEC_LAUNCH(kDecTokBlock, true);
+  } else {
+    if (n == 1) GDN2_DEC_LAUNCH(1, false);
+    else GDN2_DEC_LAUNCH(kDecTokBlock, false);
+  }
+#undef GDN2_DEC_LAUNCH
   return hipGetLastError();
 }
 
