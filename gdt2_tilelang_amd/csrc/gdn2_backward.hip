@@ -91,8 +91,9 @@ __device__ __forceinline__ f32x4 mm_tile(const float* a, int as, int ak, const f
   return acc;
 }
 
+constexpr int LA = L + 2;        // LDS pitch of the L x L arrays of kernel 1 (rows two banks apart)
 template <int DK>
-constexpr int local_lds_floats() { return 3 * L * (DK + 4) + L * (DK + 4 > L ? DK + 4 : L) + L * L + DK + 9 * 256; }
+constexpr int local_lds_floats() { return 3 * L * (DK + 4) + L * (DK + 4 > LA ? DK + 4 : LA) + L * LA + DK + 9 * 256; }
 
 template <int DK>
 __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __restrict__ q, const float* __restrict__ k,
@@ -104,10 +105,10 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
   extern __shared__ __align__(16) float sm[];
   float* sq = sm;                 // q, then Qg
   float* sk = sq + L * P;         // k, then KG
-  float* sbk = sk + L * P;        // b k, then E, then Aqk (L x L: the slot is at least that large)
-  float* sG = sbk + L * (P > L ? P : L);   // G, then W = Ai E
-  float* sA = sG + L * P;         // Akk, then Ai   [L][L]
-  float* sgam = sA + L * L;       // gamma          [DK]
+  float* sbk = sk + L * P;        // b k, then E, then Aqk (pitch LA: the slot is at least that large)
+  float* sG = sbk + L * (P > LA ? P : LA);   // G, then W = Ai E
+  float* sA = sG + L * P;         // Akk, then Ai   [L][LA]
+  float* sgam = sA + L * LA;      // gamma          [DK]
   float* sXo = sgam + DK;         // off-diagonal 16 x 16 blocks of Ai [6][16][16]
   float* sT = sXo + 6 * 256;      // block products [3][16][16]
   const int tid = threadIdx.x;
@@ -163,7 +164,7 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
       for (int e = 0; e < 4; ++e) {
         const int row = 16 * tb + 4 * gq + e, col = 16 * sb + m;
         rc[R::AQ + row * L + col] = scale * aq[e];
-        sA[row * L + col] = ak[e];
+        sA[row * LA + col] = ak[e];
       }
     }
     // diagonal blocks exactly: thread (block db, row tl, columns 4 sq4 ..), every
@@ -192,7 +193,7 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
     for (int j = 0; j < 4; ++j) {
       const int s2 = 16 * db + 4 * sq4 + j;
       rc[R::AQ + t * L + s2] = s2 <= t ? scale * aq[j] : 0.f;
-      sA[t * L + s2] = s2 < t ? ak[j] : 0.f;
+      sA[t * LA + s2] = s2 < t ? ak[j] : 0.f;
     }
     // above the diagonal blocks: zeros
 #pragma unroll
@@ -200,7 +201,7 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
       const int e = e0 + tid, r = e / L, c2 = e % L;
       if ((c2 >> 4) > (r >> 4)) {
         rc[R::AQ + e] = 0.f;
-        sA[e] = 0.f;
+        sA[r * LA + c2] = 0.f;
       }
     }
   }
@@ -217,15 +218,15 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
     const int bb = tid >> 4, j = tid & 15, o = 16 * bb;
     for (int r = 0; r < 16; ++r) {
       float s = 0.f;
-      for (int u = j; u < r; ++u) s += sA[(o + r) * L + o + u] * sA[(o + u) * L + o + j];
-      sA[(o + r) * L + o + j] = j < r ? -s : (j == r ? 1.f : 0.f);
+      for (int u = j; u < r; ++u) s += sA[(o + r) * LA + o + u] * sA[(o + u) * LA + o + j];
+      sA[(o + r) * LA + o + j] = j < r ? -s : (j == r ? 1.f : 0.f);
     }
   }
   __syncthreads();
   {
     // X block (k, j), k >= j: diagonal in sA, off-diagonal in sXo[k (k-1) / 2 + j]
     auto xb = [&](int kb, int jb, int r, int c) -> float {
-      return kb == jb ? sA[(16 * kb + r) * L + 16 * jb + c] : sXo[((kb * (kb - 1) / 2 + jb) * 16 + r) * 16 + c];
+      return kb == jb ? sA[(16 * kb + r) * LA + 16 * jb + c] : sXo[((kb * (kb - 1) / 2 + jb) * 16 + r) * 16 + c];
     };
     for (int d = 1; d < 4; ++d) {
       // T = sum_{k=j}^{i-1} Akk_ik X_kj for the 4 - d blocks (i = j + d); 256 entries each
@@ -238,7 +239,7 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
           const int jb = e >> 8, ib = jb + d, r = (e >> 4) & 15, c = e & 15;
           float s = 0.f;
           for (int kb = jb; kb < ib; ++kb)
-            for (int u = 0; u < 16; ++u) s += sA[(16 * ib + r) * L + 16 * kb + u] * xb(kb, jb, u, c);
+            for (int u = 0; u < 16; ++u) s += sA[(16 * ib + r) * LA + 16 * kb + u] * xb(kb, jb, u, c);
           tv[n] = s;
         }
       }
@@ -255,7 +256,7 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
         if (e < (4 - d) * 256) {
           const int jb = e >> 8, ib = jb + d, r = (e >> 4) & 15, c = e & 15;
           float s = 0.f;
-          for (int u = 0; u <= r; ++u) s += sA[(16 * ib + r) * L + 16 * ib + u] * sT[(jb * 16 + u) * 16 + c];
+          for (int u = 0; u <= r; ++u) s += sA[(16 * ib + r) * LA + 16 * ib + u] * sT[(jb * 16 + u) * 16 + c];
           sXo[((ib * (ib - 1) / 2 + jb) * 16 + r) * 16 + c] = -s;
         }
       }
@@ -266,12 +267,15 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
       const int e = e0 + tid;
       const int blk = e >> 8, r = (e >> 4) & 15, c = e & 15;
       const int ib = blk < 1 ? 1 : (blk < 3 ? 2 : 3), jb = blk - ib * (ib - 1) / 2;
-      sA[(16 * ib + r) * L + 16 * jb + c] = sXo[e];
+      sA[(16 * ib + r) * LA + 16 * jb + c] = sXo[e];
     }
   }
   __syncthreads();
 #pragma unroll
-  for (int e0 = 0; e0 < L * L; e0 += kThreads) rc[R::AI + e0 + tid] = sA[e0 + tid];
+  for (int e0 = 0; e0 < L * L; e0 += kThreads) {
+    const int e = e0 + tid;
+    rc[R::AI + e] = sA[(e / L) * LA + e % L];
+  }
   if (tid < DK) rc[R::GM + tid] = sgam[tid];
   // q -> Qg, b k -> E, k -> KG (G_L: row L-1 of G)
 #pragma unroll
@@ -292,7 +296,7 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
   // W = Ai E over G (dead)
   for (int tile = wave; tile < 4 * NT; tile += 4) {
     const int tt = tile / NT, it = tile % NT;
-    const f32x4 acc = mm_tile(sA + 16 * tt * L, L, 1, sbk + 16 * it, P, 1, L, gq, m);
+    const f32x4 acc = mm_tile(sA + 16 * tt * LA, LA, 1, sbk + 16 * it, P, 1, L, gq, m);
 #pragma unroll
     for (int e = 0; e < 4; ++e) sG[(16 * tt + 4 * gq + e) * P + 16 * it + m] = acc[e];
   }
@@ -300,7 +304,10 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
   // Aqk back from the record into the E slot (E is dead once W is formed)
   float* sAq = sbk;
 #pragma unroll
-  for (int e0 = 0; e0 < L * L; e0 += kThreads) sAq[e0 + tid] = rc[R::AQ + e0 + tid];
+  for (int e0 = 0; e0 < L * L; e0 += kThreads) {
+    const int e = e0 + tid;
+    sAq[(e / L) * LA + e % L] = rc[R::AQ + e];
+  }
   // A = diag(gamma) - KG^T W, also stored transposed; KG^T[i][t] is sk[t P + i]
   for (int tile = wave; tile < NT * NT; tile += 4) {
     const int ia = tile / NT, ja = tile % NT;
@@ -317,7 +324,7 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
   // KA = KG^T Ai
   for (int tile = wave; tile < NT * 4; tile += 4) {
     const int ia = tile / 4, ua = tile % 4;
-    const f32x4 acc = mm_tile(sk + 16 * ia, 1, P, sA + 16 * ua, L, 1, L, gq, m);
+    const f32x4 acc = mm_tile(sk + 16 * ia, 1, P, sA + 16 * ua, LA, 1, L, gq, m);
 #pragma unroll
     for (int e = 0; e < 4; ++e) rc[R::KA + static_cast<long>(16 * ia + 4 * gq + e) * L + 16 * ua + m] = acc[e];
   }
@@ -325,7 +332,7 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
   // QP = Qg - Aqk W, also stored transposed
   for (int tile = wave; tile < 4 * NT; tile += 4) {
     const int tt = tile / NT, it = tile % NT;
-    f32x4 acc = mm_tile(sAq + 16 * tt * L, L, 1, sG + 16 * it, P, 1, L, gq, m);
+    f32x4 acc = mm_tile(sAq + 16 * tt * LA, LA, 1, sG + 16 * it, P, 1, L, gq, m);
     const int i = 16 * it + m;
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
