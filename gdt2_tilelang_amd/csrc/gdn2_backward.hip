@@ -75,6 +75,29 @@ __device__ __forceinline__ size_t key_index(int bi, long S, long t, int HK, int 
   return ((static_cast<size_t>(bi) * S + t) * HK + hk) * DK + i;
 }
 
+// Inclusive prefix sums down the L rows of nch channels (x[t pitch + c]),
+// forward or from the last row back, on all kThreads threads: each channel's
+// rows split into kThreads / nch consecutive segments, scanned locally, then
+// offset by the totals of the segments before them (tmp: kThreads floats).
+// Ends with a barrier.
+template <bool REVERSE>
+__device__ __forceinline__ void rows_scan(float* x, int pitch, int nch, float* tmp) {
+  const int tpc = kThreads / nch, rpt = L / tpc;
+  const int c = threadIdx.x % nch, seg = threadIdx.x / nch;
+  auto row = [&](int j) { const int t = seg * rpt + j; return REVERSE ? L - 1 - t : t; };
+  float run = 0.f;
+  for (int j = 0; j < rpt; ++j) {
+    run += x[row(j) * pitch + c];
+    x[row(j) * pitch + c] = run;
+  }
+  tmp[seg * nch + c] = run;
+  __syncthreads();
+  float off = 0.f;
+  for (int q2 = 0; q2 < seg; ++q2) off += tmp[q2 * nch + c];
+  for (int j = 0; j < rpt; ++j) x[row(j) * pitch + c] += off;
+  __syncthreads();
+}
+
 // ---------------------------------------------------------------- kernel 1
 // One 16 x 16 tile of C = A B on v_mfma_f32_16x16x4_f32 with both operands in
 // LDS: A[r][k] at a[r as + k ak], B[k][c] at b[k bk + c bc], K a multiple of
@@ -130,15 +153,8 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
     sG[t * P + i] = gv;
   }
   __syncthreads();
-  if (tid < DK) {
-    float run = 0.f;
-    for (int t = 0; t < L; ++t) {
-      run += sG[t * P + tid];
-      sG[t * P + tid] = run;
-    }
-    sgam[tid] = __expf(run);
-  }
-  __syncthreads();
+  rows_scan<false>(sG, P, DK, sT);
+  if (tid < DK) sgam[tid] = __expf(sG[(L - 1) * P + tid]);
 
   // Aqk (to the record) and Akk (to LDS) by 16 x 16 blocks.
   // Below the diagonal blocks (t in block tb, s in an earlier block sb), on
@@ -527,6 +543,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   constexpr int EP = 4 * (KD + 1);    // LDS row pitch of -E and KG (lane groups 33 floats apart)
   __shared__ float sG[L * DK];        // G (log decay cumsum)
   __shared__ float sEn[L * EP], sKG[L * EP];   // -E, KG: row t, lane group gq at gq (KD + 1)
+  __shared__ float sScan[kThreads];
   __shared__ float sS[DK * XP], sdS[DK * XP];
   __shared__ float sdO[L * XP], sY[L * XP], sU[L * XP], sdU[L * XP], sdY[L * XP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
@@ -547,14 +564,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     sG[e] = (t0 + t < S ? 1.f : 0.f) * g[key_index(bi, S, clamp_row(t0 + t, S), HK, hk, DK, i)];
   }
   __syncthreads();
-  if (tid < DK) {
-    float run = 0.f;
-    for (int t = 0; t < L; ++t) {
-      run += sG[t * DK + tid];
-      sG[t * DK + tid] = run;
-    }
-  }
-  __syncthreads();
+  rows_scan<false>(sG, DK, DK, sScan);
   // A operands: -E, KG (LDS); Ai, Ai^T, Aqk^T rows in registers
 #pragma unroll
   for (int e0 = 0; e0 < L * DK; e0 += kThreads) {
@@ -736,6 +746,7 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
   using G = GS<DK>;
   __shared__ float pq[L * PWP], pk[L * PWP], pbk[L * PWP], pG[L * PWP];
   __shared__ float pAq[L * (L + 1)], pAk[L * (L + 1)];
+  __shared__ float pScan[kThreads];
   const int tid = threadIdx.x;
   const int c = blockIdx.x / NB, cb = blockIdx.x % NB;
   const int bh = blockIdx.y, bi = bh / H, h = bh % H, hk = h / (H / HK);
@@ -762,14 +773,7 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
     pAk[t * (L + 1) + s2] = s2 < t ? src[G::AK + e] : 0.f;
   }
   __syncthreads();
-  if (tid < CW) {
-    float run = 0.f;
-    for (int t = 0; t < L; ++t) {
-      run += pG[t * PWP + tid];
-      pG[t * PWP + tid] = run;
-    }
-  }
-  __syncthreads();
+  rows_scan<false>(pG, PWP, CW, pScan);
   // thread: one channel, EPT rows t_r = tp + (kThreads / CW) r. One pass
   // over the partners s serves every row: s <= t_r feeds the row sums, s >= t_r
   // the column sums, each pair's exponent taken in the direction that is <= 0.
@@ -829,14 +833,18 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
     pk[t * PWP + ii] = kgd[r];
   }
   __syncthreads();
-  if (tid < CW) {
-    // d G_L: sum_t KG dKG + gamma dgamma; dg = reverse cumsum of dG
-    float run = __expf(pG[(L - 1) * PWP + tid]) * src[G::GAM + i0 + tid];
-    for (int t = 0; t < L; ++t) run += pk[t * PWP + tid];
+  // d G_L = sum_t KG dKG + gamma dgamma joins the last row, then dg is the
+  // reverse cumsum of dG
+  rows_scan<false>(pk, PWP, CW, pScan);               // pk row L-1: sum_t KG dKG
+  if (tid < CW) pq[(L - 1) * PWP + tid] += pk[(L - 1) * PWP + tid] + __expf(pG[(L - 1) * PWP + tid]) * src[G::GAM + i0 + tid];
+  __syncthreads();
+  rows_scan<true>(pq, PWP, CW, pScan);
+  {
     const size_t plane = static_cast<size_t>(gridDim.y) / H * S * H * DK;
-    for (int t = L - 1; t >= 0; --t) {
-      run += pq[t * PWP + tid];
-      if (t0 + t < S) part[3 * plane + ((static_cast<size_t>(bi) * S + t0 + t) * H + h) * DK + i0 + tid] = run;
+#pragma unroll
+    for (int e0 = 0; e0 < L * CW; e0 += kThreads) {
+      const int e = e0 + tid, t = e / CW, ii = e % CW;
+      if (t0 + t < S) part[3 * plane + ((static_cast<size_t>(bi) * S + t0 + t) * H + h) * DK + i0 + ii] = pq[t * PWP + ii];
     }
   }
 }
