@@ -21,7 +21,7 @@ not part of this package.
 
 from .attention import GDN2Cache, GatedDeltaNet2, gdn2_attention, resolve_backend
 from .config import DEFAULT_KERNEL_CONFIG, GDN2Config, GatedDeltaNet2Config
-from .forward import chunk_gdn2_bwd, chunk_gdn2_fwd, chunk_gdn2_varlen_fwd
+from .forward import chunk_gdn2_bwd, chunk_gdn2_fwd, chunk_gdn2_varlen_bwd, chunk_gdn2_varlen_fwd
 from .inference import gdn2_decode, gdn2_decode_step, gdn2_prefill
 
 __all__ = [
@@ -37,5 +37,6 @@ __all__ = [
     "chunk_gdn2_fwd",
     "chunk_gdn2_varlen_fwd",
     "chunk_gdn2_bwd",
+    "chunk_gdn2_varlen_bwd",
     "resolve_backend",
 ]
