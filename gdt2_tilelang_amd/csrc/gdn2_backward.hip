@@ -774,33 +774,52 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
   }
   __syncthreads();
   rows_scan<false>(pG, PWP, CW, pScan);
-  // thread: one channel, EPT rows t_r = tp + (kThreads / CW) r. One pass
-  // over the partners s serves every row: s <= t_r feeds the row sums, s >= t_r
-  // the column sums, each pair's exponent taken in the direction that is <= 0.
+  // thread: one channel, EPT rows t_r = tp + TS r. One pass over the
+  // partners s serves every row: s < t_r feeds the row sums, s > t_r the
+  // column sums, each pair's exponent taken in the direction that is <= 0.
+  // Partners run in blocks of TS: for block j, rows r < j see only later
+  // partners (column sums), rows r > j only earlier ones (row sums), and
+  // row r = j both, so only the diagonal block carries selects.
   const int ii = tid % CW, tp = tid / CW;
   const int i = i0 + ii;
   constexpr int TS = kThreads / CW;
+  static_assert(TS * EPT == L, "row blocks of TS rows");
+  constexpr float kLog2e = 1.4426950408889634f;
   const float gl = pG[(L - 1) * PWP + ii];
   float gt[EPT], rq[EPT], rk[EPT], cq[EPT], ck[EPT];
 #pragma unroll
   for (int r = 0; r < EPT; ++r) {
-    gt[r] = pG[(tp + TS * r) * PWP + ii];
+    gt[r] = kLog2e * pG[(tp + TS * r) * PWP + ii];
     rq[r] = rk[r] = cq[r] = ck[r] = 0.f;
   }
-#pragma unroll 2
-  for (int s2 = 0; s2 < L; ++s2) {
-    const float gs2 = pG[s2 * PWP + ii], ks = pk[s2 * PWP + ii], qs = pq[s2 * PWP + ii], bks = pbk[s2 * PWP + ii];
 #pragma unroll
-    for (int r = 0; r < EPT; ++r) {
-      const int t = tp + TS * r;
-      // one exponential per pair: P[t][s] (s <= t, row sums) or P[s][t] (s >= t, column sums)
-      const float e = __expf(s2 <= t ? gt[r] - gs2 : gs2 - gt[r]);
-      const float er = s2 <= t ? e * ks : 0.f;
-      const float ec = s2 >= t ? e : 0.f;
-      rq[r] += pAq[t * (L + 1) + s2] * er;
-      rk[r] += pAk[t * (L + 1) + s2] * er;
-      cq[r] += pAq[s2 * (L + 1) + t] * qs * ec;
-      ck[r] += pAk[s2 * (L + 1) + t] * bks * ec;
+  for (int j = 0; j < EPT; ++j) {
+#pragma unroll 2
+    for (int u = 0; u < TS; ++u) {
+      const int s2 = TS * j + u;
+      const float gs2 = kLog2e * pG[s2 * PWP + ii], ks = pk[s2 * PWP + ii], qs = pq[s2 * PWP + ii],
+                  bks = pbk[s2 * PWP + ii];
+#pragma unroll
+      for (int r = 0; r < EPT; ++r) {
+        const int t = tp + TS * r;
+        if (r > j) {              // s < t
+          const float er = __builtin_amdgcn_exp2f(gt[r] - gs2) * ks;
+          rq[r] += pAq[t * (L + 1) + s2] * er;
+          rk[r] += pAk[t * (L + 1) + s2] * er;
+        } else if (r < j) {       // s > t
+          const float ec = __builtin_amdgcn_exp2f(gs2 - gt[r]);
+          cq[r] += pAq[s2 * (L + 1) + t] * ec * qs;
+          ck[r] += pAk[s2 * (L + 1) + t] * ec * bks;
+        } else {                  // same block: masked arrays zero the excluded pairs
+          const float e = __builtin_amdgcn_exp2f(s2 <= t ? gt[r] - gs2 : gs2 - gt[r]);
+          const float er = s2 <= t ? e * ks : 0.f;
+          const float ec = s2 >= t ? e : 0.f;
+          rq[r] += pAq[t * (L + 1) + s2] * er;
+          rk[r] += pAk[t * (L + 1) + s2] * er;
+          cq[r] += pAq[s2 * (L + 1) + t] * qs * ec;
+          ck[r] += pAk[s2 * (L + 1) + t] * bks * ec;
+        }
+      }
     }
   }
   float dG[EPT], kgd[EPT];
@@ -810,7 +829,7 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
     const float qv = pq[t * PWP + ii], kv = pk[t * PWP + ii], bkv = pbk[t * PWP + ii];
     const bool valid = t0 + t < S;
     const float bv = valid ? b[key_index(bi, S, t0 + t, HK, hk, DK, i)] : 0.f;
-    const float ga = __expf(gt[r]), gd = __expf(gl - gt[r]);
+    const float ga = __builtin_amdgcn_exp2f(gt[r]), gd = __builtin_amdgcn_exp2f(kLog2e * gl - gt[r]);
     const float fQg = src[G::QG + t * DK + i], fE = src[G::E + t * DK + i], fKG = src[G::KG + t * DK + i];
     const float dq = scale * (ga * fQg + rq[r]);
     const float dk = bv * ga * fE + scale * cq[r] + bv * rk[r] + ck[r] + gd * fKG;
