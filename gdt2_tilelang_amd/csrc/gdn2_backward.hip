@@ -735,6 +735,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 
 constexpr int PWC = 32;               // channels per pairwise workgroup
 constexpr int PWP = PWC + 1;          // LDS pitch
+constexpr int LQ = L + 4;             // pitch of the L x L arrays (16-byte rows)
 
 template <int DK>
 __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
@@ -745,7 +746,7 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
   constexpr int EPT = L * CW / kThreads;             // elements per thread
   using G = GS<DK>;
   __shared__ float pq[L * PWP], pk[L * PWP], pbk[L * PWP], pG[L * PWP];
-  __shared__ float pAq[L * (L + 1)], pAk[L * (L + 1)];
+  __shared__ __align__(16) float pAq[L * LQ], pAk[L * LQ];   // symmetric: [t][s] = [s][t] = A[max][min]
   __shared__ float pScan[kThreads];
   const int tid = threadIdx.x;
   const int c = blockIdx.x / NB, cb = blockIdx.x % NB;
@@ -767,23 +768,31 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
   }
 #pragma unroll
   for (int e0 = 0; e0 < L * L; e0 += kThreads) {
-    const int e = e0 + tid;   // masked: dAqk on s <= t, dAkk on s < t
+    const int e = e0 + tid;   // masked: dAqk on s <= t, dAkk on s < t; mirrored above the diagonal
     const int t = e / L, s2 = e % L;
-    pAq[t * (L + 1) + s2] = s2 <= t ? src[G::AQ + e] : 0.f;
-    pAk[t * (L + 1) + s2] = s2 < t ? src[G::AK + e] : 0.f;
+    const float aq = src[G::AQ + e], ak = s2 < t ? src[G::AK + e] : 0.f;
+    if (s2 <= t) {
+      pAq[t * LQ + s2] = pAq[s2 * LQ + t] = aq;
+      pAk[t * LQ + s2] = pAk[s2 * LQ + t] = ak;
+    }
   }
   __syncthreads();
   rows_scan<false>(pG, PWP, CW, pScan);
-  // thread: one channel, EPT rows t_r = tp + TS r. One pass over the
-  // partners s serves every row: s < t_r feeds the row sums, s > t_r the
-  // column sums, each pair's exponent taken in the direction that is <= 0.
-  // Partners run in blocks of TS: for block j, rows r < j see only later
-  // partners (column sums), rows r > j only earlier ones (row sums), and
-  // row r = j both, so only the diagonal block carries selects.
+  // thread: one channel, EPT rows t_r = tp + TS r; partners s in blocks j of
+  // TS rows. Row sums take s < t, column sums s > t, the diagonal pair both.
+  // For row r > j (every s of block j earlier than t) the pair factor splits
+  // at the block's last row R = TS j + TS - 1:
+  //   exp(G_t - G_s) = exp(G_t - G_R) exp(G_R - G_s),
+  // and for r < j (every s later than t) at R' = TS j - 1, the last row
+  // before the block: exp(G_s - G_t) = exp(G_s - G_R') exp(G_R' - G_t). Both
+  // factors are <= 1 for a non-positive log decay, so nothing overflows; the
+  // per-partner factor scales the partner's operand once per block and the
+  // per-row factor a block's partial sum, leaving two FMAs per pair. The
+  // diagonal block takes each pair's exponent exactly.
   const int ii = tid % CW, tp = tid / CW;
   const int i = i0 + ii;
   constexpr int TS = kThreads / CW;
-  static_assert(TS * EPT == L, "row blocks of TS rows");
+  static_assert(TS * EPT == L && TS == 8, "row blocks of 8 rows");
   constexpr float kLog2e = 1.4426950408889634f;
   const float gl = pG[(L - 1) * PWP + ii];
   float gt[EPT], rq[EPT], rk[EPT], cq[EPT], ck[EPT];
@@ -792,32 +801,63 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
     gt[r] = kLog2e * pG[(tp + TS * r) * PWP + ii];
     rq[r] = rk[r] = cq[r] = ck[r] = 0.f;
   }
-#pragma unroll
+#pragma unroll 1
   for (int j = 0; j < EPT; ++j) {
-#pragma unroll 2
+    const float gR = kLog2e * pG[(TS * j + TS - 1) * PWP + ii];
+    const float gRc = j > 0 ? kLog2e * pG[(TS * j - 1) * PWP + ii] : 0.f;
+    float gsv[TS], ksv[TS], qsv[TS], bsv[TS], kt[TS], qt[TS], bt[TS];
+#pragma unroll
     for (int u = 0; u < TS; ++u) {
       const int s2 = TS * j + u;
-      const float gs2 = kLog2e * pG[s2 * PWP + ii], ks = pk[s2 * PWP + ii], qs = pq[s2 * PWP + ii],
-                  bks = pbk[s2 * PWP + ii];
+      gsv[u] = kLog2e * pG[s2 * PWP + ii];
+      ksv[u] = pk[s2 * PWP + ii];
+      qsv[u] = pq[s2 * PWP + ii];
+      bsv[u] = pbk[s2 * PWP + ii];
+      kt[u] = j < EPT - 1 ? ksv[u] * __builtin_amdgcn_exp2f(gR - gsv[u]) : 0.f;
+      const float fc = j > 0 ? __builtin_amdgcn_exp2f(gsv[u] - gRc) : 0.f;
+      qt[u] = qsv[u] * fc;
+      bt[u] = bsv[u] * fc;
+    }
 #pragma unroll
-      for (int r = 0; r < EPT; ++r) {
-        const int t = tp + TS * r;
-        if (r > j) {              // s < t
-          const float er = __builtin_amdgcn_exp2f(gt[r] - gs2) * ks;
-          rq[r] += pAq[t * (L + 1) + s2] * er;
-          rk[r] += pAk[t * (L + 1) + s2] * er;
-        } else if (r < j) {       // s > t
-          const float ec = __builtin_amdgcn_exp2f(gs2 - gt[r]);
-          cq[r] += pAq[s2 * (L + 1) + t] * ec * qs;
-          ck[r] += pAk[s2 * (L + 1) + t] * ec * bks;
-        } else {                  // same block: masked arrays zero the excluded pairs
-          const float e = __builtin_amdgcn_exp2f(s2 <= t ? gt[r] - gs2 : gs2 - gt[r]);
-          const float er = s2 <= t ? e * ks : 0.f;
-          const float ec = s2 >= t ? e : 0.f;
-          rq[r] += pAq[t * (L + 1) + s2] * er;
-          rk[r] += pAk[t * (L + 1) + s2] * er;
-          cq[r] += pAq[s2 * (L + 1) + t] * qs * ec;
-          ck[r] += pAk[s2 * (L + 1) + t] * bks * ec;
+    for (int r = 0; r < EPT; ++r) {
+      const int t = tp + TS * r;
+      const f32x4 q0 = *reinterpret_cast<const f32x4*>(pAq + t * LQ + TS * j);
+      const f32x4 q1 = *reinterpret_cast<const f32x4*>(pAq + t * LQ + TS * j + 4);
+      const f32x4 k0 = *reinterpret_cast<const f32x4*>(pAk + t * LQ + TS * j);
+      const f32x4 k1 = *reinterpret_cast<const f32x4*>(pAk + t * LQ + TS * j + 4);
+      const float xq[TS] = {q0[0], q0[1], q0[2], q0[3], q1[0], q1[1], q1[2], q1[3]};
+      const float xk[TS] = {k0[0], k0[1], k0[2], k0[3], k1[0], k1[1], k1[2], k1[3]};
+      if (r > j) {                 // rows: every partner earlier
+        float aq = 0.f, ak = 0.f;
+#pragma unroll
+        for (int u = 0; u < TS; ++u) {
+          aq += xq[u] * kt[u];
+          ak += xk[u] * kt[u];
+        }
+        const float f = __builtin_amdgcn_exp2f(gt[r] - gR);
+        rq[r] += f * aq;
+        rk[r] += f * ak;
+      } else if (r < j) {          // columns: every partner later
+        float aq = 0.f, ak = 0.f;
+#pragma unroll
+        for (int u = 0; u < TS; ++u) {
+          aq += xq[u] * qt[u];
+          ak += xk[u] * bt[u];
+        }
+        const float f = __builtin_amdgcn_exp2f(gRc - gt[r]);
+        cq[r] += f * aq;
+        ck[r] += f * ak;
+      } else {                     // same block: exact exponent per pair
+#pragma unroll
+        for (int u = 0; u < TS; ++u) {
+          const bool row = u <= tp, col = u >= tp;
+          const float e = __builtin_amdgcn_exp2f(row ? gt[r] - gsv[u] : gsv[u] - gt[r]);
+          const float er = row ? e * ksv[u] : 0.f;
+          const float ec = col ? e : 0.f;
+          rq[r] += xq[u] * er;
+          rk[r] += xk[u] * er;
+          cq[r] += xq[u] * qsv[u] * ec;
+          ck[r] += xk[u] * bsv[u] * ec;
         }
       }
     }
