@@ -394,8 +394,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   __shared__ float sZ[L * C::XP];
   const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
   const int g = lane >> 4, m = lane & 15;
-  const int bh = blockIdx.y, bi = bh / H, h = bh % H, hk = h / (H / HK);
-  const int c0 = blockIdx.x * CT;
+  // XCD-aware block -> (head, tile) map (workgroups are dealt round-robin to
+  // 8 XCDs): every tile of the value heads that share a key head, hence a
+  // record stream, lands on one XCD and shares its L2.
+  const int ntile = DV / CT, rep = H / HK, per = ntile * rep, BHK = gridDim.x / per;
+  const int lb = blockIdx.x;
+  int bhk, rr;
+  if (BHK % 8 == 0) {
+    bhk = ((lb >> 3) / per) * 8 + (lb & 7);
+    rr = (lb >> 3) % per;
+  } else {
+    bhk = lb / per;
+    rr = lb % per;
+  }
+  const int bi = bhk / HK, hk = bhk % HK, h = hk * rep + rr / ntile, bh = bi * H + h;
+  const int c0 = (rr % ntile) * CT;
   const bool computes = wave * C::TPW < C::TILES;   // DK = 32: two waves hold the tiles
   const float* rbase = rec + static_cast<size_t>(bi * HK + hk) * NC * R::STRIDE;
 #pragma unroll
@@ -749,8 +762,19 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
   __shared__ __align__(16) float pAq[L * LQ], pAk[L * LQ];   // symmetric: [t][s] = [s][t] = A[max][min]
   __shared__ float pScan[kThreads];
   const int tid = threadIdx.x;
-  const int c = blockIdx.x / NB, cb = blockIdx.x % NB;
-  const int bh = blockIdx.y, bi = bh / H, h = bh % H, hk = h / (H / HK);
+  // XCD-aware block -> (chunk, channel block) map (workgroups are dealt
+  // round-robin to 8 XCDs): the NB channel blocks of one (head, chunk) share
+  // its dAqk / dAkk through one XCD's L2.
+  const int units = gridDim.x / NB, lb = blockIdx.x;
+  int u, cb;
+  if (units % 8 == 0) {
+    u = ((lb >> 3) / NB) * 8 + (lb & 7);
+    cb = (lb >> 3) % NB;
+  } else {
+    u = lb / NB;
+    cb = lb % NB;
+  }
+  const int c = u % NC, bh = u / NC, bi = bh / H, h = bh % H, hk = h / (H / HK);
   const long t0 = static_cast<long>(c) * L;
   const float* src = gs + (static_cast<size_t>(bh) * NC + c) * G::STRIDE;
   const int i0 = cb * CW;
@@ -878,7 +902,7 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
     dG[r] = scale * qv * (ga * fQg + rq[r]) + bkv * (ga * fE + rk[r]) - kgd[r] - kv * (scale * cq[r] + ck[r]);
     if (valid) {
       const size_t ix = ((static_cast<size_t>(bi) * S + t0 + t) * H + h) * DK + i;
-      const size_t plane = static_cast<size_t>(gridDim.y) / H * S * H * DK;   // B S H DK
+      const size_t plane = static_cast<size_t>(units / NC) * S * DK;   // B S H DK
       part[ix] = dq;
       part[plane + ix] = dk;
       part[2 * plane + ix] = db;
@@ -899,7 +923,7 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
   __syncthreads();
   rows_scan<true>(pq, PWP, CW, pScan);
   {
-    const size_t plane = static_cast<size_t>(gridDim.y) / H * S * H * DK;
+    const size_t plane = static_cast<size_t>(units / NC) * S * DK;
 #pragma unroll
     for (int e0 = 0; e0 < L * CW; e0 += kThreads) {
       const int e = e0 + tid, t = e / CW, ii = e % CW;
@@ -995,7 +1019,7 @@ hipError_t launch_backward_t(const void* q, const void* k, const void* v, const 
   }
   if (NC == 0) {   // no tokens: the initial-state gradient is the final-state one (or zero)
     if (ds0)
-      hipLaunchKernelGGL((bw::bwd_scan_kernel<DK, true>), dim3(DV / bw::CT, B * H), dim3(bw::kThreads), 0, stream,
+      hipLaunchKernelGGL((bw::bwd_scan_kernel<DK, true>), dim3(DV / bw::CT * B * H), dim3(bw::kThreads), 0, stream,
                          nullptr, nullptr, nullptr, dht, nullptr, ds0, H, HK, DV, S, 0);
     return hipGetLastError();
   }
@@ -1030,14 +1054,14 @@ hipError_t launch_backward_t(const void* q, const void* k, const void* v, const 
 
   hipLaunchKernelGGL(bw::bwd_local_kernel<DK>, dim3(NC, B * HK), dim3(bw::kThreads), lds1, stream, qf, kf, bf, g,
                      HK, S, NC, scale, rec);
-  hipLaunchKernelGGL((bw::bwd_scan_kernel<DK, false>), dim3(DV / bw::CT, B * H), dim3(bw::kThreads), 0, stream, vf,
+  hipLaunchKernelGGL((bw::bwd_scan_kernel<DK, false>), dim3(DV / bw::CT * B * H), dim3(bw::kThreads), 0, stream, vf,
                      wf, rec, s0, sck, nullptr, H, HK, DV, S, NC);
-  hipLaunchKernelGGL((bw::bwd_scan_kernel<DK, true>), dim3(DV / bw::CT, B * H), dim3(bw::kThreads), 0, stream, of,
+  hipLaunchKernelGGL((bw::bwd_scan_kernel<DK, true>), dim3(DV / bw::CT * B * H), dim3(bw::kThreads), 0, stream, of,
                      nullptr, rec, dht, dsck, ds0, H, HK, DV, S, NC);
   hipLaunchKernelGGL(bw::bwd_gradmm_kernel<DK>, dim3(NC, B * H), dim3(bw::kThreads), 0, stream, kf, vf, g, bf, wf, dt,
                      of, rec, sck, dsck, dv, dw, gsc, H, HK, DV, S, NC);
   constexpr int NB = DK / bw::PWC > 0 ? DK / bw::PWC : 1;
-  hipLaunchKernelGGL(bw::bwd_gradpw_kernel<DK>, dim3(NC * NB, B * H), dim3(bw::kThreads), 0, stream, qf, kf, g, bf,
+  hipLaunchKernelGGL(bw::bwd_gradpw_kernel<DK>, dim3(NC * NB * B * H), dim3(bw::kThreads), 0, stream, qf, kf, g, bf,
                      gsc, part, H, HK, S, NC, scale);
   const long n_key = static_cast<long>(B) * S * HK * DK;
   hipLaunchKernelGGL(bw::bwd_sum_kernel, dim3(static_cast<unsigned>((n_key + bw::kThreads - 1) / bw::kThreads)),

@@ -350,6 +350,7 @@ static int backward_shape(int B, long S, int H, int HK, int DK, int DV) {
   const long NC = (S + gdn2::kBS - 1) / gdn2::kBS;
   // grid dimensions and 32-bit element counts of the fp32 intermediates
   if (NC > 65535 || static_cast<long>(B) * H > 65535) return GDN2_ERR_SHAPE;
+  if (NC * (DK / 32) * B * H > 0x7fffffffL) return GDN2_ERR_SHAPE;   // pairwise pass: one-dimensional grid
   if (static_cast<long>(B) * S * HK * DK > 0x7fffffffL) return GDN2_ERR_SHAPE;
   return 0;
 }
