@@ -369,10 +369,11 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
 //   backward: X <- A^T X + QP^T Z, X = dS', Z = dO,  A^T, QP^T from the record
 // X (DK x 16) and Z (L x 16) live in LDS; wave w owns the 16-row output tiles
 // TPW w .., its A-operand rows come straight from the record into registers
-// (the next chunk's requested while the current one is applied). The k index
-// of lane group g = l / 16 runs over its own contiguous quarter of each
-// matrix's columns, so those rows load as 16-byte vectors; the B operand
-// follows the same order.
+// (the next chunk's requested while the current one is applied). Lane group
+// g = l / 16 takes k = 16 q + 4 g + e (q-th load, element e), so a load
+// instruction reads 64 contiguous bytes of each of its 16 rows (the address
+// unit pays per cache line an instruction touches); the B operand follows the
+// same order.
 template <int DK>
 struct ScanCfg {
   static constexpr int TILES = DK / 16;                     // output row tiles
@@ -409,7 +410,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   }
   const int bi = bhk / HK, hk = bhk % HK, h = hk * rep + rr / ntile, bh = bi * H + h;
   const int c0 = (rr % ntile) * CT;
-  const bool computes = wave * C::TPW < C::TILES;   // DK = 32: two waves hold the tiles
+  const bool computes = C::TILES >= 4 || wave * C::TPW < C::TILES;   // DK = 32: two waves hold the tiles
   const float* rbase = rec + static_cast<size_t>(bi * HK + hk) * NC * R::STRIDE;
 #pragma unroll
   for (int e0 = 0; e0 < DK * CT; e0 += kThreads) {
@@ -426,12 +427,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
     for (int r = 0; r < C::TPW; ++r) {
       const int row = 16 * (wave * C::TPW + r) + m;
-      const f32x4* pa = reinterpret_cast<const f32x4*>(rc + M1 + static_cast<long>(row) * DK + g * C::KA_);
-      const f32x4* pz = reinterpret_cast<const f32x4*>(rc + M2 + static_cast<long>(row) * L + g * C::KZ);
+      const f32x4* pa = reinterpret_cast<const f32x4*>(rc + M1 + static_cast<long>(row) * DK + 4 * g);
+      const f32x4* pz = reinterpret_cast<const f32x4*>(rc + M2 + static_cast<long>(row) * L + 4 * g);
 #pragma unroll
-      for (int q = 0; q < C::KA_ / 4; ++q) aA[r][q] = pa[q];
+      for (int q = 0; q < C::KA_ / 4; ++q) aA[r][q] = pa[4 * q];
 #pragma unroll
-      for (int q = 0; q < C::KZ / 4; ++q) aZ[r][q] = pz[q];
+      for (int q = 0; q < C::KZ / 4; ++q) aZ[r][q] = pz[4 * q];
     }
   };
   constexpr int NT = L * CT / kThreads;
@@ -457,9 +458,10 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
       const int e = tid + n * kThreads;
       sZ[(e / CT) * C::XP + e % CT] = pk1[n] * (BACK ? p1[n] : p1[n] * p2[n]);
     }
-    if (step + 1 < NC) {
-      fetch_m(chunk_of(step + 1), nA, nZ);
-      fetch_z(chunk_of(step + 1));
+    {                            // the token values first: the next step's staging waits only for them;
+      const int nx = chunk_of(step + 1 < NC ? step + 1 : step);   // unconditional (the last step re-reads its own)
+      fetch_z(nx);
+      fetch_m(nx, nA, nZ);
     }
     float* out = ck + (static_cast<size_t>(bh) * NC + c) * DK * DV;
     #pragma unroll
@@ -478,13 +480,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
         for (int q = 0; q < C::KA_ / 4; ++q)
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(aA[r][q][e], sX[(g * C::KA_ + 4 * q + e) * C::XP + m],
+            acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(aA[r][q][e], sX[(16 * q + 4 * g + e) * C::XP + m],
                                                           acc[r], 0, 0, 0);
 #pragma unroll
         for (int q = 0; q < C::KZ / 4; ++q)
 #pragma unroll
           for (int e = 0; e < 4; ++e)
-            acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(aZ[r][q][e], sZ[(g * C::KZ + 4 * q + e) * C::XP + m],
+            acc[r] = __builtin_amdgcn_mfma_f32_16x16x4f32(aZ[r][q][e], sZ[(16 * q + 4 * g + e) * C::XP + m],
                                                           acc[r], 0, 0, 0);
       }
     }
@@ -497,8 +499,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     }
   };
   if (NC > 0) {
-    fetch_m(chunk_of(0), aA0, aZ0);
     fetch_z(chunk_of(0));
+    fetch_m(chunk_of(0), aA0, aZ0);
   }
   for (int step = 0; step < NC; step += 2) {
     run(step, aA0, aZ0, aA1, aZ1);
