@@ -31,7 +31,7 @@
 //      DV-contracted sums (fp32 matrix cores); bwd_gradpw_kernel per (b,
 //      value head, chunk, 32 channels): the value head's share of dq, dk, db,
 //      dg
-//   5. bwd_sum_kernel    sums the shares of the value heads of each key head
+//   5. bwd_sum_kernel    (grouped heads only) sums the shares of the value heads of each key head
 //      and rounds to the output dtypes
 // Every exponent taken is G_t - G_s for s <= t (or G_L - G_t, or G_t), <= 0
 // for a non-positive log decay, so nothing overflows whatever the decay.
@@ -755,7 +755,11 @@ constexpr int LQ = L + 4;             // pitch of the L x L arrays (16-byte rows
 template <int DK>
 __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ g, const float* __restrict__ b,
-    const float* __restrict__ gs, float* __restrict__ part, int H, int HK, long S, int NC, float scale) {
+    const float* __restrict__ gs, float* __restrict__ part, void* __restrict__ odq, void* __restrict__ odk,
+    void* __restrict__ odb, float* __restrict__ odg, int dt, int H, int HK, long S, int NC, float scale) {
+  // one value head per key head: the shares are the gradients and go straight
+  // to the outputs (dtype dt, dg fp32); otherwise to the fp32 planes of part
+  const bool direct = H == HK;
   constexpr int NB = DK / PWC > 0 ? DK / PWC : 1;   // channel blocks
   constexpr int CW = DK < PWC ? DK : PWC;            // channels in a block
   constexpr int EPT = L * CW / kThreads;             // elements per thread
@@ -905,9 +909,15 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
     if (valid) {
       const size_t ix = ((static_cast<size_t>(bi) * S + t0 + t) * H + h) * DK + i;
       const size_t plane = static_cast<size_t>(units / NC) * S * DK;   // B S H DK
-      part[ix] = dq;
-      part[plane + ix] = dk;
-      part[2 * plane + ix] = db;
+      if (direct) {
+        store_elem(odq, ix, dt, dq);
+        store_elem(odk, ix, dt, dk);
+        store_elem(odb, ix, dt, db);
+      } else {
+        part[ix] = dq;
+        part[plane + ix] = dk;
+        part[2 * plane + ix] = db;
+      }
     }
   }
   __syncthreads();   // q, k are read no more
@@ -929,7 +939,8 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
 #pragma unroll
     for (int e0 = 0; e0 < L * CW; e0 += kThreads) {
       const int e = e0 + tid, t = e / CW, ii = e % CW;
-      if (t0 + t < S) part[3 * plane + ((static_cast<size_t>(bi) * S + t0 + t) * H + h) * DK + i0 + ii] = pq[t * PWP + ii];
+      const size_t ix = ((static_cast<size_t>(bi) * S + t0 + t) * H + h) * DK + i0 + ii;
+      if (t0 + t < S) (direct ? odg : part + 3 * plane)[ix] = pq[t * PWP + ii];
     }
   }
 }
@@ -1064,7 +1075,8 @@ hipError_t launch_backward_t(const void* q, const void* k, const void* v, const 
                      of, rec, sck, dsck, dv, dw, gsc, H, HK, DV, S, NC);
   constexpr int NB = DK / bw::PWC > 0 ? DK / bw::PWC : 1;
   hipLaunchKernelGGL(bw::bwd_gradpw_kernel<DK>, dim3(NC * NB * B * H), dim3(bw::kThreads), 0, stream, qf, kf, g, bf,
-                     gsc, part, H, HK, S, NC, scale);
+                     gsc, part, dq, dk, db, dg, dt, H, HK, S, NC, scale);
+  if (H == HK) return hipGetLastError();   // the pairwise pass wrote the outputs
   const long n_key = static_cast<long>(B) * S * HK * DK;
   hipLaunchKernelGGL(bw::bwd_sum_kernel, dim3(static_cast<unsigned>((n_key + bw::kThreads - 1) / bw::kThreads)),
                      dim3(bw::kThreads), 0, stream, part, dq, dk, db, dg, dt, n_key, H, HK, DK);
