@@ -950,24 +950,47 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
 // workspace first (one pass), so their loads carry no dtype dispatch (a
 // run-time dtype switch around a load makes the compiler wait for each load
 // inside its branch).
-__global__ __launch_bounds__(kThreads) void bwd_widen_kernel(const void* __restrict__ src, int dt,
-                                                             float* __restrict__ dst, long n) {
-  const long i0 = (static_cast<long>(blockIdx.x) * kThreads + threadIdx.x) * 4;
-  if (i0 + 4 <= n && (reinterpret_cast<uintptr_t>(src) & 7) == 0) {
-    if (dt == DT_BF16) {
-      const uint2 r = *reinterpret_cast<const uint2*>(static_cast<const unsigned short*>(src) + i0);
-      *reinterpret_cast<f32x4*>(dst + i0) = f32x4{bf16_lo_f32(r.x), bf16_hi_f32(r.x), bf16_lo_f32(r.y), bf16_hi_f32(r.y)};
-      return;
+struct WidenJobs {                // up to six 16-bit tensors widened in one launch
+  const void* src[6];
+  float* dst[6];
+  long n[6];
+  int dt[6];
+  int first[7];                   // first workgroup of each job; first[njobs] = grid size
+  int njobs;
+};
+constexpr int kWidenPer = 8;      // elements per thread (one 16-byte load)
+
+__global__ __launch_bounds__(kThreads) void bwd_widen_kernel(WidenJobs jobs) {
+  int j = 0;
+  while (j + 1 < jobs.njobs && static_cast<int>(blockIdx.x) >= jobs.first[j + 1]) ++j;
+  const void* src = jobs.src[j];
+  float* dst = jobs.dst[j];
+  const long n = jobs.n[j];
+  const int dt = jobs.dt[j];
+  const long i0 = (static_cast<long>(blockIdx.x - jobs.first[j]) * kThreads + threadIdx.x) * kWidenPer;
+  if (i0 + kWidenPer <= n && (reinterpret_cast<uintptr_t>(src) & 15) == 0) {
+    const uint4 r = *reinterpret_cast<const uint4*>(static_cast<const unsigned short*>(src) + i0);
+    const unsigned int w[4] = {r.x, r.y, r.z, r.w};
+    f32x4 lo, hi;
+#pragma unroll
+    for (int e = 0; e < 2; ++e) {
+      if (dt == DT_BF16) {
+        lo[2 * e] = bf16_lo_f32(w[e]);
+        lo[2 * e + 1] = bf16_hi_f32(w[e]);
+        hi[2 * e] = bf16_lo_f32(w[2 + e]);
+        hi[2 * e + 1] = bf16_hi_f32(w[2 + e]);
+      } else {
+        lo[2 * e] = f16_bits_to_f32(w[e] & 0xffff);
+        lo[2 * e + 1] = f16_bits_to_f32(w[e] >> 16);
+        hi[2 * e] = f16_bits_to_f32(w[2 + e] & 0xffff);
+        hi[2 * e + 1] = f16_bits_to_f32(w[2 + e] >> 16);
+      }
     }
-    if (dt == DT_F16) {
-      const uint2 r = *reinterpret_cast<const uint2*>(static_cast<const unsigned short*>(src) + i0);
-      *reinterpret_cast<f32x4*>(dst + i0) =
-          f32x4{f16_bits_to_f32(r.x & 0xffff), f16_bits_to_f32(r.x >> 16), f16_bits_to_f32(r.y & 0xffff),
-                f16_bits_to_f32(r.y >> 16)};
-      return;
-    }
+    *reinterpret_cast<f32x4*>(dst + i0) = lo;
+    *reinterpret_cast<f32x4*>(dst + i0 + 4) = hi;
+    return;
   }
-  for (long i = i0; i < i0 + 4 && i < n; ++i) dst[i] = load_elem(src, i, dt);
+  for (long i = i0; i < i0 + kWidenPer && i < n; ++i) dst[i] = load_elem(src, i, dt);
 }
 
 // ---------------------------------------------------------------- kernel 5
@@ -1049,13 +1072,20 @@ hipError_t launch_backward_t(const void* q, const void* k, const void* v, const 
   float* gsc = reinterpret_cast<float*>(ws);
   ws += up(static_cast<size_t>(B) * H * NC * bw::GS<DK>::STRIDE * 4);
   const long nk = static_cast<long>(B) * S * HK * DK, nv = static_cast<long>(B) * S * H * DV;
-  // fp32 operands: the inputs themselves when they are fp32, else widened copies
+  // fp32 operands: the inputs themselves when they are fp32, else widened
+  // copies (every 16-bit input in one launch)
+  bw::WidenJobs jobs{};
   auto widen = [&](const void* src, int sdt, long n) -> const float* {
     float* dst = reinterpret_cast<float*>(ws);
     ws += up(static_cast<size_t>(n) * 4);
     if (sdt == DT_F32) return static_cast<const float*>(src);
-    hipLaunchKernelGGL(bw::bwd_widen_kernel, dim3(static_cast<unsigned>((n + 4L * bw::kThreads - 1) / (4L * bw::kThreads))),
-                       dim3(bw::kThreads), 0, stream, src, sdt, dst, n);
+    const int j = jobs.njobs++;
+    jobs.src[j] = src;
+    jobs.dst[j] = dst;
+    jobs.n[j] = n;
+    jobs.dt[j] = sdt;
+    jobs.first[j + 1] = jobs.first[j] + static_cast<int>((n + bw::kWidenPer * bw::kThreads - 1) /
+                                                         (bw::kWidenPer * bw::kThreads));
     return dst;
   };
   const float* qf = widen(q, dt, nk);
@@ -1064,6 +1094,8 @@ hipError_t launch_backward_t(const void* q, const void* k, const void* v, const 
   const float* vf = widen(v, dt, nv);
   const float* wf = widen(w, dt, nv);
   const float* of = widen(dout, do_dt, nv);
+  if (jobs.first[jobs.njobs] > 0)
+    hipLaunchKernelGGL(bw::bwd_widen_kernel, dim3(jobs.first[jobs.njobs]), dim3(bw::kThreads), 0, stream, jobs);
 
   hipLaunchKernelGGL(bw::bwd_local_kernel<DK>, dim3(NC, B * HK), dim3(bw::kThreads), lds1, stream, qf, kf, bf, g,
                      HK, S, NC, scale, rec);
