@@ -412,11 +412,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const int c0 = (rr % ntile) * CT;
   const bool computes = C::TILES >= 4 || wave * C::TPW < C::TILES;   // DK = 32: two waves hold the tiles
   const float* rbase = rec + static_cast<size_t>(bi * HK + hk) * NC * R::STRIDE;
+  auto chunk_of = [&](int step) { return BACK ? NC - 1 - step : step; };
 #pragma unroll
   for (int e0 = 0; e0 < DK * CT; e0 += kThreads) {
     const int e = e0 + tid;
     const int r = e / CT, cl = e % CT;
-    sX[r * C::XP + cl] = init ? init[(static_cast<size_t>(bh) * DK + r) * DV + c0 + cl] : 0.f;
+    const float x = init ? init[(static_cast<size_t>(bh) * DK + r) * DV + c0 + cl] : 0.f;
+    sX[r * C::XP + cl] = x;
+    if (NC > 0) ck[((static_cast<size_t>(bh) * NC + chunk_of(0)) * DK + r) * DV + c0 + cl] = x;   // first chunk's entry value
   }
   // two register sets of A-operand rows: the next chunk's are requested
   // before the current chunk's products are issued
@@ -448,7 +451,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
       p2[n] = BACK ? 0.f : x2[ix];
     }
   };
-  auto chunk_of = [&](int step) { return BACK ? NC - 1 - step : step; };
   auto run = [&](int step, f32x4 (&aA)[C::TPW][C::KA_ / 4], f32x4 (&aZ)[C::TPW][C::KZ / 4],
                  f32x4 (&nA)[C::TPW][C::KA_ / 4], f32x4 (&nZ)[C::TPW][C::KZ / 4]) {
     const int c = chunk_of(step);
@@ -462,13 +464,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
       const int nx = chunk_of(step + 1 < NC ? step + 1 : step);   // unconditional (the last step re-reads its own)
       fetch_z(nx);
       fetch_m(nx, nA, nZ);
-    }
-    float* out = ck + (static_cast<size_t>(bh) * NC + c) * DK * DV;
-    #pragma unroll
-    for (int e0 = 0; e0 < DK * CT; e0 += kThreads) {
-      const int e = e0 + tid;
-      const int r = e / CT, cl = e % CT;
-      out[static_cast<size_t>(r) * DV + c0 + cl] = sX[r * C::XP + cl];
     }
     lds_barrier();
     f32x4 acc[C::TPW];
@@ -496,6 +491,13 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
       for (int r = 0; r < C::TPW; ++r)
 #pragma unroll
         for (int e = 0; e < 4; ++e) sX[(16 * (wave * C::TPW + r) + 4 * g + e) * C::XP + m] = acc[r][e];
+      if (step + 1 < NC) {                      // the next chunk's entry value, from registers
+        float* out = ck + (static_cast<size_t>(bh) * NC + chunk_of(step + 1)) * DK * DV + c0 + m;
+#pragma unroll
+        for (int r = 0; r < C::TPW; ++r)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) out[static_cast<size_t>(16 * (wave * C::TPW + r) + 4 * g + e) * DV] = acc[r][e];
+      }
     }
   };
   if (NC > 0) {
