@@ -80,9 +80,9 @@ __device__ __forceinline__ size_t key_index(int bi, long S, long t, int HK, int 
 // rows split into kThreads / nch consecutive segments, scanned locally, then
 // offset by the totals of the segments before them (tmp: kThreads floats).
 // Ends with a barrier.
-template <bool REVERSE>
+template <bool REVERSE, int NTH = kThreads>
 __device__ __forceinline__ void rows_scan(float* x, int pitch, int nch, float* tmp) {
-  const int tpc = kThreads / nch, rpt = L / tpc;
+  const int tpc = NTH / nch, rpt = L / tpc;
   const int c = threadIdx.x % nch, seg = threadIdx.x / nch;
   auto row = [&](int j) { const int t = seg * rpt + j; return REVERSE ? L - 1 - t : t; };
   float run = 0.f;
@@ -114,16 +114,19 @@ __device__ __forceinline__ f32x4 mm_tile(const float* a, int as, int ak, const f
   return acc;
 }
 
+constexpr int kLocalThreads = 512;   // kernel 1: 8 waves (its LDS admits one workgroup per CU)
 constexpr int LA = L + 2;        // LDS pitch of the L x L arrays of kernel 1 (rows two banks apart)
 template <int DK>
 constexpr int local_lds_floats() { return 3 * L * (DK + 4) + L * (DK + 4 > LA ? DK + 4 : LA) + L * LA + DK + 9 * 256; }
 
 template <int DK>
-__global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __restrict__ q, const float* __restrict__ k,
+__global__ __launch_bounds__(kLocalThreads) void bwd_local_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                              const float* __restrict__ b, const float* __restrict__ g,
                                                              int HK, long S, int NC, float scale,
                                                              float* __restrict__ rec) {
   constexpr int P = DK + 4;
+  constexpr int LT = kLocalThreads, NW = LT / 64;   // threads, waves
+  constexpr int NV = (3 * 256 + LT - 1) / LT;      // inverse entries per thread and round
   using R = Rec<DK>;
   extern __shared__ __align__(16) float sm[];
   float* sq = sm;                 // q, then Qg
@@ -141,7 +144,7 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
   float* rc = rec + (static_cast<size_t>(bhk) * NC + c) * R::STRIDE;
 
 #pragma unroll
-  for (int e0 = 0; e0 < L * DK; e0 += kThreads) {
+  for (int e0 = 0; e0 < L * DK; e0 += LT) {
     const int e = e0 + tid;       // rows past the sequence are zeros (inert)
     const int t = e / DK, i = e % DK;
     const size_t ix = key_index(bi, S, clamp_row(t0 + t, S), HK, hk, DK, i);
@@ -153,7 +156,7 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
     sG[t * P + i] = gv;
   }
   __syncthreads();
-  rows_scan<false>(sG, P, DK, sT);
+  rows_scan<false, LT>(sG, P, DK, sT);
   if (tid < DK) sgam[tid] = __expf(sG[(L - 1) * P + tid]);
 
   // Aqk (to the record) and Akk (to LDS) by 16 x 16 blocks.
@@ -163,7 +166,7 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
   // product over the channels of (q or b k) exp(G_t - G_R) and k exp(G_R - G_s).
   {
     const int lane = tid & 63, wave = tid >> 6, gq = lane >> 4, m = lane & 15;
-    for (int tile = wave; tile < 6; tile += 4) {
+    for (int tile = wave; tile < 6; tile += NW) {
       const int tb = tile < 1 ? 1 : (tile < 3 ? 2 : 3), sb = tile - tb * (tb - 1) / 2;
       const int R = 16 * tb - 1, t = 16 * tb + m, sr = 16 * sb + m;
       f32x4 aq = zero4(), ak = zero4();
@@ -185,17 +188,20 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
     }
     // diagonal blocks exactly: thread (block db, row tl, columns 4 sq4 ..), every
     // exponent taken for s <= t only (exp(-inf) = 0 elsewhere)
-    const int db = tid >> 6, tl = (tid & 63) >> 2, sq4 = tid & 3;
+    constexpr int NJ = 4 * kThreads / LT;    // columns per thread
+    const int db = tid / (LT / 4), tl = (tid % (LT / 4)) / (16 / NJ), sq4 = tid % (16 / NJ);
     const int t = 16 * db + tl;
-    float aq[4] = {0.f, 0.f, 0.f, 0.f}, ak[4] = {0.f, 0.f, 0.f, 0.f};
+    float aq[NJ], ak[NJ];
+#pragma unroll
+    for (int j = 0; j < NJ; ++j) aq[j] = ak[j] = 0.f;
     const float ninf = -__builtin_huge_valf();
     for (int i = 0; i < DK; i += 4) {
       const float4 qt = *reinterpret_cast<const float4*>(&sq[t * P + i]);
       const float4 bt = *reinterpret_cast<const float4*>(&sbk[t * P + i]);
       const float4 gt = *reinterpret_cast<const float4*>(&sG[t * P + i]);
 #pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const int s2 = 16 * db + 4 * sq4 + j;
+      for (int j = 0; j < NJ; ++j) {
+        const int s2 = 16 * db + NJ * sq4 + j;
         const bool in = s2 <= t;
         const float4 ks = *reinterpret_cast<const float4*>(&sk[s2 * P + i]);
         const float4 gs = *reinterpret_cast<const float4*>(&sG[s2 * P + i]);
@@ -206,14 +212,14 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
       }
     }
 #pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      const int s2 = 16 * db + 4 * sq4 + j;
+    for (int j = 0; j < NJ; ++j) {
+      const int s2 = 16 * db + NJ * sq4 + j;
       rc[R::AQ + t * L + s2] = s2 <= t ? scale * aq[j] : 0.f;
       sA[t * LA + s2] = s2 < t ? ak[j] : 0.f;
     }
     // above the diagonal blocks: zeros
 #pragma unroll
-    for (int e0 = 0; e0 < L * L; e0 += kThreads) {
+    for (int e0 = 0; e0 < L * L; e0 += LT) {
       const int e = e0 + tid, r = e / L, c2 = e % L;
       if ((c2 >> 4) > (r >> 4)) {
         rc[R::AQ + e] = 0.f;
@@ -246,11 +252,11 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
     };
     for (int d = 1; d < 4; ++d) {
       // T = sum_{k=j}^{i-1} Akk_ik X_kj for the 4 - d blocks (i = j + d); 256 entries each
-      float tv[3];
+      float tv[NV];
 #pragma unroll
-      for (int n = 0; n < 3; ++n) {
+      for (int n = 0; n < NV; ++n) {
         tv[n] = 0.f;
-        const int e = tid + n * kThreads;
+        const int e = tid + n * LT;
         if (e < (4 - d) * 256) {
           const int jb = e >> 8, ib = jb + d, r = (e >> 4) & 15, c = e & 15;
           float s = 0.f;
@@ -261,14 +267,14 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
       }
       __syncthreads();
 #pragma unroll
-      for (int n = 0; n < 3; ++n) {
-        const int e = tid + n * kThreads;
+      for (int n = 0; n < NV; ++n) {
+        const int e = tid + n * LT;
         if (e < (4 - d) * 256) sT[e] = tv[n];
       }
       __syncthreads();
 #pragma unroll
-      for (int n = 0; n < 3; ++n) {
-        const int e = tid + n * kThreads;
+      for (int n = 0; n < NV; ++n) {
+        const int e = tid + n * LT;
         if (e < (4 - d) * 256) {
           const int jb = e >> 8, ib = jb + d, r = (e >> 4) & 15, c = e & 15;
           float s = 0.f;
@@ -279,7 +285,7 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
       __syncthreads();
     }
     #pragma unroll
-    for (int e0 = 0; e0 < 6 * 256; e0 += kThreads) {
+    for (int e0 = 0; e0 < 6 * 256; e0 += LT) {
       const int e = e0 + tid;
       const int blk = e >> 8, r = (e >> 4) & 15, c = e & 15;
       const int ib = blk < 1 ? 1 : (blk < 3 ? 2 : 3), jb = blk - ib * (ib - 1) / 2;
@@ -288,14 +294,14 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
   }
   __syncthreads();
 #pragma unroll
-  for (int e0 = 0; e0 < L * L; e0 += kThreads) {
+  for (int e0 = 0; e0 < L * L; e0 += LT) {
     const int e = e0 + tid;
     rc[R::AI + e] = sA[(e / L) * LA + e % L];
   }
   if (tid < DK) rc[R::GM + tid] = sgam[tid];
   // q -> Qg, b k -> E, k -> KG (G_L: row L-1 of G)
 #pragma unroll
-  for (int e0 = 0; e0 < L * DK; e0 += kThreads) {
+  for (int e0 = 0; e0 < L * DK; e0 += LT) {
     const int e = e0 + tid;
     const int t = e / DK, i = e % DK;
     const float gt = sG[t * P + i], gl = sG[(L - 1) * P + i];
@@ -310,7 +316,7 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
   const int lane = tid & 63, wave = tid >> 6, gq = lane >> 4, m = lane & 15;
   constexpr int NT = DK / 16;
   // W = Ai E over G (dead)
-  for (int tile = wave; tile < 4 * NT; tile += 4) {
+  for (int tile = wave; tile < 4 * NT; tile += NW) {
     const int tt = tile / NT, it = tile % NT;
     const f32x4 acc = mm_tile(sA + 16 * tt * LA, LA, 1, sbk + 16 * it, P, 1, L, gq, m);
 #pragma unroll
@@ -320,12 +326,12 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
   // Aqk back from the record into the E slot (E is dead once W is formed)
   float* sAq = sbk;
 #pragma unroll
-  for (int e0 = 0; e0 < L * L; e0 += kThreads) {
+  for (int e0 = 0; e0 < L * L; e0 += LT) {
     const int e = e0 + tid;
     sAq[(e / L) * LA + e % L] = rc[R::AQ + e];
   }
   // A = diag(gamma) - KG^T W, also stored transposed; KG^T[i][t] is sk[t P + i]
-  for (int tile = wave; tile < NT * NT; tile += 4) {
+  for (int tile = wave; tile < NT * NT; tile += NW) {
     const int ia = tile / NT, ja = tile % NT;
     f32x4 acc = mm_tile(sk + 16 * ia, 1, P, sG + 16 * ja, P, 1, L, gq, m);
     const int j = 16 * ja + m;
@@ -338,7 +344,7 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
     *reinterpret_cast<f32x4*>(rc + R::AT + static_cast<long>(j) * DK + 16 * ia + 4 * gq) = acc;
   }
   // KA = KG^T Ai
-  for (int tile = wave; tile < NT * 4; tile += 4) {
+  for (int tile = wave; tile < NT * 4; tile += NW) {
     const int ia = tile / 4, ua = tile % 4;
     const f32x4 acc = mm_tile(sk + 16 * ia, 1, P, sA + 16 * ua, LA, 1, L, gq, m);
 #pragma unroll
@@ -346,7 +352,7 @@ __global__ __launch_bounds__(kThreads) void bwd_local_kernel(const float* __rest
   }
   __syncthreads();   // Aqk staged
   // QP = Qg - Aqk W, also stored transposed
-  for (int tile = wave; tile < 4 * NT; tile += 4) {
+  for (int tile = wave; tile < 4 * NT; tile += NW) {
     const int tt = tile / NT, it = tile % NT;
     f32x4 acc = mm_tile(sAq + 16 * tt * LA, LA, 1, sG + 16 * it, P, 1, L, gq, m);
     const int i = 16 * it + m;
@@ -1099,7 +1105,7 @@ hipError_t launch_backward_t(const void* q, const void* k, const void* v, const 
   if (jobs.first[jobs.njobs] > 0)
     hipLaunchKernelGGL(bw::bwd_widen_kernel, dim3(jobs.first[jobs.njobs]), dim3(bw::kThreads), 0, stream, jobs);
 
-  hipLaunchKernelGGL(bw::bwd_local_kernel<DK>, dim3(NC, B * HK), dim3(bw::kThreads), lds1, stream, qf, kf, bf, g,
+  hipLaunchKernelGGL(bw::bwd_local_kernel<DK>, dim3(NC, B * HK), dim3(bw::kLocalThreads), lds1, stream, qf, kf, bf, g,
                      HK, S, NC, scale, rec);
   hipLaunchKernelGGL((bw::bwd_scan_kernel<DK, false>), dim3(DV / bw::CT * B * H), dim3(bw::kThreads), 0, stream, vf,
                      wf, rec, s0, sck, nullptr, H, HK, DV, S, NC);
