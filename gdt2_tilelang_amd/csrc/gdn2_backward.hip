@@ -427,9 +427,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     sX[r * C::XP + cl] = x;
     if (NC > 0) ck[((static_cast<size_t>(bh) * NC + chunk_of(0)) * DK + r) * DV + c0 + cl] = x;   // first chunk's entry value
   }
-  // two register sets of A-operand rows: the next chunk's are requested
-  // before the current chunk's products are issued
-  f32x4 aA0[C::TPW][C::KA_ / 4], aZ0[C::TPW][C::KZ / 4], aA1[C::TPW][C::KA_ / 4], aZ1[C::TPW][C::KZ / 4];
+  // three register sets of A-operand rows: the rows of the chunk two steps
+  // ahead are requested before the current chunk's products are issued
+  f32x4 aA0[C::TPW][C::KA_ / 4], aZ0[C::TPW][C::KZ / 4], aA1[C::TPW][C::KA_ / 4], aZ1[C::TPW][C::KZ / 4], aA2[C::TPW][C::KA_ / 4], aZ2[C::TPW][C::KZ / 4];
   auto fetch_m = [&](int c, f32x4 (&aA)[C::TPW][C::KA_ / 4], f32x4 (&aZ)[C::TPW][C::KZ / 4]) {
     if (!computes) return;
     const float* rc = rbase + static_cast<size_t>(c) * R::STRIDE;
@@ -467,9 +467,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
       sZ[(e / CT) * C::XP + e % CT] = pk1[n] * (BACK ? p1[n] : p1[n] * p2[n]);
     }
     {                            // the token values first: the next step's staging waits only for them;
-      const int nx = chunk_of(step + 1 < NC ? step + 1 : step);   // unconditional (the last step re-reads its own)
-      fetch_z(nx);
-      fetch_m(nx, nA, nZ);
+      fetch_z(chunk_of(step + 1 < NC ? step + 1 : NC - 1));
+      fetch_m(chunk_of(step + 2 < NC ? step + 2 : NC - 1), nA, nZ);
     }
     lds_barrier();
     f32x4 acc[C::TPW];
@@ -509,10 +508,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   if (NC > 0) {
     fetch_z(chunk_of(0));
     fetch_m(chunk_of(0), aA0, aZ0);
+    fetch_m(chunk_of(NC > 1 ? 1 : 0), aA1, aZ1);
   }
-  for (int step = 0; step < NC; step += 2) {
-    run(step, aA0, aZ0, aA1, aZ1);
+  for (int step = 0; step < NC; step += 3) {
+    run(step, aA0, aZ0, aA2, aZ2);
     if (step + 1 < NC) run(step + 1, aA1, aZ1, aA0, aZ0);
+    if (step + 2 < NC) run(step + 2, aA2, aZ2, aA1, aZ1);
   }
   __syncthreads();
   if (fin) {
