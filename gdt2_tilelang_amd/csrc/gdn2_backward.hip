@@ -388,11 +388,15 @@ struct ScanCfg {
   static constexpr int XP = CT + 1;                         // LDS pitch of X and Z rows
 };
 
-template <int DK, bool BACK>
-__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void bwd_scan_kernel(
-    const float* __restrict__ x1, const float* __restrict__ x2, const float* __restrict__ rec,
-    const float* __restrict__ init, float* __restrict__ ck, float* __restrict__ fin, int H, int HK, int DV, long S,
-    int NC) {
+// The scan of one workgroup (block lb of nblk): NBUF register sets of
+// A-operand rows, so the rows of the chunk NBUF - 1 steps ahead are requested
+// before the current chunk's products are issued.
+template <int DK, bool BACK, int NBUF>
+__device__ __forceinline__ void scan_body(const float* __restrict__ x1, const float* __restrict__ x2,
+                                          const float* __restrict__ rec, const float* __restrict__ init,
+                                          float* __restrict__ ck, float* __restrict__ fin, int H, int HK, int DV,
+                                          long S, int NC, int lb, int nblk) {
+  static_assert(NBUF >= 1 && NBUF <= 3, "one to three register sets");
   using R = Rec<DK>;
   using C = ScanCfg<DK>;
   constexpr long M1 = BACK ? R::AT : R::A;
@@ -404,8 +408,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   // XCD-aware block -> (head, tile) map (workgroups are dealt round-robin to
   // 8 XCDs): every tile of the value heads that share a key head, hence a
   // record stream, lands on one XCD and shares its L2.
-  const int ntile = DV / CT, rep = H / HK, per = ntile * rep, BHK = gridDim.x / per;
-  const int lb = blockIdx.x;
+  const int ntile = DV / CT, rep = H / HK, per = ntile * rep, BHK = nblk / per;
   int bhk, rr;
   if (BHK % 8 == 0) {
     bhk = ((lb >> 3) / per) * 8 + (lb & 7);
@@ -427,8 +430,6 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     sX[r * C::XP + cl] = x;
     if (NC > 0) ck[((static_cast<size_t>(bh) * NC + chunk_of(0)) * DK + r) * DV + c0 + cl] = x;   // first chunk's entry value
   }
-  // three register sets of A-operand rows: the rows of the chunk two steps
-  // ahead are requested before the current chunk's products are issued
   f32x4 aA0[C::TPW][C::KA_ / 4], aZ0[C::TPW][C::KZ / 4], aA1[C::TPW][C::KA_ / 4], aZ1[C::TPW][C::KZ / 4], aA2[C::TPW][C::KA_ / 4], aZ2[C::TPW][C::KZ / 4];
   auto fetch_m = [&](int c, f32x4 (&aA)[C::TPW][C::KA_ / 4], f32x4 (&aZ)[C::TPW][C::KZ / 4]) {
     if (!computes) return;
@@ -468,7 +469,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     }
     {                            // the token values first: the next step's staging waits only for them;
       fetch_z(chunk_of(step + 1 < NC ? step + 1 : NC - 1));
-      fetch_m(chunk_of(step + 2 < NC ? step + 2 : NC - 1), nA, nZ);
+      if constexpr (NBUF > 1) fetch_m(chunk_of(step + NBUF - 1 < NC ? step + NBUF - 1 : NC - 1), nA, nZ);
     }
     lds_barrier();
     f32x4 acc[C::TPW];
@@ -490,6 +491,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
                                                           acc[r], 0, 0, 0);
       }
     }
+    if constexpr (NBUF == 1) fetch_m(chunk_of(step + 1 < NC ? step + 1 : NC - 1), nA, nZ);   // nA is aA: read
     lds_barrier();                              // every wave has read X
     if (computes) {
 #pragma unroll
@@ -508,12 +510,21 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   if (NC > 0) {
     fetch_z(chunk_of(0));
     fetch_m(chunk_of(0), aA0, aZ0);
-    fetch_m(chunk_of(NC > 1 ? 1 : 0), aA1, aZ1);
+    if constexpr (NBUF == 3) fetch_m(chunk_of(NC > 1 ? 1 : 0), aA1, aZ1);
   }
-  for (int step = 0; step < NC; step += 3) {
-    run(step, aA0, aZ0, aA2, aZ2);
-    if (step + 1 < NC) run(step + 1, aA1, aZ1, aA0, aZ0);
-    if (step + 2 < NC) run(step + 2, aA2, aZ2, aA1, aZ1);
+  if constexpr (NBUF == 3) {
+    for (int step = 0; step < NC; step += 3) {
+      run(step, aA0, aZ0, aA2, aZ2);
+      if (step + 1 < NC) run(step + 1, aA1, aZ1, aA0, aZ0);
+      if (step + 2 < NC) run(step + 2, aA2, aZ2, aA1, aZ1);
+    }
+  } else if constexpr (NBUF == 2) {
+    for (int step = 0; step < NC; step += 2) {
+      run(step, aA0, aZ0, aA1, aZ1);
+      if (step + 1 < NC) run(step + 1, aA1, aZ1, aA0, aZ0);
+    }
+  } else {
+    for (int step = 0; step < NC; ++step) run(step, aA0, aZ0, aA0, aZ0);
   }
   __syncthreads();
   if (fin) {
@@ -524,6 +535,31 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
       fin[(static_cast<size_t>(bh) * DK + r) * DV + c0 + cl] = sX[r * C::XP + cl];
     }
   }
+}
+
+template <int DK, bool BACK>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void bwd_scan_kernel(
+    const float* __restrict__ x1, const float* __restrict__ x2, const float* __restrict__ rec,
+    const float* __restrict__ init, float* __restrict__ ck, float* __restrict__ fin, int H, int HK, int DV, long S,
+    int NC) {
+  scan_body<DK, BACK, 3>(x1, x2, rec, init, ck, fin, H, HK, DV, S, NC, blockIdx.x, gridDim.x);
+}
+
+// Both scans in one launch: they read only the records and their own inputs,
+// so the first half of the workgroups runs the forward scan and the second
+// half the backward one, and with two waves per SIMD a CU holds one of each,
+// each hiding the other's per-step latency chain.
+template <int DK>
+__global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_scan2_kernel(
+    const float* __restrict__ v, const float* __restrict__ w, const float* __restrict__ dout,
+    const float* __restrict__ rec, const float* __restrict__ s0, const float* __restrict__ dht,
+    float* __restrict__ sck, float* __restrict__ dsck, float* __restrict__ ds0, int H, int HK, int DV, long S,
+    int NC) {
+  const int half = gridDim.x / 2;
+  if (static_cast<int>(blockIdx.x) < half)
+    scan_body<DK, false, 1>(v, w, rec, s0, sck, nullptr, H, HK, DV, S, NC, blockIdx.x, half);
+  else
+    scan_body<DK, true, 1>(dout, nullptr, rec, dht, dsck, ds0, H, HK, DV, S, NC, blockIdx.x - half, half);
 }
 
 // ---------------------------------------------------------------- kernel 4
@@ -1108,10 +1144,8 @@ hipError_t launch_backward_t(const void* q, const void* k, const void* v, const 
 
   hipLaunchKernelGGL(bw::bwd_local_kernel<DK>, dim3(NC, B * HK), dim3(bw::kLocalThreads), lds1, stream, qf, kf, bf, g,
                      HK, S, NC, scale, rec);
-  hipLaunchKernelGGL((bw::bwd_scan_kernel<DK, false>), dim3(DV / bw::CT * B * H), dim3(bw::kThreads), 0, stream, vf,
-                     wf, rec, s0, sck, nullptr, H, HK, DV, S, NC);
-  hipLaunchKernelGGL((bw::bwd_scan_kernel<DK, true>), dim3(DV / bw::CT * B * H), dim3(bw::kThreads), 0, stream, of,
-                     nullptr, rec, dht, dsck, ds0, H, HK, DV, S, NC);
+  hipLaunchKernelGGL(bw::bwd_scan2_kernel<DK>, dim3(2 * (DV / bw::CT) * B * H), dim3(bw::kThreads), 0, stream, vf,
+                     wf, of, rec, s0, dht, sck, dsck, ds0, H, HK, DV, S, NC);
   hipLaunchKernelGGL(bw::bwd_gradmm_kernel<DK>, dim3(NC, B * H), dim3(bw::kThreads), 0, stream, kf, vf, g, bf, wf, dt,
                      of, rec, sck, dsck, dv, dw, gsc, H, HK, DV, S, NC);
   constexpr int NB = DK / bw::PWC > 0 ? DK / bw::PWC : 1;
