@@ -23,16 +23,17 @@
 //
 // Kernels, in order on one stream:
 //   1. bwd_local_kernel  per (b, key head, chunk): A, KA, QP, Ai, Aqk, gamma
-//   2. bwd_scan_kernel<forward>  per (b, value head, 16 columns): the
-//      chunk-entry states S_c, forward over the chunks
-//   3. bwd_scan_kernel<backward> per (b, value head, 16 columns): dS' of every
-//      chunk, backward over the chunks; dS_0 is the initial-state gradient
+//   0. bwd_widen_kernel  fp32 copies of the 16-bit inputs (one launch)
+//   2, 3. bwd_scan2_kernel, both scans in one launch, per (b, value head, 16
+//      columns): the chunk-entry states S_c forward over the chunks, and dS'
+//      of every chunk backward over the chunks (dS_0 is the initial-state
+//      gradient); bwd_scan_kernel is the same scan alone (zero-token calls)
 //   4. bwd_gradmm_kernel per (b, value head, chunk): dv, dw and the
 //      DV-contracted sums (fp32 matrix cores); bwd_gradpw_kernel per (b,
 //      value head, chunk, 32 channels): the value head's share of dq, dk, db,
 //      dg
-//   5. bwd_sum_kernel    (grouped heads only) sums the shares of the value heads of each key head
-//      and rounds to the output dtypes
+//   5. bwd_sum_kernel    (grouped heads only) sums the shares of the value
+//      heads of each key head and rounds to the output dtypes
 // Every exponent taken is G_t - G_s for s <= t (or G_L - G_t, or G_t), <= 0
 // for a non-positive log decay, so nothing overflows whatever the decay.
 #include "gdn2_common.h"
