@@ -338,6 +338,42 @@ def bench_layer(reps=3):
                 timing="eager Python calls, HIP events, best of %d" % reps)
 
 
+def measure_copy_peak(reps=10, nbytes=2 ** 30):
+    """Measured streaming-copy rate of this GPU: a plain device copy of
+    ``nbytes`` (torch ``copy_``, read + write), timed with HIP events; the
+    practical HBM ceiling each roofline fraction is also reported against."""
+    src = torch.ones(nbytes // 4, device="cuda")
+    dst = torch.empty_like(src)
+    for _ in range(3):
+        dst.copy_(src)
+    torch.cuda.synchronize()
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record()
+    for _ in range(reps):
+        dst.copy_(src)
+    e1.record()
+    torch.cuda.synchronize()
+    ms = e0.elapsed_time(e1) / reps
+    del src, dst
+    return {"GBps": round(2 * nbytes / (ms * 1e-3) / 1e9, 1), "bytes_read_plus_written": 2 * nbytes,
+            "us_per_copy": round(ms * 1e3, 1),
+            "how": "torch dst.copy_(src) of 1 GiB fp32, %d copies timed with HIP events" % reps}
+
+
+def decode_sweep(B, ns=(1, 2, 4, 8, 16), copy_gbps=None):
+    """State GB/s over tokens per call, the reference's decode benchmark sweep
+    (bench/bench_decode.py:57, state bytes as its :71), with rotated states."""
+    rows = []
+    for n in ns:
+        r = bench_decode(B, n, calls=64, steps_per_buf_min=1)
+        row = {"n": n, "us_per_call": r["us_per_call"], "us_per_token": round(r["us_per_call"] / n, 3),
+               "state_GBps": r["state_GBps"], "state_frac_of_peak": r["state_frac_of_peak"]}
+        if copy_gbps:
+            row["state_frac_of_measured_copy"] = round(r["state_GBps"] / copy_gbps, 4)
+        rows.append(row)
+    return {"B": B, "H": 16, "DK": 128, "DV": 128, "dtype": "bf16 tokens, fp32 state", "rows": rows}
+
+
 def cpu_model():
     """The host CPU's model string (``/proc/cpuinfo``), or the platform's."""
     try:
@@ -465,6 +501,7 @@ def main():
     ap.add_argument("--layer-only", action="store_true", help="config-4 layer run only (for profilers)")
     ap.add_argument("--no-backward", action="store_true", help="skip the training-backward run")
     ap.add_argument("--backward-only", action="store_true", help="training backward only (for profilers)")
+    ap.add_argument("--decode-sweep-only", action="store_true", help="copy peak + decode n-sweep only")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="three plain 1 GiB device copies (scales rocprofv3 byte counters)")
     args = ap.parse_args()
@@ -477,6 +514,11 @@ def main():
         sys.exit(2)
 
     log(f"device: {torch.cuda.get_device_name()}")
+    if args.decode_sweep_only:
+        copy = measure_copy_peak()
+        log(json.dumps({"hbm_copy": copy, "sweep_B8": decode_sweep(8, copy_gbps=copy["GBps"]),
+                        "sweep_B32": decode_sweep(32, copy_gbps=copy["GBps"])}))
+        return
     if args.copy_calibration:
         src = torch.ones(2 ** 28, device="cuda")          # 1 GiB fp32
         dst = torch.empty_like(src)
@@ -502,6 +544,8 @@ def main():
     if args.prefill_only:
         log(f"prefill {ms_step * 1e3:.1f} us/step (chunk_local {cl_ms * 1e3:.1f}, scan {sc_ms * 1e3:.1f})")
         return
+    copy = measure_copy_peak()
+    copy_gbps = copy["GBps"]
     tokens = B1 * S1
     value = tokens / (ms_step * 1e-3)
     kern_s = (cl_ms + sc_ms) * 1e-3
@@ -531,19 +575,30 @@ def main():
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",
             "frac": round(achieved / HBM_PEAK_GBS, 4),
+            "frac_of_measured_copy": round(achieved / copy_gbps, 4),
+            "hbm_copy_GBps": copy_gbps,
             "traffic": traffic,
+            "traffic_source": "profiles/hbm_traffic_pmc.txt (rocprofv3 --pmc FETCH_SIZE / WRITE_SIZE runs of "
+                              "this bench, committed; not counted in this run)",
             "algorithmic_bytes": ALG_BYTES_PREFILL,
             "kernel_us": {"chunk_local": round(cl_ms * 1e3, 2), "scan": round(sc_ms * 1e3, 2)},
             "gemm_tflops": round(ALG_FLOPS_PREFILL / kern_s / 1e12, 1),
             "gemm_frac_of_bf16_peak": round(ALG_FLOPS_PREFILL / kern_s / 1e12 / BF16_DENSE_TFLOPS, 4),
             "mfma_busy_pmc": read_mfma_busy(),
+            "mfma_busy_source": "profiles/mfma_busy_pmc.txt (rocprofv3 --pmc run of this bench, committed; "
+                                "not counted in this run)",
         },
+        "hbm_copy": copy,
     }
     if not args.no_decode:
         out["decode"] = {
             "config2_decode_step": bench_decode(64, 1, calls=64, steps_per_buf_min=1),
             "config3_decode_multi_n8": bench_decode(32, 8, calls=64, steps_per_buf_min=1),
         }
+        for r in out["decode"].values():
+            r["state_frac_of_measured_copy"] = round(r["state_GBps"] / copy_gbps, 4)
+        out["decode"]["sweep_reference_bench_B8"] = decode_sweep(8, copy_gbps=copy_gbps)
+        out["decode"]["sweep_B32"] = decode_sweep(32, copy_gbps=copy_gbps)
     out["public_prefill"] = bench_public_prefill()
     if not args.no_varlen:
         out["varlen"] = bench_varlen()

@@ -6,7 +6,9 @@ Mirrors the reference's ``gdn2/attention.py``: ``gdn2_attention`` (``:102-164``)
 reference ``state_dict`` loads unchanged.
 
 Backends: ``"auto"`` resolves to ``"hip"`` on a GPU and to ``"torch"``
-elsewhere, like the reference's ``"tilelang"`` policy. The ``"torch"`` backend
+elsewhere, like the reference's ``"tilelang"`` policy. ``"tilelang"``, the
+reference's name for its GPU backend, is accepted and selects ``"hip"``, so a
+reference config that names it explicitly runs the gfx950 kernels. The ``"torch"`` backend
 is the reference package's own CPU path and is not part of this package, so it
 raises ``NotImplementedError`` here. Autograd through ``gdn2_attention`` runs
 the hip backward (``chunk_gdn2_bwd``).
@@ -44,14 +46,18 @@ from .inference import gdn2_decode, gdn2_prefill
 
 __all__ = ["gdn2_attention", "GatedDeltaNet2", "GDN2Cache", "resolve_backend"]
 
-_BACKENDS = ("auto", "hip", "torch")
+_BACKENDS = ("auto", "hip", "tilelang", "torch")
+# the reference's GPU backend name (gdn2/attention.py:41) selects this package's GPU path
+_GPU_ALIASES = {"tilelang": "hip"}
 
 
 def resolve_backend(backend: str, on_cuda: bool, needs_grad: bool) -> str:
     """Turn ``"auto"`` into a concrete backend, or validate an explicit one.
 
     Returns ``"hip"`` or ``"torch"``; raises ``ValueError`` for an unknown name
-    or for ``"hip"`` without a GPU.
+    or for a GPU backend (``"hip"``, or the reference's ``"tilelang"``, which
+    maps to it) without a GPU, as the reference does for ``"tilelang"``
+    (``gdn2/attention.py:44-61``).
     """
     if backend not in _BACKENDS:
         raise ValueError(f"unknown backend {backend!r}; expected one of {_BACKENDS}")
@@ -59,7 +65,7 @@ def resolve_backend(backend: str, on_cuda: bool, needs_grad: bool) -> str:
         return "hip" if on_cuda else "torch"
     if backend != "torch" and not on_cuda:
         raise ValueError(f"backend {backend!r} requires a CUDA device")
-    return backend
+    return _GPU_ALIASES.get(backend, backend)
 
 
 class _GDN2Function(torch.autograd.Function):

@@ -27,8 +27,12 @@ class GDN2Config:
         sub_chunk_size: ``BC``; must divide ``chunk_size`` with >= 2 blocks.
         block_DK, block_DV, threads, num_stages: accepted for compatibility
             with the reference's TileLang tiling; unused by the hip kernels.
-        state_dtype: dtype of the carried state; the hip kernels keep fp32.
-        backend: ``"auto"``, ``"hip"`` or ``"torch"``.
+        state_dtype: dtype of the state a call accepts and returns (fp32,
+            bf16 or fp16): an initial state is first cast to it and the final
+            state is returned in it, as in the reference; the kernels carry
+            the state in fp32 between those two casts.
+        backend: ``"auto"``, ``"hip"``, ``"tilelang"`` (the reference's GPU
+            backend name; selects ``"hip"``) or ``"torch"``.
         backward: accepted for compatibility; autograd runs the hip backward.
         output_dtype: dtype of ``o``; ``None`` means ``v.dtype``.
     """

@@ -1092,12 +1092,10 @@ hipError_t launch_backward_t(const void* q, const void* k, const void* v, const 
                              float* ds0, void* workspace, int B, int H, int HK, int DV, long S, hipStream_t stream) {
   const int NC = static_cast<int>((S + bw::L - 1) / bw::L);
   constexpr int lds1 = bw::local_lds_floats<DK>() * 4;
-  static bool configured = false;   // attributes set once per process (same values always)
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&bw::bwd_local_kernel<DK>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, lds1);
+  static std::atomic<unsigned long long> lds_set{0};   // per device
+  {
+    const hipError_t e = set_dyn_lds_once(reinterpret_cast<const void*>(&bw::bwd_local_kernel<DK>), lds1, lds_set);
     if (e != hipSuccess) return e;
-    configured = true;
   }
   if (NC == 0) {   // no tokens: the initial-state gradient is the final-state one (or zero)
     if (ds0)

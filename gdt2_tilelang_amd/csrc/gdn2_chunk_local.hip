@@ -426,13 +426,10 @@ static hipError_t launch_chunk_local_t(const void* q, const void* k, const void*
                                        int B, int H, long s_alloc, long t0, int NC, long n_tok,
                                        float scale, unsigned short* ws, Varlen vl, hipStream_t stream) {
   constexpr size_t smem = ChunkSmem<DK>::BYTES;
-  static bool configured = false;   // attribute set once per process (same value always)
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_local_kernel<DK, IN_DT>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       static_cast<int>(smem));
+  static std::atomic<unsigned long long> lds_set{0};   // per device
+  {
+    const hipError_t e = set_dyn_lds_once(reinterpret_cast<const void*>(&chunk_local_kernel<DK, IN_DT>), static_cast<int>(smem), lds_set);
     if (e != hipSuccess) return e;
-    configured = true;
   }
   const unsigned grid = static_cast<unsigned>(B) * H * NC;
   hipLaunchKernelGGL((chunk_local_kernel<DK, IN_DT>), dim3(grid), dim3(256), smem, stream, q, k,

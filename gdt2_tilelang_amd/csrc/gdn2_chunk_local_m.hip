@@ -1094,12 +1094,10 @@ static hipError_t launch_chunk_pair_t(const void* q, const void* k, const void* 
                                       long s_alloc, long t0, int NP, long n_tok, float scale, unsigned short* ws,
                                       hipStream_t stream) {
   constexpr int smem = clp::LDS_BYTES;
-  static bool configured = false;   // attribute set once per process (same value always)
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_pair_kernel<IN_DT>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  static std::atomic<unsigned long long> lds_set{0};   // per device
+  {
+    const hipError_t e = set_dyn_lds_once(reinterpret_cast<const void*>(&chunk_pair_kernel<IN_DT>), smem, lds_set);
     if (e != hipSuccess) return e;
-    configured = true;
   }
   const int npairs = B * H * NP;
   const unsigned grid = static_cast<unsigned>(npairs);
@@ -1123,12 +1121,10 @@ static hipError_t launch_chunk_local_m_t(const void* q, const void* k, const voi
                                          int B, int H, long s_alloc, long t0, int NC, long n_tok,
                                          float scale, unsigned short* ws, Varlen vl, hipStream_t stream) {
   constexpr int smem = clm::LDS_BYTES;
-  static bool configured = false;   // attribute set once per process (same value always)
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&chunk_local_m_kernel<IN_DT>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  static std::atomic<unsigned long long> lds_set{0};   // per device
+  {
+    const hipError_t e = set_dyn_lds_once(reinterpret_cast<const void*>(&chunk_local_m_kernel<IN_DT>), smem, lds_set);
     if (e != hipSuccess) return e;
-    configured = true;
   }
   const unsigned grid = static_cast<unsigned>(B) * H * NC;
   hipLaunchKernelGGL((chunk_local_m_kernel<IN_DT>), dim3(grid), dim3(256), smem, stream, q, k, b, g,

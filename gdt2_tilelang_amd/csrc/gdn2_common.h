@@ -15,6 +15,8 @@
 #include <hip/hip_runtime.h>
 #include <stdint.h>
 
+#include <atomic>
+
 namespace gdn2 {
 
 typedef __bf16 bf16x8 __attribute__((ext_vector_type(8)));
@@ -186,5 +188,20 @@ __device__ __forceinline__ void f16x8_to_bf16_hilo(const uint4& raw, bf16x8& hi,
 }
 
 __device__ __forceinline__ float fast_exp2(float x) { return __builtin_amdgcn_exp2f(x); }
+
+// Raises a kernel's dynamic-LDS limit once per device. The attribute belongs
+// to the current device, so "done" is a bit per device id (ids past 63 set it
+// on every call); two threads that race both set the same value, which is
+// harmless, and the bit is published only after a successful call.
+inline hipError_t set_dyn_lds_once(const void* fn, int bytes, std::atomic<unsigned long long>& done) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return e;
+  const unsigned long long bit = dev < 64 ? 1ull << dev : 0ull;
+  if (bit && (done.load(std::memory_order_acquire) & bit)) return hipSuccess;
+  e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, bytes);
+  if (e == hipSuccess && bit) done.fetch_or(bit, std::memory_order_release);
+  return e;
+}
 
 }  // namespace gdn2

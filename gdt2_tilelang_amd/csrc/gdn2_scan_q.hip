@@ -396,12 +396,10 @@ static hipError_t launch_scan_q_t(const void* v, const void* w, const unsigned s
                                   float* s_out, void* o, int B, int H, int HK, int DV, long s_alloc, long t0, int NC,
                                   long n_tok, hipStream_t stream) {
   constexpr int smem = sizeof(sq::Smem);
-  static bool configured = false;   // attribute set once per process (same value always)
-  if (!configured) {
-    hipError_t e = hipFuncSetAttribute(reinterpret_cast<const void*>(&scan_q_kernel<IN_DT, OUT_DT>),
-                                       hipFuncAttributeMaxDynamicSharedMemorySize, smem);
+  static std::atomic<unsigned long long> lds_set{0};   // per device
+  {
+    const hipError_t e = set_dyn_lds_once(reinterpret_cast<const void*>(&scan_q_kernel<IN_DT, OUT_DT>), smem, lds_set);
     if (e != hipSuccess) return e;
-    configured = true;
   }
   const unsigned grid = static_cast<unsigned>(B) * H * (DV / sq::DVT);
   hipLaunchKernelGGL((scan_q_kernel<IN_DT, OUT_DT>), dim3(grid), dim3(sq::kThreads), smem, stream, v, w, ws, s_in,

@@ -136,8 +136,13 @@ def test_backend_policy():
     assert resolve_backend("torch", on_cuda=True, needs_grad=False) == "torch"
     with pytest.raises(ValueError, match="requires a CUDA device"):
         resolve_backend("hip", on_cuda=False, needs_grad=False)
+    # the reference's GPU backend name selects the hip kernels (gdn2/attention.py:41)
+    assert resolve_backend("tilelang", on_cuda=True, needs_grad=False) == "hip"
+    assert resolve_backend("tilelang", on_cuda=True, needs_grad=True) == "hip"
+    with pytest.raises(ValueError, match="requires a CUDA device"):
+        resolve_backend("tilelang", on_cuda=False, needs_grad=False)
     with pytest.raises(ValueError, match="unknown backend"):
-        resolve_backend("tilelang", on_cuda=True, needs_grad=False)
+        resolve_backend("triton", on_cuda=True, needs_grad=False)
 
 
 def test_cpu_tensors_fail_loudly():
