@@ -28,7 +28,7 @@ bool dtype_ok(int dt) { return dt == GDN2_DTYPE_F32 || dt == GDN2_DTYPE_BF16 || 
 
 long record_elems(int DK) {
   if (DK == 64) return gdn2::ChunkLayout<64>::STRIDE;
-  if (DK == 128) return gdn2::ChunkLayoutM<128>::STRIDE;
+  if (DK == 128) return gdn2::ChunkLayoutE<128>::STRIDE;
   return 0;
 }
 

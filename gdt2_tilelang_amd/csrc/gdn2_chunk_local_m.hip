@@ -257,7 +257,7 @@ __device__ __forceinline__ void clm_chunk(
     unsigned char* __restrict__ smem, const int tid, const int mode, ClmIn<IN_DT>& in, int nvalid, float scale,
     unsigned short* __restrict__ rec, PairRegs& po) {
   using namespace clm;
-  using L = ChunkLayoutM<DK>;
+  using LE = ChunkLayoutE<DK>;
   using LP = ChunkLayoutP;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
@@ -385,7 +385,7 @@ __device__ __forceinline__ void clm_chunk(
     sFac[3 * DK + c] = pr * ise;
     sFac[4 * DK + c] = fast_exp2(gla - ben) * isk;
     if (mode == CLM_SINGLE) {
-      if (rb == 0) reinterpret_cast<float*>(rec + L::GL_OFF)[c] = fast_exp2(gla);   // gamma_last
+      if (rb == 0) reinterpret_cast<float*>(rec + LE::GL_OFF)[c] = fast_exp2(gla);   // gamma_last
     } else {
       po.gl[h2] = gla;
     }
@@ -688,6 +688,16 @@ __device__ __forceinline__ void clm_chunk(
         for (int kk = 0; kk < 2; ++kk) acc = mfma16(ait[m][kk], bk[kk], acc);
         kaq[c2][m] = pack_f16x4(acc, u);
       }
+      if (mode == CLM_SINGLE) {
+        // lane (lr, lq) holds KA[16nn + lr][16m + 4lq ..+3]: in accumulator k
+        // order that is lane (lr, lq) of fragment (nn, m / 2), elements
+        // 4 (m % 2) .. +3, so each lane stores its own 16 bytes
+#pragma unroll
+        for (int kt = 0; kt < 2; ++kt) {
+          const uint2 lo = kaq[c2][2 * kt], hi = kaq[c2][2 * kt + 1];
+          *reinterpret_cast<uint4*>(rec + LE::ka_frag(nn, kt) + lane * 8) = make_uint4(lo.x, lo.y, hi.x, hi.y);
+        }
+      }
       if (mode == CLM_PAIR_A) {
         // KA_a with the operands swapped: rows c = 16 nn + 4lq .., column t = 16m + lr
 #pragma unroll
@@ -706,12 +716,14 @@ __device__ __forceinline__ void clm_chunk(
   for (int m = 0; m < 4; ++m)
     *reinterpret_cast<uint2*>(&sMozF[(rb * 2 + (m >> 1)) * kFrag + quad_in_frag(m, lr, lq)]) =
         m <= rb ? mozq[m] : make_uint2(0u, 0u);
+  if (mode != CLM_SINGLE) {   // KA fragments for the M product of the pair combine
 #pragma unroll
-  for (int c2 = 0; c2 < 2; ++c2)
+    for (int c2 = 0; c2 < 2; ++c2)
 #pragma unroll
-    for (int m = 0; m < 4; ++m)
-      *reinterpret_cast<uint2*>(&sKaF[((2 * rb + c2) * 2 + (m >> 1)) * kFrag + quad_in_frag(m, lr, lq)]) =
-          kaq[c2][m];
+      for (int m = 0; m < 4; ++m)
+        *reinterpret_cast<uint2*>(&sKaF[((2 * rb + c2) * 2 + (m >> 1)) * kFrag + quad_in_frag(m, lr, lq)]) =
+            kaq[c2][m];
+  }
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) *reinterpret_cast<uint4*>(&sQg[row * KHP + 32 * kk + 8 * lq]) = qg16[kk];
   __syncthreads();   // #9
@@ -720,12 +732,9 @@ __device__ __forceinline__ void clm_chunk(
   {
     const uint4* src = reinterpret_cast<const uint4*>(sMozF);
     if (mode == CLM_SINGLE) {
-      uint4* dm = reinterpret_cast<uint4*>(rec + L::MOZ_OFF);
-      uint4* dk = reinterpret_cast<uint4*>(rec + L::KA_OFF);
+      uint4* dm = reinterpret_cast<uint4*>(rec + LE::MOZ_OFF);
 #pragma unroll
       for (int it = 0; it < 2; ++it) dm[tid + 256 * it] = src[tid + 256 * it];
-#pragma unroll
-      for (int it = 0; it < 4; ++it) dk[tid + 256 * it] = src[512 + tid + 256 * it];
     } else if (mode == CLM_PAIR_A) {
       // MOZ_a: the pair's MOZ row blocks 0-3, same fragment order
       uint4* dm = reinterpret_cast<uint4*>(rec + LP::MOZ_OFF);
@@ -755,7 +764,23 @@ __device__ __forceinline__ void clm_chunk(
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
       et[c2][kk] = *reinterpret_cast<const uint4*>(&sEt[(32 * rb + 16 * c2 + lr) * TTP + 32 * kk + 8 * lq]);
-  {
+  if (mode == CLM_SINGLE) {
+    // E fragments (token row block rb, accumulator k order over channels): the
+    // selection product of an E^T fragment (rows = channels 16 cb .., k =
+    // tokens 32 (rb / 2) ..) picks tokens 16 rb .. and leaves lane (lr, lq)
+    // E[16 rb + lr][16 cb + 4lq ..+3], elements 4 (cb % 2) .. of fragment (rb, cb / 2)
+    const uint4 sel = select_b(rb & 1, lr, lq);
+#pragma unroll
+    for (int kk = 0; kk < 4; ++kk) {
+      uint2 h[2];
+#pragma unroll
+      for (int hh = 0; hh < 2; ++hh) {
+        const uint4 a = *reinterpret_cast<const uint4*>(&sEt[(32 * kk + 16 * hh + lr) * TTP + 32 * (rb >> 1) + 8 * lq]);
+        h[hh] = pack_f16x4(mfma16(a, sel, zero4()), 1.f);
+      }
+      *reinterpret_cast<uint4*>(rec + LE::e_frag(rb, kk) + lane * 8) = make_uint4(h[0].x, h[0].y, h[1].x, h[1].y);
+    }
+  } else {
     const float u = se * sc_ka / sc_m;
 #pragma unroll
     for (int nn = 0; nn < 8; ++nn) {
@@ -775,10 +800,7 @@ __device__ __forceinline__ void clm_chunk(
 #pragma unroll
           for (int kk = 0; kk < 2; ++kk) acc = mfma16(et[c2][kk], bk[kk], acc);
           // M^T block (m = 2 rb + c2, nn): M[16nn + lr][32 rb + 16 c2 + 4lq ..]
-          if (mode == CLM_SINGLE)
-            *reinterpret_cast<uint2*>(rec + L::m_frag(nn, rb) + quad_in_frag(c2, lr, lq)) = pack_f16x4(acc, u);
-          else
-            po.mq[c2][nn] = pack_f16x4(acc, u);
+          po.mq[c2][nn] = pack_f16x4(acc, u);
         }
       }
     }
@@ -805,7 +827,7 @@ __device__ __forceinline__ void clm_chunk(
         v[2] = f16_bits_to_f32(static_cast<unsigned short>(qraw.y & 0xffffu)) * sqg - acc[2] * u;
         v[3] = f16_bits_to_f32(static_cast<unsigned short>(qraw.y >> 16)) * sqg - acc[3] * u;
         if (mode == CLM_SINGLE)
-          *reinterpret_cast<uint2*>(rec + L::qp_frag(nn, rb) + quad_in_frag(c2, lr, lq)) = pack_f16x4(v, iqp);
+          *reinterpret_cast<uint2*>(rec + LE::qp_frag(nn, rb) + quad_in_frag(c2, lr, lq)) = pack_f16x4(v, iqp);
         else if (mode == CLM_PAIR_A)
           *reinterpret_cast<uint2*>(rec + LP::qp_frag(nn, rb) + quad_in_frag(c2, lr, lq)) = pack_f16x4(v, iqp);
         else
@@ -815,11 +837,11 @@ __device__ __forceinline__ void clm_chunk(
   }
   if (mode == CLM_SINGLE) {
     if (tid == 0) {
-      float* sc = reinterpret_cast<float*>(rec + L::SC_OFF);
-      sc[SCM_M] = sc_m;
-      sc[SCM_KA] = sc_ka;
-      sc[SCM_QP] = sc_qp;
-      sc[SCM_MOZ] = sc_moz;
+      float* sc = reinterpret_cast<float*>(rec + LE::SC_OFF);
+      sc[SCE_E] = se;
+      sc[SCE_KA] = sc_ka;
+      sc[SCE_QP] = sc_qp;
+      sc[SCE_MOZ] = sc_moz;
     }
   } else {
     po.sc[SCM_M] = sc_m;
@@ -834,7 +856,7 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
     const void* __restrict__ qp, const void* __restrict__ kp, const void* __restrict__ bp,
     const float* __restrict__ g, int H, long s_alloc, long t0, int NC, long n_tok, float scale,
     unsigned short* __restrict__ ws, Varlen vl) {
-  using L = ChunkLayoutM<clm::DK>;
+  using L = ChunkLayoutE<clm::DK>;
   extern __shared__ __align__(16) unsigned char smem[];
   // workgroups run chunk-major from the last chunk back, so the records the scan
   // reads first (chunk 0 of every head) are written last and are still in the

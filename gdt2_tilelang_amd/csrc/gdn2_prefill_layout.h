@@ -96,6 +96,59 @@ struct ChunkLayoutM {
 
 static_assert((ChunkLayoutM<128>::STRIDE * 2) % 256 == 0, "record must keep 256-byte alignment");
 
+// Factored transition record (DK = 128). With Y = Z - E S (the chunk's
+// tokens against the entering state) the scan needs
+//
+//   S <- diag(gamma_last) S + KA Y        o = QP S + MOZ Z
+//
+// (the transition form above with M = KA E applied as its two factors), so
+// the record holds E [64 x DK] in place of M [DK x DK]: 22% fewer bytes to
+// write, and to fetch per scan workgroup and chunk.
+//
+// Two of the matrices are contracted against values that the scan holds in
+// MFMA accumulator order: E against S (state rows) and KA against Y (tokens).
+// Their fragments take the k index in "accumulator order": within a 32-wide k
+// step, lane group g = lane / 16, element j holds
+//
+//   k = 4 g + j (j < 4),   k = 16 + 4 g + (j - 4) (j >= 4),
+//
+// which are exactly the rows that lane (lr, g) holds of two consecutive
+// 16-row accumulator blocks (rows 4g .. 4g+3 of each). A product's
+// accumulators then serve as the next product's B operand in place. QP and
+// MOZ keep the natural k order (lane group g holds k = 8g .. 8g+7).
+//
+//   E   [4 m][DK/32 kk]   rows = token,     k = state row (acc. order) / SC[0]
+//   KA  [DK/16 m][2 kk]   rows = state row, k = token (acc. order)     / SC[1]
+//   QP  [4 m][DK/32 kk]   rows = token,     k = state row              / SC[2]
+//   MOZ [4 m][2 kk]       rows = token,     k = token                  / SC[3]
+//   GL  [DK] fp32 gamma_last;  SC [8] fp32
+//
+// E and KA are adjacent, so the scan's state stage reads one contiguous
+// 32 KiB block per chunk.
+enum RecordScaleE : int { SCE_E = 0, SCE_KA = 1, SCE_QP = 2, SCE_MOZ = 3 };
+
+template <int DK>
+struct ChunkLayoutE {
+  static constexpr int KT = DK / 32;
+  static constexpr int MT = DK / 16;
+  static constexpr long E_OFF = 0;
+  static constexpr long KA_OFF = E_OFF + 4L * KT * kFrag;
+  static constexpr long QP_OFF = KA_OFF + static_cast<long>(MT) * 2 * kFrag;
+  static constexpr long MOZ_OFF = QP_OFF + 4L * KT * kFrag;
+  static constexpr long GL_OFF = MOZ_OFF + 4L * 2 * kFrag;
+  static constexpr long SC_OFF = GL_OFF + 2L * DK;
+  static constexpr long STRIDE = ((SC_OFF + 2L * 8) + 127) / 128 * 128;   // 256-byte records
+  static constexpr int STATE_FRAGS = 4 * KT + MT * 2;                      // E and KA
+
+  __host__ __device__ static constexpr long e_frag(int m, int kk) { return E_OFF + (m * KT + kk) * kFrag; }
+  __host__ __device__ static constexpr long ka_frag(int m, int kk) { return KA_OFF + (m * 2 + kk) * kFrag; }
+  __host__ __device__ static constexpr long qp_frag(int m, int kk) { return QP_OFF + (m * KT + kk) * kFrag; }
+  __host__ __device__ static constexpr long moz_frag(int m, int kk) { return MOZ_OFF + (m * 2 + kk) * kFrag; }
+};
+
+static_assert((ChunkLayoutE<128>::STRIDE * 2) % 256 == 0, "record must keep 256-byte alignment");
+static_assert(ChunkLayoutE<128>::STRIDE * 2 == 58112, "factored record size");
+
 // Pair record (DK = 128): the transition of two consecutive 64-token chunks a, b
 // as one 128-token step of the scan, in the same form
 //
@@ -155,7 +208,7 @@ static_assert((ChunkLayoutP::STRIDE * 2) % 256 == 0, "record must keep 256-byte 
 constexpr long kPairMaxKeyHeads = 16;
 constexpr long kPairMinChunks = 32;
 inline bool use_pair_records(int B, int HK, int DK, long n_tokens, bool varlen) {
-  return !varlen && DK == 128 && static_cast<long>(B) * HK <= kPairMaxKeyHeads &&
+  return false && !varlen && DK == 128 && static_cast<long>(B) * HK <= kPairMaxKeyHeads &&
          (n_tokens + kBS - 1) / kBS >= kPairMinChunks;
 }
 

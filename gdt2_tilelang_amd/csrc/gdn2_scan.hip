@@ -583,7 +583,7 @@ int scan_nt_for(int B, int H, int DV) {
   return 1;
 }
 
-hipError_t launch_scan_m(const void* v, const void* w, int in_dt, const unsigned short* ws, const float* s_in,
+hipError_t launch_scan_e(const void* v, const void* w, int in_dt, const unsigned short* ws, const float* s_in,
                          float* s_out, void* o, int out_dt, int B, int H, int HK, int DV, long s_alloc, long t0,
                          int NC, long n_tok, Varlen vl, hipStream_t stream);
 
@@ -600,7 +600,7 @@ hipError_t launch_scan(const void* v, const void* w, int in_dt, const unsigned s
     return launch_scan_p(v, w, in_dt, ws, s_in, s_out, o, out_dt, B, H, HK, DV, s_alloc, t0, (NC + 1) / 2, n_tok,
                          stream);
   if (DK == 128)
-    return launch_scan_m(v, w, in_dt, ws, s_in, s_out, o, out_dt, B, H, HK, DV, s_alloc, t0, NC, n_tok, vl, stream);
+    return launch_scan_e(v, w, in_dt, ws, s_in, s_out, o, out_dt, B, H, HK, DV, s_alloc, t0, NC, n_tok, vl, stream);
   const int nt = scan_nt_for(B, H, DV);
 #define GDN2_SCAN_CASE(DKV, NTV, DTV, ODV)                                                     \
   if (DK == DKV && nt == NTV && in_dt == DTV && out_dt == ODV)                                 \
