@@ -16,22 +16,30 @@
 // state is the B operand of E S straight from the registers, and Y (the
 // accumulators of E S) the B operand of KA Y: the chain of a chunk is two
 // products and two fp16 roundings inside one wave, with no LDS round trip and
-// no barrier between them. Wave roles:
+// no barrier between them. (One wave's products and VALU work issue in order:
+// ~22 clocks per product and ~4.6 per VALU instruction on this part, so the
+// state wave's step is the scan's critical path. Splitting the tile's rows
+// over two waves that swap partial products through LDS with flag handshakes
+// measured slower: the two swaps per chunk cost more than the halved work.)
+// Wave roles:
 //   wave 0      the state: Y = Z - E S, S <- gamma S + KA Y; hands S to the
-//               output waves through LDS as fp16 (one buffer per parity);
-//   wave 1      stages Z = w * v of the next chunk (fp32 for the state wave,
-//               fp16 for the output) from registers fetched two chunks ahead,
-//               and stores the previous chunk's o rows from LDS;
-//   waves 2-3   output row blocks 2u, 2u + 1: QP S + MOZ Z, to LDS;
-//   waves 4-7   copy the E and KA fragments, gamma_last and the scales of
-//               chunk c + 2 into a three-slot LDS ring (loads issued two chunks
-//               before their LDS stores), so the state wave reads its
-//               operands from LDS and issues no global loads.
+//               output waves through LDS as fp16 (one buffer per parity).
+//               It also stores the previous chunk's o tile from LDS to HBM
+//               (it issues no global loads, and a wave's stores and loads
+//               retire in order);
+//   waves 1-2   stage Z = w * v of the next chunk (fp32 for the state wave,
+//               fp16 for the output), 32 tokens each, from registers fetched
+//               two chunks ahead;
+//   waves 3, 5-7  output row block m: QP S + MOZ Z, to LDS;
+//   wave 4      copies the E and KA fragments, gamma_last and the scales of
+//               chunk c + 3 into a four-slot LDS ring with direct-to-LDS
+//               loads, so the state wave reads its operands from LDS and
+//               issues no global loads.
 // One __syncthreads per chunk.
 //
-// fp16 operands carry power-of-two scales: the record's one per matrix; S, Y
-// and Z one per column (largest entry in [2^14, 2^15)), undone on the fp32
-// accumulators.
+// fp16 operands carry power-of-two scales: the record's one per matrix; S and Y
+// one per column, Z one per column and 32 tokens (largest entry in
+// [2^14, 2^15)), undone on the fp32 accumulators.
 //
 // All global accesses go through buffer resources whose range is the call's
 // tokens (or one record): out-of-range loads return 0 and out-of-range stores
@@ -237,6 +245,30 @@ __global__ __launch_bounds__(sce::kThreads) void scan_e_kernel(
     };
     read_e(sm.rec[0]);
     read_g(sm.rec[0]);
+    // The o tile of the previous chunk goes from LDS (where the output waves
+    // left it) to HBM from this wave, which issues no global loads: a wave's
+    // stores and loads retire in order, so in a loading wave each store's
+    // write-back would hold up the next wait for its loads.
+    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
+        static_cast<char*>(o) + tok_base * DV * OS, 0, static_cast<int>(n_tok * H * DV * OS), kBufWord3);
+    constexpr int RU = DVT * OS / 16;               // 16-byte units per token row; RU per lane
+    int ooff[RU];
+#pragma unroll
+    for (int it = 0; it < RU; ++it) {
+      const int e = lane + 64 * it;
+      ooff[it] = (((e / RU) * H + h) * DV + d0) * OS + 16 * (e % RU);
+    }
+    const int ochunk = kBS * H * DV * OS;
+    u32x4 otile[RU];
+    auto read_o = [&](int b) {
+#pragma unroll
+      for (int it = 0; it < RU; ++it) otile[it] = *reinterpret_cast<const u32x4*>(&sm.o[b][(lane + 64 * it) * 16]);
+    };
+    auto store_o = [&](int nc) {
+#pragma unroll
+      for (int it = 0; it < RU; ++it)
+        __builtin_amdgcn_raw_buffer_store_b128(otile[it], ro, ooff[it] + nc * ochunk, 0, 0);
+    };
 
     loop([&](auto parity, int nc) {
       constexpr int ph = decltype(parity)::value;
@@ -254,6 +286,7 @@ __global__ __launch_bounds__(sce::kThreads) void scan_e_kernel(
       f32x4 Zc[4];
 #pragma unroll
       for (int m = 0; m < 4; ++m) Zc[m] = *reinterpret_cast<const f32x4*>(&sm.zf[ph][lr * ZFP + 16 * m + 4 * lq]);
+      if (nc > 0) read_o(ph ^ 1);                    // the previous chunk's o tile
       __builtin_amdgcn_sched_barrier(0);
       // X = E S (token rows 16 m + 4 lq + e)
       f32x4 X[4];
@@ -322,9 +355,12 @@ __global__ __launch_bounds__(sce::kThreads) void scan_e_kernel(
       read_e(sm.rec[(nc + 1) % kSlots]);
       read_g(sm.rec[(nc + 1) % kSlots]);
       pack_state(ph ^ 1, mxs);
+      if (nc > 0) store_o(nc - 1);
       __syncthreads();
     });
 
+    read_o((NC - 1) & 1);
+    store_o(NC - 1);
 #pragma unroll
     for (int m = 0; m < 8; ++m)
 #pragma unroll
@@ -333,8 +369,11 @@ __global__ __launch_bounds__(sce::kThreads) void scan_e_kernel(
         s_out[(static_cast<size_t>(bh) * DK + row) * DV + d0 + lr] = S[m][e];
       }
   } else if (wave == 1 || wave == 2) {
-    // ---------------- Z staging and o stores (wave 1 + u: tokens 32u .. 32u + 31) ---------
+    // ---------------- Z staging (wave 1 + u: tokens 32 u .. 32 u + 31) ---------------------
     // lane e = (token, column quad): tokens 32 u + lane / 4 + 16 it, columns 4 (lane % 4) ..
+    // These waves issue loads only (the o stores are the state wave's): a wave's
+    // stores and loads retire in order, so a store's write-back would hold up the
+    // wait for the prefetched v and w behind it.
     const int u = wave - 1;
     constexpr int ZQ = 2;
     using RawT = typename std::conditional<IN_DT == DT_F32, u32x4, u32x2v>::type;
@@ -408,25 +447,6 @@ __global__ __launch_bounds__(sce::kThreads) void scan_e_kernel(
         if (lane < 4) sm.zinv[zb][col][u] = inv;
       }
     };
-    const __amdgpu_buffer_rsrc_t ro = __builtin_amdgcn_make_buffer_rsrc(
-        static_cast<char*>(o) + tok_base * DV * OS, 0, static_cast<int>(n_tok * H * DV * OS), kBufWord3);
-    constexpr int RU = DVT * OS / 16;               // 16-byte units per token row
-    constexpr int OQ = 32 * RU / 64;                // units per lane
-    int ooff[OQ];
-#pragma unroll
-    for (int it = 0; it < OQ; ++it) {
-      const int e = lane + 64 * it;
-      ooff[it] = (((32 * u + e / RU) * H + h) * DV + d0) * OS + 16 * (e % RU);
-    }
-    const int ochunk = kBS * H * DV * OS;
-    auto flush_o = [&](int b, int nc) {
-      const int cb = nc * ochunk;
-#pragma unroll
-      for (int it = 0; it < OQ; ++it) {
-        const u32x4 x = *reinterpret_cast<const u32x4*>(&sm.o[b][(32 * u * RU + lane + 64 * it) * 16]);
-        __builtin_amdgcn_raw_buffer_store_b128(x, ro, ooff[it] + cb, 0, 0);
-      }
-    };
     fetch_z(0, 0);
     fetch_z(1, 1);
     put_z(0, 0);
@@ -434,14 +454,11 @@ __global__ __launch_bounds__(sce::kThreads) void scan_e_kernel(
     __syncthreads();
     loop([&](auto parity, int nc) {
       constexpr int ph = decltype(parity)::value;
-      // Z of chunk nc + 1 (fetched two steps ago), then the fetch for nc + 3; this
-      // wave issues no other loads, so the wait is for those alone
+      // Z of chunk nc + 1 (fetched two steps ago), then the fetch for nc + 3
       put_z(ph ^ 1, ph ^ 1);
       fetch_z(ph ^ 1, nc + 3);
-      if (nc > 0) flush_o(ph ^ 1, nc - 1);
       __syncthreads();
     });
-    flush_o((NC - 1) & 1, NC - 1);
   } else if (wave != 4) {
     // ---------------- output: row block m (waves 3, 5, 6, 7) -----------------------------
     const int m = wave == 3 ? 0 : wave - 4;
