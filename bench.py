@@ -570,7 +570,7 @@ def main():
                    "arithmetic": "bf16 and fp16 MFMA (hi/lo splits where precision needs it), fp32 accumulate"},
         "roofline": {
             "bound": "hbm",
-            "kernel": "prefill step = gdn2 chunk_local_m_kernel + scan_m_kernel (DK=128 transition form)",
+            "kernel": "prefill step = gdn2 chunk_local_m_kernel + scan_e_kernel (DK=128 factored transition records)",
             "achieved": round(achieved, 1),
             "peak": HBM_PEAK_GBS,
             "unit": "GB/s",

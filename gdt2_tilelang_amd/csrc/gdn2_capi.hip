@@ -81,8 +81,6 @@ size_t gdn2_hip_prefill_workspace_bytes(int B, int HK, int DK, long n_tokens) {
   const long rec = record_elems(DK);
   if (rec == 0 || B < 1 || HK < 1 || n_tokens < 0) return 0;
   const long nc = (n_tokens + gdn2::kBS - 1) / gdn2::kBS;
-  if (gdn2::use_pair_records(B, HK, DK, n_tokens, false))
-    return static_cast<size_t>(B) * HK * ((nc + 1) / 2) * gdn2::ChunkLayoutP::STRIDE * 2;
   return static_cast<size_t>(B) * HK * nc * rec * 2;
 }
 

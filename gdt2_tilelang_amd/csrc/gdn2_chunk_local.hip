@@ -441,16 +441,10 @@ hipError_t launch_chunk_local_m(const void* q, const void* k, const void* b, con
                                 int in_dt, int B, int H, long s_alloc, long t0, int NC, long n_tok,
                                 float scale, unsigned short* ws, Varlen vl, hipStream_t stream);
 
-hipError_t launch_chunk_pair(const void* q, const void* k, const void* b, const float* g, int in_dt, int B, int H,
-                             long s_alloc, long t0, int NP, long n_tok, float scale, unsigned short* ws,
-                             hipStream_t stream);
-
 hipError_t launch_chunk_local(const void* q, const void* k, const void* b, const float* g,
                               int in_dt, int B, int H, int DK, long s_alloc, long t0, int NC,
                               long n_tok, float scale, unsigned short* ws, Varlen vl, hipStream_t stream) {
-  if (use_pair_records(B, H, DK, n_tok, vl.cu != nullptr))
-    return launch_chunk_pair(q, k, b, g, in_dt, B, H, s_alloc, t0, (NC + 1) / 2, n_tok, scale, ws, stream);
-  // DK = 128 writes the transition-form record (gdn2_chunk_local_m.hip); DK = 64 this one.
+  // DK = 128 writes the factored transition record (gdn2_chunk_local_m.hip); DK = 64 this one.
   if (DK == 128) return launch_chunk_local_m(q, k, b, g, in_dt, B, H, s_alloc, t0, NC, n_tok, scale, ws, vl, stream);
 #define GDN2_CL_CASE(DKV, DTV)                                                             \
   if (DK == DKV && in_dt == DTV)                                                           \

@@ -1,6 +1,6 @@
 // GDN-2 prefill, stage 1 for DK = 128: the chunk-local work of one 64-token
-// chunk, producing the transition-form record (gdn2_prefill_layout.h:
-// ChunkLayoutM) that the scan consumes with one state product per chunk.
+// chunk, producing the factored transition record (gdn2_prefill_layout.h:
+// ChunkLayoutE) that the scan consumes with two short products per chunk.
 //
 // Maths (reference gdn2/forward.py:65-535 -- cumsum, intra-diag, inter-blocks,
 // solve, wy -- followed by the products the reference's scan would form per
@@ -9,7 +9,7 @@
 //   Aqk[t][s] = scale sum_c q_tc k_sc 2^(G_tc - G_sc)   (s <= t)
 //   Akk[t][s] =       sum_c b_tc k_tc k_sc 2^(G_tc - G_sc)  (s < t)
 //   Ai = (I + Akk)^-1,  E = b k 2^G,  KG = k 2^(G_last - G),  Qg = scale q 2^G
-//   MOZ = Aqk Ai,  KA = KG^T Ai,  M = KA E,  QP = Qg - MOZ E.
+//   MOZ = Aqk Ai,  KA = KG^T Ai,  QP = Qg - MOZ E,  and E itself.
 //
 // Layout: one 256-thread workgroup per chunk, wave w owns token rows
 // 16w .. 16w+15 and all 128 channels; lane (lr, lq) holds row 16w + lr and
@@ -35,8 +35,10 @@
 //
 // The record products contract over tokens; they are formed transposed
 // (C^T = B^T A^T) so that each lane's accumulator holds four consecutive
-// columns of one row of C, which is a half of an A-operand fragment row: the
-// fragments are written with 8-byte stores and no further transpose.
+// columns of one row of C: half of an A-operand fragment row in natural k
+// order (QP, MOZ: 8-byte stores), or, for KA and E, whose k index the record
+// keeps in accumulator order, the lane's own half of its own fragment (one
+// 16-byte store per lane, no transpose).
 #include "gdn2_common.h"
 #include "gdn2_prefill_layout.h"
 
@@ -64,9 +66,8 @@ constexpr int AQ_OFF = KGT_OFF + DK * TTP * 2;       // fp16 [64 t][72]: Aqk (ro
 constexpr int AKK_OFF = AQ_OFF + 64 * TTP * 2;       // fp32 Akk tiles (row-major)
 constexpr int LDS_BYTES = AKK_OFF + NPAIR * TF * 4;
 constexpr int MOZF_OFF = KGT_OFF;                    // MOZ fragments [4][2], over KG^T (dead after KA)
-constexpr int KAF_OFF = KGT_OFF + 8 * 1024;          // KA fragments [8][2]
 static_assert(XT_OFF + NPAIR * TF * 4 <= ET_OFF, "Ai tiles overlap E^T");
-static_assert(KAF_OFF + 16 * 1024 <= AKK_OFF, "fragment staging overlaps Akk");
+static_assert(MOZF_OFF + 8 * 1024 <= AKK_OFF, "fragment staging overlaps Akk");
 static_assert(LDS_BYTES <= 81920, "two workgroups per CU");
 // Per-wave channel tables, live from barrier #1 through the end of phase A (in
 // the Akk tiles' space, first written in phase B): the block sum t and the
@@ -187,23 +188,6 @@ __device__ __forceinline__ int quad_in_frag(int m, int lr, int lq) {
 
 }  // namespace clm
 
-// What the chunk body writes where: a chunk record (CLM_SINGLE), or the parts of
-// a pair record that pass through unchanged, the rest left in registers for
-// the pair combine (CLM_PAIR_A: the first chunk of the pair, CLM_PAIR_B: the second).
-enum ClmMode : int { CLM_SINGLE = 0, CLM_PAIR_A = 1, CLM_PAIR_B = 2 };
-
-// A pair half's results for the combine (lane quads of packed fp16, each at
-// the chunk's own scale):
-//   PAIR_B: mq[c2][nn] = M_b[16nn + lr][32rb + 16c2 + 4lq ..]   qq[c2][nn] = QP_b[16nn + lr][32rb + 16c2 + 4lq ..]
-//   PAIR_A: mq[c2][nn] = M_a[16nn + 4lq ..][32rb + 16c2 + lr]   qq[c2][m]  = KA_a[32rb + 16c2 + 4lq ..][16m + lr]
-// gl: G_last (log2) of channels lane, lane + 64 (wave 0); sc: SCM_M .. SCM_MOZ.
-struct PairRegs {
-  uint2 mq[2][8];
-  uint2 qq[2][4];
-  float gl[2];
-  float sc[4];
-};
-
 // A chunk's inputs for one lane: row 16 rb + lr of its wave's block, channels
 // 32kk + 8lq .. +7 of g (fp32) and q, k, b (storage format).
 template <int IN_DT>
@@ -254,11 +238,10 @@ __device__ __forceinline__ void clm_load(ClmIn<IN_DT>& in, const int tid, const 
 // from inputs loaded by clm_load. Rows past nvalid are zeros.
 template <int IN_DT>
 __device__ __forceinline__ void clm_chunk(
-    unsigned char* __restrict__ smem, const int tid, const int mode, ClmIn<IN_DT>& in, int nvalid, float scale,
-    unsigned short* __restrict__ rec, PairRegs& po) {
+    unsigned char* __restrict__ smem, const int tid, ClmIn<IN_DT>& in, int nvalid, float scale,
+    unsigned short* __restrict__ rec) {
   using namespace clm;
   using LE = ChunkLayoutE<DK>;
-  using LP = ChunkLayoutP;
   const int lane = tid & 63;
   const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
   const int lr = lane & 15;
@@ -274,7 +257,6 @@ __device__ __forceinline__ void clm_chunk(
   unsigned short* sAq = reinterpret_cast<unsigned short*>(smem + AQ_OFF);
   float* sAkk = reinterpret_cast<float*>(smem + AKK_OFF);
   unsigned short* sMozF = reinterpret_cast<unsigned short*>(smem + MOZF_OFF);
-  unsigned short* sKaF = reinterpret_cast<unsigned short*>(smem + KAF_OFF);
 
   const int row = 16 * rb + lr;
   auto& G = in.G;
@@ -384,11 +366,7 @@ __device__ __forceinline__ void clm_chunk(
     sFac[2 * DK + c] = scale * pr * isqg;
     sFac[3 * DK + c] = pr * ise;
     sFac[4 * DK + c] = fast_exp2(gla - ben) * isk;
-    if (mode == CLM_SINGLE) {
-      if (rb == 0) reinterpret_cast<float*>(rec + LE::GL_OFF)[c] = fast_exp2(gla);   // gamma_last
-    } else {
-      po.gl[h2] = gla;
-    }
+    if (rb == 0) reinterpret_cast<float*>(rec + LE::GL_OFF)[c] = fast_exp2(gla);   // gamma_last
     // 2^(B_rb - B_{j+1}) = 2^(t_{j+1} + .. + t_{rb-1}) for j = rb - 2, rb - 3
     if (rb >= 2) {
       float gp = 0.f;
@@ -688,25 +666,13 @@ __device__ __forceinline__ void clm_chunk(
         for (int kk = 0; kk < 2; ++kk) acc = mfma16(ait[m][kk], bk[kk], acc);
         kaq[c2][m] = pack_f16x4(acc, u);
       }
-      if (mode == CLM_SINGLE) {
-        // lane (lr, lq) holds KA[16nn + lr][16m + 4lq ..+3]: in accumulator k
-        // order that is lane (lr, lq) of fragment (nn, m / 2), elements
-        // 4 (m % 2) .. +3, so each lane stores its own 16 bytes
+      // lane (lr, lq) holds KA[16nn + lr][16m + 4lq ..+3]: in accumulator k
+      // order that is lane (lr, lq) of fragment (nn, m / 2), elements
+      // 4 (m % 2) .. +3, so each lane stores its own 16 bytes
 #pragma unroll
-        for (int kt = 0; kt < 2; ++kt) {
-          const uint2 lo = kaq[c2][2 * kt], hi = kaq[c2][2 * kt + 1];
-          *reinterpret_cast<uint4*>(rec + LE::ka_frag(nn, kt) + lane * 8) = make_uint4(lo.x, lo.y, hi.x, hi.y);
-        }
-      }
-      if (mode == CLM_PAIR_A) {
-        // KA_a with the operands swapped: rows c = 16 nn + 4lq .., column t = 16m + lr
-#pragma unroll
-        for (int m = 0; m < 4; ++m) {
-          f32x4 acc = zero4();
-#pragma unroll
-          for (int kk = 0; kk < 2; ++kk) acc = mfma16(bk[kk], ait[m][kk], acc);
-          po.qq[c2][m] = pack_f16x4(acc, u);
-        }
+      for (int kt = 0; kt < 2; ++kt) {
+        const uint2 lo = kaq[c2][2 * kt], hi = kaq[c2][2 * kt + 1];
+        *reinterpret_cast<uint4*>(rec + LE::ka_frag(nn, kt) + lane * 8) = make_uint4(lo.x, lo.y, hi.x, hi.y);
       }
     }
   }
@@ -716,47 +682,19 @@ __device__ __forceinline__ void clm_chunk(
   for (int m = 0; m < 4; ++m)
     *reinterpret_cast<uint2*>(&sMozF[(rb * 2 + (m >> 1)) * kFrag + quad_in_frag(m, lr, lq)]) =
         m <= rb ? mozq[m] : make_uint2(0u, 0u);
-  if (mode != CLM_SINGLE) {   // KA fragments for the M product of the pair combine
-#pragma unroll
-    for (int c2 = 0; c2 < 2; ++c2)
-#pragma unroll
-      for (int m = 0; m < 4; ++m)
-        *reinterpret_cast<uint2*>(&sKaF[((2 * rb + c2) * 2 + (m >> 1)) * kFrag + quad_in_frag(m, lr, lq)]) =
-            kaq[c2][m];
-  }
 #pragma unroll
   for (int kk = 0; kk < 4; ++kk) *reinterpret_cast<uint4*>(&sQg[row * KHP + 32 * kk + 8 * lq]) = qg16[kk];
   __syncthreads();   // #9
 
-  // MOZ and KA fragments to the record (24 KiB, 16 bytes per lane per step)
+  // MOZ fragments to the record (8 KiB, 16 bytes per lane per step)
   {
     const uint4* src = reinterpret_cast<const uint4*>(sMozF);
-    if (mode == CLM_SINGLE) {
-      uint4* dm = reinterpret_cast<uint4*>(rec + LE::MOZ_OFF);
+    uint4* dm = reinterpret_cast<uint4*>(rec + LE::MOZ_OFF);
 #pragma unroll
-      for (int it = 0; it < 2; ++it) dm[tid + 256 * it] = src[tid + 256 * it];
-    } else if (mode == CLM_PAIR_A) {
-      // MOZ_a: the pair's MOZ row blocks 0-3, same fragment order
-      uint4* dm = reinterpret_cast<uint4*>(rec + LP::MOZ_OFF);
-#pragma unroll
-      for (int it = 0; it < 2; ++it) dm[tid + 256 * it] = src[tid + 256 * it];
-    } else {
-      // MOZ_b: pair MOZ row blocks 4-7, token steps 2-3; KA_b: pair KA token steps 2-3
-#pragma unroll
-      for (int it = 0; it < 2; ++it) {
-        const int f = (tid + 256 * it) >> 6;             // fragment (m, kk) = (f / 2, f % 2)
-        reinterpret_cast<uint4*>(rec + LP::moz_frag(4 + (f >> 1), 2 + (f & 1)))[lane] = src[tid + 256 * it];
-      }
-#pragma unroll
-      for (int it = 0; it < 4; ++it) {
-        const int f = (tid + 256 * it) >> 6;
-        reinterpret_cast<uint4*>(rec + LP::ka_frag(f >> 1, 2 + (f & 1)))[lane] = src[512 + tid + 256 * it];
-      }
-    }
+    for (int it = 0; it < 2; ++it) dm[tid + 256 * it] = src[tid + 256 * it];
   }
 
-  // ---- E: M = KA E and QP = Qg - MOZ E (transposed: E^T as the A operand) ------------
-  const float sc_m = fp16_range_scale(4096.f * maxk * mai * maxbk);                  // 64 max|KA| max|E|
+  // ---- E: the E fragments, and QP = Qg - MOZ E (transposed: E^T as the A operand) -----
   const float sc_qp = fp16_range_scale(scale * maxq + 4096.f * aqk_bound * mai * maxbk);  // |Qg| + 64 max|MOZ| max|E|
   uint4 et[2][2];                           // E^T fragments, rows = channels 32 rb + 16 c2 + lr
 #pragma unroll
@@ -764,7 +702,7 @@ __device__ __forceinline__ void clm_chunk(
 #pragma unroll
     for (int kk = 0; kk < 2; ++kk)
       et[c2][kk] = *reinterpret_cast<const uint4*>(&sEt[(32 * rb + 16 * c2 + lr) * TTP + 32 * kk + 8 * lq]);
-  if (mode == CLM_SINGLE) {
+  {
     // E fragments (token row block rb, accumulator k order over channels): the
     // selection product of an E^T fragment (rows = channels 16 cb .., k =
     // tokens 32 (rb / 2) ..) picks tokens 16 rb .. and leaves lane (lr, lq)
@@ -779,30 +717,6 @@ __device__ __forceinline__ void clm_chunk(
         h[hh] = pack_f16x4(mfma16(a, sel, zero4()), 1.f);
       }
       *reinterpret_cast<uint4*>(rec + LE::e_frag(rb, kk) + lane * 8) = make_uint4(h[0].x, h[0].y, h[1].x, h[1].y);
-    }
-  } else {
-    const float u = se * sc_ka / sc_m;
-#pragma unroll
-    for (int nn = 0; nn < 8; ++nn) {
-      uint4 bk[2];
-#pragma unroll
-      for (int kk = 0; kk < 2; ++kk)
-        bk[kk] = *reinterpret_cast<const uint4*>(&sKaF[(nn * 2 + kk) * kFrag + lane * 8]);
-#pragma unroll
-      for (int c2 = 0; c2 < 2; ++c2) {
-        f32x4 acc = zero4();
-        if (mode == CLM_PAIR_A) {
-          // M with the operands swapped: rows 16nn + 4lq .., column 32 rb + 16 c2 + lr
-#pragma unroll
-          for (int kk = 0; kk < 2; ++kk) acc = mfma16(bk[kk], et[c2][kk], acc);
-          po.mq[c2][nn] = pack_f16x4(acc, u);
-        } else {
-#pragma unroll
-          for (int kk = 0; kk < 2; ++kk) acc = mfma16(et[c2][kk], bk[kk], acc);
-          // M^T block (m = 2 rb + c2, nn): M[16nn + lr][32 rb + 16 c2 + 4lq ..]
-          po.mq[c2][nn] = pack_f16x4(acc, u);
-        }
-      }
     }
   }
   {
@@ -826,28 +740,16 @@ __device__ __forceinline__ void clm_chunk(
         v[1] = f16_bits_to_f32(static_cast<unsigned short>(qraw.x >> 16)) * sqg - acc[1] * u;
         v[2] = f16_bits_to_f32(static_cast<unsigned short>(qraw.y & 0xffffu)) * sqg - acc[2] * u;
         v[3] = f16_bits_to_f32(static_cast<unsigned short>(qraw.y >> 16)) * sqg - acc[3] * u;
-        if (mode == CLM_SINGLE)
-          *reinterpret_cast<uint2*>(rec + LE::qp_frag(nn, rb) + quad_in_frag(c2, lr, lq)) = pack_f16x4(v, iqp);
-        else if (mode == CLM_PAIR_A)
-          *reinterpret_cast<uint2*>(rec + LP::qp_frag(nn, rb) + quad_in_frag(c2, lr, lq)) = pack_f16x4(v, iqp);
-        else
-          po.qq[c2][nn] = pack_f16x4(v, iqp);
+        *reinterpret_cast<uint2*>(rec + LE::qp_frag(nn, rb) + quad_in_frag(c2, lr, lq)) = pack_f16x4(v, iqp);
       }
     }
   }
-  if (mode == CLM_SINGLE) {
-    if (tid == 0) {
-      float* sc = reinterpret_cast<float*>(rec + LE::SC_OFF);
-      sc[SCE_E] = se;
-      sc[SCE_KA] = sc_ka;
-      sc[SCE_QP] = sc_qp;
-      sc[SCE_MOZ] = sc_moz;
-    }
-  } else {
-    po.sc[SCM_M] = sc_m;
-    po.sc[SCM_KA] = sc_ka;
-    po.sc[SCM_QP] = sc_qp;
-    po.sc[SCM_MOZ] = sc_moz;
+  if (tid == 0) {
+    float* sc = reinterpret_cast<float*>(rec + LE::SC_OFF);
+    sc[SCE_E] = se;
+    sc[SCE_KA] = sc_ka;
+    sc[SCE_QP] = sc_qp;
+    sc[SCE_MOZ] = sc_moz;
   }
 }
 
@@ -870,272 +772,9 @@ __global__ __launch_bounds__(256, 2) void chunk_local_m_kernel(
   // the chunkwise form treats as inert; their loads re-read the last valid row
   int nvalid = static_cast<int>(min(static_cast<long>(kBS), n_tok - static_cast<long>(n) * kBS));
   if (vl.cu && !varlen_chunk(vl, s_alloc, n, tok0, nvalid)) return;
-  PairRegs pr;
   ClmIn<IN_DT> in;
   clm_load<IN_DT>(in, threadIdx.x, qp, kp, bp, g, H, s_alloc, bh / H, bh % H, tok0, nvalid, tok0 + nvalid - 1);
-  clm_chunk<IN_DT>(smem, threadIdx.x, CLM_SINGLE, in, nvalid, scale, ws + static_cast<size_t>(ch) * L::STRIDE, pr);
-}
-
-namespace clp {
-
-constexpr int HALF = (clm::LDS_BYTES + 255) / 256 * 256;   // LDS of one chunk half
-constexpr int LDS_BYTES = 2 * HALF;
-constexpr int XP = 136;                   // 16-bit pitch of the combine operands
-constexpr int X_OFF = 0;                  // fp16 [192][XP]: rows 0-127 M_b [i][j], 128-191 QP_b [s][j]
-constexpr int Y_OFF = X_OFF + 192 * XP * 2;   // fp16 [192][XP]: rows 0-127 M_a^T [j][i], 128-191 KA_a^T [t][i]
-constexpr int GL_OFF = Y_OFF + 192 * XP * 2;  // fp32 [2][128]: gamma_last of a, b
-constexpr int GLA_OFF = GL_OFF + 2 * 128 * 4; // fp32 [64][2]: G_last (log2) of a, channels (l, l + 64)
-constexpr int SC_OFF = GLA_OFF + 128 * 4;     // fp32 [2][4]: scales of a, b
-constexpr int MX_OFF = SC_OFF + 8 * 4;        // fp32 [8 waves][4]: maxima of the combined blocks
-static_assert(MX_OFF + 8 * 4 * 4 <= LDS_BYTES, "combine staging exceeds the pair's LDS");
-static_assert(LDS_BYTES <= 163840, "one pair workgroup per CU");
-
-}  // namespace clp
-
-// Two consecutive chunks a = 2p, b = 2p + 1 of a key head on 512 threads (waves
-// 0-3: chunk a, 4-7: chunk b, each with its own LDS half), then their
-// composition into one pair record (gdn2_prefill_layout.h: ChunkLayoutP). The
-// blocks that pass through unchanged (QP_a, MOZ_a, KA_b, MOZ_b) are written by
-// the chunk bodies; the rest come from one product C = X Y in LDS,
-//   X = [M_b ; QP_b] (192 x 128),  Y = [M_a | KA_a] (128 x 192),
-//   M = gamma_b M_a + M_b gamma_a - C_11    KA_left = gamma_b KA_a - C_12
-//   QP_bottom = QP_b gamma_a - C_21          MOZ_lower_left = C_22,
-// the elementwise terms in fp32 and each block scaled by its largest entry. A
-// chunk b past the call's end is all padding: A_b = I and its blocks are zero.
-template <int IN_DT>
-__global__ __launch_bounds__(512, 1) void chunk_pair_kernel(
-    const void* __restrict__ qp, const void* __restrict__ kp, const void* __restrict__ bp,
-    const float* __restrict__ g, int H, long s_alloc, long t0, int NP, int npairs, long n_tok, float scale,
-    unsigned short* __restrict__ ws) {
-  using namespace clm;
-  using LP = ChunkLayoutP;
-  extern __shared__ __align__(16) unsigned char smem[];
-  const int tid = threadIdx.x;
-  const int lane = tid & 63;
-  const int wave = __builtin_amdgcn_readfirstlane(tid >> 6);
-  const int half = wave >> 2;
-  const int lr = lane & 15;
-  const int lq = lane >> 4;
-  const int nbh = npairs / NP;
-  // pair order: pair-major from the last pair back, so the records the scan reads
-  // first are written last (see chunk_local_m_kernel)
-  auto pair_of = [&](int it) { return (it % nbh) * NP + (NP - 1 - it / nbh); };
-  auto chunk_of = [&](int pi) { return 2 * (pi % NP) + half; };
-  auto row_base = [&](int pi) {
-    const int bh = pi / NP, n = chunk_of(pi);
-    const int nvalid = static_cast<int>(min(static_cast<long>(kBS), n_tok - static_cast<long>(n) * kBS));
-    return clm_row_base(tid & 255, H, s_alloc, bh / H, bh % H, t0 + static_cast<long>(n) * kBS, nvalid,
-                        t0 + n_tok - 1);
-  };
-
-  unsigned short* sX = reinterpret_cast<unsigned short*>(smem + clp::X_OFF);
-  unsigned short* sY = reinterpret_cast<unsigned short*>(smem + clp::Y_OFF);
-  float* sGa = reinterpret_cast<float*>(smem + clp::GL_OFF);   // [2][128]: gamma_a, gamma_b
-  float* sSc = reinterpret_cast<float*>(smem + clp::SC_OFF);
-  float* sMx = reinterpret_cast<float*>(smem + clp::MX_OFF);
-  constexpr int XP = clp::XP;
-
-  {
-    const int pi = pair_of(blockIdx.x);
-    ClmIn<IN_DT> in;
-    {
-      const size_t rbase = row_base(pi);
-      clm_load_g<IN_DT>(in, rbase, g);
-      clm_load_qkb<IN_DT>(in, rbase, qp, kp, bp);
-    }
-    unsigned short* rec = ws + static_cast<size_t>(pi) * LP::STRIDE;
-    {
-      const int n = chunk_of(pi);
-      const int nvalid = static_cast<int>(min(static_cast<long>(kBS), n_tok - static_cast<long>(n) * kBS));
-      PairRegs pr;
-      clm_chunk<IN_DT>(smem + half * clp::HALF, tid & 255, half ? CLM_PAIR_B : CLM_PAIR_A, in, nvalid, scale, rec,
-                       pr);
-      __syncthreads();   // both chunks' LDS is dead
-
-      const int rb = wave & 3;
-      if (half == 0) {
-#pragma unroll
-        for (int c2 = 0; c2 < 2; ++c2) {
-          const int j = 32 * rb + 16 * c2 + lr;
-#pragma unroll
-          for (int nn = 0; nn < 8; ++nn)
-            *reinterpret_cast<uint2*>(&sY[j * XP + 16 * nn + 4 * lq]) = pr.mq[c2][nn];
-#pragma unroll
-          for (int m = 0; m < 4; ++m)
-            *reinterpret_cast<uint2*>(&sY[(128 + 16 * m + lr) * XP + 32 * rb + 16 * c2 + 4 * lq]) = pr.qq[c2][m];
-        }
-      } else {
-#pragma unroll
-        for (int c2 = 0; c2 < 2; ++c2) {
-          const int j = 32 * rb + 16 * c2 + 4 * lq;
-#pragma unroll
-          for (int nn = 0; nn < 8; ++nn)
-            *reinterpret_cast<uint2*>(&sX[(16 * nn + lr) * XP + j]) = pr.mq[c2][nn];
-#pragma unroll
-          for (int nn = 0; nn < 4; ++nn)
-            *reinterpret_cast<uint2*>(&sX[(128 + 16 * nn + lr) * XP + j]) = pr.qq[c2][nn];
-        }
-      }
-      if (rb == 0) {
-        // gamma of the chunk (the pair's comes from the sum of the exponents)
-        sGa[128 * half + lane] = fast_exp2(pr.gl[0]);
-        sGa[128 * half + 64 + lane] = fast_exp2(pr.gl[1]);
-        if (half == 0)
-          reinterpret_cast<float2*>(smem + clp::GLA_OFF)[lane] = make_float2(pr.gl[0], pr.gl[1]);
-        if (lane < 4) sSc[4 * half + lane] = lane == 0 ? pr.sc[0] : lane == 1 ? pr.sc[1] : lane == 2 ? pr.sc[2] : pr.sc[3];
-      }
-      __syncthreads();
-      if (half == 1 && wave == 4) {
-        const float2 ga = reinterpret_cast<const float2*>(smem + clp::GLA_OFF)[lane];
-        reinterpret_cast<float*>(rec + LP::GL_OFF)[lane] = fast_exp2(ga.x + pr.gl[0]);
-        reinterpret_cast<float*>(rec + LP::GL_OFF)[64 + lane] = fast_exp2(ga.y + pr.gl[1]);
-      }
-    }
-
-    // C = X Y: wave (rg, ch) forms X row blocks 3rg .. 3rg+2 times Y column blocks
-    // 6ch .. 6ch+5 (A operand: Y^T rows, B operand: X rows), so lane (lr, lq) of
-    // tile (r, c) holds C[16(3rg + r) + lr][16(6ch + c) + 4lq .. +3]
-    const int rg = wave >> 1, chh = wave & 1;
-    f32x4 acc[3][6];
-#pragma unroll
-    for (int r = 0; r < 3; ++r)
-#pragma unroll
-      for (int c = 0; c < 6; ++c) acc[r][c] = zero4();
-#pragma unroll
-    for (int kk = 0; kk < 4; ++kk) {
-      uint4 xa[3];
-#pragma unroll
-      for (int r = 0; r < 3; ++r)
-        xa[r] = *reinterpret_cast<const uint4*>(&sX[(16 * (3 * rg + r) + lr) * XP + 32 * kk + 8 * lq]);
-#pragma unroll
-      for (int c = 0; c < 6; ++c) {
-        const uint4 yb = *reinterpret_cast<const uint4*>(&sY[(16 * (6 * chh + c) + lr) * XP + 32 * kk + 8 * lq]);
-#pragma unroll
-        for (int r = 0; r < 3; ++r) acc[r][c] = mfma16(yb, xa[r], acc[r][c]);
-      }
-    }
-    // the elementwise terms; blocks: 0 M, 1 KA left, 2 QP bottom, 3 MOZ lower left
-    const float sam = sSc[SCM_M], saka = sSc[SCM_KA], sbm = sSc[4 + SCM_M], sbqp = sSc[4 + SCM_QP];
-    float mx[4] = {0.f, 0.f, 0.f, 0.f};
-#pragma unroll
-    for (int r = 0; r < 3; ++r) {
-      const int nb = 3 * rg + r;
-      const int nrow = 16 * nb + lr;                  // X row: i (nb < 8) or 128 + s
-      const float gbi = nb < 8 ? sGa[128 + nrow] : 0.f;
-#pragma unroll
-      for (int c = 0; c < 6; ++c) {
-        const int mb = 6 * chh + c;
-        const int m0 = 16 * mb + 4 * lq;              // Y column: j (mb < 8) or 128 + t
-        f32x4& v = acc[r][c];
-        if (mb < 8) {
-          const float4 ga = *reinterpret_cast<const float4*>(&sGa[m0]);
-          const float gav[4] = {ga.x, ga.y, ga.z, ga.w};
-          const uint2 xb = *reinterpret_cast<const uint2*>(&sX[nrow * XP + m0]);
-          const float xv[4] = {f16_bits_to_f32(xb.x & 0xffffu), f16_bits_to_f32(xb.x >> 16),
-                               f16_bits_to_f32(xb.y & 0xffffu), f16_bits_to_f32(xb.y >> 16)};
-          if (nb < 8) {
-            const float ua = gbi * sam, ub = sbm, uc = sbm * sam;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              const float ma = f16_bits_to_f32(sY[(m0 + e) * XP + nrow]);
-              v[e] = ma * ua + xv[e] * ub * gav[e] - v[e] * uc;
-              mx[0] = fmaxf(mx[0], fabsf(v[e]));
-            }
-          } else {
-            const float uc = sbqp * sam;
-#pragma unroll
-            for (int e = 0; e < 4; ++e) {
-              v[e] = xv[e] * sbqp * gav[e] - v[e] * uc;
-              mx[2] = fmaxf(mx[2], fabsf(v[e]));
-            }
-          }
-        } else if (nb < 8) {
-          const float ua = gbi * saka, uc = sbm * saka;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            const float ka = f16_bits_to_f32(sY[(m0 + e) * XP + nrow]);
-            v[e] = ka * ua - v[e] * uc;
-            mx[1] = fmaxf(mx[1], fabsf(v[e]));
-          }
-        } else {
-          const float uc = sbqp * saka;
-#pragma unroll
-          for (int e = 0; e < 4; ++e) {
-            v[e] = v[e] * uc;
-            mx[3] = fmaxf(mx[3], fabsf(v[e]));
-          }
-        }
-      }
-    }
-#pragma unroll
-    for (int t = 0; t < 4; ++t) mx[t] = wave_max(mx[t]);
-    if (lane == 0) *reinterpret_cast<float4*>(&sMx[4 * wave]) = make_float4(mx[0], mx[1], mx[2], mx[3]);
-    __syncthreads();
-    float scl[4], inv[4];
-#pragma unroll
-    for (int t = 0; t < 4; ++t) {
-      float m = 0.f;
-#pragma unroll
-      for (int w = 0; w < 8; ++w) m = fmaxf(m, sMx[4 * w + t]);
-      scl[t] = fp16_range_scale(m);
-      inv[t] = 1.f / scl[t];
-    }
-#pragma unroll
-    for (int r = 0; r < 3; ++r) {
-      const int nb = 3 * rg + r;
-#pragma unroll
-      for (int c = 0; c < 6; ++c) {
-        const int mb = 6 * chh + c;
-        const int q = quad_in_frag(mb & 1, lr, lq);
-        if (nb < 8 && mb < 8)
-          *reinterpret_cast<uint2*>(rec + LP::m_frag(nb, mb >> 1) + q) = pack_f16x4(acc[r][c], inv[0]);
-        else if (nb < 8)
-          *reinterpret_cast<uint2*>(rec + LP::ka_frag(nb, (mb - 8) >> 1) + q) = pack_f16x4(acc[r][c], inv[1]);
-        else if (mb < 8)
-          *reinterpret_cast<uint2*>(rec + LP::qp_frag(nb - 4, mb >> 1) + q) = pack_f16x4(acc[r][c], inv[2]);
-        else
-          *reinterpret_cast<uint2*>(rec + LP::moz_frag(nb - 4, (mb - 8) >> 1) + q) = pack_f16x4(acc[r][c], inv[3]);
-      }
-    }
-    if (tid == 0) {
-      float* sc = reinterpret_cast<float*>(rec + LP::SC_OFF);
-      sc[SCP_M] = scl[0];
-      sc[SCP_KAL] = scl[1];
-      sc[SCP_KAR] = sSc[4 + SCM_KA];
-      sc[SCP_QPT] = sSc[SCM_QP];
-      sc[SCP_QPB] = scl[2];
-      sc[SCP_MOZTL] = sSc[SCM_MOZ];
-      sc[SCP_MOZLL] = scl[3];
-      sc[SCP_MOZBR] = sSc[4 + SCM_MOZ];
-    }
-  }
-}
-
-template <int IN_DT>
-static hipError_t launch_chunk_pair_t(const void* q, const void* k, const void* b, const float* g, int B, int H,
-                                      long s_alloc, long t0, int NP, long n_tok, float scale, unsigned short* ws,
-                                      hipStream_t stream) {
-  constexpr int smem = clp::LDS_BYTES;
-  static std::atomic<unsigned long long> lds_set{0};   // per device
-  {
-    const hipError_t e = set_dyn_lds_once(reinterpret_cast<const void*>(&chunk_pair_kernel<IN_DT>), smem, lds_set);
-    if (e != hipSuccess) return e;
-  }
-  const int npairs = B * H * NP;
-  const unsigned grid = static_cast<unsigned>(npairs);
-  hipLaunchKernelGGL((chunk_pair_kernel<IN_DT>), dim3(grid), dim3(512), smem, stream, q, k, b, g, H, s_alloc, t0,
-                     NP, npairs, n_tok, scale, ws);
-  return hipGetLastError();
-}
-
-// Pair records (ChunkLayoutP) of a dense call: NP = ceil(chunks / 2) per key head.
-hipError_t launch_chunk_pair(const void* q, const void* k, const void* b, const float* g, int in_dt, int B, int H,
-                             long s_alloc, long t0, int NP, long n_tok, float scale, unsigned short* ws,
-                             hipStream_t stream) {
-  if (in_dt == DT_BF16) return launch_chunk_pair_t<DT_BF16>(q, k, b, g, B, H, s_alloc, t0, NP, n_tok, scale, ws, stream);
-  if (in_dt == DT_F16) return launch_chunk_pair_t<DT_F16>(q, k, b, g, B, H, s_alloc, t0, NP, n_tok, scale, ws, stream);
-  if (in_dt == DT_F32) return launch_chunk_pair_t<DT_F32>(q, k, b, g, B, H, s_alloc, t0, NP, n_tok, scale, ws, stream);
-  return hipErrorInvalidValue;
+  clm_chunk<IN_DT>(smem, threadIdx.x, in, nvalid, scale, ws + static_cast<size_t>(ch) * L::STRIDE);
 }
 
 template <int IN_DT>

@@ -54,56 +54,21 @@ struct ChunkLayout {
 static_assert((ChunkLayout<128>::STRIDE * 2) % 256 == 0, "record must keep 256-byte alignment");
 static_assert((ChunkLayout<64>::STRIDE * 2) % 256 == 0, "record must keep 256-byte alignment");
 
-// Transition-form record (DK = 128). With Z = w * v of the chunk, the scan
-// needs only
+// Factored transition record (DK = 128). From the chunk's WY factors (Ai =
+// (I + Akk)^-1, E = b*k*gamma, KG = k*gamma_last/gamma, Qg = scale*q*gamma,
+// Aqk with its diagonal):
 //
-//   S <- diag(gamma_last) S - M S + KA Z        o = QP S + MOZ Z
+//   MOZ = Aqk Ai  [64 x 64]    KA = KG^T Ai  [DK x 64]    QP = Qg - MOZ E  [64 x DK]
 //
-// where, from the chunk's WY factors (Ai = (I + Akk)^-1, E = b*k*gamma,
-// KG = k*gamma_last/gamma, Qg = scale*q*gamma, Aqk with its diagonal):
-//
-//   MOZ = Aqk Ai  [64 x 64]    KA = KG^T Ai  [DK x 64]
-//   M   = KA E    [DK x DK]    QP = Qg - MOZ E  [64 x DK]
-//
-// so one chunk of the scan is a single state product on its critical path.
-// Fragments are fp16 MFMA A operands as above, each matrix with its own
-// power-of-two scale:
-//
-//   M   [DK/16 m][DK/32 kk]   rows = state row, k = state row      / SC[0]
-//   KA  [DK/16 m][2 kk]       rows = state row, k = token          / SC[1]
-//   QP  [4 m][DK/32 kk]       rows = token,     k = state row      / SC[2]
-//   MOZ [4 m][2 kk]           rows = token,     k = token          / SC[3]
-//   GL  [DK] fp32 gamma_last;  SC [8] fp32
-enum RecordScaleM : int { SCM_M = 0, SCM_KA = 1, SCM_QP = 2, SCM_MOZ = 3 };
-
-template <int DK>
-struct ChunkLayoutM {
-  static constexpr int KT = DK / 32;
-  static constexpr int MT = DK / 16;
-  static constexpr long M_OFF = 0;
-  static constexpr long KA_OFF = M_OFF + static_cast<long>(MT) * KT * kFrag;
-  static constexpr long QP_OFF = KA_OFF + static_cast<long>(MT) * 2 * kFrag;
-  static constexpr long MOZ_OFF = QP_OFF + 4L * KT * kFrag;
-  static constexpr long GL_OFF = MOZ_OFF + 4L * 2 * kFrag;
-  static constexpr long SC_OFF = GL_OFF + 2L * DK;
-  static constexpr long STRIDE = ((SC_OFF + 2L * 8) + 127) / 128 * 128;   // 256-byte records
-
-  __host__ __device__ static constexpr long m_frag(int m, int kk) { return M_OFF + (m * KT + kk) * kFrag; }
-  __host__ __device__ static constexpr long ka_frag(int m, int kk) { return KA_OFF + (m * 2 + kk) * kFrag; }
-  __host__ __device__ static constexpr long qp_frag(int m, int kk) { return QP_OFF + (m * KT + kk) * kFrag; }
-  __host__ __device__ static constexpr long moz_frag(int m, int kk) { return MOZ_OFF + (m * 2 + kk) * kFrag; }
-};
-
-static_assert((ChunkLayoutM<128>::STRIDE * 2) % 256 == 0, "record must keep 256-byte alignment");
-
-// Factored transition record (DK = 128). With Y = Z - E S (the chunk's
-// tokens against the entering state) the scan needs
+// and with Z = w * v and Y = Z - E S (the chunk's tokens against the
+// entering state) the scan needs only
 //
 //   S <- diag(gamma_last) S + KA Y        o = QP S + MOZ Z
 //
-// (the transition form above with M = KA E applied as its two factors), so
-// the record holds E [64 x DK] in place of M [DK x DK]: 22% fewer bytes to
-// write, and to fetch per scan workgroup and chunk.
+// (the reference's Un = Ai Z - W S, S <- gamma_last S + KG^T Un, o = Qg S +
+// Aqk Un with W = Ai E). The transition S <- (diag(gamma_last) - KA E) S + ..
+// is kept as its two factors: the 128 x 128 product M = KA E has rank 64, so
+// E (16 KiB) replaces M (32 KiB), and the record is 58 112 bytes.
 //
 // Two of the matrices are contracted against values that the scan holds in
 // MFMA accumulator order: E against S (state rows) and KA against Y (tokens).
@@ -148,69 +113,6 @@ struct ChunkLayoutE {
 
 static_assert((ChunkLayoutE<128>::STRIDE * 2) % 256 == 0, "record must keep 256-byte alignment");
 static_assert(ChunkLayoutE<128>::STRIDE * 2 == 58112, "factored record size");
-
-// Pair record (DK = 128): the transition of two consecutive 64-token chunks a, b
-// as one 128-token step of the scan, in the same form
-//
-//   S <- diag(gamma) S - M S + KA Z        o = QP S + MOZ Z       (Z: 128 tokens)
-//
-// With A_c = diag(gamma_c) - M_c the transition of chunk c, composing
-// S_b = A_b (A_a S + KA_a Z_a) + KA_b Z_b and o_b = QP_b (A_a S + KA_a Z_a) + MOZ_b Z_b:
-//
-//   gamma = gamma_a gamma_b       M = gamma_b M_a + M_b gamma_a - M_b M_a
-//   KA  = [ gamma_b KA_a - M_b KA_a | KA_b ]
-//   QP  = [ QP_a ; QP_b gamma_a - QP_b M_a ]
-//   MOZ = [ MOZ_a  0 ; QP_b KA_a  MOZ_b ]
-//
-// (gamma_b M_a scales rows, M_b gamma_a columns). Fragments as above, each
-// block with its own power-of-two scale:
-//
-//   M   [8 m][4 kk]   / SC[0]
-//   KA  [8 m][4 kk]   kk 0-1: tokens of a / SC[1], kk 2-3: tokens of b / SC[2]
-//   QP  [8 m][4 kk]   m 0-3: tokens of a / SC[3],  m 4-7: tokens of b / SC[4]
-//   MOZ m 0-3: [kk 0-1] / SC[5];  m 4-7: [kk 0-1] / SC[6], [kk 2-3] / SC[7]
-//       (the zero block above the diagonal is not stored)
-//   GL  [DK] fp32 gamma;  SC [8] fp32
-enum RecordScaleP : int {
-  SCP_M = 0, SCP_KAL = 1, SCP_KAR = 2, SCP_QPT = 3, SCP_QPB = 4, SCP_MOZTL = 5, SCP_MOZLL = 6, SCP_MOZBR = 7
-};
-
-struct ChunkLayoutP {
-  static constexpr int DK = 128;
-  static constexpr int TOK = 2 * kBS;   // tokens per record
-  static constexpr long M_OFF = 0;
-  static constexpr long KA_OFF = M_OFF + 32L * kFrag;
-  static constexpr long QP_OFF = KA_OFF + 32L * kFrag;
-  static constexpr long MOZ_OFF = QP_OFF + 32L * kFrag;
-  static constexpr long GL_OFF = MOZ_OFF + 24L * kFrag;
-  static constexpr long SC_OFF = GL_OFF + 2L * DK;
-  static constexpr long STRIDE = ((SC_OFF + 2L * 8) + 127) / 128 * 128;
-
-  __host__ __device__ static constexpr long m_frag(int m, int kk) { return M_OFF + (m * 4 + kk) * kFrag; }
-  __host__ __device__ static constexpr long ka_frag(int m, int kk) { return KA_OFF + (m * 4 + kk) * kFrag; }
-  __host__ __device__ static constexpr long qp_frag(int m, int kk) { return QP_OFF + (m * 4 + kk) * kFrag; }
-  __host__ __device__ static constexpr long moz_frag(int m, int kk) {
-    return MOZ_OFF + (m < 4 ? m * 2 + kk : 8 + (m - 4) * 4 + kk) * kFrag;
-  }
-};
-
-static_assert((ChunkLayoutP::STRIDE * 2) % 256 == 0, "record must keep 256-byte alignment");
-
-// Which record form a DK = 128 call uses; the chunk-local and scan entry points
-// decide it from the arguments both receive. Pair records halve the scan's
-// serial steps but cost the chunk-local stage more (two chunks and their
-// composition in one workgroup, one per CU); they pay off where the scan has
-// fewer workgroups than the GPU has CUs, so they are used for dense calls of
-// up to 16 key heads (at most 128 16-column value tiles per key head group of
-// DV = 128) and at least 32 chunks: a short call's chunk-local stage runs as
-// few workgroups whose latency the pair form lengthens, while its scan has few
-// steps to save. Chunk records for packed batches and the other calls.
-constexpr long kPairMaxKeyHeads = 16;
-constexpr long kPairMinChunks = 32;
-inline bool use_pair_records(int B, int HK, int DK, long n_tokens, bool varlen) {
-  return false && !varlen && DK == 128 && static_cast<long>(B) * HK <= kPairMaxKeyHeads &&
-         (n_tokens + kBS - 1) / kBS >= kPairMinChunks;
-}
 
 // Packed variable-length batches (cu_seqlens). Sequence s holds tokens
 // [cu[s], cu[s+1]) of one [T, H, D] allocation and its chunk c (64 tokens, the

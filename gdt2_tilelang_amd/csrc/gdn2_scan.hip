@@ -577,7 +577,7 @@ static hipError_t launch_scan_t(const void* v, const void* w, const unsigned sho
 }
 
 // Value-tile width: enough workgroups to cover the CUs, else wider tiles.
-int scan_nt_for(int B, int H, int DV) {
+static int scan_nt_for(int B, int H, int DV) {
   const long heads = static_cast<long>(B) * H;
   if (DV % 32 == 0 && heads * (DV / 16) > 512) return 2;
   return 1;
@@ -587,18 +587,10 @@ hipError_t launch_scan_e(const void* v, const void* w, int in_dt, const unsigned
                          float* s_out, void* o, int out_dt, int B, int H, int HK, int DV, long s_alloc, long t0,
                          int NC, long n_tok, Varlen vl, hipStream_t stream);
 
-hipError_t launch_scan_p(const void* v, const void* w, int in_dt, const unsigned short* ws, const float* s_in,
-                         float* s_out, void* o, int out_dt, int B, int H, int HK, int DV, long s_alloc, long t0,
-                         int NP, long n_tok, hipStream_t stream);
-
 hipError_t launch_scan(const void* v, const void* w, int in_dt, const unsigned short* ws,
                        const float* s_in, float* s_out, void* o, int out_dt, int B, int H, int HK, int DK,
                        int DV, long s_alloc, long t0, int NC, long n_tok, Varlen vl, hipStream_t stream) {
-  // DK = 128 runs on the transition-form records (gdn2_scan_p.hip on pair
-  // records, gdn2_scan_m.hip on chunk records); DK = 64 here.
-  if (use_pair_records(B, HK, DK, n_tok, vl.cu != nullptr))
-    return launch_scan_p(v, w, in_dt, ws, s_in, s_out, o, out_dt, B, H, HK, DV, s_alloc, t0, (NC + 1) / 2, n_tok,
-                         stream);
+  // DK = 128 runs on the factored transition records (gdn2_scan_e.hip); DK = 64 here.
   if (DK == 128)
     return launch_scan_e(v, w, in_dt, ws, s_in, s_out, o, out_dt, B, H, HK, DV, s_alloc, t0, NC, n_tok, vl, stream);
   const int nt = scan_nt_for(B, H, DV);

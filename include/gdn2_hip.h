@@ -112,7 +112,7 @@ int gdn2_hip_prefill_chunks(const void* q, const void* k, const void* v, const f
  * gdn2_hip_prefill_chunks without the workspace argument: the chunk records go
  * to a scratch array the library holds in device memory, one per GPU, of
  * GDN2_NOALLOC_SCRATCH_BYTES (64 MiB of gdn2_hip_prefill_workspace_bytes: e.g.
- * 1792 tokens of 32 key heads on chunk records, 8576 tokens of 8 key heads on pair records).
+ * 2304 tokens of 32 key heads, 9216 tokens of 8 key heads).
  * A larger call returns GDN2_ERR_SCRATCH and launches nothing (prefill it in
  * segments, passing state_out back as state_in). The call allocates nothing:
  * no hipMalloc / hipFree, nothing from a caching allocator, so it can run

@@ -1,29 +1,23 @@
-"""The DK = 128 chunk-local stage on its own: the transition-form records it
-writes (csrc/gdn2_prefill_layout.h) against the same matrices formed in
+"""The DK = 128 chunk-local stage on its own: the factored transition records
+it writes (csrc/gdn2_prefill_layout.h) against the same matrices formed in
 float64 from their definitions (reference gdn2/reference.py:116-197 for Aqk,
 Akk, Ai and the WY factors; the record products as the scan uses them):
 
-    MOZ = Aqk Ai,  KA = KG^T Ai,  M = KA E,  QP = Qg - MOZ E,  gamma_last,
+    E = b k gamma,  MOZ = Aqk Ai,  KA = KG^T Ai,  QP = Qg - MOZ E,  gamma_last,
 
-and, for pair records (two consecutive chunks a, b as one 128-token scan
-step), their composition, checked against two 64-token steps of the scan:
-
-    gamma = gamma_a gamma_b,  M = gamma_b M_a + M_b gamma_a - M_b M_a,
-    KA = [gamma_b KA_a - M_b KA_a | KA_b],  QP = [QP_a ; QP_b gamma_a - QP_b M_a],
-    MOZ = [MOZ_a 0 ; QP_b KA_a  MOZ_b].
+and the transition's rank-64 product M = KA E formed from the decoded E and
+KA, against M from the float64 factors.
 
 Every matrix is stored as fp16 (11-bit significand) after products of fp16
 operands, so each is held to 3e-3 of its own largest entry, plus an absolute
 2^-22 (four steps of fp16's subnormal spacing) for entries below fp16's
-normal range: with strong decay the whole of M is ~1e-19 (a full chunk of
+normal range: with strong decay the whole of E is ~1e-19 (a full chunk of
 decay) and is stored as zeros, which moves the state by less than 2^-17 of
 its own scale per chunk. Inputs are fp32
 and cover every path of the kernel's decay handling: small decay (fp16
 off-diagonal blocks, split-bf16 diagonal), the test suite's default decay
 scale 4, and decay scale 30, where a 16-token block's decay spread exceeds
-the split operands' range and the diagonal block is summed exactly. Dense
-calls of up to 16 key heads and at least 32 chunks write pair records, the
-others chunk records."""
+the split operands' range and the diagonal block is summed exactly."""
 
 from __future__ import annotations
 
@@ -102,58 +96,6 @@ def reference_record(q, k, g, b, scale):
     return dict(E=E, M=ka @ E, KA=ka, QP=Qg - moz @ E, MOZ=moz, GL=np.exp(G[-1]))
 
 
-P_M, P_KA, P_QP, P_MOZ, P_GL, P_SC, P_STRIDE = 0, 16384, 32768, 49152, 61440, 61696, 61824
-
-
-def decode_pair_record(rec):
-    sc = rec[P_SC:P_SC + 16].view(np.float32).astype(np.float64)
-    ka = frags_to_matrix(rec, P_KA, 8, 4)
-    ka[:, :64] *= sc[1]
-    ka[:, 64:] *= sc[2]
-    qp = frags_to_matrix(rec, P_QP, 8, 4)
-    qp[:64] *= sc[3]
-    qp[64:] *= sc[4]
-    moz = np.zeros((128, 128))
-    moz[:64, :64] = frags_to_matrix(rec, P_MOZ, 4, 2) * sc[5]
-    low = frags_to_matrix(rec, P_MOZ + 8 * FRAG, 4, 4)
-    moz[64:, :64] = low[:, :64] * sc[6]
-    moz[64:, 64:] = low[:, 64:] * sc[7]
-    return dict(M=frags_to_matrix(rec, P_M, 8, 4) * sc[0], KA=ka, QP=qp, MOZ=moz,
-                GL=rec[P_GL:P_GL + 256].view(np.float32).astype(np.float64))
-
-
-def compose_pair(a, b):
-    """The pair record of chunks a then b (float64 records of reference_record)."""
-    ga, gb = a["GL"], b["GL"]
-    moz = np.zeros((128, 128))
-    moz[:64, :64], moz[64:, :64], moz[64:, 64:] = a["MOZ"], b["QP"] @ a["KA"], b["MOZ"]
-    return dict(M=gb[:, None] * a["M"] + b["M"] * ga[None, :] - b["M"] @ a["M"],
-                KA=np.hstack([gb[:, None] * a["KA"] - b["M"] @ a["KA"], b["KA"]]),
-                QP=np.vstack([a["QP"], b["QP"] * ga[None, :] - b["QP"] @ a["M"]]), MOZ=moz, GL=ga * gb)
-
-
-def test_pair_composition_is_two_scan_steps():
-    """compose_pair's algebra (host, float64): one 128-token step of the composed
-    record equals two 64-token steps of the scan (o = QP S + MOZ Z,
-    S <- gamma S - M S + KA Z) on random records."""
-    rng = np.random.default_rng(0)
-
-    def rec():
-        return dict(M=rng.normal(size=(128, 128)) * 0.1, KA=rng.normal(size=(128, 64)) * 0.1,
-                    QP=rng.normal(size=(64, 128)), MOZ=np.tril(rng.normal(size=(64, 64))),
-                    GL=np.exp(-rng.random(128)))
-
-    def step(r, S, Z):
-        return r["QP"] @ S + r["MOZ"] @ Z, r["GL"][:, None] * S - r["M"] @ S + r["KA"] @ Z
-
-    a, b = rec(), rec()
-    S, Z = rng.normal(size=(128, 16)), rng.normal(size=(128, 16))
-    oa, S1 = step(a, S, Z[:64])
-    ob, S2 = step(b, S1, Z[64:])
-    o, S3 = step(compose_pair(a, b), S, Z)
-    assert np.abs(o - np.vstack([oa, ob])).max() < 1e-12 and np.abs(S3 - S2).max() < 1e-12
-
-
 def _max_rel(a, b):
     return float(np.abs(a - b).max() / max(np.abs(b).max(), 2.0 ** -22 / 3e-3))
 
@@ -162,9 +104,8 @@ def _max_rel(a, b):
 @pytest.mark.parametrize("H,S", [(2, 150), (2, 2070)])
 @pytest.mark.parametrize("dist,decay", [("cfg", None), ("ref", 0.3), ("ref", 4.0), ("ref", 30.0)])
 def test_chunk_local_records(dist, decay, H, S):
-    """S = 150: 3 chunk records, the last chunk ragged (22 rows). S = 2070: 17
-    pair records of 33 chunks, the last chunk ragged (22 rows) and the last
-    pair's second chunk all padding."""
+    """S = 150: 3 chunk records, the last chunk ragged (22 rows). S = 2070: 33
+    chunk records, the last ragged (22 rows)."""
     print(f"records DK=128 H={H} S={S} {dist} decay={decay}", flush=True)
     B = 1
     if dist == "cfg":
@@ -182,10 +123,8 @@ def test_chunk_local_records(dist, decay, H, S):
     torch.cuda.synchronize()
     raw = ws.cpu().numpy().view(np.uint16)
     NC = (S + 63) // 64
-    pair = nbytes != B * H * NC * STRIDE * 2    # pair records: few key heads, long calls
-    NR = (NC + 1) // 2 if pair else NC
-    stride = raw.size // (B * H * NR)
-    assert stride == (P_STRIDE if pair else STRIDE)
+    assert nbytes == B * H * NC * STRIDE * 2
+    NR, stride = NC, STRIDE
 
     def chunk_ref(h, n):
         sl = slice(64 * n, min(64 * n + 64, S))
@@ -197,15 +136,11 @@ def test_chunk_local_records(dist, decay, H, S):
     for h in range(H):
         for n in range(NR):
             got_raw = raw[(h * NR + n) * stride:(h * NR + n + 1) * stride].copy()
-            if pair:
-                want = compose_pair(chunk_ref(h, 2 * n), chunk_ref(h, 2 * n + 1))
-                got = decode_pair_record(got_raw)
-            else:
-                want, got = chunk_ref(h, n), decode_record(got_raw)
+            want, got = chunk_ref(h, n), decode_record(got_raw)
             for name in got:
                 e = _max_rel(got[name], want[name])
                 worst[name] = max(worst.get(name, 0.0), e)
     print("  " + " ".join(f"{k_}={v_:.1e}" for k_, v_ in worst.items()), flush=True)
     assert worst["GL"] < 1e-5
-    for name in ("M", "KA", "QP", "MOZ") + (() if pair else ("E",)):
+    for name in ("E", "M", "KA", "QP", "MOZ"):
         assert worst[name] < 3e-3, (name, worst[name])

@@ -46,16 +46,13 @@ def test_version_and_status_strings():
 
 def test_workspace_size():
     lib = _hip.lib()
-    # one record per (b, key head, 64-token chunk): 74496 bytes at DK=128 (transition form:
-    # M 32 KiB, KA 16, QP 16, MOZ 8, gamma_last, scales), 41472 at DK=64
-    assert lib.gdn2_hip_prefill_workspace_bytes(2, 16, 128, 4096) == 2 * 16 * 64 * 74496
-    assert lib.gdn2_hip_prefill_workspace_bytes(1, 2, 128, 100) == 1 * 2 * 2 * 74496
-    # dense DK = 128 calls of up to 16 key heads and at least 32 chunks use pair records
-    # (two chunks each, 123648 bytes)
-    assert lib.gdn2_hip_prefill_workspace_bytes(2, 8, 128, 4096) == 2 * 8 * 32 * 123648
-    assert lib.gdn2_hip_prefill_workspace_bytes(1, 2, 128, 2049) == 1 * 2 * 17 * 123648
-    assert lib.gdn2_hip_prefill_workspace_bytes(1, 2, 128, 1984) == 1 * 2 * 31 * 74496
-    assert lib.gdn2_hip_prefill_workspace_bytes(8, 16, 128, 4096) == 8 * 16 * 64 * 74496
+    # one record per (b, key head, 64-token chunk): 58112 bytes at DK=128 (factored
+    # transition form: E 16 KiB, KA 16, QP 16, MOZ 8, gamma_last, scales), 41472 at DK=64
+    assert lib.gdn2_hip_prefill_workspace_bytes(2, 16, 128, 4096) == 2 * 16 * 64 * 58112
+    assert lib.gdn2_hip_prefill_workspace_bytes(1, 2, 128, 100) == 1 * 2 * 2 * 58112
+    assert lib.gdn2_hip_prefill_workspace_bytes(2, 8, 128, 4096) == 2 * 8 * 64 * 58112
+    assert lib.gdn2_hip_prefill_workspace_bytes(1, 2, 128, 2049) == 1 * 2 * 33 * 58112
+    assert lib.gdn2_hip_prefill_workspace_bytes(8, 16, 128, 4096) == 8 * 16 * 64 * 58112
     assert lib.gdn2_hip_prefill_workspace_bytes(1, 2, 64, 100) == 1 * 2 * 2 * 41472
     assert lib.gdn2_hip_prefill_workspace_bytes(1, 2, 96, 64) == 0
 
@@ -99,7 +96,7 @@ def test_c_abi_rejects_bad_arguments_before_launch():
     assert lib.gdn2_hip_prefill_varlen(*args, 1, fake, 2, nul, fake, fake, 1, fake, 6, 4, 128, 128, 100, 0.1,
                                        nul) == -1
     # ceil(T / 64) + nseq record slots per key head, 64-token chunk records
-    assert lib.gdn2_hip_prefill_varlen_workspace_bytes(3, 2, 128, 100) == 2 * (2 + 3) * 74496
+    assert lib.gdn2_hip_prefill_varlen_workspace_bytes(3, 2, 128, 100) == 2 * (2 + 3) * 58112
     assert lib.gdn2_hip_prefill_varlen_workspace_bytes(0, 2, 128, 100) == 0
     lds = [256] * 6
     #                                               x*6    ld*6  dt conv_w conv_b K cin  cout a_log dtb  es

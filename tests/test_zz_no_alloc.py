@@ -46,7 +46,7 @@ def _inputs(B, S, H, HK, DK, DV, seed):
 
 
 @pytest.mark.parametrize("B,S,H,HK,DK,DV,seed", [(2, 1000, 4, 2, 128, 128, 0), (1, 300, 3, 3, 64, 96, 1),
-                                                (1, 2100, 4, 2, 128, 128, 2)])   # the last on pair records
+                                                (1, 2100, 4, 2, 128, 128, 2)])   # the last: 33 chunks of 2 key heads
 def test_noalloc_prefill_equals_workspace_prefill(B, S, H, HK, DK, DV, seed):
     print(f"noalloc prefill B={B} S={S} H={H} HK={HK} DK={DK} DV={DV}", flush=True)
     dev = _inputs(B, S, H, HK, DK, DV, seed)
