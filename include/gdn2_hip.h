@@ -60,11 +60,8 @@ int gdn2_hip_decode(const void* q, const void* k, const void* v, const float* g,
 
 /* Bytes of workspace gdn2_hip_chunk_local / gdn2_hip_prefill_chunks need for
  * n_tokens tokens (rounded up to whole 64-token chunks) of B x HK key heads; 0 for an unsupported
- * DK. One record per key head and chunk (74 496 B at DK = 128, 41 472 B at DK = 64), except that
- * dense DK = 128 calls of at most 16 key heads (B * HK <= 16) and at least 32 chunks use one
- * record per two consecutive chunks (123 648 B), which halves the scan's serial steps. Both stages
- * derive the form from (B, HK, DK, n_tokens), so they must be called with the same values. The
- * records depend on q, k, b, g only, so grouped value heads share them. */
+ * DK. One record per key head and chunk (58 112 B at DK = 128, 41 472 B at DK = 64). The records
+ * depend on q, k, b, g only, so grouped value heads share them. */
 size_t gdn2_hip_prefill_workspace_bytes(int B, int HK, int DK, long n_tokens);
 
 /*

@@ -4,11 +4,16 @@
   ragged tail, a second segment, a multi-token decode and single steps.
 * config 4: hidden 2048, 16 value heads over 8 key heads, DK=DV=128, bf16
   weights, a 32700-token prompt prefilled in 4 segments (cache passed back)
-  vs one-shot prefill, then 128 decode steps from each cache. The fp32
-  recurrent state must agree within 2e-3. The layer outputs are bf16 (gated
-  norm and o_proj run in bf16), so one bf16 rounding flip of an o element is
-  already 2^-8 relative; they are held to 1e-2. The op-level segmented ==
-  one-shot bar at 2e-3 on fp32 o is tests/test_gpu_prefill.py.
+  vs one-shot prefill, then 128 decode steps from each cache. Held to 2e-3:
+  the fp32 recurrent state, and the attention output before the gated norm
+  and o_proj recomputed in fp32 from the op inputs the bf16 layer produced
+  (bf16 values are exact in fp32, so this isolates the segmentation). The
+  bf16 attention output itself is held to 2^-7 (one bf16 rounding step of
+  its largest element is 2^-8 of max|o|; segment boundaries that are not
+  chunk-aligned change fp32 round-off and so can flip one rounding per
+  element on each side). Only the final layer output, which passes through
+  the bf16 gated norm and the bf16 o_proj GEMM (2048-term bf16 products with
+  a bf16 result), gets 1e-2.
 """
 
 from __future__ import annotations
@@ -17,6 +22,7 @@ import pytest
 import torch
 
 from gdt2_tilelang_amd import GatedDeltaNet2, GatedDeltaNet2Config
+from gdt2_tilelang_amd import attention as attention_mod
 from oracle import LayerOracle, rel_err
 
 pytestmark = pytest.mark.gpu
@@ -46,8 +52,17 @@ def test_fp32_layer_matches_oracle():
     assert rel_err(cache.recurrent_state.cpu(), rc[0]) < 2e-3
 
 
-def test_config4_segmented_prefill_then_decode():
+def test_config4_segmented_prefill_then_decode(monkeypatch):
     print("config 4 layer: 32700-token prompt in 4 segments + 128 decode steps", flush=True)
+    calls = []
+    real_prefill = attention_mod.gdn2_prefill
+
+    def recording_prefill(q, k, v, g, b, w, state=None, scale=None, **kw):
+        o, st = real_prefill(q, k, v, g, b, w, state, scale=scale, **kw)
+        calls.append(((q, k, v, g, b, w), scale, o))
+        return o, st
+
+    monkeypatch.setattr(attention_mod, "gdn2_prefill", recording_prefill)
     torch.manual_seed(0)
     cfg = GatedDeltaNet2Config(hidden_size=2048, num_heads=16, num_kv_heads=8,
                                head_dim_k=128, head_dim_v=128)
@@ -70,7 +85,22 @@ def test_config4_segmented_prefill_then_decode():
     e_pre, e_dec = rel_err(seg.float(), one.float()), rel_err(d2.float(), d1.float())
     e_st = rel_err(c2.recurrent_state, c1.recurrent_state)
     print(f"  segmented vs one-shot: prefill {e_pre:.2e} decode {e_dec:.2e} state {e_st:.2e}", flush=True)
-    assert e_st < 2e-3
+    assert len(calls) == 5                        # one-shot, then the 4 segments
+    o_one = calls[0][2]
+    o_seg = torch.cat([c[2] for c in calls[1:]], 1)
+    e_o16 = rel_err(o_seg.float(), o_one.float())
+    # the same op inputs in fp32: segmented vs one-shot attention output and state
+    f32 = lambda ins: [t.float() for t in ins]
+    ro, rs = real_prefill(*f32(calls[0][0]), None, scale=calls[0][1])
+    so, ss = [], None
+    for ins, scale, _ in calls[1:]:
+        o, ss = real_prefill(*f32(ins), ss, scale=scale)
+        so.append(o)
+    e_o32, e_s32 = rel_err(torch.cat(so, 1), ro), rel_err(ss, rs)
+    torch.cuda.synchronize()
+    print(f"  attention output: bf16 {e_o16:.2e}; fp32 recomputation o {e_o32:.2e} state {e_s32:.2e}", flush=True)
+    assert e_st < 2e-3 and e_o32 < 2e-3 and e_s32 < 2e-3
+    assert e_o16 < 2.0 ** -7
     assert e_pre < 1e-2 and e_dec < 1e-2
 
 
