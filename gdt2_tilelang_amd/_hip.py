@@ -45,6 +45,9 @@ SIGNATURES = {
     "gdn2_hip_backward_workspace_bytes": (_S, [_I, _I, _I, _I, _I, _L]),
     "gdn2_hip_backward": (_I, [_P, _P, _P, _P, _P, _P, _I, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P, _P,
                                _I, _L, _I, _I, _I, _I, _P]),
+    "gdn2_hip_backward_varlen_workspace_bytes": (_S, [_I, _I, _I, _I, _I, _L]),
+    "gdn2_hip_backward_varlen": (_I, [_P, _P, _P, _P, _P, _P, _I, _F, _P, _P, _I, _P, _P, _P, _P, _P, _P, _P, _P,
+                                      _P, _P, _I, _L, _I, _I, _I, _I, _P]),
     "gdn2_hip_layer_decode": (_I, [_P, _P, _P, _P, _I, _P, _P, _P, _P, _F, _P, _P, _F, _P, _P, _P, _I, _I,
                                    _I, _I, _I, _I, _I, _I, _F, _P]),
 }

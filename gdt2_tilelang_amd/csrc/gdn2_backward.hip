@@ -72,6 +72,23 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // inside the branch); rows past the end are then zeroed by the caller.
 __device__ __forceinline__ long clamp_row(long t, long S) { return t < S ? t : S - 1; }
 
+// The tokens [t0, tend) of one chunk's workgroup. Dense batches: chunk c of
+// batch row bi, tend = S. Packed sequences (vl.cu, one batch row of S tokens):
+// c is a record slot (the forward's slot map, gdn2_prefill_layout.h), t0 its
+// chunk's first token and tend its sequence's end; a slot between two
+// sequences holds no chunk (live = false).
+struct ChunkWin {
+  long t0, tend;
+  bool live;
+};
+__device__ __forceinline__ ChunkWin chunk_win(int c, long S, Varlen vl) {
+  if (!vl.cu) return {static_cast<long>(c) * L, S, true};
+  const int sq = varlen_seq(vl.cu, vl.nseq, S, c);
+  const long a = varlen_off(vl.cu, sq, S), e = varlen_off(vl.cu, sq + 1, S);
+  const long t0 = a + (c - (sq + a / L)) * L;
+  return {t0, e, t0 < e};
+}
+
 __device__ __forceinline__ size_t key_index(int bi, long S, long t, int HK, int hk, int DK, int i) {
   return ((static_cast<size_t>(bi) * S + t) * HK + hk) * DK + i;
 }
@@ -124,7 +141,7 @@ template <int DK>
 __global__ __launch_bounds__(kLocalThreads) void bwd_local_kernel(const float* __restrict__ q, const float* __restrict__ k,
                                                              const float* __restrict__ b, const float* __restrict__ g,
                                                              int HK, long S, int NC, float scale,
-                                                             float* __restrict__ rec) {
+                                                             float* __restrict__ rec, Varlen vl) {
   constexpr int P = DK + 4;
   constexpr int LT = kLocalThreads, NW = LT / 64;   // threads, waves
   constexpr int NV = (3 * 256 + LT - 1) / LT;      // inverse entries per thread and round
@@ -141,15 +158,17 @@ __global__ __launch_bounds__(kLocalThreads) void bwd_local_kernel(const float* _
   const int tid = threadIdx.x;
   const int c = blockIdx.x, bhk = blockIdx.y;
   const int bi = bhk / HK, hk = bhk % HK;
-  const long t0 = static_cast<long>(c) * L;
+  const ChunkWin win = chunk_win(c, S, vl);
+  if (!win.live) return;
+  const long t0 = win.t0, tend = win.tend;
   float* rc = rec + (static_cast<size_t>(bhk) * NC + c) * R::STRIDE;
 
 #pragma unroll
   for (int e0 = 0; e0 < L * DK; e0 += LT) {
     const int e = e0 + tid;       // rows past the sequence are zeros (inert)
     const int t = e / DK, i = e % DK;
-    const size_t ix = key_index(bi, S, clamp_row(t0 + t, S), HK, hk, DK, i);
-    const float keep = t0 + t < S ? 1.f : 0.f;
+    const size_t ix = key_index(bi, S, clamp_row(t0 + t, tend), HK, hk, DK, i);
+    const float keep = t0 + t < tend ? 1.f : 0.f;
     const float qv = keep * q[ix], kv = keep * k[ix], bv = keep * b[ix], gv = keep * g[ix];
     sq[t * P + i] = qv;
     sk[t * P + i] = kv;
@@ -396,7 +415,7 @@ template <int DK, bool BACK, int NBUF>
 __device__ __forceinline__ void scan_body(const float* __restrict__ x1, const float* __restrict__ x2,
                                           const float* __restrict__ rec, const float* __restrict__ init,
                                           float* __restrict__ ck, float* __restrict__ fin, int H, int HK, int DV,
-                                          long S, int NC, int lb, int nblk) {
+                                          long S, int NC, int lb, int nblk, Varlen vl) {
   static_assert(NBUF >= 1 && NBUF <= 3, "one to three register sets");
   using R = Rec<DK>;
   using C = ScanCfg<DK>;
@@ -421,15 +440,29 @@ __device__ __forceinline__ void scan_body(const float* __restrict__ x1, const fl
   const int bi = bhk / HK, hk = bhk % HK, h = hk * rep + rr / ntile, bh = bi * H + h;
   const int c0 = (rr % ntile) * CT;
   const bool computes = C::TILES >= 4 || wave * C::TPW < C::TILES;   // DK = 32: two waves hold the tiles
-  const float* rbase = rec + static_cast<size_t>(bi * HK + hk) * NC * R::STRIDE;
-  auto chunk_of = [&](int step) { return BACK ? NC - 1 - step : step; };
+  // the chunks this workgroup walks: dense, NC chunks of batch row bi; packed
+  // sequences (vl.cu), the chunks of sequence bi, record and checkpoint slots
+  // slot0 .. slot0 + nloop - 1 of its head, tokens [tbase, tend) of row 0
+  long tbase = 0, tend = S;
+  int nloop = NC, slot0 = 0, bit = bi, bck = bh;
+  if (vl.cu) {
+    const long a = varlen_off(vl.cu, bi, S), e = varlen_off(vl.cu, bi + 1, S);
+    tbase = a;
+    tend = e;
+    nloop = static_cast<int>((e - a + L - 1) / L);
+    slot0 = bi + static_cast<int>(a / L);
+    bit = 0;
+    bck = h;
+  }
+  const float* rbase = rec + (static_cast<size_t>(bit * HK + hk) * NC + slot0) * R::STRIDE;
+  auto chunk_of = [&](int step) { return BACK ? nloop - 1 - step : step; };
 #pragma unroll
   for (int e0 = 0; e0 < DK * CT; e0 += kThreads) {
     const int e = e0 + tid;
     const int r = e / CT, cl = e % CT;
     const float x = init ? init[(static_cast<size_t>(bh) * DK + r) * DV + c0 + cl] : 0.f;
     sX[r * C::XP + cl] = x;
-    if (NC > 0) ck[((static_cast<size_t>(bh) * NC + chunk_of(0)) * DK + r) * DV + c0 + cl] = x;   // first chunk's entry value
+    if (nloop > 0) ck[((static_cast<size_t>(bck) * NC + slot0 + chunk_of(0)) * DK + r) * DV + c0 + cl] = x;   // first chunk's entry value
   }
   f32x4 aA0[C::TPW][C::KA_ / 4], aZ0[C::TPW][C::KZ / 4], aA1[C::TPW][C::KA_ / 4], aZ1[C::TPW][C::KZ / 4], aA2[C::TPW][C::KA_ / 4], aZ2[C::TPW][C::KZ / 4];
   auto fetch_m = [&](int c, f32x4 (&aA)[C::TPW][C::KA_ / 4], f32x4 (&aZ)[C::TPW][C::KZ / 4]) {
@@ -452,9 +485,9 @@ __device__ __forceinline__ void scan_body(const float* __restrict__ x1, const fl
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
       const int e = tid + n * kThreads, t = e / CT, cl = e % CT;
-      const long tok = static_cast<long>(c) * L + t;
-      const size_t ix = ((static_cast<size_t>(bi) * S + clamp_row(tok, S)) * H + h) * DV + c0 + cl;
-      pk1[n] = tok < S ? 1.f : 0.f;
+      const long tok = tbase + static_cast<long>(c) * L + t;
+      const size_t ix = ((static_cast<size_t>(bit) * S + clamp_row(tok, tend)) * H + h) * DV + c0 + cl;
+      pk1[n] = tok < tend ? 1.f : 0.f;
       p1[n] = x1[ix];
       p2[n] = BACK ? 0.f : x2[ix];
     }
@@ -469,8 +502,8 @@ __device__ __forceinline__ void scan_body(const float* __restrict__ x1, const fl
       sZ[(e / CT) * C::XP + e % CT] = pk1[n] * (BACK ? p1[n] : p1[n] * p2[n]);
     }
     {                            // the token values first: the next step's staging waits only for them;
-      fetch_z(chunk_of(step + 1 < NC ? step + 1 : NC - 1));
-      if constexpr (NBUF > 1) fetch_m(chunk_of(step + NBUF - 1 < NC ? step + NBUF - 1 : NC - 1), nA, nZ);
+      fetch_z(chunk_of(step + 1 < nloop ? step + 1 : nloop - 1));
+      if constexpr (NBUF > 1) fetch_m(chunk_of(step + NBUF - 1 < nloop ? step + NBUF - 1 : nloop - 1), nA, nZ);
     }
     lds_barrier();
     f32x4 acc[C::TPW];
@@ -492,15 +525,15 @@ __device__ __forceinline__ void scan_body(const float* __restrict__ x1, const fl
                                                           acc[r], 0, 0, 0);
       }
     }
-    if constexpr (NBUF == 1) fetch_m(chunk_of(step + 1 < NC ? step + 1 : NC - 1), nA, nZ);   // nA is aA: read
+    if constexpr (NBUF == 1) fetch_m(chunk_of(step + 1 < nloop ? step + 1 : nloop - 1), nA, nZ);   // nA is aA: read
     lds_barrier();                              // every wave has read X
     if (computes) {
 #pragma unroll
       for (int r = 0; r < C::TPW; ++r)
 #pragma unroll
         for (int e = 0; e < 4; ++e) sX[(16 * (wave * C::TPW + r) + 4 * g + e) * C::XP + m] = acc[r][e];
-      if (step + 1 < NC) {                      // the next chunk's entry value, from registers
-        float* out = ck + (static_cast<size_t>(bh) * NC + chunk_of(step + 1)) * DK * DV + c0 + m;
+      if (step + 1 < nloop) {                   // the next chunk's entry value, from registers
+        float* out = ck + (static_cast<size_t>(bck) * NC + slot0 + chunk_of(step + 1)) * DK * DV + c0 + m;
 #pragma unroll
         for (int r = 0; r < C::TPW; ++r)
 #pragma unroll
@@ -508,24 +541,24 @@ __device__ __forceinline__ void scan_body(const float* __restrict__ x1, const fl
       }
     }
   };
-  if (NC > 0) {
+  if (nloop > 0) {
     fetch_z(chunk_of(0));
     fetch_m(chunk_of(0), aA0, aZ0);
-    if constexpr (NBUF == 3) fetch_m(chunk_of(NC > 1 ? 1 : 0), aA1, aZ1);
+    if constexpr (NBUF == 3) fetch_m(chunk_of(nloop > 1 ? 1 : 0), aA1, aZ1);
   }
   if constexpr (NBUF == 3) {
-    for (int step = 0; step < NC; step += 3) {
+    for (int step = 0; step < nloop; step += 3) {
       run(step, aA0, aZ0, aA2, aZ2);
-      if (step + 1 < NC) run(step + 1, aA1, aZ1, aA0, aZ0);
-      if (step + 2 < NC) run(step + 2, aA2, aZ2, aA1, aZ1);
+      if (step + 1 < nloop) run(step + 1, aA1, aZ1, aA0, aZ0);
+      if (step + 2 < nloop) run(step + 2, aA2, aZ2, aA1, aZ1);
     }
   } else if constexpr (NBUF == 2) {
-    for (int step = 0; step < NC; step += 2) {
+    for (int step = 0; step < nloop; step += 2) {
       run(step, aA0, aZ0, aA1, aZ1);
-      if (step + 1 < NC) run(step + 1, aA1, aZ1, aA0, aZ0);
+      if (step + 1 < nloop) run(step + 1, aA1, aZ1, aA0, aZ0);
     }
   } else {
-    for (int step = 0; step < NC; ++step) run(step, aA0, aZ0, aA0, aZ0);
+    for (int step = 0; step < nloop; ++step) run(step, aA0, aZ0, aA0, aZ0);
   }
   __syncthreads();
   if (fin) {
@@ -543,7 +576,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     const float* __restrict__ x1, const float* __restrict__ x2, const float* __restrict__ rec,
     const float* __restrict__ init, float* __restrict__ ck, float* __restrict__ fin, int H, int HK, int DV, long S,
     int NC) {
-  scan_body<DK, BACK, 3>(x1, x2, rec, init, ck, fin, H, HK, DV, S, NC, blockIdx.x, gridDim.x);
+  scan_body<DK, BACK, 3>(x1, x2, rec, init, ck, fin, H, HK, DV, S, NC, blockIdx.x, gridDim.x, Varlen{nullptr, 0});
 }
 
 // Both scans in one launch: they read only the records and their own inputs,
@@ -555,12 +588,12 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))
     const float* __restrict__ v, const float* __restrict__ w, const float* __restrict__ dout,
     const float* __restrict__ rec, const float* __restrict__ s0, const float* __restrict__ dht,
     float* __restrict__ sck, float* __restrict__ dsck, float* __restrict__ ds0, int H, int HK, int DV, long S,
-    int NC) {
+    int NC, Varlen vl) {
   const int half = gridDim.x / 2;
   if (static_cast<int>(blockIdx.x) < half)
-    scan_body<DK, false, 1>(v, w, rec, s0, sck, nullptr, H, HK, DV, S, NC, blockIdx.x, half);
+    scan_body<DK, false, 1>(v, w, rec, s0, sck, nullptr, H, HK, DV, S, NC, blockIdx.x, half, vl);
   else
-    scan_body<DK, true, 1>(dout, nullptr, rec, dht, dsck, ds0, H, HK, DV, S, NC, blockIdx.x - half, half);
+    scan_body<DK, true, 1>(dout, nullptr, rec, dht, dsck, ds0, H, HK, DV, S, NC, blockIdx.x - half, half, vl);
 }
 
 // ---------------------------------------------------------------- kernel 4
@@ -594,7 +627,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     const float* __restrict__ k, const float* __restrict__ v, const float* __restrict__ g, const float* __restrict__ b,
     const float* __restrict__ w, int dt, const float* __restrict__ dout, const float* __restrict__ rec,
     const float* __restrict__ sck, const float* __restrict__ dsck, void* __restrict__ dv, void* __restrict__ dw,
-    float* __restrict__ gs, int H, int HK, int DV, long S, int NC) {
+    float* __restrict__ gs, int H, int HK, int DV, long S, int NC, Varlen vl) {
   constexpr int XP = CT + 1;          // LDS pitch of the 16-column arrays
   constexpr int KD = DK / 4;          // k steps per lane group over DK
   constexpr int KL = L / 4;           // over the 64 rows
@@ -611,7 +644,9 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   const int gq = lane >> 4, m = lane & 15;
   const int c = blockIdx.x, bh = blockIdx.y;
   const int bi = bh / H, h = bh % H, hk = h / (H / HK);
-  const long t0 = static_cast<long>(c) * L;
+  const ChunkWin win = chunk_win(c, S, vl);
+  if (!win.live) return;
+  const long t0 = win.t0, tend = win.tend;
   const float* rc = rec + (static_cast<size_t>(bi * HK + hk) * NC + c) * R::STRIDE;
   const float* Sc = sck + (static_cast<size_t>(bh) * NC + c) * DK * DV;
   const float* dSc = dsck + (static_cast<size_t>(bh) * NC + c) * DK * DV;
@@ -622,7 +657,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   for (int e0 = 0; e0 < L * DK; e0 += kThreads) {
     const int e = e0 + tid;
     const int t = e / DK, i = e % DK;
-    sG[e] = (t0 + t < S ? 1.f : 0.f) * g[key_index(bi, S, clamp_row(t0 + t, S), HK, hk, DK, i)];
+    sG[e] = (t0 + t < tend ? 1.f : 0.f) * g[key_index(bi, S, clamp_row(t0 + t, tend), HK, hk, DK, i)];
   }
   __syncthreads();
   rows_scan<false>(sG, DK, DK, sScan);
@@ -631,8 +666,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   for (int e0 = 0; e0 < L * DK; e0 += kThreads) {
     const int e = e0 + tid;
     const int t = e / DK, i = e % DK;
-    const size_t ix = key_index(bi, S, clamp_row(t0 + t, S), HK, hk, DK, i);
-    const float keep = t0 + t < S ? 1.f : 0.f;
+    const size_t ix = key_index(bi, S, clamp_row(t0 + t, tend), HK, hk, DK, i);
+    const float keep = t0 + t < tend ? 1.f : 0.f;
     const float kv = keep * k[ix], bv = keep * b[ix];
     const float gt = sG[t * DK + i];
     const int o = t * EP + (i / KD) * (KD + 1) + i % KD;
@@ -673,14 +708,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
     for (int n = 0; n < NTE; ++n) {
       const int e = tid + n * kThreads, t = e / CT, cl = e % CT;
-      kO[n] = t0 + t < S ? 1.f : 0.f;
-      pO[n] = dout[((static_cast<size_t>(bi) * S + clamp_row(t0 + t, S)) * H + h) * DV + cb + cl];
+      kO[n] = t0 + t < tend ? 1.f : 0.f;
+      pO[n] = dout[((static_cast<size_t>(bi) * S + clamp_row(t0 + t, tend)) * H + h) * DV + cb + cl];
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int t = 16 * wave + 4 * gq + e;
-      const size_t ix = ((static_cast<size_t>(bi) * S + clamp_row(t0 + t, S)) * H + h) * DV + cb + m;
-      kVW[e] = t0 + t < S ? 1.f : 0.f;
+      const size_t ix = ((static_cast<size_t>(bi) * S + clamp_row(t0 + t, tend)) * H + h) * DV + cb + m;
+      kVW[e] = t0 + t < tend ? 1.f : 0.f;
       pV[e] = v[ix];
       pW[e] = w[ix];
     }
@@ -742,7 +777,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
       for (int e = 0; e < 4; ++e) {
         const int t = 16 * wave + 4 * gq + e;
         sdY[t * XP + m] = -dy[e];
-        if (t0 + t < S) {
+        if (t0 + t < tend) {
           const size_t ix = ((static_cast<size_t>(bi) * S + t0 + t) * H + h) * DV + cb + m;
           store_elem(dv, ix, dt, ww[e] * dy[e]);
           store_elem(dw, ix, dt, vv[e] * dy[e]);
@@ -802,7 +837,8 @@ template <int DK>
 __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
     const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ g, const float* __restrict__ b,
     const float* __restrict__ gs, float* __restrict__ part, void* __restrict__ odq, void* __restrict__ odk,
-    void* __restrict__ odb, float* __restrict__ odg, int dt, int H, int HK, long S, int NC, float scale) {
+    void* __restrict__ odb, float* __restrict__ odg, int dt, int H, int HK, long S, int NC, float scale,
+    Varlen vl) {
   // one value head per key head: the shares are the gradients and go straight
   // to the outputs (dtype dt, dg fp32); otherwise to the fp32 planes of part
   const bool direct = H == HK;
@@ -827,15 +863,17 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
     cb = lb % NB;
   }
   const int c = u % NC, bh = u / NC, bi = bh / H, h = bh % H, hk = h / (H / HK);
-  const long t0 = static_cast<long>(c) * L;
+  const ChunkWin win = chunk_win(c, S, vl);
+  if (!win.live) return;
+  const long t0 = win.t0, tend = win.tend;
   const float* src = gs + (static_cast<size_t>(bh) * NC + c) * G::STRIDE;
   const int i0 = cb * CW;
 #pragma unroll
   for (int e0 = 0; e0 < L * CW; e0 += kThreads) {
     const int e = e0 + tid;
     const int t = e / CW, ii = e % CW;
-    const size_t ix = key_index(bi, S, clamp_row(t0 + t, S), HK, hk, DK, i0 + ii);
-    const float keep = t0 + t < S ? 1.f : 0.f;
+    const size_t ix = key_index(bi, S, clamp_row(t0 + t, tend), HK, hk, DK, i0 + ii);
+    const float keep = t0 + t < tend ? 1.f : 0.f;
     const float qv = keep * q[ix], kv = keep * k[ix], bv = keep * b[ix], gv = keep * g[ix];
     pq[t * PWP + ii] = qv;
     pk[t * PWP + ii] = kv;
@@ -943,7 +981,7 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
   for (int r = 0; r < EPT; ++r) {
     const int t = tp + TS * r;
     const float qv = pq[t * PWP + ii], kv = pk[t * PWP + ii], bkv = pbk[t * PWP + ii];
-    const bool valid = t0 + t < S;
+    const bool valid = t0 + t < tend;
     const float bv = valid ? b[key_index(bi, S, t0 + t, HK, hk, DK, i)] : 0.f;
     const float ga = __builtin_amdgcn_exp2f(gt[r]), gd = __builtin_amdgcn_exp2f(kLog2e * gl - gt[r]);
     const float fQg = src[G::QG + t * DK + i], fE = src[G::E + t * DK + i], fKG = src[G::KG + t * DK + i];
@@ -986,7 +1024,7 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
     for (int e0 = 0; e0 < L * CW; e0 += kThreads) {
       const int e = e0 + tid, t = e / CW, ii = e % CW;
       const size_t ix = ((static_cast<size_t>(bi) * S + t0 + t) * H + h) * DK + i0 + ii;
-      if (t0 + t < S) (direct ? odg : part + 3 * plane)[ix] = pq[t * PWP + ii];
+      if (t0 + t < tend) (direct ? odg : part + 3 * plane)[ix] = pq[t * PWP + ii];
     }
   }
 }
@@ -1066,8 +1104,9 @@ __global__ __launch_bounds__(kThreads) void bwd_sum_kernel(const float* __restri
 
 }  // namespace bw
 
-size_t backward_workspace_bytes(int B, int H, int HK, int DK, int DV, long S) {
-  const long NC = (S + bw::L - 1) / bw::L;
+// NC chunk records per (batch row, key head): ceil(S / 64) for a dense batch;
+// for packed sequences (B = 1 row of S tokens) the forward's slot count.
+static size_t backward_ws(int B, int H, int HK, int DK, int DV, long S, long NC) {
   long stride = 0;
   if (DK == 32) stride = bw::Rec<32>::STRIDE;
   else if (DK == 64) stride = bw::Rec<64>::STRIDE;
@@ -1084,22 +1123,35 @@ size_t backward_workspace_bytes(int B, int H, int HK, int DK, int DV, long S) {
   return rec + 2 * ck + part + gsb + wide;
 }
 
+size_t backward_workspace_bytes(int B, int H, int HK, int DK, int DV, long S) {
+  return backward_ws(B, H, HK, DK, DV, S, (S + bw::L - 1) / bw::L);
+}
+
+size_t backward_varlen_workspace_bytes(int nseq, int H, int HK, int DK, int DV, long T) {
+  return backward_ws(1, H, HK, DK, DV, T, (T + bw::L - 1) / bw::L + nseq);
+}
+
 namespace {
 template <int DK>
 hipError_t launch_backward_t(const void* q, const void* k, const void* v, const float* g, const void* b,
                              const void* w, int dt, float scale, const float* s0, const void* dout, int do_dt,
                              const float* dht, void* dq, void* dk, void* dv, float* dg, void* db, void* dw,
-                             float* ds0, void* workspace, int B, int H, int HK, int DV, long S, hipStream_t stream) {
-  const int NC = static_cast<int>((S + bw::L - 1) / bw::L);
+                             float* ds0, void* workspace, int B, int H, int HK, int DV, long S, hipStream_t stream,
+                             Varlen vl = Varlen{nullptr, 0}) {
+  // dense: B rows of S tokens, NC chunks each; packed (vl.cu): one row of S
+  // tokens, vl.nseq sequences, NC record slots per head, the scans run per
+  // (sequence, value head, tile) and the state arrays hold nseq rows
+  const int NC = static_cast<int>((S + bw::L - 1) / bw::L) + (vl.cu ? vl.nseq : 0);
+  const int NSQ = vl.cu ? vl.nseq : B;   // state rows
   constexpr int lds1 = bw::local_lds_floats<DK>() * 4;
   static std::atomic<unsigned long long> lds_set{0};   // per device
   {
     const hipError_t e = set_dyn_lds_once(reinterpret_cast<const void*>(&bw::bwd_local_kernel<DK>), lds1, lds_set);
     if (e != hipSuccess) return e;
   }
-  if (NC == 0) {   // no tokens: the initial-state gradient is the final-state one (or zero)
+  if (S == 0) {   // no tokens: the initial-state gradient is the final-state one (or zero)
     if (ds0)
-      hipLaunchKernelGGL((bw::bwd_scan_kernel<DK, true>), dim3(DV / bw::CT * B * H), dim3(bw::kThreads), 0, stream,
+      hipLaunchKernelGGL((bw::bwd_scan_kernel<DK, true>), dim3(DV / bw::CT * NSQ * H), dim3(bw::kThreads), 0, stream,
                          nullptr, nullptr, nullptr, dht, nullptr, ds0, H, HK, DV, S, 0);
     return hipGetLastError();
   }
@@ -1142,14 +1194,14 @@ hipError_t launch_backward_t(const void* q, const void* k, const void* v, const 
     hipLaunchKernelGGL(bw::bwd_widen_kernel, dim3(jobs.first[jobs.njobs]), dim3(bw::kThreads), 0, stream, jobs);
 
   hipLaunchKernelGGL(bw::bwd_local_kernel<DK>, dim3(NC, B * HK), dim3(bw::kLocalThreads), lds1, stream, qf, kf, bf, g,
-                     HK, S, NC, scale, rec);
-  hipLaunchKernelGGL(bw::bwd_scan2_kernel<DK>, dim3(2 * (DV / bw::CT) * B * H), dim3(bw::kThreads), 0, stream, vf,
-                     wf, of, rec, s0, dht, sck, dsck, ds0, H, HK, DV, S, NC);
+                     HK, S, NC, scale, rec, vl);
+  hipLaunchKernelGGL(bw::bwd_scan2_kernel<DK>, dim3(2 * (DV / bw::CT) * NSQ * H), dim3(bw::kThreads), 0, stream, vf,
+                     wf, of, rec, s0, dht, sck, dsck, ds0, H, HK, DV, S, NC, vl);
   hipLaunchKernelGGL(bw::bwd_gradmm_kernel<DK>, dim3(NC, B * H), dim3(bw::kThreads), 0, stream, kf, vf, g, bf, wf, dt,
-                     of, rec, sck, dsck, dv, dw, gsc, H, HK, DV, S, NC);
+                     of, rec, sck, dsck, dv, dw, gsc, H, HK, DV, S, NC, vl);
   constexpr int NB = DK / bw::PWC > 0 ? DK / bw::PWC : 1;
   hipLaunchKernelGGL(bw::bwd_gradpw_kernel<DK>, dim3(NC * NB * B * H), dim3(bw::kThreads), 0, stream, qf, kf, g, bf,
-                     gsc, part, dq, dk, db, dg, dt, H, HK, S, NC, scale);
+                     gsc, part, dq, dk, db, dg, dt, H, HK, S, NC, scale, vl);
   if (H == HK) return hipGetLastError();   // the pairwise pass wrote the outputs
   const long n_key = static_cast<long>(B) * S * HK * DK;
   hipLaunchKernelGGL(bw::bwd_sum_kernel, dim3(static_cast<unsigned>((n_key + bw::kThreads - 1) / bw::kThreads)),
@@ -1168,6 +1220,22 @@ hipError_t launch_backward(const void* q, const void* k, const void* v, const fl
   if (DK == DKV)                                                                                             \
     return launch_backward_t<DKV>(q, k, v, g, b, w, dt, scale, s0, dout, do_dt, dht, dq, dk, dv, dg, db, dw, \
                                   ds0, workspace, B, H, HK, DV, S, stream);
+  GDN2_BWD(32) GDN2_BWD(64) GDN2_BWD(128)
+#undef GDN2_BWD
+  return hipErrorInvalidValue;
+}
+
+hipError_t launch_backward_varlen(const void* q, const void* k, const void* v, const float* g, const void* b,
+                                  const void* w, int dt, float scale, const float* s0, const void* dout, int do_dt,
+                                  const float* dht, void* dq, void* dk, void* dv, float* dg, void* db, void* dw,
+                                  float* ds0, void* workspace, const int* cu, int nseq, int H, int HK, int DK,
+                                  int DV, long T, hipStream_t stream) {
+  if (DV % bw::CT) return hipErrorInvalidValue;
+  const Varlen vl{cu, nseq};
+#define GDN2_BWD(DKV)                                                                                        \
+  if (DK == DKV)                                                                                             \
+    return launch_backward_t<DKV>(q, k, v, g, b, w, dt, scale, s0, dout, do_dt, dht, dq, dk, dv, dg, db, dw, \
+                                  ds0, workspace, 1, H, HK, DV, T, stream, vl);
   GDN2_BWD(32) GDN2_BWD(64) GDN2_BWD(128)
 #undef GDN2_BWD
   return hipErrorInvalidValue;

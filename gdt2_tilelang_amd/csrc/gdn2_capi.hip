@@ -18,6 +18,11 @@ size_t backward_workspace_bytes(int, int, int, int, int, long);
 hipError_t launch_backward(const void*, const void*, const void*, const float*, const void*, const void*, int, float,
                            const float*, const void*, int, const float*, void*, void*, void*, float*, void*, void*,
                            float*, void*, int, int, int, int, int, long, hipStream_t);
+size_t backward_varlen_workspace_bytes(int, int, int, int, int, long);
+hipError_t launch_backward_varlen(const void*, const void*, const void*, const float*, const void*, const void*, int,
+                                  float, const float*, const void*, int, const float*, void*, void*, void*, float*,
+                                  void*, void*, float*, void*, const int*, int, int, int, int, int, long,
+                                  hipStream_t);
 }  // namespace gdn2
 
 namespace {
@@ -371,6 +376,40 @@ int gdn2_hip_backward(const void* q, const void* k, const void* v, const float* 
   return status(gdn2::launch_backward(q, k, v, g, b, w, in_dtype, scale, initial_state, d_out, do_dtype,
                                       d_final_state, dq, dk, dv, dg, db, dw, d_initial_state, workspace, B, H, HK,
                                       DK, DV, S, static_cast<hipStream_t>(stream)));
+}
+
+static int backward_varlen_shape(int nseq, long T, int H, int HK, int DK, int DV) {
+  if (nseq < 1 || T < 0 || H < 1 || HK < 1 || H % HK) return GDN2_ERR_ARG;
+  if (DK != 32 && DK != 64 && DK != 128) return GDN2_ERR_SHAPE;
+  if (DV < 16 || DV % 16 || DV > 4096) return GDN2_ERR_SHAPE;
+  const long NC = varlen_slots(nseq, T);
+  if (NC > 0x7fffffffL / 4 || H > 65535) return GDN2_ERR_SHAPE;
+  if (NC * (DK / 32) * H > 0x7fffffffL) return GDN2_ERR_SHAPE;   // pairwise pass: one-dimensional grid
+  if (static_cast<long>(nseq) * H * (DV / 16) * 2 > 0x7fffffffL) return GDN2_ERR_SHAPE;   // scan grid
+  if (T * HK * DK > 0x7fffffffL) return GDN2_ERR_SHAPE;
+  return 0;
+}
+
+size_t gdn2_hip_backward_varlen_workspace_bytes(int nseq, int H, int HK, int DK, int DV, long T) {
+  if (backward_varlen_shape(nseq, T, H, HK, DK, DV)) return 0;
+  return gdn2::backward_varlen_workspace_bytes(nseq, H, HK, DK, DV, T);
+}
+
+int gdn2_hip_backward_varlen(const void* q, const void* k, const void* v, const float* g, const void* b,
+                             const void* w, int in_dtype, float scale, const float* initial_state,
+                             const void* d_out, int do_dtype, const float* d_final_state, void* dq, void* dk,
+                             void* dv, float* dg, void* db, void* dw, float* d_initial_state, void* workspace,
+                             const int* cu_seqlens, int nseq, long T, int H, int HK, int DK, int DV,
+                             void* stream) {
+  if (!dtype_ok(in_dtype) || !dtype_ok(do_dtype)) return GDN2_ERR_ARG;
+  if (int e = backward_varlen_shape(nseq, T, H, HK, DK, DV)) return e;
+  if (!cu_seqlens) return GDN2_ERR_ARG;
+  if (T > 0 && (!q || !k || !v || !g || !b || !w || !d_out || !dq || !dk || !dv || !dg || !db || !dw || !workspace))
+    return GDN2_ERR_ARG;
+  if (reinterpret_cast<uintptr_t>(workspace) % 256) return GDN2_ERR_ARG;
+  return status(gdn2::launch_backward_varlen(q, k, v, g, b, w, in_dtype, scale, initial_state, d_out, do_dtype,
+                                             d_final_state, dq, dk, dv, dg, db, dw, d_initial_state, workspace,
+                                             cu_seqlens, nseq, H, HK, DK, DV, T, static_cast<hipStream_t>(stream)));
 }
 
 }  // extern "C"

@@ -175,29 +175,47 @@ def chunk_gdn2_bwd(q, k, v, g, b, w, scale, initial_state, do, dht, config: GDN2
 def chunk_gdn2_varlen_bwd(q, k, v, g, b, w, scale, cu_seqlens, initial_state, do, dht,
                           config: GDN2Config = DEFAULT_KERNEL_CONFIG):
     """Backward of ``chunk_gdn2_varlen_fwd``: each packed sequence is an
-    independent recurrence, so its gradients are ``chunk_gdn2_bwd`` of its own
-    tokens (one gdn2_hip_backward call per sequence; an empty sequence passes
-    its final-state gradient through to its initial state).
+    independent recurrence and gets the gradients of its own tokens and
+    initial state (an empty sequence passes its final-state gradient through
+    to its initial state). All sequences run in one ``gdn2_hip_backward_varlen``
+    call: the per-chunk kernels take the forward's record slots and the scans
+    run per (sequence, value head, column tile).
 
     Returns ``(dq, dk, dv, dg, db, dw, dinitial_state [N, H, DK, DV] or None)``.
     """
     dev = _require_device(q, k, v, g, b, w, do)
     _check_shapes(q, k, v, g, b, w)
-    T = q.shape[1]
-    cu = check_cu_seqlens(cu_seqlens, T).tolist()
-    N = len(cu) - 1
-    grads = [torch.zeros_like(t) for t in (q, k, v)] + [torch.zeros_like(g)] + [torch.zeros_like(t) for t in (b, w)]
-    ds0 = None if initial_state is None else torch.empty_like(initial_state)
-    for i in range(N):
-        a, e = cu[i], cu[i + 1]
-        piece = lambda t: t[:, a:e]
-        s0 = None if initial_state is None else initial_state[i:i + 1]
-        dh = None if dht is None else dht[i:i + 1]
-        if e == a and s0 is None:
-            continue
-        res = chunk_gdn2_bwd(*(piece(t) for t in (q, k, v, g, b, w)), scale, s0, piece(do), dh, config)
-        for full, part in zip(grads, res[:6]):
-            full[:, a:e] = part
-        if ds0 is not None:
-            ds0[i:i + 1] = res[6]
-    return (*grads, ds0)
+    B, T, HK, DK = q.shape
+    H, DV = v.shape[2], v.shape[3]
+    if B != 1:
+        raise ValueError(f"packed sequences (cu_seqlens) need batch size 1; got {B}")
+    if DK not in (32, 64, 128) or DV % 16:
+        raise ValueError(f"hip backward supports DK in (32, 64, 128) and DV % 16 == 0; got DK={DK}, DV={DV}")
+    if tuple(do.shape) != (1, T, H, DV):
+        raise ValueError(f"do has shape {tuple(do.shape)}, expected {(1, T, H, DV)}")
+    cu = check_cu_seqlens(cu_seqlens, T).to(dev)
+    N = cu.numel() - 1
+    scale = DK ** -0.5 if scale is None else scale
+    q, k, v, b, w, do = (t.contiguous() for t in (q, k, v, b, w, do))
+    g32 = g.float().contiguous()
+    s0 = None
+    if initial_state is not None:
+        _require_device(q, initial_state)
+        if tuple(initial_state.shape) != (N, H, DK, DV):
+            raise ValueError(f"initial_state has shape {tuple(initial_state.shape)}, expected {(N, H, DK, DV)}")
+        s0 = initial_state.to(config.state_dtype).to(torch.float32).contiguous()
+    dht32 = None if dht is None else dht.to(torch.float32).contiguous()
+    dq, dk, db = (torch.empty(1, T, HK, DK, dtype=q.dtype, device=dev) for _ in range(3))
+    dv, dw = (torch.empty(1, T, H, DV, dtype=q.dtype, device=dev) for _ in range(2))
+    dg = torch.empty(1, T, HK, DK, dtype=torch.float32, device=dev)
+    ds0 = None if s0 is None else torch.empty(N, H, DK, DV, dtype=torch.float32, device=dev)
+    lib = _hip.lib()
+    ws = torch.empty(max(lib.gdn2_hip_backward_varlen_workspace_bytes(N, H, HK, DK, DV, T), 1),
+                     dtype=torch.uint8, device=dev)
+    _hip.check(lib.gdn2_hip_backward_varlen(
+        _hip.ptr(q), _hip.ptr(k), _hip.ptr(v), _hip.ptr(g32), _hip.ptr(b), _hip.ptr(w), _hip.dtype_code(q.dtype),
+        float(scale), _hip.ptr(s0), _hip.ptr(do), _hip.dtype_code(do.dtype), _hip.ptr(dht32),
+        _hip.ptr(dq), _hip.ptr(dk), _hip.ptr(dv), _hip.ptr(dg), _hip.ptr(db), _hip.ptr(dw), _hip.ptr(ds0),
+        _hip.ptr(ws), _hip.ptr(cu), N, T, H, HK, DK, DV, _hip.stream_of(dev)), "gdn2_hip_backward_varlen")
+    return (dq, dk, dv, dg.to(g.dtype), db, dw,
+            None if ds0 is None else ds0.to(initial_state.dtype))

@@ -242,6 +242,32 @@ int gdn2_hip_backward(const void* q, const void* k, const void* v, const float* 
                       void* stream);
 
 /*
+ * Training backward of packed variable-length sequences (the backward of
+ * gdn2_hip_prefill_varlen's forward): one row of T tokens holding nseq
+ * sequences, sequence s at tokens [cu_seqlens[s], cu_seqlens[s+1]) (int32,
+ * device memory, non-decreasing from 0 to T), each its own recurrence from
+ * initial_state[s]. Tensors as for gdn2_hip_backward with B = 1 and S = T;
+ * initial_state, d_final_state and d_initial_state are [nseq, H, DK, DV]. An
+ * empty sequence passes its final-state gradient through to d_initial_state.
+ * All sequences run in one set of launches: the per-chunk kernels take the
+ * forward's record slots (chunk c of sequence s at slot s + floor(cu[s]/64)
+ * + c; slots between sequences exit at once) and the scans run per
+ * (sequence, value head, 16 columns). Workspace (256-byte aligned):
+ * gdn2_hip_backward_varlen_workspace_bytes, the dense formula with
+ * ceil(T/64) + nseq chunk slots per head.
+ * No reference counterpart: the reference raises for cu_seqlens
+ * (gdn2/attention.py:142-145); this replaces one gdn2_hip_backward call per
+ * sequence.
+ */
+size_t gdn2_hip_backward_varlen_workspace_bytes(int nseq, int H, int HK, int DK, int DV, long T);
+int gdn2_hip_backward_varlen(const void* q, const void* k, const void* v, const float* g, const void* b,
+                             const void* w, int in_dtype, float scale, const float* initial_state,
+                             const void* d_out, int do_dtype, const float* d_final_state, void* dq, void* dk,
+                             void* dv, float* dg, void* db, void* dw, float* d_initial_state, void* workspace,
+                             const int* cu_seqlens, int nseq, long T, int H, int HK, int DK, int DV,
+                             void* stream);
+
+/*
  * One GatedDeltaNet2 decode call of n tokens for B sequences (B*n <= 8), as
  * three launches on one stream: the projections (the fused weight w_proj
  * [4*HK*DK + 3*H*DV, hidden], rows q | k | v | b | w | f | o_gate) with the

@@ -186,3 +186,43 @@ def test_backward_sixteen_chunks_full_head_dims():
         e = rel_err(a, r)
         print(f"  {name} rel err {e:.2e}", flush=True)
         assert e < 1e-4, name
+
+
+@pytest.mark.parametrize("lens,H,HK,DK,DV,dtype,state,dht", [
+    ([70, 0, 130, 5, 64, 1, 200], 4, 2, 64, 48, torch.float32, True, True),
+    ([300, 17, 0, 0, 128, 65], 2, 2, 128, 128, torch.bfloat16, True, False),
+    ([33] * 20 + [0, 190], 3, 3, 32, 32, torch.float32, False, True),
+    ([0, 0], 2, 1, 64, 64, torch.float32, True, True),
+])
+def test_packed_backward_equals_per_sequence_calls(lens, H, HK, DK, DV, dtype, state, dht):
+    """chunk_gdn2_varlen_bwd (one gdn2_hip_backward_varlen call) gives
+    bit-identical gradients to chunk_gdn2_bwd run on each sequence alone:
+    each record slot repeats the dense chunk's arithmetic and each scan
+    workgroup walks one sequence's chunks in the same order."""
+    from gdt2_tilelang_amd import chunk_gdn2_varlen_bwd
+    print(f"packed backward lens={lens} H={H} HK={HK} DK={DK} DV={DV} {dtype} state={state} dht={dht}", flush=True)
+    cu = torch.tensor([0] + list(torch.tensor(lens).cumsum(0)), dtype=torch.int32)
+    T, N = int(cu[-1]), len(lens)
+    q, k, v, g, b, w = (t.to(dtype).cuda() for t in _inputs(1, max(T, 1), H, HK, DK, DV, 4.0, 11))
+    q, k, v, g, b, w = (t[:, :T] for t in (q, k, v, g, b, w))
+    g = g.float()
+    gen = torch.Generator().manual_seed(12)
+    s0 = (torch.randn(N, H, DK, DV, generator=gen) * 0.3).cuda() if state else None
+    do = torch.randn(1, T, H, DV, generator=gen).to(dtype).cuda()
+    dh = (torch.randn(N, H, DK, DV, generator=gen) * 0.5).cuda() if dht else None
+    got = chunk_gdn2_varlen_bwd(q, k, v, g, b, w, None, cu.cuda(), s0, do, dh)
+    torch.cuda.synchronize()
+    for i, n in enumerate(lens):
+        a = int(cu[i])
+        sl = lambda t: t[:, a:a + n]
+        if n == 0:
+            if state:
+                want = dh[i] if dht else torch.zeros_like(s0[i])
+                assert torch.equal(got[6][i], want), (i, "dS0 pass-through")
+            continue
+        ref = chunk_gdn2_bwd(*(sl(t) for t in (q, k, v, g, b, w)), None,
+                             None if s0 is None else s0[i:i + 1], sl(do), None if dh is None else dh[i:i + 1])
+        for name, full, r in zip(NAMES[:6], got[:6], ref[:6]):
+            assert torch.equal(sl(full), r), (i, name)
+        if state:
+            assert torch.equal(got[6][i:i + 1], ref[6]), (i, "dS0")
