@@ -72,6 +72,26 @@ __device__ __forceinline__ void lds_barrier() { asm volatile("s_waitcnt lgkmcnt(
 // inside the branch); rows past the end are then zeroed by the caller.
 __device__ __forceinline__ long clamp_row(long t, long S) { return t < S ? t : S - 1; }
 
+// One input element in its storage format (DT fixed at compile time, so no
+// load sits inside a dtype branch): ld_raw returns its bits, as_f32 the value.
+// A prefetch keeps the bits and converts at the use, so that the compiler does
+// not wait for the load where it is issued.
+template <int DT>
+__device__ __forceinline__ uint32_t ld_raw(const void* __restrict__ p, size_t i) {
+  if constexpr (DT == DT_F32) return static_cast<const uint32_t*>(p)[i];
+  else return static_cast<const unsigned short*>(p)[i];
+}
+template <int DT>
+__device__ __forceinline__ float as_f32(uint32_t u) {
+  if constexpr (DT == DT_F32) return __uint_as_float(u);
+  else if constexpr (DT == DT_BF16) return __uint_as_float(u << 16);
+  else return f16_bits_to_f32(static_cast<unsigned short>(u));
+}
+template <int DT>
+__device__ __forceinline__ float ld_in(const void* __restrict__ p, size_t i) {
+  return as_f32<DT>(ld_raw<DT>(p, i));
+}
+
 // The tokens [t0, tend) of one chunk's workgroup. Dense batches: chunk c of
 // batch row bi, tend = S. Packed sequences (vl.cu, one batch row of S tokens):
 // c is a record slot (the forward's slot map, gdn2_prefill_layout.h), t0 its
@@ -137,9 +157,9 @@ constexpr int LA = L + 2;        // LDS pitch of the L x L arrays of kernel 1 (r
 template <int DK>
 constexpr int local_lds_floats() { return 3 * L * (DK + 4) + L * (DK + 4 > LA ? DK + 4 : LA) + L * LA + DK + 9 * 256; }
 
-template <int DK>
-__global__ __launch_bounds__(kLocalThreads) void bwd_local_kernel(const float* __restrict__ q, const float* __restrict__ k,
-                                                             const float* __restrict__ b, const float* __restrict__ g,
+template <int DK, int IDT>
+__global__ __launch_bounds__(kLocalThreads) void bwd_local_kernel(const void* __restrict__ q, const void* __restrict__ k,
+                                                             const void* __restrict__ b, const float* __restrict__ g,
                                                              int HK, long S, int NC, float scale,
                                                              float* __restrict__ rec, Varlen vl) {
   constexpr int P = DK + 4;
@@ -169,7 +189,8 @@ __global__ __launch_bounds__(kLocalThreads) void bwd_local_kernel(const float* _
     const int t = e / DK, i = e % DK;
     const size_t ix = key_index(bi, S, clamp_row(t0 + t, tend), HK, hk, DK, i);
     const float keep = t0 + t < tend ? 1.f : 0.f;
-    const float qv = keep * q[ix], kv = keep * k[ix], bv = keep * b[ix], gv = keep * g[ix];
+    const float qv = keep * ld_in<IDT>(q, ix), kv = keep * ld_in<IDT>(k, ix), bv = keep * ld_in<IDT>(b, ix);
+    const float gv = keep * g[ix];
     sq[t * P + i] = qv;
     sk[t * P + i] = kv;
     sbk[t * P + i] = bv * kv;
@@ -411,8 +432,8 @@ struct ScanCfg {
 // The scan of one workgroup (block lb of nblk): NBUF register sets of
 // A-operand rows, so the rows of the chunk NBUF - 1 steps ahead are requested
 // before the current chunk's products are issued.
-template <int DK, bool BACK, int NBUF>
-__device__ __forceinline__ void scan_body(const float* __restrict__ x1, const float* __restrict__ x2,
+template <int DK, bool BACK, int NBUF, int XDT>
+__device__ __forceinline__ void scan_body(const void* __restrict__ x1, const void* __restrict__ x2,
                                           const float* __restrict__ rec, const float* __restrict__ init,
                                           float* __restrict__ ck, float* __restrict__ fin, int H, int HK, int DV,
                                           long S, int NC, int lb, int nblk, Varlen vl) {
@@ -480,7 +501,8 @@ __device__ __forceinline__ void scan_body(const float* __restrict__ x1, const fl
     }
   };
   constexpr int NT = L * CT / kThreads;
-  float p1[NT], p2[NT], pk1[NT];   // raw values and their keep factors (applied when staged)
+  uint32_t p1[NT], p2[NT];         // raw input bits, converted when staged
+  float pk1[NT];                   // their keep factors
   auto fetch_z = [&](int c) {
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
@@ -488,8 +510,8 @@ __device__ __forceinline__ void scan_body(const float* __restrict__ x1, const fl
       const long tok = tbase + static_cast<long>(c) * L + t;
       const size_t ix = ((static_cast<size_t>(bit) * S + clamp_row(tok, tend)) * H + h) * DV + c0 + cl;
       pk1[n] = tok < tend ? 1.f : 0.f;
-      p1[n] = x1[ix];
-      p2[n] = BACK ? 0.f : x2[ix];
+      p1[n] = ld_raw<XDT>(x1, ix);
+      p2[n] = BACK ? 0u : ld_raw<XDT>(x2, ix);
     }
   };
   auto run = [&](int step, f32x4 (&aA)[C::TPW][C::KA_ / 4], f32x4 (&aZ)[C::TPW][C::KZ / 4],
@@ -499,7 +521,8 @@ __device__ __forceinline__ void scan_body(const float* __restrict__ x1, const fl
 #pragma unroll
     for (int n = 0; n < NT; ++n) {
       const int e = tid + n * kThreads;
-      sZ[(e / CT) * C::XP + e % CT] = pk1[n] * (BACK ? p1[n] : p1[n] * p2[n]);
+      const float a = as_f32<XDT>(p1[n]);
+      sZ[(e / CT) * C::XP + e % CT] = pk1[n] * (BACK ? a : a * as_f32<XDT>(p2[n]));
     }
     {                            // the token values first: the next step's staging waits only for them;
       fetch_z(chunk_of(step + 1 < nloop ? step + 1 : nloop - 1));
@@ -573,27 +596,27 @@ __device__ __forceinline__ void scan_body(const float* __restrict__ x1, const fl
 
 template <int DK, bool BACK>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void bwd_scan_kernel(
-    const float* __restrict__ x1, const float* __restrict__ x2, const float* __restrict__ rec,
+    const void* __restrict__ x1, const void* __restrict__ x2, const float* __restrict__ rec,
     const float* __restrict__ init, float* __restrict__ ck, float* __restrict__ fin, int H, int HK, int DV, long S,
     int NC) {
-  scan_body<DK, BACK, 3>(x1, x2, rec, init, ck, fin, H, HK, DV, S, NC, blockIdx.x, gridDim.x, Varlen{nullptr, 0});
+  scan_body<DK, BACK, 3, DT_F32>(x1, x2, rec, init, ck, fin, H, HK, DV, S, NC, blockIdx.x, gridDim.x, Varlen{nullptr, 0});
 }
 
 // Both scans in one launch: they read only the records and their own inputs,
 // so the first half of the workgroups runs the forward scan and the second
 // half the backward one, and with two waves per SIMD a CU holds one of each,
 // each hiding the other's per-step latency chain.
-template <int DK>
+template <int DK, int IDT, int ODT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(2, 2))) void bwd_scan2_kernel(
-    const float* __restrict__ v, const float* __restrict__ w, const float* __restrict__ dout,
+    const void* __restrict__ v, const void* __restrict__ w, const void* __restrict__ dout,
     const float* __restrict__ rec, const float* __restrict__ s0, const float* __restrict__ dht,
     float* __restrict__ sck, float* __restrict__ dsck, float* __restrict__ ds0, int H, int HK, int DV, long S,
     int NC, Varlen vl) {
   const int half = gridDim.x / 2;
   if (static_cast<int>(blockIdx.x) < half)
-    scan_body<DK, false, 1>(v, w, rec, s0, sck, nullptr, H, HK, DV, S, NC, blockIdx.x, half, vl);
+    scan_body<DK, false, 1, IDT>(v, w, rec, s0, sck, nullptr, H, HK, DV, S, NC, blockIdx.x, half, vl);
   else
-    scan_body<DK, true, 1>(dout, nullptr, rec, dht, dsck, ds0, H, HK, DV, S, NC, blockIdx.x - half, half, vl);
+    scan_body<DK, true, 1, ODT>(dout, nullptr, rec, dht, dsck, ds0, H, HK, DV, S, NC, blockIdx.x - half, half, vl);
 }
 
 // ---------------------------------------------------------------- kernel 4
@@ -622,10 +645,10 @@ __device__ __forceinline__ f32x4 mma(float a, float b, f32x4 c) {
   return __builtin_amdgcn_mfma_f32_16x16x4f32(a, b, c, 0, 0, 0);
 }
 
-template <int DK>
+template <int DK, int IDT, int ODT>
 __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))) void bwd_gradmm_kernel(
-    const float* __restrict__ k, const float* __restrict__ v, const float* __restrict__ g, const float* __restrict__ b,
-    const float* __restrict__ w, int dt, const float* __restrict__ dout, const float* __restrict__ rec,
+    const void* __restrict__ k, const void* __restrict__ v, const float* __restrict__ g, const void* __restrict__ b,
+    const void* __restrict__ w, int dt, const void* __restrict__ dout, const float* __restrict__ rec,
     const float* __restrict__ sck, const float* __restrict__ dsck, void* __restrict__ dv, void* __restrict__ dw,
     float* __restrict__ gs, int H, int HK, int DV, long S, int NC, Varlen vl) {
   constexpr int XP = CT + 1;          // LDS pitch of the 16-column arrays
@@ -668,7 +691,7 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     const int t = e / DK, i = e % DK;
     const size_t ix = key_index(bi, S, clamp_row(t0 + t, tend), HK, hk, DK, i);
     const float keep = t0 + t < tend ? 1.f : 0.f;
-    const float kv = keep * k[ix], bv = keep * b[ix];
+    const float kv = keep * ld_in<IDT>(k, ix), bv = keep * ld_in<IDT>(b, ix);
     const float gt = sG[t * DK + i];
     const int o = t * EP + (i / KD) * (KD + 1) + i % KD;
     sEn[o] = -bv * kv * __expf(gt);
@@ -697,7 +720,8 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
   // dv, dw. The next block's are requested while the current one is worked on.
   constexpr int NSE = DK * CT / kThreads, NTE = L * CT / kThreads;
   float pS[NSE], pdS[NSE];
-  float pO[NTE], pV[4], pW[4], kO[NTE], kVW[4];   // raw values and their keep factors
+  uint32_t pO[NTE], pV[4], pW[4];   // raw input bits, converted at their use
+  float kO[NTE], kVW[4];             // their keep factors
   auto fetch = [&](int cb) {
 #pragma unroll
     for (int n = 0; n < NSE; ++n) {
@@ -709,15 +733,15 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
     for (int n = 0; n < NTE; ++n) {
       const int e = tid + n * kThreads, t = e / CT, cl = e % CT;
       kO[n] = t0 + t < tend ? 1.f : 0.f;
-      pO[n] = dout[((static_cast<size_t>(bi) * S + clamp_row(t0 + t, tend)) * H + h) * DV + cb + cl];
+      pO[n] = ld_raw<ODT>(dout, ((static_cast<size_t>(bi) * S + clamp_row(t0 + t, tend)) * H + h) * DV + cb + cl);
     }
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
       const int t = 16 * wave + 4 * gq + e;
       const size_t ix = ((static_cast<size_t>(bi) * S + clamp_row(t0 + t, tend)) * H + h) * DV + cb + m;
       kVW[e] = t0 + t < tend ? 1.f : 0.f;
-      pV[e] = v[ix];
-      pW[e] = w[ix];
+      pV[e] = ld_raw<IDT>(v, ix);
+      pW[e] = ld_raw<IDT>(w, ix);
     }
   };
   fetch(0);
@@ -732,14 +756,14 @@ __global__ __launch_bounds__(kThreads) __attribute__((amdgpu_waves_per_eu(1, 1))
 #pragma unroll
     for (int n = 0; n < NTE; ++n) {
       const int e = tid + n * kThreads, t = e / CT, cl = e % CT;
-      sdO[t * XP + cl] = kO[n] * pO[n];
+      sdO[t * XP + cl] = kO[n] * as_f32<ODT>(pO[n]);
     }
     f32x4 zc;
     float vv[4], ww[4];
 #pragma unroll
     for (int e = 0; e < 4; ++e) {
-      vv[e] = kVW[e] * pV[e];
-      ww[e] = kVW[e] * pW[e];
+      vv[e] = kVW[e] * as_f32<IDT>(pV[e]);
+      ww[e] = kVW[e] * as_f32<IDT>(pW[e]);
       zc[e] = ww[e] * vv[e];
     }
     if (cb + CT < DV) fetch(cb + CT);
@@ -833,9 +857,9 @@ constexpr int PWC = 32;               // channels per pairwise workgroup
 constexpr int PWP = PWC + 1;          // LDS pitch
 constexpr int LQ = L + 4;             // pitch of the L x L arrays (16-byte rows)
 
-template <int DK>
+template <int DK, int IDT>
 __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
-    const float* __restrict__ q, const float* __restrict__ k, const float* __restrict__ g, const float* __restrict__ b,
+    const void* __restrict__ q, const void* __restrict__ k, const float* __restrict__ g, const void* __restrict__ b,
     const float* __restrict__ gs, float* __restrict__ part, void* __restrict__ odq, void* __restrict__ odk,
     void* __restrict__ odb, float* __restrict__ odg, int dt, int H, int HK, long S, int NC, float scale,
     Varlen vl) {
@@ -868,13 +892,18 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
   const long t0 = win.t0, tend = win.tend;
   const float* src = gs + (static_cast<size_t>(bh) * NC + c) * G::STRIDE;
   const int i0 = cb * CW;
+  // pass n stages row 8 n + tid / CW, channel tid % CW: the rows t_r and the
+  // channel this thread takes in the pairwise loop below, so it keeps its b
+  float bkeep[L * CW / kThreads];
 #pragma unroll
   for (int e0 = 0; e0 < L * CW; e0 += kThreads) {
     const int e = e0 + tid;
     const int t = e / CW, ii = e % CW;
     const size_t ix = key_index(bi, S, clamp_row(t0 + t, tend), HK, hk, DK, i0 + ii);
     const float keep = t0 + t < tend ? 1.f : 0.f;
-    const float qv = keep * q[ix], kv = keep * k[ix], bv = keep * b[ix], gv = keep * g[ix];
+    const float qv = keep * ld_in<IDT>(q, ix), kv = keep * ld_in<IDT>(k, ix), bv = keep * ld_in<IDT>(b, ix);
+    const float gv = keep * g[ix];
+    bkeep[e0 / kThreads] = bv;
     pq[t * PWP + ii] = qv;
     pk[t * PWP + ii] = kv;
     pbk[t * PWP + ii] = bv * kv;
@@ -982,7 +1011,7 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
     const int t = tp + TS * r;
     const float qv = pq[t * PWP + ii], kv = pk[t * PWP + ii], bkv = pbk[t * PWP + ii];
     const bool valid = t0 + t < tend;
-    const float bv = valid ? b[key_index(bi, S, t0 + t, HK, hk, DK, i)] : 0.f;
+    const float bv = bkeep[r];
     const float ga = __builtin_amdgcn_exp2f(gt[r]), gd = __builtin_amdgcn_exp2f(kLog2e * gl - gt[r]);
     const float fQg = src[G::QG + t * DK + i], fE = src[G::E + t * DK + i], fKG = src[G::KG + t * DK + i];
     const float dq = scale * (ga * fQg + rq[r]);
@@ -1030,10 +1059,10 @@ __global__ __launch_bounds__(kThreads) void bwd_gradpw_kernel(
 }
 
 // ---------------------------------------------------------------- input copies
-// The kernels above read fp32 operands: a 16-bit input is widened into the
-// workspace first (one pass), so their loads carry no dtype dispatch (a
-// run-time dtype switch around a load makes the compiler wait for each load
-// inside its branch).
+// The kernels above read q, k, b, v, w in their storage dtype and d_out in
+// the same dtype or fp32 (template parameters, so no load sits inside a dtype
+// branch). A d_out of another 16-bit dtype is widened into the workspace
+// first.
 struct WidenJobs {                // up to six 16-bit tensors widened in one launch
   const void* src[6];
   float* dst[6];
@@ -1115,11 +1144,13 @@ static size_t backward_ws(int B, int H, int HK, int DK, int DV, long S, long NC)
   auto up = [](size_t x) { return (x + 255) / 256 * 256; };
   const size_t rec = up(static_cast<size_t>(B) * HK * NC * stride * 4);
   const size_t ck = up(static_cast<size_t>(B) * H * NC * DK * DV * 4);
-  const size_t part = up(4 * static_cast<size_t>(B) * S * H * DK * 4);
+  // per-value-head shares of dq, dk, db, dg: only with grouped heads (with one
+  // value head per key head the pairwise pass writes the outputs itself)
+  const size_t part = H == HK ? 0 : up(4 * static_cast<size_t>(B) * S * H * DK * 4);
   long gstride = DK == 32 ? bw::GS<32>::STRIDE : DK == 64 ? bw::GS<64>::STRIDE : bw::GS<128>::STRIDE;
   const size_t gsb = up(static_cast<size_t>(B) * H * NC * gstride * 4);
-  const size_t nk = static_cast<size_t>(B) * S * HK * DK, nv = static_cast<size_t>(B) * S * H * DV;
-  const size_t wide = 3 * up(nk * 4) + 3 * up(nv * 4);   // fp32 q, k, b, v, w, do
+  const size_t nv = static_cast<size_t>(B) * S * H * DV;
+  const size_t wide = up(nv * 4);   // fp32 d_out, when its dtype is neither the inputs' nor fp32
   return rec + 2 * ck + part + gsb + wide;
 }
 
@@ -1132,6 +1163,35 @@ size_t backward_varlen_workspace_bytes(int nseq, int H, int HK, int DK, int DV, 
 }
 
 namespace {
+// The five launches for one (input dtype, d_out dtype) pair.
+template <int DK, int IDT, int ODT>
+hipError_t backward_launches(const void* q, const void* k, const void* v, const float* g, const void* b,
+                             const void* w, float scale, const float* s0, const void* dout, const float* dht,
+                             void* dq, void* dk, void* dv, float* dg, void* db, void* dw, float* ds0, float* rec,
+                             float* sck, float* dsck, float* part, float* gsc, int B, int NSQ, int H, int HK, int DV,
+                             long S, int NC, Varlen vl, hipStream_t stream) {
+  constexpr int lds1 = bw::local_lds_floats<DK>() * 4;
+  static std::atomic<unsigned long long> lds_set{0};   // per device
+  {
+    const hipError_t e = set_dyn_lds_once(reinterpret_cast<const void*>(&bw::bwd_local_kernel<DK, IDT>), lds1, lds_set);
+    if (e != hipSuccess) return e;
+  }
+  hipLaunchKernelGGL((bw::bwd_local_kernel<DK, IDT>), dim3(NC, B * HK), dim3(bw::kLocalThreads), lds1, stream, q, k,
+                     b, g, HK, S, NC, scale, rec, vl);
+  hipLaunchKernelGGL((bw::bwd_scan2_kernel<DK, IDT, ODT>), dim3(2 * (DV / bw::CT) * NSQ * H), dim3(bw::kThreads), 0,
+                     stream, v, w, dout, rec, s0, dht, sck, dsck, ds0, H, HK, DV, S, NC, vl);
+  hipLaunchKernelGGL((bw::bwd_gradmm_kernel<DK, IDT, ODT>), dim3(NC, B * H), dim3(bw::kThreads), 0, stream, k, v, g,
+                     b, w, IDT, dout, rec, sck, dsck, dv, dw, gsc, H, HK, DV, S, NC, vl);
+  constexpr int NB = DK / bw::PWC > 0 ? DK / bw::PWC : 1;
+  hipLaunchKernelGGL((bw::bwd_gradpw_kernel<DK, IDT>), dim3(NC * NB * B * H), dim3(bw::kThreads), 0, stream, q, k, g,
+                     b, gsc, part, dq, dk, db, dg, IDT, H, HK, S, NC, scale, vl);
+  if (H == HK) return hipGetLastError();   // the pairwise pass wrote the outputs
+  const long n_key = static_cast<long>(B) * S * HK * DK;
+  hipLaunchKernelGGL(bw::bwd_sum_kernel, dim3(static_cast<unsigned>((n_key + bw::kThreads - 1) / bw::kThreads)),
+                     dim3(bw::kThreads), 0, stream, part, dq, dk, db, dg, IDT, n_key, H, HK, DK);
+  return hipGetLastError();
+}
+
 template <int DK>
 hipError_t launch_backward_t(const void* q, const void* k, const void* v, const float* g, const void* b,
                              const void* w, int dt, float scale, const float* s0, const void* dout, int do_dt,
@@ -1143,12 +1203,6 @@ hipError_t launch_backward_t(const void* q, const void* k, const void* v, const 
   // (sequence, value head, tile) and the state arrays hold nseq rows
   const int NC = static_cast<int>((S + bw::L - 1) / bw::L) + (vl.cu ? vl.nseq : 0);
   const int NSQ = vl.cu ? vl.nseq : B;   // state rows
-  constexpr int lds1 = bw::local_lds_floats<DK>() * 4;
-  static std::atomic<unsigned long long> lds_set{0};   // per device
-  {
-    const hipError_t e = set_dyn_lds_once(reinterpret_cast<const void*>(&bw::bwd_local_kernel<DK>), lds1, lds_set);
-    if (e != hipSuccess) return e;
-  }
   if (S == 0) {   // no tokens: the initial-state gradient is the final-state one (or zero)
     if (ds0)
       hipLaunchKernelGGL((bw::bwd_scan_kernel<DK, true>), dim3(DV / bw::CT * NSQ * H), dim3(bw::kThreads), 0, stream,
@@ -1163,50 +1217,35 @@ hipError_t launch_backward_t(const void* q, const void* k, const void* v, const 
   ws += up(static_cast<size_t>(B) * H * NC * DK * DV * 4);
   float* dsck = reinterpret_cast<float*>(ws);
   ws += up(static_cast<size_t>(B) * H * NC * DK * DV * 4);
-  float* part = reinterpret_cast<float*>(ws);
-  ws += up(4 * static_cast<size_t>(B) * S * H * DK * 4);
+  float* part = H == HK ? nullptr : reinterpret_cast<float*>(ws);
+  if (H != HK) ws += up(4 * static_cast<size_t>(B) * S * H * DK * 4);
   float* gsc = reinterpret_cast<float*>(ws);
   ws += up(static_cast<size_t>(B) * H * NC * bw::GS<DK>::STRIDE * 4);
-  const long nk = static_cast<long>(B) * S * HK * DK, nv = static_cast<long>(B) * S * H * DV;
-  // fp32 operands: the inputs themselves when they are fp32, else widened
-  // copies (every 16-bit input in one launch)
-  bw::WidenJobs jobs{};
-  auto widen = [&](const void* src, int sdt, long n) -> const float* {
-    float* dst = reinterpret_cast<float*>(ws);
-    ws += up(static_cast<size_t>(n) * 4);
-    if (sdt == DT_F32) return static_cast<const float*>(src);
-    const int j = jobs.njobs++;
-    jobs.src[j] = src;
-    jobs.dst[j] = dst;
-    jobs.n[j] = n;
-    jobs.dt[j] = sdt;
-    jobs.first[j + 1] = jobs.first[j] + static_cast<int>((n + bw::kWidenPer * bw::kThreads - 1) /
-                                                         (bw::kWidenPer * bw::kThreads));
-    return dst;
-  };
-  const float* qf = widen(q, dt, nk);
-  const float* kf = widen(k, dt, nk);
-  const float* bf = widen(b, dt, nk);
-  const float* vf = widen(v, dt, nv);
-  const float* wf = widen(w, dt, nv);
-  const float* of = widen(dout, do_dt, nv);
-  if (jobs.first[jobs.njobs] > 0)
-    hipLaunchKernelGGL(bw::bwd_widen_kernel, dim3(jobs.first[jobs.njobs]), dim3(bw::kThreads), 0, stream, jobs);
-
-  hipLaunchKernelGGL(bw::bwd_local_kernel<DK>, dim3(NC, B * HK), dim3(bw::kLocalThreads), lds1, stream, qf, kf, bf, g,
-                     HK, S, NC, scale, rec, vl);
-  hipLaunchKernelGGL(bw::bwd_scan2_kernel<DK>, dim3(2 * (DV / bw::CT) * NSQ * H), dim3(bw::kThreads), 0, stream, vf,
-                     wf, of, rec, s0, dht, sck, dsck, ds0, H, HK, DV, S, NC, vl);
-  hipLaunchKernelGGL(bw::bwd_gradmm_kernel<DK>, dim3(NC, B * H), dim3(bw::kThreads), 0, stream, kf, vf, g, bf, wf, dt,
-                     of, rec, sck, dsck, dv, dw, gsc, H, HK, DV, S, NC, vl);
-  constexpr int NB = DK / bw::PWC > 0 ? DK / bw::PWC : 1;
-  hipLaunchKernelGGL(bw::bwd_gradpw_kernel<DK>, dim3(NC * NB * B * H), dim3(bw::kThreads), 0, stream, qf, kf, g, bf,
-                     gsc, part, dq, dk, db, dg, dt, H, HK, S, NC, scale, vl);
-  if (H == HK) return hipGetLastError();   // the pairwise pass wrote the outputs
-  const long n_key = static_cast<long>(B) * S * HK * DK;
-  hipLaunchKernelGGL(bw::bwd_sum_kernel, dim3(static_cast<unsigned>((n_key + bw::kThreads - 1) / bw::kThreads)),
-                     dim3(bw::kThreads), 0, stream, part, dq, dk, db, dg, dt, n_key, H, HK, DK);
-  return hipGetLastError();
+  // d_out in the inputs' dtype or fp32 is read in place; another 16-bit
+  // dtype is widened to fp32 first
+  int odt = do_dt;
+  if (do_dt != dt && do_dt != DT_F32) {
+    const long nv = static_cast<long>(B) * S * H * DV;
+    bw::WidenJobs jobs{};
+    jobs.src[0] = dout;
+    jobs.dst[0] = reinterpret_cast<float*>(ws);
+    jobs.n[0] = nv;
+    jobs.dt[0] = do_dt;
+    jobs.first[1] = static_cast<int>((nv + bw::kWidenPer * bw::kThreads - 1) / (bw::kWidenPer * bw::kThreads));
+    jobs.njobs = 1;
+    hipLaunchKernelGGL(bw::bwd_widen_kernel, dim3(jobs.first[1]), dim3(bw::kThreads), 0, stream, jobs);
+    dout = ws;
+    odt = DT_F32;
+  }
+#define GDN2_BWL(IDTV, ODTV)                                                                                  \
+  if (dt == IDTV && odt == ODTV)                                                                               \
+    return backward_launches<DK, IDTV, ODTV>(q, k, v, g, b, w, scale, s0, dout, dht, dq, dk, dv, dg, db, dw, ds0, \
+                                             rec, sck, dsck, part, gsc, B, NSQ, H, HK, DV, S, NC, vl, stream);
+  GDN2_BWL(DT_F32, DT_F32)
+  GDN2_BWL(DT_BF16, DT_BF16) GDN2_BWL(DT_BF16, DT_F32)
+  GDN2_BWL(DT_F16, DT_F16) GDN2_BWL(DT_F16, DT_F32)
+#undef GDN2_BWL
+  return hipErrorInvalidValue;
 }
 }  // namespace
 

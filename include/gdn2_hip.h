@@ -227,10 +227,11 @@ int gdn2_hip_gemv(const void* x, long ldx, const void* W, void* y, long ldy, int
  * holds gdn2_hip_backward_workspace_bytes(B, H, HK, DK, DV, S) bytes, which
  * grows linearly in B * S: with NC = ceil(S / 64) it is the fp32 chunk
  * records (B * HK * NC * 65.6 K floats at DK = 128), two fp32 per-chunk state
- * checkpoints (2 * B * H * NC * DK * DV * 4), four fp32 per-value-head
- * partial gradients (4 * B * S * H * DK * 4), the per-chunk gradient sums,
- * and fp32 copies of q, k, b, v, w and d_out. Examples at DK = DV = 128:
- * B=2 S=4096 H=HK=16: 1.75 GB; B=1 S=32768 H=HK=16: 7.0 GB.
+ * checkpoints (2 * B * H * NC * DK * DV * 4), with grouped heads (H > HK)
+ * four fp32 per-value-head partial gradients (4 * B * S * H * DK * 4), the
+ * per-chunk gradient sums, and room for an fp32 copy of d_out (used when
+ * do_dtype is neither in_dtype nor fp32). Examples at DK = DV = 128: B=2
+ * S=4096 H=HK=16: 1.14 GB; B=1 S=32768 H=HK=16: 4.6 GB.
  * Replaces: chunk_gdn2_bwd (gdn2/backward.py:912-994), called from
  * _GDN2Function.backward (gdn2/attention.py:79-99).
  */

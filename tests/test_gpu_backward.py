@@ -226,3 +226,23 @@ def test_packed_backward_equals_per_sequence_calls(lens, H, HK, DK, DV, dtype, s
             assert torch.equal(sl(full), r), (i, name)
         if state:
             assert torch.equal(got[6][i:i + 1], ref[6]), (i, "dS0")
+
+
+@pytest.mark.parametrize("in_dtype,do_dtype", [(torch.bfloat16, torch.float16), (torch.float16, torch.bfloat16),
+                                               (torch.float32, torch.bfloat16), (torch.bfloat16, torch.bfloat16)])
+def test_backward_output_gradient_dtypes(in_dtype, do_dtype):
+    """The inputs are read in their own dtype and do in the inputs' dtype or
+    fp32 in place; a do of another 16-bit dtype is widened first. Every
+    combination gives exactly the gradients of the same do values in fp32
+    (16-bit values are exact in fp32)."""
+    print(f"backward in={in_dtype} do={do_dtype}", flush=True)
+    B, S, H, HK, DK, DV = 1, 150, 4, 2, 64, 32
+    q, k, v, g, b, w = (t.cuda() for t in _inputs(B, S, H, HK, DK, DV, 4.0, 21))
+    q, k, v, b, w = (t.to(in_dtype) for t in (q, k, v, b, w))
+    do = torch.randn(B, S, H, DV, generator=torch.Generator().manual_seed(22)).to(do_dtype).cuda()
+    s0 = (torch.randn(B, H, DK, DV, generator=torch.Generator().manual_seed(23)) * 0.3).cuda()
+    got = chunk_gdn2_bwd(q, k, v, g, b, w, None, s0, do, None)
+    ref = chunk_gdn2_bwd(q, k, v, g, b, w, None, s0, do.float(), None)
+    torch.cuda.synchronize()
+    for name, a, r in zip(NAMES, got, ref):
+        assert torch.equal(a, r), name

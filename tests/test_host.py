@@ -236,8 +236,11 @@ def test_backward_host_validation():
     ck = 2 * 4 * 2 * 64 * 32 * 4
     part = 4 * 2 * 100 * 4 * 64 * 4
     up = lambda x: (x + 255) // 256 * 256
-    wide = 3 * up(2 * 100 * 2 * 64 * 4) + 3 * up(2 * 100 * 4 * 32 * 4)   # fp32 copies of q, k, b and v, w, do
+    wide = up(2 * 100 * 4 * 32 * 4)   # an fp32 copy of do (a 16-bit do of another dtype than the inputs)
     assert wsb(2, 4, 2, 64, 32, 100) == up(rec) + 2 * up(ck) + up(part) + up(gs) + wide
+    # one value head per key head: the pairwise pass writes the outputs, no gradient shares
+    rec1 = 2 * 4 * 2 * (64 * 64 + 64 * 64 + 64 * 64 + 4096 + 4096 + 64 + 64 * 64 + 64 * 64) * 4
+    assert wsb(2, 4, 4, 64, 32, 100) == up(rec1) + 2 * up(ck) + up(gs) + wide
     fake = ctypes.c_void_p(256)   # never dereferenced: validation fails first
     args = [fake] * 6
     tail = [fake] * 8
