@@ -42,6 +42,9 @@ ALG_BYTES_PREFILL = (5 * B1 * S1 * H1 * D1 * 2) + (B1 * S1 * H1 * D1 * 4) \
 BS = 64
 FLOPS_PER_CHUNK = 2 * BS * BS * (3 * D1 + 2 * D1) + 6 * BS * D1 * D1
 ALG_FLOPS_PREFILL = FLOPS_PER_CHUNK * B1 * H1 * (S1 // BS)
+# the reference benchmark's count (bench/bench_gdn2.py:55-64): four [BS, BS] x
+# [BS, D] products and two [BS, DK] x [DK, DV] products per chunk
+REF_FLOPS_PREFILL = (2 * BS * BS * (2 * D1 + 2 * D1) + 2 * 2 * BS * D1 * D1) * B1 * H1 * (S1 // BS)
 
 
 def log(msg):
@@ -584,6 +587,9 @@ def main():
             "kernel_us": {"chunk_local": round(cl_ms * 1e3, 2), "scan": round(sc_ms * 1e3, 2)},
             "gemm_tflops": round(ALG_FLOPS_PREFILL / kern_s / 1e12, 1),
             "gemm_frac_of_bf16_peak": round(ALG_FLOPS_PREFILL / kern_s / 1e12 / BF16_DENSE_TFLOPS, 4),
+            "gemm_gflop_per_step": round(ALG_FLOPS_PREFILL / 1e9, 2),
+            "reference_formula_gflop_per_step": round(REF_FLOPS_PREFILL / 1e9, 2),
+            "reference_formula_tflops": round(REF_FLOPS_PREFILL / kern_s / 1e12, 1),
             "mfma_busy_pmc": read_mfma_busy(),
             "mfma_busy_source": "profiles/mfma_busy_pmc.txt (rocprofv3 --pmc run of this bench, committed; "
                                 "not counted in this run)",
