@@ -128,6 +128,17 @@ def chunk_gdn2_varlen_fwd(q, k, v, g, b, w, scale, cu_seqlens, initial_state=Non
     return o, (final.to(st_dt) if output_final_state else None)
 
 
+def _check_state_arg(name, t, shape, dev):
+    """A per-sequence state argument (initial state or final-state gradient):
+    None, or a tensor of ``shape`` on the op's device."""
+    if t is None:
+        return
+    if t.device != dev:
+        raise ValueError(f"all tensors must be on {dev}; got {t.device} for {name}")
+    if tuple(t.shape) != tuple(shape):
+        raise ValueError(f"{name} has shape {tuple(t.shape)}, expected {tuple(shape)}")
+
+
 def chunk_gdn2_bwd(q, k, v, g, b, w, scale, initial_state, do, dht, config: GDN2Config = DEFAULT_KERNEL_CONFIG):
     """Chunkwise training backward on the gfx950 kernels.
 
@@ -148,6 +159,8 @@ def chunk_gdn2_bwd(q, k, v, g, b, w, scale, initial_state, do, dht, config: GDN2
         raise ValueError(f"hip backward supports DK in (32, 64, 128) and DV % 16 == 0; got DK={DK}, DV={DV}")
     if tuple(do.shape) != (B, S, H, DV):
         raise ValueError(f"do has shape {tuple(do.shape)}, expected {(B, S, H, DV)}")
+    _check_state_arg("initial_state", initial_state, (B, H, DK, DV), dev)
+    _check_state_arg("dht", dht, (B, H, DK, DV), dev)
     scale = DK ** -0.5 if scale is None else scale
     q, k, v, b, w, do = (t.contiguous() for t in (q, k, v, b, w, do))
     g32 = g.float().contiguous()
@@ -198,11 +211,10 @@ def chunk_gdn2_varlen_bwd(q, k, v, g, b, w, scale, cu_seqlens, initial_state, do
     scale = DK ** -0.5 if scale is None else scale
     q, k, v, b, w, do = (t.contiguous() for t in (q, k, v, b, w, do))
     g32 = g.float().contiguous()
+    _check_state_arg("initial_state", initial_state, (N, H, DK, DV), dev)
+    _check_state_arg("dht", dht, (N, H, DK, DV), dev)
     s0 = None
     if initial_state is not None:
-        _require_device(q, initial_state)
-        if tuple(initial_state.shape) != (N, H, DK, DV):
-            raise ValueError(f"initial_state has shape {tuple(initial_state.shape)}, expected {(N, H, DK, DV)}")
         s0 = initial_state.to(config.state_dtype).to(torch.float32).contiguous()
     dht32 = None if dht is None else dht.to(torch.float32).contiguous()
     dq, dk, db = (torch.empty(1, T, HK, DK, dtype=q.dtype, device=dev) for _ in range(3))

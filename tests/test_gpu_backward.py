@@ -246,3 +246,22 @@ def test_backward_output_gradient_dtypes(in_dtype, do_dtype):
     torch.cuda.synchronize()
     for name, a, r in zip(NAMES, got, ref):
         assert torch.equal(a, r), name
+
+
+def test_backward_state_argument_shapes():
+    """A wrong-shaped initial state or final-state gradient is refused before
+    any launch (the kernels would read past it)."""
+    from gdt2_tilelang_amd import chunk_gdn2_varlen_bwd
+    q, k, v, g, b, w = (t.cuda() for t in _inputs(1, 100, 2, 2, 64, 64, 4.0, 31))
+    do = torch.randn(1, 100, 2, 64, device="cuda")
+    good = torch.zeros(1, 2, 64, 64, device="cuda")
+    bad = torch.zeros(2, 2, 64, 64, device="cuda")
+    with pytest.raises(ValueError, match="dht"):
+        chunk_gdn2_bwd(q, k, v, g, b, w, None, good, do, bad)
+    with pytest.raises(ValueError, match="initial_state"):
+        chunk_gdn2_bwd(q, k, v, g, b, w, None, bad, do, None)
+    cu = torch.tensor([0, 40, 100], dtype=torch.int32, device="cuda")
+    with pytest.raises(ValueError, match="dht"):
+        chunk_gdn2_varlen_bwd(q, k, v, g, b, w, None, cu, None, do, good)
+    chunk_gdn2_varlen_bwd(q, k, v, g, b, w, None, cu, None, do, bad)   # two sequences: [2, H, DK, DV]
+    torch.cuda.synchronize()
