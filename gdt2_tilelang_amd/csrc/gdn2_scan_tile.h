@@ -1,5 +1,5 @@
-// Helpers shared by the transition-form scan kernels (DK = 128): fp16 MFMA,
-// per-column power-of-two scales of the fp16 state and Z operands.
+// Helpers of the factored-record scan (DK = 128): fp16 MFMA, per-column
+// power-of-two scales of the fp16 state, Y and Z operands.
 #pragma once
 
 #include "gdn2_common.h"
@@ -37,11 +37,6 @@ __device__ __forceinline__ float col_scale(float mx, float* inv) {
   se = se < -126 ? -126 : (se > 126 ? 126 : se);
   *inv = __uint_as_float(static_cast<uint32_t>(127 - se) << 23);
   return __uint_as_float(static_cast<uint32_t>(127 + se) << 23);
-}
-
-// A D-layout quad (4 consecutive k of one column) times sc as fp16 (round to nearest even).
-__device__ __forceinline__ void put_quad_f16(unsigned short* dst, const f32x4& x, float sc) {
-  *reinterpret_cast<uint2*>(dst) = make_uint2(pack2_f16(x[0], x[1], sc), pack2_f16(x[2], x[3], sc));
 }
 
 // max over the lanes that hold the same column quad: lane % CQ (CQ in {4, 8,
