@@ -251,3 +251,33 @@ def test_backward_host_validation():
     assert call(1, 64, 24) == -2
     assert call(1, 64, 64, ws=ctypes.c_void_p(264)) == -1
     assert call(1, 64, 64, ptrs=[None] + args[1:]) == -1
+
+
+def test_backward_varlen_host_validation():
+    """gdn2_hip_backward_varlen: the workspace size is the dense formula with
+    ceil(T/64) + nseq chunk slots, and bad arguments are refused before any
+    launch (no GPU needed)."""
+    lib = _hip.lib()
+    wsv = lib.gdn2_hip_backward_varlen_workspace_bytes
+    wsb = lib.gdn2_hip_backward_workspace_bytes
+    up = lambda x: (x + 255) // 256 * 256
+    assert wsv(0, 2, 2, 64, 64, 100) == 0            # nseq >= 1
+    assert wsv(3, 2, 2, 48, 64, 100) == 0            # DK not in (32, 64, 128)
+    assert wsv(3, 3, 2, 64, 64, 100) == 0            # HK must divide H
+    # T = 100, 3 sequences: 2 + 3 = 5 slots per head, against 2 chunks for a dense row
+    H, HK, DK, DV, T, N = 4, 2, 64, 32, 100, 3
+    rec = HK * 5 * (64 * 64 + 64 * 64 + 64 * 64 + 4096 + 4096 + 64 + 64 * 64 + 64 * 64) * 4
+    ck = H * 5 * DK * DV * 4
+    part = 4 * T * H * DK * 4
+    gs = H * 5 * (3 * 64 * DK + 2 * 4096 + DK) * 4
+    wide = up(T * H * DV * 4)
+    assert wsv(N, H, HK, DK, DV, T) == up(rec) + 2 * up(ck) + up(part) + up(gs) + wide
+    assert wsv(N, H, HK, DK, DV, T) > wsb(1, H, HK, DK, DV, T)
+    fake = ctypes.c_void_p(256)   # never dereferenced: validation fails first
+    call = lambda dt, dk, cu=fake, ws=fake, nseq=N: lib.gdn2_hip_backward_varlen(
+        *([fake] * 6), dt, 0.1, None, fake, 1, None, *([fake] * 6), None, ws, cu, nseq, T, H, HK, dk, DV, None)
+    assert call(7, 64) == -1                  # dtype
+    assert call(1, 48) == -2                  # DK
+    assert call(1, 64, cu=None) == -1         # offsets missing
+    assert call(1, 64, nseq=0) == -1
+    assert call(1, 64, ws=ctypes.c_void_p(264)) == -1   # workspace alignment
