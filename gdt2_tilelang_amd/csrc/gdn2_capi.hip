@@ -27,7 +27,8 @@ hipError_t launch_backward_varlen(const void*, const void*, const void*, const f
 
 namespace {
 
-constexpr int kAbiVersion = 3;   // 2: grouped key heads (HK); 3: packed sequences
+constexpr int kAbiVersion = 4;   // 2: grouped key heads (HK); 3: packed sequences; 4: factored
+                                 // DK = 128 records (58 112 B), packed training backward
 
 bool dtype_ok(int dt) { return dt == GDN2_DTYPE_F32 || dt == GDN2_DTYPE_BF16 || dt == GDN2_DTYPE_F16; }
 

@@ -38,7 +38,7 @@ def test_library_exports_every_declared_symbol():
 
 def test_version_and_status_strings():
     lib = _hip.lib()
-    assert lib.gdn2_hip_version() >= 2
+    assert lib.gdn2_hip_version() >= 4
     assert lib.gdn2_hip_status_string(0) == b"success"
     assert b"invalid argument" in lib.gdn2_hip_status_string(-1)
     assert b"unsupported shape" in lib.gdn2_hip_status_string(-2)
